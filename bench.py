@@ -1,0 +1,223 @@
+#!/usr/bin/env python3
+"""Benchmark of the fovi hot path on one MI355X.
+
+Primary line (``value``): the C3 large kNN-conv layer forward -- B=64,
+16384 log-polar points in and out, k=25 (5x5 ref grid), 256 -> 256 channels,
+bf16 operands with fp32 accumulation -- in TFLOP/s of algorithmic work
+2*B*N_out*C_out*C_in*V, with its bf16-MFMA roofline fraction.
+
+Alongside, in the same JSON line: the C4 foveated sampler (128 images
+3x512x512 bf16, 4 fixations each = 512 views of 16384 points) in algorithmic
+GB/s against HBM peak, and the CPU baseline (the oracle's torch-CPU
+restatement of the reference op sequence on a bounded batch slice).
+
+Inputs are synthetic (seeded) and resident in HBM before timing starts.
+Timing: ``warmup`` untimed steps, then ``steps`` steps between HIP events on
+the stream the kernels are launched on, bracketed by device synchronisation.
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_FP8_TFLOPS = 5000.0
+PEAK_HBM_GBS = 8000.0
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def time_steps(fn, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms per step
+
+
+def bench_c3(steps, warmup, dev):
+    import torch
+    from fovi_amd.arch.knn import KNNConvLayer
+    from fovi_amd.sensing.coords import SamplingCoords
+    B, C, K, RES = 64, 256, 25, 128
+    t0 = time.time()
+    coords = SamplingCoords(16, 2.78, RES, style="logpolar")
+    layer = KNNConvLayer(C, C, K, coords, coords, device=dev)
+    log(f"[c3] tables built in {time.time() - t0:.1f}s")
+    g = torch.Generator(device=dev).manual_seed(1)
+    with torch.no_grad():
+        layer.weight.copy_(torch.randn(layer.weight.shape, generator=g, device=dev) * (1.0 / (C * K)) ** 0.5)
+    gx = torch.Generator(device=dev).manual_seed(0)
+    # channels-last storage [B, N, C], handed to the layer as the [B, C, N] view
+    x = torch.randn(B, RES * RES, C, generator=gx, device=dev, dtype=torch.bfloat16).transpose(1, 2)
+    with torch.no_grad():
+        ms = time_steps(lambda: layer(x), steps, warmup)
+    flops = 2.0 * B * RES * RES * C * C * layer.ref_coords.shape[0]
+    tflops = flops / (ms * 1e-3) / 1e12
+    log(f"[c3] {ms:.3f} ms/step  {tflops:.1f} TFLOP/s  ({100 * tflops / PEAK_BF16_TFLOPS:.1f}% of bf16 peak)")
+    return dict(ms=ms, flops=flops, tflops=tflops, layer=layer, x=x)
+
+
+def sampler_algorithmic_bytes(sampler, img, fix, sizes, vmap, mode):
+    """Output bytes + sum over views of distinct in-bounds tap pixels x C x element size."""
+    import torch
+    _, grid = sampler.sample_views(img, fix, sizes, view_image=vmap, return_grid=True)
+    n_img, C, H, W = img.shape
+    ix = (grid[..., 0] + 1.0) * (W * 0.5) - 0.5
+    iy = (grid[..., 1] + 1.0) * (H * 0.5) - 0.5
+    taps = []
+    if mode == "nearest":
+        taps.append((torch.round(ix), torch.round(iy)))
+    else:
+        fx, fy = torch.floor(ix), torch.floor(iy)
+        taps += [(fx, fy), (fx + 1, fy), (fx, fy + 1), (fx + 1, fy + 1)]
+    V = grid.shape[0]
+    view = torch.arange(V, device=grid.device).view(V, 1)
+    keys = []
+    for tx, ty in taps:
+        ok = (tx >= 0) & (tx < W) & (ty >= 0) & (ty < H)
+        k = view * (H * W) + ty.long() * W + tx.long()
+        keys.append(k[ok])
+    distinct = torch.unique(torch.cat(keys)).numel()
+    es = img.element_size()
+    out_bytes = V * C * grid.shape[1] * es
+    return out_bytes + distinct * C * es, out_bytes, distinct
+
+
+def bench_c4_sampler(steps, warmup, dev, mode="nearest"):
+    import numpy as np
+    import torch
+    from fovi_amd.sensing.samplers import GridSampler
+    B, Fx, RES, S = 128, 4, 128, 512
+    gi = torch.Generator(device=dev).manual_seed(0)
+    # two image sets (2 x 201 MB) rotated so the 256 MB MALL cannot hold the input
+    imgs = [torch.rand(B, 3, S, S, generator=gi, device=dev).bfloat16() for _ in range(2)]
+    gf = torch.Generator().manual_seed(2)
+    fix = 0.25 + 0.5 * torch.rand(B * Fx, 2, generator=gf)
+    sizes = np.array([[S, S]] * (B * Fx))
+    vmap = torch.arange(B).repeat_interleave(Fx)
+    sampler = GridSampler(16, 2.78, RES, device=dev, mode=mode, style="logpolar")
+    out = torch.empty(B * Fx, 3, RES * RES, device=dev, dtype=torch.bfloat16)
+    state = {"i": 0}
+    fix_d = fix.to(dev)
+
+    def step():
+        sampler.sample_views(imgs[state["i"] & 1], fix_d, sizes, view_image=vmap, out=out)
+        state["i"] += 1
+
+    with torch.no_grad():
+        ms = time_steps(step, steps, warmup)
+        nbytes, out_bytes, distinct = sampler_algorithmic_bytes(sampler, imgs[0], fix_d, sizes, vmap, mode)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"[c4 sampler {mode}] {ms:.3f} ms/step  {gbs:.0f} GB/s algorithmic "
+        f"({100 * gbs / PEAK_HBM_GBS:.1f}% of HBM peak); bytes {nbytes / 1e6:.1f} MB "
+        f"(out {out_bytes / 1e6:.1f} MB, {distinct} distinct taps)")
+    return dict(ms=ms, bytes=nbytes, gbs=gbs, images_per_s=B / (ms * 1e-3))
+
+
+def cpu_baseline_c3(c3, seconds_budget=25.0):
+    """Oracle (torch CPU fp32 restatement of knn.py:484-557) on a B=2 slice of C3."""
+    import torch
+    from oracle import knnconv_ref
+    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16") or 16), 16)
+    torch.set_num_threads(threads)
+    layer = c3["layer"]
+    bs = 2
+    x = c3["x"][:bs].float().cpu().contiguous()
+    idx = layer.knn_indices.cpu()
+    rf = layer.local_rf.cpu()
+    w = layer.weight.detach().float().cpu()
+    n_in = layer.in_coords.shape[0]
+    knnconv_ref.knnconv_forward(x, idx, n_in, rf, w)  # warmup
+    times = []
+    t_start = time.time()
+    while len(times) < 5 and (time.time() - t_start) < seconds_budget:
+        t = time.time()
+        knnconv_ref.knnconv_forward(x, idx, n_in, rf, w)
+        times.append(time.time() - t)
+    times.sort()
+    med = times[len(times) // 2]
+    flops = c3["flops"] * bs / 64
+    model = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": flops / med / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"C3 slice B={bs} of 64 (fp32 torch-CPU restatement of the reference op "
+                      f"sequence), median of {len(times)} runs = {med:.2f} s, linear in B; host "
+                      f"{model}, os.cpu_count()={os.cpu_count()}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-sampler", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              f"(the forward shards over batch with no communication, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    dev = torch.device("cuda:0")
+    c3 = bench_c3(args.steps, args.warmup, dev)
+    c4 = None if args.no_sampler else bench_c4_sampler(args.steps, args.warmup, dev, "nearest")
+    c4b = None if args.no_sampler else bench_c4_sampler(args.steps, args.warmup, dev, "bilinear")
+    cpu = None if args.no_cpu_baseline else cpu_baseline_c3(c3)
+    line = {
+        "metric": "kNN-conv fwd TFLOP/s + sampler GB/s (% of MI355X roofline); images/sec",
+        "value": round(c3["tflops"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(c3["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded randn activations, N(0,1/(C_in*k)) weights)",
+        "config": {"workload": "C3 large kNN-conv layer: B=64, N_in=N_out=16384 log-polar (a=2.78), "
+                               "k=25, V=25, C_in=C_out=256, bf16 in/out, fp32 accumulate",
+                   "batch": 64, "points": 16384, "k": 25, "c_in": 256, "c_out": 256},
+        "roofline": {"bound": "mfma", "achieved": round(c3["tflops"], 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(c3["tflops"] / PEAK_BF16_TFLOPS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    if c4 is not None:
+        line["sampler_c4"] = {
+            "workload": "C4 sampler: 128 images 3x512x512 bf16, 4 fixations each (512 views), "
+                        "16384 log-polar points, bf16 out",
+            "nearest": {"GB/s": round(c4["gbs"], 1), "frac": round(c4["gbs"] / PEAK_HBM_GBS, 4),
+                        "ms": round(c4["ms"], 4), "images/s": round(c4["images_per_s"], 1)},
+            "bilinear": {"GB/s": round(c4b["gbs"], 1), "frac": round(c4b["gbs"] / PEAK_HBM_GBS, 4),
+                         "ms": round(c4b["ms"], 4), "images/s": round(c4b["images_per_s"], 1)},
+            "roofline": {"bound": "hbm", "peak": PEAK_HBM_GBS, "unit": "GB/s"},
+        }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,113 @@
+"""ctypes binding of libfovi_hip.so (declarations in include/fovi_hip.h).
+
+There is no fallback: if the library is missing or fails to load, every call
+raises. Tensors are passed as raw device pointers with element strides, and
+calls are enqueued on torch's current HIP stream.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
+
+ABI_VERSION = 1
+F32, BF16, F8E4M3 = 0, 1, 2
+NEAREST, BILINEAR = 0, 1
+PAD_ZEROS, PAD_BORDER = 0, 1
+
+_DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float8_e4m3fn: F8E4M3}
+
+# Every symbol include/fovi_hip.h declares.
+EXPORTED = ("fovi_abi_version", "fovi_last_error", "fovi_sampler_fwd", "fovi_knnconv_fwd",
+            "fovi_knnconv_pack_weight")
+
+
+class SamplerArgs(C.Structure):
+    _fields_ = [
+        ("img", C.c_void_p), ("img_dtype", C.c_int32), ("reserved0", C.c_int32),
+        ("n_img", C.c_int64), ("channels", C.c_int64), ("height", C.c_int64), ("width", C.c_int64),
+        ("img_stride", C.c_int64 * 4),
+        ("grid", C.c_void_p), ("n_points", C.c_int64), ("n_views", C.c_int64),
+        ("fix_loc", C.c_void_p), ("fix_half", C.c_void_p),
+        ("fix_half_wide", C.c_int32), ("reserved1", C.c_int32),
+        ("view_image", C.c_void_p),
+        ("mode", C.c_int32), ("padding", C.c_int32),
+        ("out", C.c_void_p), ("out_dtype", C.c_int32), ("reserved2", C.c_int32),
+        ("out_stride", C.c_int64 * 3),
+        ("grid_out", C.c_void_p),
+    ]
+
+
+class KnnConvArgs(C.Structure):
+    _fields_ = [
+        ("x", C.c_void_p), ("x_dtype", C.c_int32), ("reserved0", C.c_int32),
+        ("batch", C.c_int64), ("c_in", C.c_int64), ("n_in", C.c_int64),
+        ("x_stride", C.c_int64 * 3),
+        ("n_out", C.c_int64), ("k", C.c_int64), ("n_ref", C.c_int64),
+        ("slot_ptr", C.c_void_p), ("nbr_sorted", C.c_void_p),
+        ("w", C.c_void_p), ("w_dtype", C.c_int32), ("reserved1", C.c_int32),
+        ("c_out", C.c_int64), ("k_pad", C.c_int64),
+        ("bias", C.c_void_p), ("w_scale", C.c_void_p),
+        ("x_scale", C.c_float), ("reserved2", C.c_int32),
+        ("y", C.c_void_p), ("y_dtype", C.c_int32), ("reserved3", C.c_int32),
+        ("y_stride", C.c_int64 * 3),
+    ]
+
+
+_lib = None
+
+
+def load(path: str = LIB_PATH):
+    """Loads the library once; raises if it is missing or of another ABI."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built: run `python -m fovi_amd.build` (hipcc, gfx950)")
+    lib = C.CDLL(path)
+    lib.fovi_abi_version.restype = C.c_int
+    lib.fovi_last_error.restype = C.c_char_p
+    lib.fovi_sampler_fwd.argtypes = [C.POINTER(SamplerArgs), C.c_void_p]
+    lib.fovi_sampler_fwd.restype = C.c_int
+    lib.fovi_knnconv_fwd.argtypes = [C.POINTER(KnnConvArgs), C.c_void_p]
+    lib.fovi_knnconv_fwd.restype = C.c_int
+    lib.fovi_knnconv_pack_weight.argtypes = [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_void_p,
+                                             C.c_int32, C.c_int64, C.c_void_p, C.c_void_p]
+    lib.fovi_knnconv_pack_weight.restype = C.c_int
+    got = lib.fovi_abi_version()
+    if got != ABI_VERSION:
+        raise RuntimeError(f"{path}: ABI version {got}, expected {ABI_VERSION}")
+    _lib = lib
+    return lib
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODE[dt]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dt}") from None
+
+
+def ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def stream_handle(device=None):
+    return C.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def check(rc: int, what: str):
+    if rc != 0:
+        msg = load().fovi_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed: {msg}")
+
+
+def require_device(*tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("fovi_amd HIP kernels need GPU tensors (got a CPU tensor); "
+                               "there is no CPU fallback")

@@ -1,0 +1,291 @@
+"""kNN-convolution layer, drop-in for the reference ``fovi.arch.knn.KNNConvLayer``.
+
+Same constructor, parameters (``weight [C_out, C_in*V]``, ``bias [C_out]``,
+so state dicts load unchanged) and attributes (``k``/``_k``, ``knn_indices``,
+``knn_indices_pad_token``, ``ref_coords``, ``ref_grid_size``, ``local_rf``,
+``in_coords``/``out_coords``) as the reference (``fovi/arch/knn.py:401-719``).
+
+The forward is one HIP launch (``fovi_knnconv_fwd``): gather, slot sum and
+GEMM fused, with neighbour lists in slot-major CSR form in HBM. Input
+``[B, C_in, N_in]`` may have any strides; a channels-last view (a previous
+layer's output) takes the vectorised path. The output is ``[B, C_out, N_out]``
+as a transposed view of channels-last ``[B, N_out, C_out]`` storage, which is
+also what the reference returns (``F.linear(...).transpose(1,2)``,
+``knn.py:555``).
+
+Compute dtype: bf16 inputs, or any input under ``torch.autocast('cuda',
+dtype=torch.bfloat16)``, run the bf16 MFMA kernel with fp32 accumulation and
+return bf16 (the reference's autocast behaviour); fp32 inputs run the fp32
+kernel. Backward is not built: calling it raises.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+from einops import rearrange
+
+from .. import _lib
+from ..sensing.coords import SamplingCoords
+from . import knn_tables as T
+
+__all__ = [
+    "KNNBaseLayer",
+    "KNNConvLayer",
+    "KNN_CONV_REGISTRY",
+    "get_knn_conv_layer",
+    "get_in_out_coords",
+]
+
+_KCHUNK = 64  # reduction chunk of the MFMA kernel; packed weights are padded to it
+
+
+class KNNBaseLayer:
+    """Neighbour search shared by kNN layers (reference ``knn.py:14-224``)."""
+
+    def _compute_knns(self, batch_size=None):
+        if self.sample_cortex == "geodesic":
+            raise NotImplementedError("geodesic neighbourhoods need pygeodesic, which is not available")
+        if not self.sample_cortex:
+            raise NotImplementedError("visual-field (sample_cortex=False) neighbourhoods need the "
+                                      "isotropic pad ring, which is not built")
+        in_c, out_c = self.in_coords, self.out_coords
+        self.sample_coords_cart = torch.cat([in_c.cartesian.cpu(), in_c.cartesian_pad_coords.cpu()], 0)
+        if in_c.style in ("image", "logpolar"):
+            assert out_c.style == in_c.style
+            idx, dist, src = T.knn_logpolar(in_c.cortical.cpu(), out_c.cortical.cpu(), self._k, batch_size)
+            self.sample_coords = src
+            return idx, dist
+        raise NotImplementedError(f"style {in_c.style!r}: only log-polar neighbourhoods are built")
+
+
+class _KnnConvFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, layer, weight, bias):
+        return layer._launch(x)
+
+    @staticmethod
+    def backward(ctx, grad):
+        raise NotImplementedError("fovi_amd KNNConvLayer: backward is not implemented (forward-only "
+                                  "HIP kernels)")
+
+
+class KNNConvLayer(nn.Module, KNNBaseLayer):
+    """K-nearest-neighbour convolution on a sensor point cloud (HIP forward)."""
+
+    def __init__(self, in_channels, out_channels, k, in_coords, out_coords,
+                 device="cuda",
+                 arch_flag="",
+                 sample_cortex=True,
+                 bias=False,
+                 ref_frame_side_length=None,
+                 batch_size=None,
+                 ):
+        super().__init__()
+        assert isinstance(in_coords, SamplingCoords) and isinstance(out_coords, SamplingCoords)
+        self.in_channels = in_channels
+        self.out_channels = out_channels
+        self.in_coords = in_coords
+        self.out_coords = out_coords
+        self.device = device
+        self.arch_flag = arch_flag
+        self.sample_cortex = sample_cortex
+        self.ref_frame_side_length = ref_frame_side_length
+        self.batch_size = batch_size
+
+        n_in = in_coords.shape[0]
+        self.k = torch.minimum(torch.tensor(k), torch.tensor(n_in))
+        self._k = int(self.k.item())
+
+        knn_indices, knn_distances = self._compute_knns(batch_size)
+        self.knn_indices_pad_mask = knn_indices >= n_in
+        pad_token = knn_indices.clone()
+        pad_token[self.knn_indices_pad_mask] = n_in
+        self.knn_indices_batch_cache = pad_token
+
+        self.compute_reference_coords(arch_flag)
+        n_ref = self.ref_coords.shape[0]
+        self.weight = nn.Parameter(torch.empty(out_channels, in_channels * n_ref, device=device))
+        if bias:
+            self.bias = nn.Parameter(torch.empty(out_channels, device=device))
+        else:
+            self.register_parameter("bias", None)
+        self._init_conv_like()
+
+        self.slots = self.compute_local_rf_slots(knn_indices)
+        slot_ptr, nbr_sorted = T.csr_tables(knn_indices, self.slots, n_in, n_ref)
+        self.knn_indices = knn_indices.to(device)
+        self.knn_distances = knn_distances.to(device)
+        self.knn_indices_pad_token = pad_token.to(device)
+        self.knn_indices_pad_mask = self.knn_indices_pad_mask.to(device)
+        self.register_buffer("slot_ptr", slot_ptr.to(device), persistent=False)
+        self.register_buffer("nbr_sorted", nbr_sorted.to(device), persistent=False)
+        self._packed = {}
+
+    # -- setup ---------------------------------------------------------------
+    def _init_conv_like(self):
+        nn.init.kaiming_normal_(self.weight)
+        if self.bias is not None:
+            nn.init.zeros_(self.bias)
+
+    def compute_reference_coords(self, arch_flag):
+        """Square ref grid of side ``ref_frame_side_length`` or ceil(sqrt(k)) (``knn.py:559-597``)."""
+        if self.ref_frame_side_length is not None:
+            assert not len(arch_flag), "self.ref_frame_side_length is incompatible with use of arch_flag"
+            ref, side = T.reference_grid(self._k, side_length=self.ref_frame_side_length)
+        else:
+            if "fovref" in arch_flag or "circref" in arch_flag:
+                raise NotImplementedError(f"arch_flag {arch_flag!r}: only square ref grids are built")
+            ref, side = T.reference_grid(self._k, doubleres="doubleres" in arch_flag)
+        self.ref_grid_size = side
+        self.ref_coords = ref.to(self.device, dtype=self.in_coords.dtype)
+
+    def compute_local_rf_slots(self, knn_indices):
+        return T.local_rf_slots(knn_indices, self.sample_coords, self.sample_coords_cart,
+                                self.out_coords.cortical.cpu(), self.out_coords.cartesian.cpu(),
+                                self.ref_coords.cpu())
+
+    @property
+    def local_rf(self):
+        """One-hot ``[N_out, k, V]`` neighbour -> ref-slot map (built on demand)."""
+        return T.slots_to_one_hot(self.slots, self.ref_coords.shape[0]).to(self.weight.device)
+
+    def compute_local_rf(self):
+        return self.local_rf
+
+    def _apply_local_rf_to_weights(self):
+        weights = rearrange(self.weight, "d (c v) -> d c v", c=self.in_channels, v=self.ref_coords.shape[0])
+        return torch.einsum("dcv,nkv->ncdk", weights, self.local_rf)
+
+    # -- weights -------------------------------------------------------------
+    def _packed_weight(self, dtype):
+        w = self.weight
+        key = (dtype, w._version, w.data_ptr())
+        hit = self._packed.get(dtype)
+        if hit is not None and hit[0] == key:
+            return hit[1]
+        n_ref = self.ref_coords.shape[0]
+        k_pad = -(-self.in_channels * n_ref // _KCHUNK) * _KCHUNK
+        src = w.detach().to(torch.float32).contiguous()
+        out = torch.empty(self.out_channels, k_pad, dtype=dtype, device=w.device)
+        lib = _lib.load()
+        _lib.check(lib.fovi_knnconv_pack_weight(_lib.ptr(src), self.out_channels, self.in_channels, n_ref,
+                                                _lib.ptr(out), _lib.dtype_code(dtype), k_pad, None,
+                                                _lib.stream_handle(w.device)),
+                   "fovi_knnconv_pack_weight")
+        self._packed[dtype] = (key, out)
+        return out
+
+    # -- forward -------------------------------------------------------------
+    def _compute_dtype(self, x):
+        if x.dtype == torch.bfloat16:
+            return torch.bfloat16
+        if torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16:
+            return torch.bfloat16
+        if x.dtype == torch.float32:
+            return torch.float32
+        raise TypeError(f"KNNConvLayer: unsupported input dtype {x.dtype}")
+
+    def _launch(self, x):
+        _lib.require_device(x, self.weight)
+        if x.dim() != 3 or x.shape[1] != self.in_channels or x.shape[2] != self.in_coords.shape[0]:
+            raise ValueError(f"KNNConvLayer: expected [B, {self.in_channels}, {self.in_coords.shape[0]}], "
+                             f"got {tuple(x.shape)}")
+        dt = self._compute_dtype(x)
+        if x.dtype != dt:
+            x = x.to(dt)
+        w = self._packed_weight(dt)
+        bsz, n_out = x.shape[0], self.out_coords.shape[0]
+        y = torch.empty(bsz, n_out, self.out_channels, dtype=dt, device=x.device)
+        bias = None if self.bias is None else self.bias.detach().to(torch.float32).contiguous()
+        a = _lib.KnnConvArgs()
+        a.x = x.data_ptr(); a.x_dtype = _lib.dtype_code(dt)
+        a.batch, a.c_in, a.n_in = bsz, self.in_channels, x.shape[2]
+        a.x_stride[:] = list(x.stride())
+        a.n_out, a.k, a.n_ref = n_out, self._k, self.ref_coords.shape[0]
+        a.slot_ptr = self.slot_ptr.data_ptr(); a.nbr_sorted = self.nbr_sorted.data_ptr()
+        a.w = w.data_ptr(); a.w_dtype = _lib.dtype_code(dt)
+        a.c_out, a.k_pad = self.out_channels, w.shape[1]
+        a.bias = None if bias is None else bias.data_ptr()
+        a.y = y.data_ptr(); a.y_dtype = _lib.dtype_code(dt)
+        a.y_stride[:] = [y.stride(0), y.stride(2), y.stride(1)]
+        lib = _lib.load()
+        _lib.check(lib.fovi_knnconv_fwd(a, _lib.stream_handle(x.device)), "fovi_knnconv_fwd")
+        return y.transpose(1, 2)
+
+    def forward(self, X_l):
+        return _KnnConvFn.apply(X_l, self, self.weight, self.bias)
+
+    # -- conv2d import (reference knn.py:649-715) -------------------------------
+    def _load_conv_2d_weight(self, conv_weight, conv_bias, strict=False):
+        if conv_weight.shape[0] != self.out_channels:
+            raise ValueError(f"Conv2d out_channels {conv_weight.shape[0]} != layer out_channels {self.out_channels}")
+        if conv_weight.shape[1] != self.in_channels:
+            raise ValueError(f"Conv2d in_channels {conv_weight.shape[1]} != layer in_channels {self.in_channels}")
+        # conv (row, col) = (-y, x) -> ref grid (x, y)
+        conv_weight = conv_weight.transpose(-1, -2).flip(-1)
+        s = self.ref_grid_size
+        if conv_weight.shape[2] != s or conv_weight.shape[3] != s:
+            if strict:
+                raise ValueError(f"Conv2d kernel size {conv_weight.shape[2]}x{conv_weight.shape[3]} != "
+                                 f"ref_grid_size {s}x{s}. Set strict=False to resample the kernel.")
+            conv_weight = F.interpolate(conv_weight, size=(s, s), mode="bilinear", align_corners=True)
+        self.weight.data.copy_(conv_weight.reshape(conv_weight.shape[0], -1))
+        if conv_bias is not None and self.bias is not None:
+            self.bias.data.copy_(conv_bias.data)
+        elif conv_bias is not None and self.bias is None:
+            raise ValueError("Conv2d has bias but layer does not. Recreate layer with bias=True.")
+
+    def load_conv2d_weights(self, conv2d, strict=False):
+        self._load_conv_2d_weight(conv2d.weight.data.clone(), conv2d.bias, strict=strict)
+
+    def load_conv3d_weights(self, conv3d, temporal_strategy="average", strict=False):
+        w = conv3d.weight.data.clone()
+        if temporal_strategy == "average":
+            w = w.mean(2)
+        elif temporal_strategy == "select_first":
+            w = w[:, :, 0]
+        else:
+            raise NotImplementedError()
+        self._load_conv_2d_weight(w, conv3d.bias, strict=strict)
+
+    def __repr__(self):
+        return (f"{self.__class__.__name__}(\n\tin_channels={self.in_channels}\n\tout_channels="
+                f"{self.out_channels}\n\tk={self.k}\n\tn_ref={self.ref_coords.shape[0]}\n\tin_coords="
+                f"{self.in_coords}\n\tout_coords={self.out_coords}\n\tsample_cortex={self.sample_cortex}\n)")
+
+
+def get_in_out_coords(in_res, fov, cmf_a, stride, style="isotropic", auto_match_cart_resources=1,
+                      in_cart_res=None, device="cuda", in_coords=None, force_out_match_less_than=True,
+                      max_out_coord_val=1):
+    """Input and strided output point sets (reference ``knn.py:958-1003``)."""
+    from ..sensing.coords import auto_match_num_coords
+    if in_coords is None:
+        if auto_match_cart_resources:
+            in_res, in_cart_res = auto_match_num_coords(fov, cmf_a, in_cart_res, style, auto_match_cart_resources,
+                                                        device, force_less_than=True, quiet=True)
+        in_coords = SamplingCoords(fov, cmf_a, in_res, device=device, style=style)
+    tmp_max = 1 if max_out_coord_val == "auto" else max_out_coord_val
+    out_coords, _, out_cart_res = in_coords.get_strided_coords(
+        stride, auto_match_cart_resources=auto_match_cart_resources, in_cart_res=in_cart_res,
+        force_less_than=force_out_match_less_than, max_val=tmp_max)
+    if max_out_coord_val == "auto":
+        radii = torch.unique(out_coords.polar[:, 0])
+        final = (radii[-1] + radii[-2]) / 2
+        out_coords, _, out_cart_res = in_coords.get_strided_coords(
+            stride, auto_match_cart_resources=auto_match_cart_resources, in_cart_res=in_cart_res,
+            force_less_than=force_out_match_less_than, max_val=final)
+    return in_coords, out_coords, out_cart_res
+
+
+KNN_CONV_REGISTRY = {
+    "default": KNNConvLayer,
+}
+
+
+def get_knn_conv_layer(name: str):
+    """Layer class by registry name (reference ``knn.py:1014-1030``)."""
+    if name not in KNN_CONV_REGISTRY:
+        raise ValueError(f"Unknown KNN conv layer: {name}. Available: {list(KNN_CONV_REGISTRY.keys())}")
+    return KNN_CONV_REGISTRY[name]

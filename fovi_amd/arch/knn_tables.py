@@ -1,0 +1,167 @@
+"""Host construction of the kNN-conv tables (neighbour indices and ref-grid slots).
+
+Runs once per layer on the host CPU with torch, in the reference's op order so
+that neighbour indices and slot ids are bit-identical to the reference's:
+
+* log-polar neighbour search: per-column min-max normalised cortical coords,
+  L1 distance per axis, angle axis wrapped to ``max - d`` when ``d`` exceeds
+  the half-range, Euclidean combination, ``topk(k, largest=False)``
+  (reference ``fovi/arch/knn.py:101-152``). The wrap period is the normalised
+  angle range, so angle indices 0 and res-1 of one ring are at distance 0;
+  this is reproduced, not corrected;
+* generic cortical/cartesian neighbour search with ``torch.cdist``
+  (``knn.py:116-120,143``);
+* square reference grid ``linspace(-1,1,s)`` x ``linspace(-1,1,s)`` in 'ij'
+  order (``knn.py:559-597``);
+* slot assignment: neighbour offsets as (cortical distance, cartesian angle),
+  per-neighbourhood min-max to [-1,1], nearest ref-grid point by
+  ``cdist``/``argmin`` (``knn.py:599-647``).
+
+The device-side format is a slot-major CSR list per output point
+(``csr_tables``). Several neighbours often land in one slot (the reference's
+one-hot einsum sums them, ``knn.py:505-526``) and many slots stay empty: on
+the 128x128 log-polar lattice with k=25, 36% of slots are empty and up to 23
+neighbours share a slot near the fovea, so a fixed one-index-per-slot table
+cannot represent the operator.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+__all__ = [
+    "knn_logpolar",
+    "knn_euclidean",
+    "reference_grid",
+    "local_rf_slots",
+    "slots_to_one_hot",
+    "csr_tables",
+]
+
+_PAIR_BUDGET = 500_000_000  # distance-matrix elements per chunk (reference knn.py:43-49)
+
+
+def _chunk(n_in, n_out, batch_size):
+    if batch_size is None:
+        pairs = n_in * n_out
+        batch_size = int(np.minimum(n_out / np.maximum(0.0001, pairs / _PAIR_BUDGET), n_out))
+    return max(1, min(batch_size, n_out))
+
+
+def _minmax01(x):
+    lo = x.min(dim=0)[0]
+    hi = x.max(dim=0)[0]
+    return (x - lo) / (hi - lo)
+
+
+def knn_logpolar(in_cortical, out_cortical, k, batch_size=None):
+    """k nearest inputs per output on the wrapped log-polar cortical lattice.
+
+    Returns ``(indices [k, N_out] int64, distances [k, N_out] fp32,
+    normalised input cortical coords [N_in, 2])``.
+    """
+    src = _minmax01(in_cortical.clone())
+    dst = _minmax01(out_cortical.clone())
+    n_out = dst.shape[0]
+    idx = torch.zeros((k, n_out), dtype=torch.long)
+    dist = torch.zeros((k, n_out), dtype=torch.float32)
+    theta_hi = src[:, 1].max()
+    theta_half = src[:, 1].min() + (theta_hi - src[:, 1].min()) / 2
+    step = _chunk(src.shape[0], n_out, batch_size)
+    for s in range(0, n_out, step):
+        e = min(s + step, n_out)
+        d_rho = torch.cdist(src[:, 0].unsqueeze(1), dst[s:e, 0].unsqueeze(1), p=1)
+        d_theta = torch.cdist(src[:, 1].unsqueeze(1), dst[s:e, 1].unsqueeze(1), p=1)
+        wrap = d_theta > theta_half
+        d_theta[wrap] = theta_hi - d_theta[wrap]
+        d = (d_rho ** 2 + d_theta ** 2) ** (1 / 2)
+        vals, inds = torch.topk(d, k, dim=0, largest=False)
+        idx[:, s:e] = inds
+        dist[:, s:e] = vals
+    return idx, dist, src
+
+
+def knn_euclidean(in_pts, out_pts, k, batch_size=None):
+    """k nearest inputs per output by plain ``cdist`` (non-log-polar styles)."""
+    n_out = out_pts.shape[0]
+    idx = torch.zeros((k, n_out), dtype=torch.long)
+    dist = torch.zeros((k, n_out), dtype=torch.float32)
+    step = _chunk(in_pts.shape[0], n_out, batch_size)
+    for s in range(0, n_out, step):
+        e = min(s + step, n_out)
+        vals, inds = torch.topk(torch.cdist(in_pts, out_pts[s:e]), k, dim=0, largest=False)
+        idx[:, s:e] = inds
+        dist[:, s:e] = vals
+    return idx, dist
+
+
+def reference_grid(k, side_length=None, doubleres=False, dtype=torch.float32):
+    """Square ref grid: (coords [s*s, 2], s); slot v = i*s + j at (lin[i], lin[j])."""
+    if side_length is None:
+        side_length = int(torch.ceil(torch.sqrt(torch.tensor(k))).long())
+        if doubleres:
+            side_length *= 2
+    lin = torch.linspace(-1, 1, side_length)
+    grid = torch.stack(torch.meshgrid(lin, lin, indexing="ij"), -1).reshape(-1, 2)
+    return grid.to(dtype=dtype), side_length
+
+
+def local_rf_slots(knn_idx, src_cortical, src_cart, out_cortical, out_cart, ref_coords):
+    """Ref slot id ``[N_out, k]`` (int64) of every neighbour.
+
+    ``src_cortical`` is the (normalised) cortical point set the neighbour
+    search ran on; ``out_cortical`` is the output set's own cortical coords.
+    The per-output radial distance is one ``cdist`` call per output point,
+    as the reference makes it, because ``cdist`` switches to its matmul
+    formulation above 25 rows and the two formulations round differently.
+    """
+    k, n_out = knn_idx.shape
+    nb = src_cortical[knn_idx]                      # [k, N_out, d]
+    nb_cart = src_cart[knn_idx]                     # [k, N_out, 2]
+    theta = torch.arctan2(nb_cart[:, :, 1] - out_cart[:, 1], nb_cart[:, :, 0] - out_cart[:, 0])
+    radial = torch.empty(n_out, k, dtype=nb.dtype)
+    for i in range(n_out):
+        radial[i] = torch.cdist(out_cortical[i].unsqueeze(0), nb[:, i]).squeeze(0)
+    radial = radial.t()
+    radial[knn_idx < 0] = 0
+    local = torch.stack([radial * torch.cos(theta), radial * torch.sin(theta)], dim=2)
+    lo = local.min(dim=0, keepdim=True)[0]
+    hi = local.max(dim=0, keepdim=True)[0]
+    local = 2 * (local - lo) / (hi - lo + 1e-6) - 1
+    nearest = torch.argmin(torch.cdist(local, ref_coords), dim=2)   # [k, N_out]
+    return nearest.t().contiguous()
+
+
+def slots_to_one_hot(slots, n_ref):
+    """One-hot ``local_rf [N_out, k, V]`` fp32 (the reference's stored form)."""
+    n_out, k = slots.shape
+    rf = torch.zeros(n_out, k, n_ref, dtype=torch.float32)
+    rf.scatter_(2, slots.unsqueeze(2), 1)
+    return rf
+
+
+def csr_tables(knn_idx, slots, n_in, n_ref):
+    """Slot-major CSR neighbour lists, the device format of the kNN-conv kernel.
+
+    Returns ``(slot_ptr [N_out, V] int32, nbr_sorted [N_out, k] int32)``:
+    ``slot_ptr[n, v] = (begin << 16) | count`` and the inputs that land in slot
+    ``v`` of output ``n`` are ``nbr_sorted[n, begin:begin+count]``, in
+    neighbour (distance) order. Pad-token neighbours (``>= n_in``) contribute
+    zeros in the reference and are dropped; unused tail entries are ``-1``.
+    """
+    k, n_out = knn_idx.shape
+    if k > 0xFFFF:
+        raise ValueError(f"k={k} does not fit the 16-bit CSR fields")
+    idx = knn_idx.t().numpy().astype(np.int64)             # [N_out, k]
+    sl = slots.numpy().astype(np.int64)
+    valid = (idx >= 0) & (idx < n_in)
+    key = np.where(valid, sl, n_ref)
+    order = np.argsort(key, axis=1, kind="stable")
+    nbr = np.take_along_axis(idx, order, axis=1)
+    nbr = np.where(np.take_along_axis(valid, order, axis=1), nbr, -1).astype(np.int32)
+    counts = np.zeros((n_out, n_ref + 1), dtype=np.int64)
+    np.add.at(counts, (np.repeat(np.arange(n_out), k), key.reshape(-1)), 1)
+    counts = counts[:, :n_ref]
+    begin = np.cumsum(counts, axis=1) - counts
+    ptr = ((begin << 16) | counts).astype(np.int32)
+    return torch.from_numpy(ptr), torch.from_numpy(nbr)

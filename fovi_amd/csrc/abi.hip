@@ -1,0 +1,32 @@
+// Library-wide C-ABI entry points: version and error reporting.
+#include "common.h"
+
+namespace fovi {
+
+static thread_local std::string g_last_error;
+
+void set_error(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+}
+
+void clear_error() { g_last_error.clear(); }
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+    return 1;
+  }
+  return 0;
+}
+
+}  // namespace fovi
+
+extern "C" int fovi_abi_version(void) { return FOVI_ABI_VERSION; }
+
+extern "C" const char* fovi_last_error(void) { return fovi::g_last_error.c_str(); }

@@ -1,0 +1,437 @@
+// kNN-convolution forward: fused neighbour gather -> slot sum -> GEMM.
+//
+// GEMM view: rows m = (b, n) output points, columns o output channels,
+// reduction index kk = v * c_in + c (ref slot major). Row m's reduction
+// vector is assembled on the fly from the slot-major CSR neighbour lists:
+//   A[m, v*c_in + c] = sum_{i < count(n,v)} x[b, c, nbr_sorted[n, begin(n,v) + i]]
+// so the [B, C, k, N] gather tensor, the one-hot einsum and its permute copies
+// of the reference (fovi/arch/knn.py:484-526) are never materialised.
+//
+// Kernels
+//  * knnconv_f32_kernel: fp32 operands, any strides, fp32 FMA SGEMM tiling.
+//    The fp32 parity path.
+//  * knnconv_bf16_kernel: bf16 operands, fp32 accumulate on
+//    v_mfma_f32_32x32x16_bf16. 128-point x NT-channel tiles, 4 waves (2x2),
+//    64-wide reduction chunks double buffered in LDS (XOR-swizzled 16-byte
+//    chunks so the MFMA fragment reads are bank-conflict free), next chunk's
+//    gather issued into registers before the current chunk's MFMAs.
+//    VEC loader: channels-last rows and c_in % 64 == 0, one 16-byte load per
+//    (row, 8 channels). Generic loader: any strides / c_in, element gathers.
+#include "common.h"
+
+namespace fovi {
+
+struct KnnParams {
+  const void* x;
+  int64_t B, C, Nin;
+  int64_t xs0, xs1, xs2;
+  int64_t Nout, K, V;
+  const int32_t* slot_ptr;
+  const int32_t* nbr;
+  const void* w;
+  int64_t Cout, Kpad;
+  const float* bias;
+  const float* w_scale;
+  float x_scale;
+  void* y;
+  int64_t ys0, ys1, ys2;
+};
+
+// ---------------------------------------------------------------------------
+// fp32 path
+// ---------------------------------------------------------------------------
+constexpr int F32_TM = 64, F32_TN = 64, F32_TK = 16;
+
+template <typename OutT>
+__global__ __launch_bounds__(256) void knnconv_f32_kernel(KnnParams p, int64_t tiles_per_b) {
+  __shared__ float As[F32_TK][F32_TM + 4];
+  __shared__ float Ws[F32_TK][F32_TN + 4];
+  const int tid = threadIdx.x;
+  const int64_t mt = blockIdx.x;
+  const int64_t b = mt / tiles_per_b;
+  const int64_t n0 = (mt % tiles_per_b) * F32_TM;
+  const int64_t o0 = static_cast<int64_t>(blockIdx.y) * F32_TN;
+  const float* x = static_cast<const float*>(p.x) + b * p.xs0;
+  const float* w = static_cast<const float*>(p.w);
+  const int tm = tid & 15, tn = tid >> 4;
+  float acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+  const int64_t ktot = p.V * p.C;
+
+  for (int64_t k0 = 0; k0 < ktot; k0 += F32_TK) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = tid + 256 * i;
+      const int pl = e & 63, kk = e >> 6;
+      const int64_t k = k0 + kk, n = n0 + pl;
+      float a = 0.0f;
+      if (k < ktot && n < p.Nout) {
+        const int64_t v = k / p.C, c = k - v * p.C;
+        const int32_t ent = p.slot_ptr[n * p.V + v];
+        const int32_t* nb = p.nbr + n * p.K + (ent >> 16);
+        const int cnt = ent & 0xffff;
+        for (int j = 0; j < cnt; ++j) a += x[c * p.xs1 + static_cast<int64_t>(nb[j]) * p.xs2];
+      }
+      As[kk][pl] = a;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = tid + 256 * i;
+      const int kk = e & 15, ol = e >> 4;
+      const int64_t o = o0 + ol;
+      Ws[kk][ol] = (o < p.Cout) ? w[o * p.Kpad + k0 + kk] : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < F32_TK; ++kk) {
+      float av[4], wv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = As[kk][tm * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wv[j] = Ws[kk][tn * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(av[i], wv[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+
+  OutT* y = static_cast<OutT*>(p.y) + b * p.ys0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t n = n0 + tm * 4 + i;
+    if (n >= p.Nout) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t o = o0 + tn * 4 + j;
+      if (o >= p.Cout) continue;
+      float r = acc[i][j];
+      if (p.bias) r += p.bias[o];
+      Elem<OutT>::store(y + o * p.ys1 + n * p.ys2, r);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// bf16 MFMA path
+// ---------------------------------------------------------------------------
+constexpr int MM_MT = 128;  // output points per tile
+constexpr int MM_KC = 64;   // reduction chunk (bf16 elements)
+
+struct Raw16 { uint32_t a, b, c, d; };
+
+__device__ __forceinline__ void add_bf16x8(float (&s)[8], const Raw16& r) {
+  const uint32_t u[4] = {r.a, r.b, r.c, r.d};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s[2 * i] += __uint_as_float(u[i] << 16);
+    s[2 * i + 1] += __uint_as_float(u[i] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ Raw16 pack_bf16x8(const float (&s)[8]) {
+  uint32_t u[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    u[i] = static_cast<uint32_t>(f32_to_bf16_bits(s[2 * i])) |
+           (static_cast<uint32_t>(f32_to_bf16_bits(s[2 * i + 1])) << 16);
+  return Raw16{u[0], u[1], u[2], u[3]};
+}
+
+// LDS offset (in bf16 elements) of 16-byte chunk `q` of row `r` in a
+// [rows][64] tile: chunk index XOR (row mod 8).
+__device__ __forceinline__ int swz(int r, int q) { return r * MM_KC + ((q ^ (r & 7)) << 3); }
+
+// Gathered 8-channel vector of row n (slot v, channels c .. c+7), VEC layout.
+__device__ __forceinline__ Raw16 gather_vec(const KnnParams& p, const uint16_t* xb, int64_t n, int64_t v,
+                                            int64_t c) {
+  Raw16 r{0u, 0u, 0u, 0u};
+  if (n >= p.Nout) return r;
+  const int32_t ent = p.slot_ptr[n * p.V + v];
+  const int cnt = ent & 0xffff;
+  if (cnt == 0) return r;
+  const int32_t* nb = p.nbr + n * p.K + (ent >> 16);
+  if (cnt == 1) return *reinterpret_cast<const Raw16*>(xb + static_cast<int64_t>(nb[0]) * p.xs2 + c);
+  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < cnt; ++j)
+    add_bf16x8(s, *reinterpret_cast<const Raw16*>(xb + static_cast<int64_t>(nb[j]) * p.xs2 + c));
+  return pack_bf16x8(s);
+}
+
+// Generic layout: 8 consecutive reduction indices kk .. kk+7, element gathers.
+__device__ __forceinline__ Raw16 gather_generic(const KnnParams& p, const uint16_t* xb, int64_t n,
+                                                int64_t kk) {
+  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const int64_t ktot = p.V * p.C;
+  if (n < p.Nout && kk < ktot) {
+    int64_t v = kk / p.C, c = kk - v * p.C;
+    int32_t ent = p.slot_ptr[n * p.V + v];
+    for (int e = 0; e < 8 && kk + e < ktot; ++e) {
+      const int cnt = ent & 0xffff;
+      const int32_t* nb = p.nbr + n * p.K + (ent >> 16);
+      for (int j = 0; j < cnt; ++j)
+        s[e] += bf16_bits_to_f32(xb[c * p.xs1 + static_cast<int64_t>(nb[j]) * p.xs2]);
+      if (++c == p.C && kk + e + 1 < ktot) {
+        c = 0;
+        ++v;
+        ent = p.slot_ptr[n * p.V + v];
+      }
+    }
+  }
+  return pack_bf16x8(s);
+}
+
+template <int NT, bool VEC, typename OutT>
+__global__ __launch_bounds__(256, 2) void knnconv_bf16_kernel(KnnParams p, int64_t tiles_per_b,
+                                                              int64_t n_tiles_n, int64_t total_tiles,
+                                                              int64_t padded_tiles) {
+  constexpr int A_VECS = MM_MT * MM_KC / 8 / 256;  // 16-byte vectors per thread
+  constexpr int B_VECS = NT * MM_KC / 8 / 256;
+  constexpr int WN = NT / 2;                       // wave tile columns
+  constexpr int CB = WN / 32;                      // 32-wide column blocks per wave
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][MM_MT * MM_KC];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][NT * MM_KC];
+
+  const int64_t tile = xcd_tile(blockIdx.x, padded_tiles);
+  if (tile >= total_tiles) return;
+  const int64_t mt = tile / n_tiles_n;
+  const int64_t o0 = (tile % n_tiles_n) * NT;
+  const int64_t b = mt / tiles_per_b;
+  const int64_t n0 = (mt % tiles_per_b) * MM_MT;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+  const uint16_t* xb = static_cast<const uint16_t*>(p.x) + b * p.xs0;
+  const uint16_t* wp = static_cast<const uint16_t*>(p.w);
+  const int64_t nk = p.Kpad / MM_KC;
+
+  Raw16 ra[A_VECS], rb[B_VECS];
+  auto load_chunk = [&](int64_t kt) {
+    const int64_t k0 = kt * MM_KC;
+#pragma unroll
+    for (int i = 0; i < A_VECS; ++i) {
+      const int q = tid + 256 * i;
+      const int row = q >> 3, part = q & 7;
+      if (VEC) {
+        const int64_t v = k0 / p.C;
+        const int64_t c = k0 - v * p.C + part * 8;
+        ra[i] = gather_vec(p, xb, n0 + row, v, c);
+      } else {
+        ra[i] = gather_generic(p, xb, n0 + row, k0 + part * 8);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < B_VECS; ++i) {
+      const int q = tid + 256 * i;
+      const int row = q >> 3, part = q & 7;
+      const int64_t o = o0 + row;
+      rb[i] = (o < p.Cout) ? *reinterpret_cast<const Raw16*>(wp + o * p.Kpad + k0 + part * 8)
+                           : Raw16{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_chunk = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_VECS; ++i) {
+      const int q = tid + 256 * i;
+      *reinterpret_cast<Raw16*>(&As[buf][swz(q >> 3, q & 7)]) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_VECS; ++i) {
+      const int q = tid + 256 * i;
+      *reinterpret_cast<Raw16*>(&Bs[buf][swz(q >> 3, q & 7)]) = rb[i];
+    }
+  };
+
+  f32x16 acc[2][CB];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < CB; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  load_chunk(0);
+  store_chunk(0);
+  __syncthreads();
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    const int buf = static_cast<int>(kt & 1);
+    if (kt + 1 < nk) load_chunk(kt + 1);
+#pragma unroll
+    for (int ks = 0; ks < MM_KC / 16; ++ks) {
+      const int q = ks * 2 + (lane >> 5);
+      bf16x8 af[2], bfr[CB];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int row = wm * 64 + i * 32 + (lane & 31);
+        af[i] = *reinterpret_cast<const bf16x8*>(&As[buf][swz(row, q)]);
+      }
+#pragma unroll
+      for (int j = 0; j < CB; ++j) {
+        const int col = wn * WN + j * 32 + (lane & 31);
+        bfr[j] = *reinterpret_cast<const bf16x8*>(&Bs[buf][swz(col, q)]);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < CB; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < nk) store_chunk(buf ^ 1);
+    __syncthreads();
+  }
+
+  OutT* y = static_cast<OutT*>(p.y) + b * p.ys0;
+#pragma unroll
+  for (int j = 0; j < CB; ++j) {
+    const int64_t o = o0 + wn * WN + j * 32 + (lane & 31);
+    if (o >= p.Cout) continue;
+    const float bo = p.bias ? p.bias[o] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t n = n0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (n < p.Nout) Elem<OutT>::store(y + o * p.ys1 + n * p.ys2, acc[i][j][r] + bo);
+      }
+  }
+}
+
+template <int NT, bool VEC>
+static void launch_bf16(const KnnParams& p, int out_t, hipStream_t s) {
+  const int64_t tiles_per_b = (p.Nout + MM_MT - 1) / MM_MT;
+  const int64_t n_tiles_n = (p.Cout + NT - 1) / NT;
+  const int64_t total = p.B * tiles_per_b * n_tiles_n;
+  const int64_t padded = (total + 7) / 8 * 8;
+  dim3 grid(static_cast<unsigned>(padded));
+  if (out_t == FOVI_BF16)
+    hipLaunchKernelGGL((knnconv_bf16_kernel<NT, VEC, uint16_t>), grid, dim3(256), 0, s, p, tiles_per_b,
+                       n_tiles_n, total, padded);
+  else
+    hipLaunchKernelGGL((knnconv_bf16_kernel<NT, VEC, float>), grid, dim3(256), 0, s, p, tiles_per_b,
+                       n_tiles_n, total, padded);
+}
+
+// ---------------------------------------------------------------------------
+// weight packing
+// ---------------------------------------------------------------------------
+// float -> OCP fp8 e4m3 (bias 7, max finite 448, no infinities), round to
+// nearest even, saturating to +-448; NaN -> 0x7f.
+__device__ __forceinline__ uint8_t f32_to_e4m3(float f) {
+  const uint32_t u = __float_as_uint(f);
+  const uint8_t sign = static_cast<uint8_t>((u >> 24) & 0x80u);
+  float a = fabsf(f);
+  if (!(a == a)) return 0x7f;
+  if (a >= 464.0f) return sign | 0x7e;  // rounds past the largest finite value
+  if (a < 0.0009765625f) {              // below 2^-10: rounds to zero or the smallest subnormal
+    if (a <= 0.0009765625f * 0.5f) return sign;
+    return sign | 0x01;
+  }
+  int e;
+  float m = frexpf(a, &e);              // a = m * 2^e, m in [0.5, 1)
+  int exp = e - 1 + 7;                  // biased exponent of 1.xxx form
+  if (exp <= 0) {                       // subnormal: value = mant * 2^-9
+    const float q = __builtin_rintf(a * 512.0f);
+    return sign | static_cast<uint8_t>(q);  // q == 8 rolls into the first normal
+  }
+  float frac = m * 2.0f - 1.0f;         // [0, 1)
+  float q = __builtin_rintf(frac * 8.0f);
+  if (q == 8.0f) { q = 0.0f; ++exp; }
+  if (exp > 15 || (exp == 15 && q > 6.0f)) return sign | 0x7e;
+  return sign | static_cast<uint8_t>((exp << 3) | static_cast<int>(q));
+}
+
+__global__ void pack_weight_kernel(const float* w_ref, int64_t c_out, int64_t c_in, int64_t n_ref,
+                                   void* out, int dtype, int64_t k_pad, const float* w_scale) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= c_out * k_pad) return;
+  const int64_t o = idx / k_pad, kk = idx - o * k_pad;
+  float val = 0.0f;
+  if (kk < c_in * n_ref) {
+    const int64_t v = kk / c_in, c = kk - v * c_in;
+    val = w_ref[o * c_in * n_ref + c * n_ref + v];
+  }
+  if (dtype == FOVI_F32) static_cast<float*>(out)[idx] = val;
+  else if (dtype == FOVI_BF16) static_cast<uint16_t*>(out)[idx] = f32_to_bf16_bits(val);
+  else static_cast<uint8_t*>(out)[idx] = f32_to_e4m3(val / w_scale[o]);
+}
+
+}  // namespace fovi
+
+extern "C" int fovi_knnconv_pack_weight(const float* w_ref, int64_t c_out, int64_t c_in, int64_t n_ref,
+                                        void* w_packed, int32_t out_dtype, int64_t k_pad,
+                                        const float* w_scale, void* stream) {
+  using namespace fovi;
+  clear_error();
+  if (!w_ref || !w_packed) { set_error("fovi_knnconv_pack_weight: null pointer"); return 1; }
+  if (c_out <= 0 || c_in <= 0 || n_ref <= 0 || k_pad < c_in * n_ref || k_pad % MM_KC != 0) {
+    set_error("fovi_knnconv_pack_weight: bad sizes c_out=%lld c_in=%lld n_ref=%lld k_pad=%lld",
+              (long long)c_out, (long long)c_in, (long long)n_ref, (long long)k_pad);
+    return 1;
+  }
+  if (out_dtype != FOVI_F32 && out_dtype != FOVI_BF16 && out_dtype != FOVI_F8E4M3) {
+    set_error("fovi_knnconv_pack_weight: bad dtype %d", out_dtype); return 1;
+  }
+  if (out_dtype == FOVI_F8E4M3 && !w_scale) { set_error("fovi_knnconv_pack_weight: fp8 needs w_scale"); return 1; }
+  const int64_t n = c_out * k_pad;
+  hipLaunchKernelGGL(pack_weight_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), w_ref, c_out, c_in, n_ref, w_packed, out_dtype, k_pad,
+                     w_scale);
+  return check_launch("fovi_knnconv_pack_weight");
+}
+
+extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
+  using namespace fovi;
+  clear_error();
+  if (!a) { set_error("fovi_knnconv_fwd: null args"); return 1; }
+  if (!a->x || !a->slot_ptr || !a->nbr_sorted || !a->w || !a->y) {
+    set_error("fovi_knnconv_fwd: null pointer argument"); return 1;
+  }
+  if (a->batch <= 0 || a->c_in <= 0 || a->n_in <= 0 || a->n_out <= 0 || a->k <= 0 || a->n_ref <= 0 ||
+      a->c_out <= 0) {
+    set_error("fovi_knnconv_fwd: bad sizes"); return 1;
+  }
+  if (a->k > 65535) { set_error("fovi_knnconv_fwd: k=%lld exceeds 65535", (long long)a->k); return 1; }
+  if (a->k_pad < a->c_in * a->n_ref || a->k_pad % MM_KC != 0) {
+    set_error("fovi_knnconv_fwd: k_pad=%lld must be a multiple of 64 >= c_in*n_ref=%lld",
+              (long long)a->k_pad, (long long)(a->c_in * a->n_ref));
+    return 1;
+  }
+  if (a->y_dtype != FOVI_F32 && a->y_dtype != FOVI_BF16) { set_error("fovi_knnconv_fwd: bad y dtype"); return 1; }
+  KnnParams p;
+  p.x = a->x; p.B = a->batch; p.C = a->c_in; p.Nin = a->n_in;
+  p.xs0 = a->x_stride[0]; p.xs1 = a->x_stride[1]; p.xs2 = a->x_stride[2];
+  p.Nout = a->n_out; p.K = a->k; p.V = a->n_ref; p.slot_ptr = a->slot_ptr; p.nbr = a->nbr_sorted;
+  p.w = a->w; p.Cout = a->c_out; p.Kpad = a->k_pad; p.bias = a->bias; p.w_scale = a->w_scale;
+  p.x_scale = a->x_scale; p.y = a->y; p.ys0 = a->y_stride[0]; p.ys1 = a->y_stride[1]; p.ys2 = a->y_stride[2];
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  if (a->x_dtype == FOVI_F32 && a->w_dtype == FOVI_F32) {
+    const int64_t tiles_per_b = (p.Nout + F32_TM - 1) / F32_TM;
+    const int64_t mt = p.B * tiles_per_b;
+    const int64_t nt = (p.Cout + F32_TN - 1) / F32_TN;
+    if (mt > 0x7fffffff || nt > 65535) { set_error("fovi_knnconv_fwd: grid too large"); return 1; }
+    dim3 grid(static_cast<unsigned>(mt), static_cast<unsigned>(nt));
+    if (a->y_dtype == FOVI_F32)
+      hipLaunchKernelGGL((knnconv_f32_kernel<float>), grid, dim3(256), 0, s, p, tiles_per_b);
+    else
+      hipLaunchKernelGGL((knnconv_f32_kernel<uint16_t>), grid, dim3(256), 0, s, p, tiles_per_b);
+    return check_launch("fovi_knnconv_fwd(f32)");
+  }
+  if (a->x_dtype == FOVI_BF16 && a->w_dtype == FOVI_BF16) {
+    const uintptr_t xa = reinterpret_cast<uintptr_t>(a->x);
+    const bool vec = p.xs1 == 1 && p.C % MM_KC == 0 && p.xs2 % 8 == 0 && p.xs0 % 8 == 0 && (xa % 16) == 0;
+    const bool wide = p.Cout % 128 == 0;
+    if (vec && wide) launch_bf16<128, true>(p, a->y_dtype, s);
+    else if (vec) launch_bf16<64, true>(p, a->y_dtype, s);
+    else if (wide) launch_bf16<128, false>(p, a->y_dtype, s);
+    else launch_bf16<64, false>(p, a->y_dtype, s);
+    return check_launch("fovi_knnconv_fwd(bf16)");
+  }
+  set_error("fovi_knnconv_fwd: unsupported dtypes x=%d w=%d", a->x_dtype, a->w_dtype);
+  return 1;
+}

@@ -1,0 +1,178 @@
+// Foveated sampler: fixation transform + grid-sample, one launch for all views.
+//
+// One thread per (view, sensor point); channels are looped inside the thread
+// so the fixation transform and tap coordinates are computed once per point.
+// Consecutive threads are consecutive sensor points (consecutive angles on a
+// log-polar ring), so output stores along the point axis are coalesced and
+// neighbouring threads read neighbouring pixels.
+//
+// Arithmetic follows the reference bit for bit where it is defined:
+//  * fixation transform (fovi/sensing/coords.py:624-640): fp32
+//    x*half + c*W, then 2*x/W - 1, each op rounded (built with
+//    -ffp-contract=off, so no fused multiply-add);
+//  * grid_sample unnormalisation for align_corners=False as the CPU kernel of
+//    torch.nn.functional.grid_sample evaluates it, (g + 1) * (size/2) - 0.5;
+//    'border' clips to [0, size-1]; 'nearest' rounds half to even;
+//  * bilinear weights from floor() and the fractional parts, blended
+//    nw, ne, sw, se in that order; out-of-image taps contribute zero.
+#include "common.h"
+
+namespace fovi {
+
+struct SamplerParams {
+  const void* img;
+  int64_t n_img, C, H, W;
+  int64_t is0, is1, is2, is3;
+  const float* grid;
+  int64_t N;
+  const float* fix_loc;
+  const double* fix_half;
+  int wide;
+  const int32_t* view_image;
+  void* out;
+  int64_t os0, os1, os2;
+  float* grid_out;
+};
+
+template <typename InT, typename OutT, int MODE, int PAD>
+__global__ __launch_bounds__(256) void sampler_kernel(SamplerParams p) {
+  const int64_t v = blockIdx.y;
+  const int64_t pt = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (pt >= p.N) return;
+
+  const float W = static_cast<float>(p.W);
+  const float H = static_cast<float>(p.H);
+  const float g0 = p.grid[2 * pt];
+  const float g1 = p.grid[2 * pt + 1];
+  const double half_h = p.fix_half[2 * v];
+  const double half_w = p.fix_half[2 * v + 1];
+  float x, y;
+  if (p.wide) {
+    x = static_cast<float>(static_cast<double>(g0) * half_w);
+    y = static_cast<float>(static_cast<double>(g1) * half_h);
+  } else {
+    x = g0 * static_cast<float>(half_w);
+    y = g1 * static_cast<float>(half_h);
+  }
+  const float centre_h = p.fix_loc[2 * v] * H;
+  const float centre_w = p.fix_loc[2 * v + 1] * W;
+  x = x + centre_w;
+  y = y + centre_h;
+  const float gx = (2.0f * x) / W - 1.0f;
+  const float gy = (2.0f * y) / H - 1.0f;
+  if (p.grid_out) {
+    p.grid_out[(v * p.N + pt) * 2] = gx;
+    p.grid_out[(v * p.N + pt) * 2 + 1] = gy;
+  }
+
+  OutT* out = static_cast<OutT*>(p.out) + v * p.os0 + pt * p.os2;
+  const int64_t img = p.view_image ? static_cast<int64_t>(p.view_image[v]) : v;
+  if (img < 0 || img >= p.n_img) {
+    for (int64_t c = 0; c < p.C; ++c) Elem<OutT>::store(out + c * p.os1, 0.0f);
+    return;
+  }
+  const InT* src = static_cast<const InT*>(p.img) + img * p.is0;
+
+  float ix = (gx + 1.0f) * (W * 0.5f) - 0.5f;
+  float iy = (gy + 1.0f) * (H * 0.5f) - 0.5f;
+  if (PAD == FOVI_PAD_BORDER) {
+    ix = fminf(fmaxf(ix, 0.0f), W - 1.0f);
+    iy = fminf(fmaxf(iy, 0.0f), H - 1.0f);
+  }
+
+  if (MODE == FOVI_NEAREST) {
+    const float rx = __builtin_rintf(ix);
+    const float ry = __builtin_rintf(iy);
+    const bool inb = rx >= 0.0f && rx < W && ry >= 0.0f && ry < H;
+    const int64_t off = inb ? static_cast<int64_t>(ry) * p.is2 + static_cast<int64_t>(rx) * p.is3 : 0;
+    for (int64_t c = 0; c < p.C; ++c) {
+      const float val = inb ? Elem<InT>::load(src + c * p.is1 + off) : 0.0f;
+      Elem<OutT>::store(out + c * p.os1, val);
+    }
+    return;
+  }
+
+  const float fx = floorf(ix);
+  const float fy = floorf(iy);
+  const float we = ix - fx;          // weight of the east column
+  const float ww = 1.0f - we;
+  const float ws = iy - fy;          // weight of the south row
+  const float wn = 1.0f - ws;
+  const float w_nw = wn * ww, w_ne = wn * we, w_sw = ws * ww, w_se = ws * we;
+  const bool x0 = fx >= 0.0f && fx < W, x1 = fx + 1.0f >= 0.0f && fx + 1.0f < W;
+  const bool y0 = fy >= 0.0f && fy < H, y1 = fy + 1.0f >= 0.0f && fy + 1.0f < H;
+  const int64_t cx = static_cast<int64_t>(fx), cy = static_cast<int64_t>(fy);
+  const bool b_nw = y0 && x0, b_ne = y0 && x1, b_sw = y1 && x0, b_se = y1 && x1;
+  const int64_t o_nw = b_nw ? cy * p.is2 + cx * p.is3 : 0;
+  const int64_t o_ne = b_ne ? cy * p.is2 + (cx + 1) * p.is3 : 0;
+  const int64_t o_sw = b_sw ? (cy + 1) * p.is2 + cx * p.is3 : 0;
+  const int64_t o_se = b_se ? (cy + 1) * p.is2 + (cx + 1) * p.is3 : 0;
+  for (int64_t c = 0; c < p.C; ++c) {
+    const InT* s = src + c * p.is1;
+    const float v_nw = b_nw ? Elem<InT>::load(s + o_nw) : 0.0f;
+    const float v_ne = b_ne ? Elem<InT>::load(s + o_ne) : 0.0f;
+    const float v_sw = b_sw ? Elem<InT>::load(s + o_sw) : 0.0f;
+    const float v_se = b_se ? Elem<InT>::load(s + o_se) : 0.0f;
+    const float val = v_nw * w_nw + v_ne * w_ne + v_sw * w_sw + v_se * w_se;
+    Elem<OutT>::store(out + c * p.os1, val);
+  }
+}
+
+template <typename InT, typename OutT>
+static void launch_typed(const SamplerParams& p, int mode, int pad, int64_t n_views, hipStream_t s) {
+  dim3 grid(static_cast<unsigned>((p.N + 255) / 256), static_cast<unsigned>(n_views));
+  if (mode == FOVI_NEAREST) {
+    if (pad == FOVI_PAD_ZEROS)
+      hipLaunchKernelGGL((sampler_kernel<InT, OutT, FOVI_NEAREST, FOVI_PAD_ZEROS>), grid, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((sampler_kernel<InT, OutT, FOVI_NEAREST, FOVI_PAD_BORDER>), grid, dim3(256), 0, s, p);
+  } else {
+    if (pad == FOVI_PAD_ZEROS)
+      hipLaunchKernelGGL((sampler_kernel<InT, OutT, FOVI_BILINEAR, FOVI_PAD_ZEROS>), grid, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((sampler_kernel<InT, OutT, FOVI_BILINEAR, FOVI_PAD_BORDER>), grid, dim3(256), 0, s, p);
+  }
+}
+
+}  // namespace fovi
+
+extern "C" int fovi_sampler_fwd(const fovi_sampler_args* a, void* stream) {
+  using namespace fovi;
+  clear_error();
+  if (!a) { set_error("fovi_sampler_fwd: null args"); return 1; }
+  if (!a->img || !a->grid || !a->fix_loc || !a->fix_half || !a->out) {
+    set_error("fovi_sampler_fwd: null pointer argument"); return 1;
+  }
+  if (a->n_img <= 0 || a->channels <= 0 || a->height <= 0 || a->width <= 0 || a->n_points < 0 ||
+      a->n_views < 0) {
+    set_error("fovi_sampler_fwd: bad sizes (n_img=%lld C=%lld H=%lld W=%lld N=%lld views=%lld)",
+              (long long)a->n_img, (long long)a->channels, (long long)a->height, (long long)a->width,
+              (long long)a->n_points, (long long)a->n_views);
+    return 1;
+  }
+  if (a->n_views > 65535) { set_error("fovi_sampler_fwd: n_views %lld > 65535", (long long)a->n_views); return 1; }
+  if (!a->view_image && a->n_views > a->n_img) {
+    set_error("fovi_sampler_fwd: %lld views but %lld images and no view_image map",
+              (long long)a->n_views, (long long)a->n_img);
+    return 1;
+  }
+  if (a->mode != FOVI_NEAREST && a->mode != FOVI_BILINEAR) { set_error("fovi_sampler_fwd: bad mode %d", a->mode); return 1; }
+  if (a->padding != FOVI_PAD_ZEROS && a->padding != FOVI_PAD_BORDER) {
+    set_error("fovi_sampler_fwd: bad padding %d", a->padding); return 1;
+  }
+  if (a->n_points == 0 || a->n_views == 0) return 0;
+  SamplerParams p;
+  p.img = a->img; p.n_img = a->n_img; p.C = a->channels; p.H = a->height; p.W = a->width;
+  p.is0 = a->img_stride[0]; p.is1 = a->img_stride[1]; p.is2 = a->img_stride[2]; p.is3 = a->img_stride[3];
+  p.grid = a->grid; p.N = a->n_points; p.fix_loc = a->fix_loc; p.fix_half = a->fix_half;
+  p.wide = a->fix_half_wide ? 1 : 0; p.view_image = a->view_image; p.out = a->out;
+  p.os0 = a->out_stride[0]; p.os1 = a->out_stride[1]; p.os2 = a->out_stride[2]; p.grid_out = a->grid_out;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int in_t = a->img_dtype, out_t = a->out_dtype;
+  if (in_t == FOVI_F32 && out_t == FOVI_F32) launch_typed<float, float>(p, a->mode, a->padding, a->n_views, s);
+  else if (in_t == FOVI_F32 && out_t == FOVI_BF16) launch_typed<float, uint16_t>(p, a->mode, a->padding, a->n_views, s);
+  else if (in_t == FOVI_BF16 && out_t == FOVI_F32) launch_typed<uint16_t, float>(p, a->mode, a->padding, a->n_views, s);
+  else if (in_t == FOVI_BF16 && out_t == FOVI_BF16) launch_typed<uint16_t, uint16_t>(p, a->mode, a->padding, a->n_views, s);
+  else { set_error("fovi_sampler_fwd: unsupported dtypes img=%d out=%d", in_t, out_t); return 1; }
+  return check_launch("fovi_sampler_fwd");
+}

@@ -1,0 +1,142 @@
+/*
+ * fovi_hip.h - C-ABI of the MI355X (gfx950) foveated sampler and kNN-conv forward.
+ *
+ * The reference (nblauch/fovi) is pure Python and exposes no FFI: its
+ * plug-in boundary is the nn.Module surface of GridSampler/RetinalTransform
+ * and KNNConvLayer. Each entry point below replaces the ATen call sites of one
+ * stage of that surface; the Python modules in fovi_amd/ bind them with ctypes.
+ *
+ * Conventions
+ *   - All memory is caller-owned device memory (HBM); no entry point
+ *     allocates. Strides are in elements, not bytes.
+ *   - Calls are asynchronous on `stream` (a hipStream_t passed as void*,
+ *     NULL = default stream), stateless and reentrant.
+ *   - Return 0 on success, non-zero on error; the message is in
+ *     fovi_last_error() (thread-local). No C++ exception crosses the ABI.
+ */
+#ifndef FOVI_HIP_H
+#define FOVI_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FOVI_ABI_VERSION 1
+
+enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
+enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
+enum fovi_padding { FOVI_PAD_ZEROS = 0, FOVI_PAD_BORDER = 1 };
+
+/* Version of this header the library was built from (FOVI_ABI_VERSION). */
+int fovi_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* fovi_last_error(void);
+
+/*
+ * Foveated sampler: fixation transform + grid-sample of image views onto
+ * sensor points.
+ *
+ * Replaces GridSampler.forward (fovi/sensing/samplers.py:91-112), i.e.
+ * transform_sampling_grid (fovi/sensing/coords.py:590-642) followed by
+ * torch.nn.functional.grid_sample(img, grid, mode, align_corners=False)
+ * (samplers.py:108), for every fixation view in one launch (the per-fixation
+ * loop of fovi/sensing/policies.py:268-270 becomes the view axis).
+ *
+ * View v samples image view_image[v] (view v if view_image is NULL) at
+ *   gx = 2 * (grid[p].x * half_w[v] + fix_loc[v].w * W) / W - 1
+ *   gy = 2 * (grid[p].y * half_h[v] + fix_loc[v].h * H) / H - 1
+ * evaluated in fp32 in that order (fp64 for the multiply by the half size
+ * when fix_half_wide != 0, as the reference does for float fixation sizes).
+ */
+typedef struct fovi_sampler_args {
+  const void* img;            /* image batch, dtype img_dtype (F32 or BF16) */
+  int32_t img_dtype;
+  int32_t reserved0;
+  int64_t n_img, channels, height, width;
+  int64_t img_stride[4];      /* image, channel, row, column */
+  const float* grid;          /* [n_points, 2] sensor grid (x, -y) in [-1, 1] */
+  int64_t n_points;
+  int64_t n_views;
+  const float* fix_loc;       /* [n_views, 2] (h, w) fixation centre in [0, 1] */
+  const double* fix_half;     /* [n_views, 2] (h, w) half fixation size in pixels */
+  int32_t fix_half_wide;      /* 0: half size is used as fp32; 1: fp64 multiply */
+  int32_t reserved1;
+  const int32_t* view_image;  /* [n_views] or NULL */
+  int32_t mode;               /* fovi_interp */
+  int32_t padding;            /* fovi_padding */
+  void* out;                  /* dtype out_dtype (F32 or BF16) */
+  int32_t out_dtype;
+  int32_t reserved2;
+  int64_t out_stride[3];      /* view, channel, point */
+  float* grid_out;            /* optional [n_views, n_points, 2] (gx, gy), or NULL */
+} fovi_sampler_args;
+
+int fovi_sampler_fwd(const fovi_sampler_args* args, void* stream);
+
+/*
+ * kNN-convolution forward.
+ *
+ * Replaces KNNConvLayer.forward (fovi/arch/knn.py:538-557): the zero pad
+ * column + gather (_pad_and_gather_knns, knn.py:484-503), the one-hot
+ * local-RF einsum (_apply_local_rf, knn.py:505-526) and F.linear with the
+ * [c_out, c_in * n_ref] weight (knn.py:555) become one fused launch:
+ *
+ *   y[b, o, n] = bias[o] + sum_v sum_c A[b, n, v, c] * w[o, v * c_in + c]
+ *   A[b, n, v, c] = sum over the neighbours j of n in ref slot v of x[b, c, j]
+ *
+ * Neighbour lists are slot-major CSR per output point:
+ *   slot_ptr[n * n_ref + v] = (begin << 16) | count, and the input indices
+ *   are nbr_sorted[n * k + begin + i], i < count.
+ * The weight is the packed form made by fovi_knnconv_pack_weight: row o holds
+ * the reduction axis in slot-major order (v * c_in + c), zero padded to
+ * k_pad (a multiple of 64).
+ *
+ * x_dtype/w_dtype: F32/F32 (fp32 parity path) or BF16/BF16 (MFMA path) or
+ * F8E4M3/F8E4M3 (MFMA path; y = x_scale * w_scale[o] * sum(q_x * q_w) + bias).
+ */
+typedef struct fovi_knnconv_args {
+  const void* x;
+  int32_t x_dtype;
+  int32_t reserved0;
+  int64_t batch, c_in, n_in;
+  int64_t x_stride[3];        /* batch, channel, point */
+  int64_t n_out, k, n_ref;
+  const int32_t* slot_ptr;    /* [n_out, n_ref] */
+  const int32_t* nbr_sorted;  /* [n_out, k] */
+  const void* w;              /* packed [c_out, k_pad] */
+  int32_t w_dtype;
+  int32_t reserved1;
+  int64_t c_out, k_pad;
+  const float* bias;          /* [c_out] or NULL */
+  const float* w_scale;       /* [c_out] (F8E4M3 only) */
+  float x_scale;              /* (F8E4M3 only) */
+  int32_t reserved2;
+  void* y;
+  int32_t y_dtype;            /* F32 or BF16 */
+  int32_t reserved3;
+  int64_t y_stride[3];        /* batch, out channel, point */
+} fovi_knnconv_args;
+
+int fovi_knnconv_fwd(const fovi_knnconv_args* args, void* stream);
+
+/*
+ * Packs the reference weight layout for fovi_knnconv_fwd.
+ *
+ * w_ref is KNNConvLayer.weight, fp32 [c_out, c_in * n_ref] with reduction
+ * index c * n_ref + v (fovi/arch/knn.py:462,524). The packed output is
+ * [c_out, k_pad] with index v * c_in + c, zero padded, in out_dtype. For
+ * F8E4M3, row o is divided by w_scale[o] and rounded to OCP e4m3 (RNE,
+ * saturating to +-448).
+ */
+int fovi_knnconv_pack_weight(const float* w_ref, int64_t c_out, int64_t c_in, int64_t n_ref,
+                             void* w_packed, int32_t out_dtype, int64_t k_pad,
+                             const float* w_scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FOVI_HIP_H */

@@ -1,0 +1,73 @@
+"""The C-ABI library loads and exports every symbol include/fovi_hip.h declares (no GPU calls)."""
+import ctypes
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+from fovi_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    text = open(os.path.join(ROOT, "include", "fovi_hip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(fovi_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert set(names) == set(_lib.EXPORTED), names
+
+
+def test_library_exports_all_symbols():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail(f"{_lib.LIB_PATH} not built (run python -m fovi_amd.build)")
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    for name in _declared():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_and_error_string():
+    lib = _lib.load()
+    assert lib.fovi_abi_version() == _lib.ABI_VERSION
+    assert lib.fovi_last_error() == b""
+
+
+def test_argument_validation_without_gpu():
+    """Host-side checks reject bad arguments before any HIP call."""
+    lib = _lib.load()
+    a = _lib.KnnConvArgs()
+    assert lib.fovi_knnconv_fwd(a, None) != 0
+    assert b"null pointer" in lib.fovi_last_error()
+    s = _lib.SamplerArgs()
+    assert lib.fovi_sampler_fwd(s, None) != 0
+    assert b"null pointer" in lib.fovi_last_error()
+    assert lib.fovi_knnconv_pack_weight(None, 1, 1, 1, None, 0, 64, None, None) != 0
+
+
+def _c_layout(struct, fields, tmp_path):
+    """offsetof/sizeof of a header struct, from a C program built with gcc."""
+    src = tmp_path / "layout.c"
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "fovi_hip.h"', "int main(void) {",
+             f'  printf("%zu\\n", sizeof({struct}));']
+    lines += [f'  printf("%zu\\n", offsetof({struct}, {f}));' for f in fields]
+    lines += ["  return 0;", "}"]
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    vals = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    return vals[0], vals[1:]
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
+@pytest.mark.parametrize("py,c", [(_lib.SamplerArgs, "fovi_sampler_args"), (_lib.KnnConvArgs, "fovi_knnconv_args")])
+def test_struct_layout_matches_header(py, c, tmp_path):
+    fields = [f for f, _ in py._fields_]
+    size, offs = _c_layout(c, fields, tmp_path)
+    assert ctypes.sizeof(py) == size
+    for f, off in zip(fields, offs):
+        assert getattr(py, f).offset == off, f

@@ -1,0 +1,144 @@
+"""GPU parity of the kNN-conv forward against the CPU oracle (torch restatement of knn.py:484-557).
+
+Bar: fp32 within 1e-5 relative (L2 and max-abs/max|ref|); bf16 within 1e-2
+relative against the oracle evaluated on the bf16-rounded operands.
+"""
+import pytest
+import torch
+
+from fovi_amd.arch.knn import KNNConvLayer
+from fovi_amd.sensing.coords import SamplingCoords
+from oracle import knnconv_ref
+from tests.helpers import assert_close_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def _layer(res_in, res_out, k, c_in, c_out, side=None, bias=False, seed=1):
+    cin = SamplingCoords(16, 2.78, res_in, style="logpolar")
+    cout = SamplingCoords(16, 2.78, res_out, style="logpolar")
+    layer = KNNConvLayer(c_in, c_out, k, cin, cout, device="cuda", bias=bias, ref_frame_side_length=side)
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        layer.weight.copy_(torch.randn(layer.weight.shape, generator=g) * (1.0 / (c_in * layer._k)) ** 0.5)
+        if bias:
+            layer.bias.copy_(torch.randn(c_out, generator=g) * 0.1)
+    return layer
+
+
+def _oracle(layer, x, w=None):
+    w = layer.weight.detach().cpu() if w is None else w
+    b = None if layer.bias is None else layer.bias.detach().cpu()
+    return knnconv_ref.knnconv_forward(x.float().cpu(), layer.knn_indices.cpu(), layer.in_coords.shape[0],
+                                       layer.local_rf.cpu(), w, b)
+
+
+def test_c1_fp32():
+    """C1: 8 x 3 x 4096 fp32, k=9 on the 64x64 log-polar lattice, 3 -> 64."""
+    layer = _layer(64, 64, 9, 3, 64)
+    x = torch.rand(8, 3, 4096, generator=torch.Generator().manual_seed(0))
+    with torch.no_grad():
+        y = layer(x.cuda())
+    assert y.shape == (8, 64, 4096) and y.dtype == torch.float32
+    assert_close_rel(y.cpu(), _oracle(layer, x), 1e-5, "C1 fp32")
+
+
+@pytest.mark.parametrize("res_in,res_out,k,c_in,c_out,side,bias", [
+    (64, 32, 49, 3, 64, None, False),     # C2 layer 1 geometry
+    (32, 16, 25, 64, 192, None, False),   # C2 layer 2
+    (16, 16, 9, 192, 384, None, True),    # C2 layer 3
+    (16, 16, 9, 384, 256, None, False),   # C2 layer 4
+    (24, 12, 30, 5, 40, None, True),      # ragged: non-square k, odd channels, partial tiles
+    (32, 4, 256, 3, 96, 16, True),        # patch-embed style: k=256, 16x16 ref grid
+])
+def test_fp32_shapes(res_in, res_out, k, c_in, c_out, side, bias):
+    layer = _layer(res_in, res_out, k, c_in, c_out, side, bias)
+    x = torch.randn(3, c_in, res_in * res_in, generator=torch.Generator().manual_seed(5))
+    with torch.no_grad():
+        y = layer(x.cuda())
+    assert_close_rel(y.cpu(), _oracle(layer, x), 1e-5)
+
+
+@pytest.mark.parametrize("res_in,res_out,k,c_in,c_out,side,bias,channels_last", [
+    (64, 32, 49, 3, 64, None, False, False),     # C2 layer 1 (generic loader)
+    (32, 16, 25, 64, 192, None, False, True),    # C2 layer 2 (vector loader)
+    (32, 16, 25, 64, 192, None, False, False),   # same, channel-major input (generic loader)
+    (16, 16, 9, 192, 384, None, True, True),     # C2 layer 3
+    (16, 16, 9, 384, 256, None, False, True),    # C2 layer 4
+    (24, 12, 30, 5, 40, None, True, False),      # ragged
+    (32, 4, 256, 3, 96, 16, True, False),        # patch-embed style
+])
+def test_bf16_shapes(res_in, res_out, k, c_in, c_out, side, bias, channels_last):
+    layer = _layer(res_in, res_out, k, c_in, c_out, side, bias)
+    n_in = res_in * res_in
+    x = torch.randn(3, c_in, n_in, generator=torch.Generator().manual_seed(6)).bfloat16()
+    xd = x.cuda()
+    if channels_last:
+        xd = xd.transpose(1, 2).contiguous().transpose(1, 2)
+    with torch.no_grad():
+        y = layer(xd)
+    assert y.dtype == torch.bfloat16
+    ref = _oracle(layer, x, layer.weight.detach().cpu().bfloat16().float())
+    assert_close_rel(y.float().cpu(), ref, 1e-2)
+
+
+def test_autocast_bf16_casts_fp32_input():
+    layer = _layer(32, 16, 25, 64, 128)
+    x = torch.randn(2, 64, 1024, generator=torch.Generator().manual_seed(7))
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        y = layer(x.cuda())
+    assert y.dtype == torch.bfloat16
+    ref = _oracle(layer, x.bfloat16(), layer.weight.detach().cpu().bfloat16().float())
+    assert_close_rel(y.float().cpu(), ref, 1e-2)
+
+
+def test_output_is_channels_last_view_and_chains():
+    """Output [B,C,N] is a view of [B,N,C]; feeding it to the next layer takes the vector path."""
+    l1 = _layer(32, 16, 25, 64, 128, seed=2)
+    l2 = _layer(16, 16, 9, 128, 64, seed=3)
+    x = torch.randn(2, 64, 1024, generator=torch.Generator().manual_seed(8)).bfloat16()
+    with torch.no_grad():
+        h = l1(x.cuda())
+        assert h.stride(1) == 1
+        y = l2(torch.relu(h))
+    h_ref = _oracle(l1, x, l1.weight.detach().cpu().bfloat16().float()).bfloat16()
+    y_ref = _oracle(l2, torch.relu(h_ref), l2.weight.detach().cpu().bfloat16().float())
+    assert_close_rel(y.float().cpu(), y_ref, 2e-2)
+
+
+def test_weight_update_repacks():
+    layer = _layer(16, 16, 9, 64, 64)
+    x = torch.randn(1, 64, 256, generator=torch.Generator().manual_seed(9)).cuda()
+    with torch.no_grad():
+        y0 = layer(x)
+        layer.weight.mul_(2.0)
+        y1 = layer(x)
+    assert_close_rel(y1.cpu(), 2 * y0.cpu(), 1e-6)
+
+
+def test_backward_raises():
+    layer = _layer(16, 16, 9, 8, 8)
+    x = torch.randn(1, 8, 256, device="cuda", requires_grad=True)
+    y = layer(x)
+    with pytest.raises(NotImplementedError):
+        y.sum().backward()
+
+
+def test_c3_large_layer_slice_and_batch_independence():
+    """C3 geometry (16384 points, k=25, 256 -> 256, bf16): B=64 launch.
+
+    Oracle on one batch row (the reference algorithm at B=64 needs ~27 GB),
+    plus a size-independent property: each row of the B=64 result equals the
+    B=1 launch of that row bit for bit.
+    """
+    layer = _layer(128, 128, 25, 256, 256, seed=11)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(64, 256, 16384, generator=g).bfloat16()
+    xd = x.cuda().transpose(1, 2).contiguous().transpose(1, 2)
+    with torch.no_grad():
+        y = layer(xd)
+        for b in (0, 37, 63):
+            yb = layer(xd[b:b + 1])
+            assert torch.equal(y[b:b + 1], yb), f"row {b} differs from its B=1 launch"
+    ref = _oracle(layer, x[:1], layer.weight.detach().cpu().bfloat16().float())
+    assert_close_rel(y[:1].float().cpu(), ref, 1e-2, "C3 row 0")

@@ -1,0 +1,141 @@
+"""GPU parity of the foveated sampler against the CPU oracle.
+
+Bar: transformed sample coordinates bit-exact; nearest-mode values bit-exact;
+bilinear fp32 values within 1e-5 relative (L2 and max-abs/max|ref|); bf16
+outputs within 1e-2 relative.
+"""
+import numpy as np
+import pytest
+import torch
+
+from fovi_amd.sensing.retina import RetinalTransform
+from fovi_amd.sensing.samplers import GridSampler
+from oracle import sampler_ref
+from tests.helpers import assert_close_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(img, res, mode, pad, fix_loc, fix_size, out_dtype=None):
+    s = GridSampler(16, 2.78, res, device="cuda", mode=mode, style="logpolar", padding_mode=pad)
+    out, grid = s.sample_views(img.cuda(), fix_loc, fix_size, out_dtype=out_dtype, return_grid=True)
+    ref, ref_grid = sampler_ref.sampler_forward(img.float(), s.sampling_grid.cpu(), torch.as_tensor(fix_loc),
+                                                fix_size, mode, pad)
+    return out.cpu(), grid.cpu(), ref, ref_grid.squeeze(1)
+
+
+@pytest.mark.parametrize("mode", ["bilinear", "nearest"])
+@pytest.mark.parametrize("pad", ["zeros", "border"])
+def test_c1_plumbing_centre_fixation(mode, pad):
+    """C1: batch 8 of 3x256x256 fp32, 64x64 log-polar sensor, centre fixation, 256 px window."""
+    g = torch.Generator().manual_seed(0)
+    img = torch.rand(8, 3, 256, 256, generator=g)
+    fix_loc = torch.full((8, 2), 0.5)
+    fix_size = np.array([[256, 256]] * 8)
+    out, grid, ref, ref_grid = _run(img, 64, mode, pad, fix_loc, fix_size)
+    assert torch.equal(grid, ref_grid), "sample coordinates differ"
+    if mode == "nearest":
+        assert torch.equal(out, ref)
+    else:
+        assert_close_rel(out, ref, 1e-5, "bilinear fp32")
+
+
+@pytest.mark.parametrize("mode", ["bilinear", "nearest"])
+def test_random_fixations_non_square(mode):
+    g = torch.Generator().manual_seed(2)
+    img = torch.rand(5, 3, 200, 312, generator=g)
+    fix_loc = 0.25 + 0.5 * torch.rand(5, 2, generator=g)
+    fix_size = np.array([[150, 170], [200, 312], [96, 96], [300, 250], [64, 128]])
+    out, grid, ref, ref_grid = _run(img, 32, mode, "zeros", fix_loc, fix_size)
+    assert torch.equal(grid, ref_grid)
+    if mode == "nearest":
+        assert torch.equal(out, ref)
+    else:
+        assert_close_rel(out, ref, 1e-5, "bilinear fp32")
+
+
+def test_float64_fixation_sizes_use_fp64_multiply():
+    """Float fixation sizes make the reference multiply in fp64 (coords.py:632-633)."""
+    g = torch.Generator().manual_seed(3)
+    img = torch.rand(3, 3, 128, 128, generator=g)
+    fix_loc = torch.tensor([[0.5, 0.5], [0.31, 0.62], [0.7, 0.41]])
+    fix_size = np.array([[127.3, 99.9], [64.7, 64.7], [111.1, 131.13]], dtype=np.float64)
+    out, grid, ref, ref_grid = _run(img, 48, "bilinear", "zeros", fix_loc, fix_size)
+    assert torch.equal(grid, ref_grid)
+    assert_close_rel(out, ref, 1e-5)
+
+
+def test_bf16_image_and_output():
+    g = torch.Generator().manual_seed(4)
+    img = torch.rand(4, 3, 256, 256, generator=g).bfloat16()
+    fix_loc = 0.25 + 0.5 * torch.rand(4, 2, generator=g)
+    fix_size = np.array([[256, 256]] * 4)
+    out, grid, ref, ref_grid = _run(img, 64, "bilinear", "zeros", fix_loc, fix_size, out_dtype=torch.bfloat16)
+    assert out.dtype == torch.bfloat16
+    assert torch.equal(grid, ref_grid)
+    assert_close_rel(out.float(), ref, 1e-2, "bf16")
+    out32, _, ref32, _ = _run(img, 64, "nearest", "zeros", fix_loc, fix_size, out_dtype=torch.float32)
+    assert torch.equal(out32, ref32)
+
+
+def test_fused_fixation_views_match_per_view_calls():
+    """F fixations x B images in one launch, view (f, b) reads image b."""
+    g = torch.Generator().manual_seed(5)
+    B, Fx = 3, 4
+    img = torch.rand(B, 3, 160, 160, generator=g)
+    fix = 0.25 + 0.5 * torch.rand(Fx, B, 2, generator=g)
+    s = GridSampler(16, 2.78, 40, device="cuda", mode="bilinear", style="logpolar")
+    view_image = torch.arange(B).repeat(Fx)
+    out = s.sample_views(img.cuda(), fix.reshape(-1, 2), np.array([[160, 160]] * (Fx * B)),
+                         view_image=view_image).cpu()
+    for f in range(Fx):
+        ref, _ = sampler_ref.sampler_forward(img, s.sampling_grid.cpu(), fix[f], np.array([[160, 160]] * B))
+        assert_close_rel(out[f * B:(f + 1) * B], ref, 1e-5, f"fixation {f}")
+
+
+def test_strided_input_and_output_layouts():
+    g = torch.Generator().manual_seed(6)
+    img = torch.rand(2, 3, 96, 96, generator=g).to(memory_format=torch.channels_last)
+    s = GridSampler(16, 2.78, 24, device="cuda", mode="bilinear", style="logpolar")
+    out_cl = torch.empty(2, 576, 3, device="cuda").transpose(1, 2)   # [V, C, N] view of [V, N, C]
+    fix_loc = torch.tensor([[0.4, 0.6], [0.5, 0.5]])
+    s.sample_views(img.cuda(), fix_loc, np.array([[96, 96]] * 2), out=out_cl)
+    ref, _ = sampler_ref.sampler_forward(img.contiguous(), s.sampling_grid.cpu(), fix_loc, np.array([[96, 96]] * 2))
+    assert_close_rel(out_cl.cpu(), ref, 1e-5)
+
+
+def test_retinal_transform_defaults():
+    """RetinalTransform argument handling: scalar fixation size, tuple fix_loc, numpy sizes."""
+    g = torch.Generator().manual_seed(7)
+    img = torch.rand(4, 3, 224, 224, generator=g)
+    rt = RetinalTransform(64, start_res=224, fov=16, cmf_a=2.78, style="logpolar", sampler="grid_bilinear",
+                          device="cuda")
+    out = rt(img.cuda(), (0.5, 0.5)).cpu()
+    ref, _ = sampler_ref.sampler_forward(img, rt.sampler.sampling_grid.cpu(), torch.full((4, 2), 0.5),
+                                         np.array([[224, 224]] * 4))
+    assert out.shape == (4, 3, 4096)
+    assert_close_rel(out, ref, 1e-5)
+
+
+def test_full_size_c4_views_match_per_view_and_are_deterministic():
+    """C4-shaped launch (512 views of 128 images, 16384 points, bf16): size-independent checks.
+
+    Each view equals the single-view launch of the same image bit for bit,
+    and a repeat launch is bit-identical.
+    """
+    g = torch.Generator().manual_seed(0)
+    B, Fx = 128, 4
+    img = torch.rand(B, 3, 512, 512, generator=g).bfloat16().cuda()
+    fix = (0.25 + 0.5 * torch.rand(B * Fx, 2, generator=g))
+    vmap = torch.arange(B).repeat_interleave(Fx)
+    s = GridSampler(16, 2.78, 128, device="cuda", mode="nearest", style="logpolar")
+    sizes = np.array([[512, 512]] * (B * Fx))
+    out = s.sample_views(img, fix, sizes, view_image=vmap)
+    out2 = s.sample_views(img, fix, sizes, view_image=vmap)
+    assert torch.equal(out, out2)
+    for v in (0, 1, 257, B * Fx - 1):
+        one = s.sample_views(img[vmap[v]:vmap[v] + 1], fix[v:v + 1], sizes[:1])
+        assert torch.equal(out[v:v + 1], one)
+    ref, _ = sampler_ref.sampler_forward(img[vmap[5]:vmap[5] + 1].float().cpu(), s.sampling_grid.cpu(),
+                                         fix[5:6], sizes[:1], mode="nearest")
+    assert torch.equal(out[5:6].float().cpu(), ref)

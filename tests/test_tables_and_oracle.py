@@ -1,0 +1,185 @@
+"""CPU tests: host geometry/tables (closed forms, CSR format) and the oracle's own pinning."""
+import numpy as np
+import pytest
+import torch
+
+from fovi_amd.arch import knn_tables as T
+from fovi_amd.sensing.coords import SamplingCoords, find_desired_res, logpolar_ring_radii
+from oracle import knnconv_ref, sampler_ref
+from tests.helpers import layer_tables
+
+
+# ---------------------------------------------------------------- geometry ---
+@pytest.mark.parametrize("res", [8, 16, 64])
+def test_logpolar_point_set_closed_form(res):
+    fov, a = 16, 2.78
+    c = SamplingCoords(fov, a, res, style="logpolar")
+    assert c.shape == (res * res, 2)
+    # ring radii: r_i = (exp(w_i) - a) / (fov/2), w evenly spaced in log(r + a)
+    w = np.linspace(np.log(a), np.log(fov / 2 + a) + (np.log(fov / 2 + a) - np.log(a)) / (res - 1), res + 1)
+    r_closed = (np.exp(w) - a) / (fov / 2)
+    radii = c.polar[::res, 0].double().numpy()
+    assert np.allclose(radii, r_closed[:-1], atol=2e-6)
+    assert abs(radii[0]) < 1e-5                   # ring 0 is degenerate (exp(log a) - a)
+    ang = c.polar[:res, 1].double().numpy()
+    assert np.allclose(ang, np.arange(res) * 2 * np.pi / res, atol=1e-6)
+    xy = c.cartesian.double().numpy()
+    rr = np.repeat(radii, res)
+    aa = np.tile(ang, res)
+    assert np.allclose(xy[:, 0], rr * np.cos(aa), atol=1e-6)
+    assert np.allclose(xy[:, 1], rr * np.sin(aa), atol=1e-6)
+    # cortical: normalised log radius per ring and normalised angle, both in [0, 1]
+    cort = c.cortical.double().numpy()
+    assert cort.min() == 0.0 and cort.max() == 1.0
+    lr = np.log(np.hypot(xy[:, 0], xy[:, 1]) * fov / 2 + a)
+    lr = (lr - lr.min()) / (lr.max() - lr.min())
+    assert np.allclose(cort[:, 0], lr, atol=1e-5)
+    assert np.allclose(cort[:res, 1], np.arange(res) / (res - 1), atol=1e-6)
+
+
+def test_find_desired_res_logpolar():
+    assert find_desired_res(16, 2.78, 64 ** 2, "logpolar", force_less_than=True, quiet=True) == (64, 4096)
+    assert find_desired_res(16, 2.78, 1000, "logpolar", force_less_than=True, quiet=True) == (31, 961)
+    assert find_desired_res(16, 2.78, 1000, "logpolar", force_less_than=False, quiet=True) == (32, 1024)
+
+
+def test_strided_coords_are_regenerated_grids():
+    c = SamplingCoords(16, 2.78, 64, style="logpolar")
+    out, radii, _ = c.get_strided_coords(2)
+    assert radii == 32 and out.shape == (1024, 2)
+    assert torch.equal(out.cartesian, SamplingCoords(16, 2.78, 32, style="logpolar").cartesian)
+
+
+def test_knn_lattice_neighbourhoods():
+    """Away from the radial edges and the angle seam, k=9/25 are the 3x3/5x5 lattice squares."""
+    res = 32
+    t = layer_tables(res, res, 25)
+    idx = t["idx"].numpy()
+    for ring in range(4, res - 4):
+        for ang in range(4, res - 4):
+            n = ring * res + ang
+            got = set(idx[:, n].tolist())
+            want = {(ring + dr) * res + ang + da for dr in range(-2, 3) for da in range(-2, 3)}
+            assert got == want, (ring, ang)
+            assert idx[0, n] == n            # self first, distance 0
+    assert torch.all(t["dist"][0] == 0)
+
+
+def test_knn_seam_wraps_with_period_res_minus_one():
+    """Angle indices 0 and res-1 of a ring are at distance 0 (reference knn.py:137-140)."""
+    res = 16
+    t = layer_tables(res, res, 9)
+    d = t["dist"].numpy()
+    idx = t["idx"].numpy()
+    n = 6 * res + 0
+    assert (n + res - 1) in idx[:, n]
+    j = list(idx[:, n]).index(n + res - 1)
+    assert d[j, n] == 0.0
+
+
+def test_slots_self_at_centre_and_ranges():
+    """Slot ids index the ref grid; an interior point (symmetric neighbourhood) maps itself to the
+    centre slot, since its own offset is (0, 0) and min-max normalisation is symmetric."""
+    t = layer_tables(32, 32, 9)
+    slots = t["slots"].numpy()
+    idx = t["idx"].numpy()
+    assert slots.min() >= 0 and slots.max() < 9
+    for ring in range(8, 30):
+        for ang in range(2, 30):
+            n = ring * 32 + ang
+            j = list(idx[:, n]).index(n)
+            assert slots[n, j] == 4, (ring, ang)
+
+
+@pytest.mark.parametrize("res_in,res_out,k,side", [(16, 16, 9, None), (24, 12, 30, None), (32, 4, 256, 16)])
+def test_csr_tables_match_one_hot(res_in, res_out, k, side):
+    t = layer_tables(res_in, res_out, k, side)
+    ptr, nbr = t["ptr"].numpy(), t["nbr"].numpy()
+    idx, slots, V = t["idx"].numpy(), t["slots"].numpy(), t["V"]
+    for n in range(t["n_out"]):
+        want = {}
+        for j in range(t["k"]):
+            want.setdefault(slots[n, j], []).append(idx[j, n])
+        for v in range(V):
+            beg, cnt = int(ptr[n, v]) >> 16, int(ptr[n, v]) & 0xFFFF
+            assert list(nbr[n, beg:beg + cnt]) == want.get(v, [])
+
+
+def _csr_forward(x, ptr, nbr, w_ref, c_in, V):
+    """The kernel's arithmetic restated in numpy (float64): packed weight + CSR slot sums."""
+    B, C, _ = x.shape
+    n_out = ptr.shape[0]
+    wp = w_ref.reshape(w_ref.shape[0], c_in, V).transpose(0, 2, 1).reshape(w_ref.shape[0], V * c_in)
+    A = np.zeros((B, n_out, V * c_in))
+    for n in range(n_out):
+        for v in range(V):
+            beg, cnt = int(ptr[n, v]) >> 16, int(ptr[n, v]) & 0xFFFF
+            for i in range(cnt):
+                A[:, n, v * c_in:(v + 1) * c_in] += x[:, :, nbr[n, beg + i]]
+    return np.einsum("bnk,ok->bon", A, wp)
+
+
+@pytest.mark.parametrize("res_in,res_out,k,c_in,c_out,side", [(16, 16, 9, 3, 8, None), (16, 8, 25, 4, 5, None),
+                                                               (24, 4, 100, 2, 3, 10)])
+def test_csr_formulation_equals_oracle_and_bruteforce(res_in, res_out, k, c_in, c_out, side):
+    t = layer_tables(res_in, res_out, k, side)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(2, c_in, t["n_in"], generator=g, dtype=torch.float64)
+    w = torch.randn(c_out, c_in * t["V"], generator=g, dtype=torch.float64)
+    bias = torch.randn(c_out, generator=g, dtype=torch.float64)
+    ref = knnconv_ref.knnconv_forward(x, t["idx"], t["n_in"], t["rf"].double(), w, bias)
+    brute = knnconv_ref.knnconv_bruteforce(x, t["idx"], t["slots"], t["n_in"], w, bias)
+    assert np.allclose(ref.numpy(), brute, rtol=1e-10, atol=1e-10)
+    csr = _csr_forward(x.numpy(), t["ptr"].numpy(), t["nbr"].numpy(), w.numpy(), c_in, t["V"]) + \
+        bias.numpy()[None, :, None]
+    assert np.allclose(csr, brute, rtol=1e-10, atol=1e-10)
+
+
+def test_oracle_weight_index_is_channel_major():
+    """A weight that is 1 at column c*V + v only selects channel c of the neighbours in slot v."""
+    t = layer_tables(16, 16, 9)
+    c_in, V = 3, t["V"]
+    x = torch.randn(1, c_in, t["n_in"], dtype=torch.float64)
+    w = torch.zeros(1, c_in * V, dtype=torch.float64)
+    c, v = 2, 4
+    w[0, c * V + v] = 1.0
+    y = knnconv_ref.knnconv_forward(x, t["idx"], t["n_in"], t["rf"].double(), w)[0, 0]
+    idx, slots = t["idx"].numpy(), t["slots"].numpy()
+    for n in (0, 50, 200):
+        want = sum(x[0, c, idx[j, n]].item() for j in range(9) if slots[n, j] == v)
+        assert abs(y[n].item() - want) < 1e-12
+
+
+def test_oracle_linearity():
+    t = layer_tables(16, 16, 9)
+    g = torch.Generator().manual_seed(1)
+    x1, x2 = (torch.randn(2, 4, t["n_in"], generator=g, dtype=torch.float64) for _ in range(2))
+    w = torch.randn(6, 4 * t["V"], generator=g, dtype=torch.float64)
+    f = lambda x: knnconv_ref.knnconv_forward(x, t["idx"], t["n_in"], t["rf"].double(), w)
+    assert torch.allclose(f(x1 + 3 * x2), f(x1) + 3 * f(x2), atol=1e-10)
+
+
+# ----------------------------------------------------------------- sampler ---
+@pytest.mark.parametrize("mode", ["bilinear", "nearest"])
+@pytest.mark.parametrize("pad", ["zeros", "border"])
+def test_grid_sample_matches_textbook(mode, pad):
+    g = torch.Generator().manual_seed(0)
+    img = torch.rand(1, 3, 5, 7, generator=g, dtype=torch.float64)
+    pts = torch.rand(1, 1, 40, 2, generator=g, dtype=torch.float64) * 2.6 - 1.3
+    got = sampler_ref.grid_sample_views(img.float(), pts.float(), mode, pad)[0]
+    want = sampler_ref.bilinear_numpy(img[0].numpy(), pts[0, 0, :, 0].float().double().numpy(),
+                                      pts[0, 0, :, 1].float().double().numpy(), mode, pad)
+    assert np.allclose(got.double().numpy(), want, atol=1e-5)
+
+
+def test_transform_sampling_grid_closed_form():
+    """The sensor centre lands on the fixation pixel; unit radius spans half the window."""
+    grid = torch.tensor([[[[0.0, 0.0], [1.0, 0.0], [0.0, -1.0]]]])
+    fix = torch.tensor([[0.25, 0.75]])      # (h, w)
+    size = np.array([[64, 128]])            # (h, w) pixels
+    g = sampler_ref.transform_sampling_grid(grid, fix, size, (256, 512))[0, 0]
+    # centre: x = 0.75*512 = 384 px -> 2*384/512 - 1 = 0.5 ; y = 0.25*256 = 64 -> -0.5
+    assert g[0].tolist() == [0.5, -0.5]
+    # +x edge: 384 + 64 = 448 -> 0.75 ; -y edge (grid y=-1): 64 - 32 = 32 -> -0.75
+    assert g[1].tolist() == [0.75, -0.5]
+    assert g[2].tolist() == [0.5, -0.75]
