@@ -115,9 +115,10 @@ def bench_c4_sampler(steps, warmup, dev, mode="nearest"):
     out = torch.empty(B * Fx, 3, RES * RES, device=dev, dtype=torch.bfloat16)
     state = {"i": 0}
     fix_d = fix.to(dev)
+    views = sampler.prepare_views(fix_d, sizes, B, dev, view_image=vmap)
 
     def step():
-        sampler.sample_views(imgs[state["i"] & 1], fix_d, sizes, view_image=vmap, out=out)
+        sampler.sample_views(imgs[state["i"] & 1], out=out, views=views)
         state["i"] += 1
 
     with torch.no_grad():

@@ -10,6 +10,8 @@
 // Kernels
 //  * knnconv_f32_kernel: fp32 operands, any strides, fp32 FMA SGEMM tiling.
 //    The fp32 parity path.
+//  * knnconv_bf16_v2_kernel: the main bf16 path (channels-last rows,
+//    c_in % 32 == 0): 256-point tiles, CSR lists staged in LDS; see below.
 //  * knnconv_bf16_kernel: bf16 operands, fp32 accumulate on
 //    v_mfma_f32_32x32x16_bf16. 128-point x NT-channel tiles, 4 waves (2x2),
 //    64-wide reduction chunks double buffered in LDS (XOR-swizzled 16-byte
@@ -301,6 +303,203 @@ __global__ __launch_bounds__(256, 2) void knnconv_bf16_kernel(KnnParams p, int64
   }
 }
 
+// ---------------------------------------------------------------------------
+// bf16 MFMA path, large tiles (channels-last input, c_in % 32 == 0)
+// ---------------------------------------------------------------------------
+// 256 output points x NT output channels per workgroup of 8 waves (4 along
+// the points, 2 along the channels; wave tile 64 x NT/2 = 2 x NT/64 blocks of
+// v_mfma_f32_32x32x16_bf16). The tile's CSR lists (slot entries and
+// neighbour indices, 256 x (V + k) int32) are copied into LDS once, so the
+// reduction loop issues only data loads to memory. The reduction runs over
+// 32-channel chunks of one slot: the chunk's gathered A tile (256 x 32) and
+// weight tile (NT x 32) are double buffered in LDS, with the next chunk's
+// global loads in flight in registers while the current chunk's MFMAs run.
+// LDS rows are 64 bytes (four 16-byte chunks); chunk q of row r is stored at
+// q ^ ((r >> 1) & 3), which makes every 8-lane group of a fragment read hit
+// eight distinct 16-byte bank groups.
+constexpr int V2_MT = 256;
+constexpr int V2_CC = 32;
+
+__device__ __forceinline__ int swz32(int r, int q) { return r * V2_CC + ((q ^ ((r >> 1) & 3)) << 3); }
+
+size_t v2_lds_bytes(int nt, int64_t V, int64_t K) {
+  return static_cast<size_t>(2 * V2_MT * V2_CC * 2 + 2 * nt * V2_CC * 2) +
+         static_cast<size_t>(V2_MT) * static_cast<size_t>(V + K) * 4;
+}
+
+template <int NT, typename OutT>
+__global__ __launch_bounds__(512, 1) void knnconv_bf16_v2_kernel(KnnParams p, int64_t tiles_per_b,
+                                                                 int64_t n_tiles_n, int64_t total_tiles,
+                                                                 int64_t padded_tiles) {
+  constexpr int WN = NT / 2;
+  constexpr int CB = WN / 32;
+  constexpr int B_VECS = (NT * V2_CC / 8 + 511) / 512;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint16_t* As = reinterpret_cast<uint16_t*>(smem);                 // [2][256*32]
+  uint16_t* Bs = As + 2 * V2_MT * V2_CC;                            // [2][NT*32]
+  int32_t* ent = reinterpret_cast<int32_t*>(Bs + 2 * NT * V2_CC);   // [256][V]
+  int32_t* nbl = ent + V2_MT * p.V;                                 // [256][K]
+
+  const int64_t tile = xcd_tile(blockIdx.x, padded_tiles);
+  if (tile >= total_tiles) return;
+  const int64_t mt = tile / n_tiles_n;
+  const int64_t o0 = (tile % n_tiles_n) * NT;
+  const int64_t b = mt / tiles_per_b;
+  const int64_t n0 = (mt % tiles_per_b) * V2_MT;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 3, wn = wave >> 2;
+  const int V = static_cast<int>(p.V), K = static_cast<int>(p.K);
+
+  // stage the tile's CSR lists
+  for (int i = tid; i < V2_MT * V; i += 512) {
+    const int64_t n = n0 + i / V;
+    ent[i] = n < p.Nout ? p.slot_ptr[n0 * p.V + i] : 0;
+  }
+  for (int i = tid; i < V2_MT * K; i += 512) {
+    const int64_t n = n0 + i / K;
+    nbl[i] = n < p.Nout ? p.nbr[n0 * p.K + i] : -1;
+  }
+  __syncthreads();
+
+  const uint16_t* xb = static_cast<const uint16_t*>(p.x) + b * p.xs0;
+  const uint16_t* wp = static_cast<const uint16_t*>(p.w);
+  const int nc = static_cast<int>(p.C / V2_CC);     // chunks per slot
+  const int nk = V * nc;
+  const int part = tid & 3;
+  const int row0 = tid >> 2;                         // rows row0 and row0 + 128
+
+  Raw16 ra[2], rb[B_VECS];
+  auto load_chunk = [&](int kt) {
+    const int v = kt / nc;
+    const int c = (kt - v * nc) * V2_CC + part * 8;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int row = row0 + 128 * i;
+      const int32_t e = ent[row * V + v];
+      const int cnt = e & 0xffff;
+      const int32_t* nb = nbl + row * K + (e >> 16);
+      Raw16 r{0u, 0u, 0u, 0u};
+      if (cnt == 1) {
+        r = *reinterpret_cast<const Raw16*>(xb + static_cast<int64_t>(nb[0]) * p.xs2 + c);
+      } else if (cnt > 1) {
+        float s8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < cnt; ++j)
+          add_bf16x8(s8, *reinterpret_cast<const Raw16*>(xb + static_cast<int64_t>(nb[j]) * p.xs2 + c));
+        r = pack_bf16x8(s8);
+      }
+      ra[i] = r;
+    }
+    const int64_t k0 = static_cast<int64_t>(v) * p.C + (kt - v * nc) * V2_CC;
+#pragma unroll
+    for (int i = 0; i < B_VECS; ++i) {
+      const int q = tid + 512 * i;
+      const int row = q >> 2;
+      const int64_t o = o0 + row;
+      rb[i] = (q < NT * 4 && o < p.Cout)
+                  ? *reinterpret_cast<const Raw16*>(wp + o * p.Kpad + k0 + (q & 3) * 8)
+                  : Raw16{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_chunk = [&](int buf) {
+    uint16_t* a = As + buf * V2_MT * V2_CC;
+    uint16_t* bsm = Bs + buf * NT * V2_CC;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int row = row0 + 128 * i;
+      *reinterpret_cast<Raw16*>(&a[swz32(row, part)]) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_VECS; ++i) {
+      const int q = tid + 512 * i;
+      if (q < NT * 4) *reinterpret_cast<Raw16*>(&bsm[swz32(q >> 2, q & 3)]) = rb[i];
+    }
+  };
+
+  f32x16 acc[2][CB];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < CB; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  load_chunk(0);
+  store_chunk(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) load_chunk(kt + 1);
+    const uint16_t* a = As + buf * V2_MT * V2_CC;
+    const uint16_t* bsm = Bs + buf * NT * V2_CC;
+#pragma unroll
+    for (int ks = 0; ks < V2_CC / 16; ++ks) {
+      const int q = ks * 2 + (lane >> 5);
+      bf16x8 af[2], bfr[CB];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        af[i] = *reinterpret_cast<const bf16x8*>(&a[swz32(wm * 64 + i * 32 + (lane & 31), q)]);
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+        bfr[j] = *reinterpret_cast<const bf16x8*>(&bsm[swz32(wn * WN + j * 32 + (lane & 31), q)]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < CB; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < nk) store_chunk(buf ^ 1);
+    __syncthreads();
+  }
+
+  OutT* y = static_cast<OutT*>(p.y) + b * p.ys0;
+#pragma unroll
+  for (int j = 0; j < CB; ++j) {
+    const int64_t o = o0 + wn * WN + j * 32 + (lane & 31);
+    if (o >= p.Cout) continue;
+    const float bo = p.bias ? p.bias[o] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t n = n0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (n < p.Nout) Elem<OutT>::store(y + o * p.ys1 + n * p.ys2, acc[i][j][r] + bo);
+      }
+  }
+}
+
+template <int NT>
+static int launch_bf16_v2(const KnnParams& p, int out_t, hipStream_t s) {
+  const int64_t tiles_per_b = (p.Nout + V2_MT - 1) / V2_MT;
+  const int64_t n_tiles_n = (p.Cout + NT - 1) / NT;
+  const int64_t total = p.B * tiles_per_b * n_tiles_n;
+  const int64_t padded = (total + 7) / 8 * 8;
+  const size_t lds = v2_lds_bytes(NT, p.V, p.K);
+  dim3 grid(static_cast<unsigned>(padded));
+  if (out_t == FOVI_BF16) {
+    hipFuncSetAttribute(reinterpret_cast<const void*>(&knnconv_bf16_v2_kernel<NT, uint16_t>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    hipLaunchKernelGGL((knnconv_bf16_v2_kernel<NT, uint16_t>), grid, dim3(512), lds, s, p, tiles_per_b,
+                       n_tiles_n, total, padded);
+  } else {
+    hipFuncSetAttribute(reinterpret_cast<const void*>(&knnconv_bf16_v2_kernel<NT, float>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    hipLaunchKernelGGL((knnconv_bf16_v2_kernel<NT, float>), grid, dim3(512), lds, s, p, tiles_per_b,
+                       n_tiles_n, total, padded);
+  }
+  return 0;
+}
+
+// Picks the widest channel tile whose LDS footprint fits; 0 if none does.
+static int v2_tile_n(const KnnParams& p) {
+  const int cands[4] = {256, 192, 128, 64};
+  for (int nt : cands) {
+    if (nt > 64 && p.Cout <= nt / 2) continue;   // avoid tiles more than half empty
+    if (v2_lds_bytes(nt, p.V, p.K) <= 160 * 1024) return nt;
+  }
+  return 0;
+}
+
 template <int NT, bool VEC>
 static void launch_bf16(const KnnParams& p, int out_t, hipStream_t s) {
   const int64_t tiles_per_b = (p.Nout + MM_MT - 1) / MM_MT;
@@ -424,7 +623,17 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
   }
   if (a->x_dtype == FOVI_BF16 && a->w_dtype == FOVI_BF16) {
     const uintptr_t xa = reinterpret_cast<uintptr_t>(a->x);
-    const bool vec = p.xs1 == 1 && p.C % MM_KC == 0 && p.xs2 % 8 == 0 && p.xs0 % 8 == 0 && (xa % 16) == 0;
+    const bool rows16 = p.xs1 == 1 && p.xs2 % 8 == 0 && p.xs0 % 8 == 0 && (xa % 16) == 0;
+    if (rows16 && p.C % V2_CC == 0) {
+      const int nt = v2_tile_n(p);
+      int rc = -1;
+      if (nt == 256) rc = launch_bf16_v2<256>(p, a->y_dtype, s);
+      else if (nt == 192) rc = launch_bf16_v2<192>(p, a->y_dtype, s);
+      else if (nt == 128) rc = launch_bf16_v2<128>(p, a->y_dtype, s);
+      else if (nt == 64) rc = launch_bf16_v2<64>(p, a->y_dtype, s);
+      if (rc == 0) return check_launch("fovi_knnconv_fwd(bf16 v2)");
+    }
+    const bool vec = rows16 && p.C % MM_KC == 0;
     const bool wide = p.Cout % 128 == 0;
     if (vec && wide) launch_bf16<128, true>(p, a->y_dtype, s);
     else if (vec) launch_bf16<64, true>(p, a->y_dtype, s);

@@ -10,11 +10,14 @@
 //  * fixation transform (fovi/sensing/coords.py:624-640): fp32
 //    x*half + c*W, then 2*x/W - 1, each op rounded (built with
 //    -ffp-contract=off, so no fused multiply-add);
-//  * grid_sample unnormalisation for align_corners=False as the CPU kernel of
-//    torch.nn.functional.grid_sample evaluates it, (g + 1) * (size/2) - 0.5;
-//    'border' clips to [0, size-1]; 'nearest' rounds half to even;
-//  * bilinear weights from floor() and the fractional parts, blended
-//    nw, ne, sw, se in that order; out-of-image taps contribute zero.
+//  * grid_sample (align_corners=False) in the rounding of the CPU kernel of
+//    torch.nn.functional.grid_sample, which is the oracle: unnormalisation as
+//    one fused multiply-add fma(g + 1, size/2, -0.5); 'border' clips to
+//    [0, size-1]; 'nearest' rounds half to even; bilinear weights
+//    (1-dy)(1-dx), (1-dy)dx, dy(1-dx), dy*dx from floor() and the fractional
+//    parts, blended as the chain fma(se, fma(sw, fma(ne, nw*v_nw)));
+//    out-of-image taps contribute zero. This matches that kernel bit for bit
+//    (checked on 20000 random points at a non-power-of-two size).
 #include "common.h"
 
 namespace fovi {
@@ -73,8 +76,8 @@ __global__ __launch_bounds__(256) void sampler_kernel(SamplerParams p) {
   }
   const InT* src = static_cast<const InT*>(p.img) + img * p.is0;
 
-  float ix = (gx + 1.0f) * (W * 0.5f) - 0.5f;
-  float iy = (gy + 1.0f) * (H * 0.5f) - 0.5f;
+  float ix = __builtin_fmaf(gx + 1.0f, W * 0.5f, -0.5f);
+  float iy = __builtin_fmaf(gy + 1.0f, H * 0.5f, -0.5f);
   if (PAD == FOVI_PAD_BORDER) {
     ix = fminf(fmaxf(ix, 0.0f), W - 1.0f);
     iy = fminf(fmaxf(iy, 0.0f), H - 1.0f);
@@ -113,7 +116,7 @@ __global__ __launch_bounds__(256) void sampler_kernel(SamplerParams p) {
     const float v_ne = b_ne ? Elem<InT>::load(s + o_ne) : 0.0f;
     const float v_sw = b_sw ? Elem<InT>::load(s + o_sw) : 0.0f;
     const float v_se = b_se ? Elem<InT>::load(s + o_se) : 0.0f;
-    const float val = v_nw * w_nw + v_ne * w_ne + v_sw * w_sw + v_se * w_se;
+    const float val = __builtin_fmaf(v_se, w_se, __builtin_fmaf(v_sw, w_sw, __builtin_fmaf(v_ne, w_ne, v_nw * w_nw)));
     Elem<OutT>::store(out + c * p.os1, val);
   }
 }

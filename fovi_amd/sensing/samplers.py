@@ -48,6 +48,14 @@ def fixation_half_sizes(fixation_size, n):
     return half.to(torch.float64).contiguous(), int(wide)
 
 
+class _Views:
+    """Device-resident fixation tables of one set of views."""
+
+    def __init__(self, fix_loc, half, wide, view_image, n_views, n_img):
+        self.fix_loc, self.half, self.wide = fix_loc, half, wide
+        self.view_image, self.n_views, self.n_img = view_image, n_views, n_img
+
+
 class BaseGridSampler(nn.Module):
     """Grid preparation shared by samplers (reference ``samplers.py:13-47``)."""
 
@@ -88,24 +96,16 @@ class GridSampler(BaseGridSampler):
             self._grid_dev = g
         return g
 
-    def sample_views(self, img, fix_loc, fixation_size, view_image=None, out=None, out_dtype=None,
-                     return_grid=False):
-        """Samples ``V`` views; returns ``out [V, C, N]`` (any strides if ``out`` is given).
+    def prepare_views(self, fix_loc, fixation_size, n_img, device, view_image=None):
+        """Device tables of a set of fixation views, reusable across calls.
 
         ``fix_loc [V, 2]`` (h, w) in [0, 1]; ``fixation_size [V, 2]`` (h, w)
-        pixels; ``view_image [V]`` int32 image index per view (default: view v
+        pixels; ``view_image [V]`` image index per view (default: view v
         reads image v).
         """
-        _lib.require_device(img)
-        if img.dim() != 4:
-            raise ValueError(f"img must be [B, C, H, W]; got {tuple(img.shape)}")
-        n_img, ch, hh, ww = img.shape
-        dev = img.device
-        fix_loc = torch.as_tensor(fix_loc, dtype=torch.float32)
-        fix_loc = fix_loc.reshape(-1, 2).to(dev).contiguous()
+        fix_loc = torch.as_tensor(fix_loc, dtype=torch.float32).reshape(-1, 2).to(device).contiguous()
         n_views = fix_loc.shape[0]
         half, wide = fixation_half_sizes(fixation_size, n_views)
-        half = half.to(dev)
         vmap = None
         if view_image is not None:
             vi = torch.as_tensor(view_image).reshape(-1)
@@ -113,9 +113,29 @@ class GridSampler(BaseGridSampler):
                 raise ValueError("view_image must have one entry per view")
             if int(vi.min()) < 0 or int(vi.max()) >= n_img:
                 raise ValueError(f"view_image entries must be in [0, {n_img})")
-            vmap = vi.to(device=dev, dtype=torch.int32).contiguous()
+            vmap = vi.to(device=device, dtype=torch.int32).contiguous()
         elif n_views > n_img:
             raise ValueError(f"{n_views} views of {n_img} images need a view_image map")
+        return _Views(fix_loc, half.to(device), wide, vmap, n_views, n_img)
+
+    def sample_views(self, img, fix_loc=None, fixation_size=None, view_image=None, out=None, out_dtype=None,
+                     return_grid=False, views=None):
+        """Samples ``V`` views in one launch; returns ``out [V, C, N]``.
+
+        Views come from ``views`` (see ``prepare_views``) or from
+        ``fix_loc``/``fixation_size``/``view_image``. ``out`` may be any
+        strided ``[V, C, N]`` tensor (e.g. a channels-last view).
+        """
+        _lib.require_device(img)
+        if img.dim() != 4:
+            raise ValueError(f"img must be [B, C, H, W]; got {tuple(img.shape)}")
+        n_img, ch, hh, ww = img.shape
+        dev = img.device
+        if views is None:
+            views = self.prepare_views(fix_loc, fixation_size, n_img, dev, view_image)
+        elif views.n_img > n_img:
+            raise ValueError(f"views were prepared for {views.n_img} images, got {n_img}")
+        n_views = views.n_views
         grid = self._grid(dev)
         n_pts = grid.shape[0]
         odt = out_dtype or (img.dtype if img.dtype in (torch.float32, torch.bfloat16) else torch.float32)
@@ -129,8 +149,8 @@ class GridSampler(BaseGridSampler):
         a.n_img, a.channels, a.height, a.width = n_img, ch, hh, ww
         a.img_stride[:] = list(img.stride())
         a.grid = grid.data_ptr(); a.n_points = n_pts; a.n_views = n_views
-        a.fix_loc = fix_loc.data_ptr(); a.fix_half = half.data_ptr(); a.fix_half_wide = wide
-        a.view_image = None if vmap is None else vmap.data_ptr()
+        a.fix_loc = views.fix_loc.data_ptr(); a.fix_half = views.half.data_ptr(); a.fix_half_wide = views.wide
+        a.view_image = None if views.view_image is None else views.view_image.data_ptr()
         a.mode = _MODES[self.mode]; a.padding = _PADS[self.padding_mode]
         a.out = out.data_ptr(); a.out_dtype = _lib.dtype_code(out.dtype)
         a.out_stride[:] = list(out.stride())

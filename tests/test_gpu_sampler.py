@@ -1,8 +1,9 @@
 """GPU parity of the foveated sampler against the CPU oracle.
 
 Bar: transformed sample coordinates bit-exact; nearest-mode values bit-exact;
-bilinear fp32 values within 1e-5 relative (L2 and max-abs/max|ref|); bf16
-outputs within 1e-2 relative.
+bilinear fp32 values within 1e-5 relative (L2 and max-abs/max|ref|) and at
+least 99.9% of them bit-identical to torch's CPU grid_sample (the kernel uses
+its fused-multiply-add rounding); bf16 outputs within 1e-2 relative.
 """
 import numpy as np
 import pytest
@@ -11,7 +12,7 @@ import torch
 from fovi_amd.sensing.retina import RetinalTransform
 from fovi_amd.sensing.samplers import GridSampler
 from oracle import sampler_ref
-from tests.helpers import assert_close_rel
+from tests.helpers import assert_close_rel, assert_mostly_bit_exact
 
 pytestmark = pytest.mark.gpu
 
@@ -38,6 +39,7 @@ def test_c1_plumbing_centre_fixation(mode, pad):
         assert torch.equal(out, ref)
     else:
         assert_close_rel(out, ref, 1e-5, "bilinear fp32")
+        assert_mostly_bit_exact(out, ref, what="bilinear fp32")
 
 
 @pytest.mark.parametrize("mode", ["bilinear", "nearest"])
@@ -52,6 +54,7 @@ def test_random_fixations_non_square(mode):
         assert torch.equal(out, ref)
     else:
         assert_close_rel(out, ref, 1e-5, "bilinear fp32")
+        assert_mostly_bit_exact(out, ref, what="bilinear fp32")
 
 
 def test_float64_fixation_sizes_use_fp64_multiply():
