@@ -14,7 +14,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 F32, BF16, F8E4M3 = 0, 1, 2
 NEAREST, BILINEAR = 0, 1
 PAD_ZEROS, PAD_BORDER = 0, 1
@@ -55,6 +55,9 @@ class KnnConvArgs(C.Structure):
         ("x_scale", C.c_float), ("reserved2", C.c_int32),
         ("y", C.c_void_p), ("y_dtype", C.c_int32), ("reserved3", C.c_int32),
         ("y_stride", C.c_int64 * 3),
+        ("tile_lo", C.c_void_p), ("tile_span", C.c_void_p),
+        ("tile_ent", C.c_void_p), ("tile_nbr", C.c_void_p),
+        ("tile_points", C.c_int32), ("max_span", C.c_int32),
     ]
 
 

@@ -121,6 +121,13 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         self.knn_indices_pad_mask = self.knn_indices_pad_mask.to(device)
         self.register_buffer("slot_ptr", slot_ptr.to(device), persistent=False)
         self.register_buffer("nbr_sorted", nbr_sorted.to(device), persistent=False)
+        tiles = T.tile_tables(knn_indices, self.slots, n_in, n_ref)
+        self._max_span = 0
+        for name, t in zip(("tile_lo", "tile_span", "tile_ent", "tile_nbr"),
+                           tiles if tiles is not None else (None,) * 4):
+            self.register_buffer(name, None if t is None else t.to(device), persistent=False)
+        if tiles is not None:
+            self._max_span = int(tiles[1].max())
         self._packed = {}
 
     # -- setup ---------------------------------------------------------------
@@ -210,6 +217,10 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         a.bias = None if bias is None else bias.data_ptr()
         a.y = y.data_ptr(); a.y_dtype = _lib.dtype_code(dt)
         a.y_stride[:] = [y.stride(0), y.stride(2), y.stride(1)]
+        if self.tile_lo is not None:
+            a.tile_lo = self.tile_lo.data_ptr(); a.tile_span = self.tile_span.data_ptr()
+            a.tile_ent = self.tile_ent.data_ptr(); a.tile_nbr = self.tile_nbr.data_ptr()
+            a.tile_points = T.TILE_POINTS; a.max_span = self._max_span
         lib = _lib.load()
         _lib.check(lib.fovi_knnconv_fwd(a, _lib.stream_handle(x.device)), "fovi_knnconv_fwd")
         return y.transpose(1, 2)

@@ -36,6 +36,8 @@ __all__ = [
     "local_rf_slots",
     "slots_to_one_hot",
     "csr_tables",
+    "tile_tables",
+    "TILE_POINTS",
 ]
 
 _PAIR_BUDGET = 500_000_000  # distance-matrix elements per chunk (reference knn.py:43-49)
@@ -165,3 +167,45 @@ def csr_tables(knn_idx, slots, n_in, n_ref):
     begin = np.cumsum(counts, axis=1) - counts
     ptr = ((begin << 16) | counts).astype(np.int32)
     return torch.from_numpy(ptr), torch.from_numpy(nbr)
+
+
+TILE_POINTS = 256  # output points per workgroup tile of the staged-row kernel
+
+
+def tile_tables(knn_idx, slots, n_in, n_ref, tile=TILE_POINTS):
+    """Per-tile compact tables for the kernel that stages input rows in LDS.
+
+    Output points are cut into tiles of ``tile`` consecutive points. The
+    inputs any point of a tile reads lie in one contiguous index range
+    ``[lo, lo + span)`` (on the ring-major log-polar lattice a tile of two
+    rings reads about six rings), which the kernel copies into LDS. Returns
+    ``(lo [T] int32, span [T] int32, ent [T*tile, V] uint16,
+    nbr [T*tile, k] uint16)`` where ``ent = (count << 8) | begin`` and
+    ``nbr`` holds input indices relative to ``lo`` in the CSR order of
+    ``csr_tables``; or ``None`` when k > 255 or a span exceeds 65535.
+    """
+    k, n_out = knn_idx.shape
+    if k > 255:
+        return None
+    ptr, nbr = csr_tables(knn_idx, slots, n_in, n_ref)
+    ptr = ptr.numpy().astype(np.int64)
+    nbr = nbr.numpy().astype(np.int64)
+    n_tiles = -(-n_out // tile)
+    lo = np.zeros(n_tiles, np.int64)
+    span = np.zeros(n_tiles, np.int64)
+    nbr_loc = np.zeros((n_tiles * tile, k), np.int64)
+    ent = np.zeros((n_tiles * tile, n_ref), np.int64)
+    for t in range(n_tiles):
+        s, e = t * tile, min((t + 1) * tile, n_out)
+        blk = nbr[s:e]
+        valid = blk >= 0
+        if not valid.any():
+            continue
+        lo[t] = blk[valid].min()
+        span[t] = blk[valid].max() - lo[t] + 1
+        nbr_loc[s:e] = np.where(valid, blk - lo[t], 0)
+        ent[s:e] = ((ptr[s:e] & 0xFFFF) << 8) | (ptr[s:e] >> 16)
+    if span.max() > 0xFFFF:
+        return None
+    return (torch.from_numpy(lo.astype(np.int32)), torch.from_numpy(span.astype(np.int32)),
+            torch.from_numpy(ent.astype(np.uint16)), torch.from_numpy(nbr_loc.astype(np.uint16)))

@@ -37,6 +37,10 @@ struct KnnParams {
   float x_scale;
   void* y;
   int64_t ys0, ys1, ys2;
+  const int32_t* tile_lo;
+  const uint16_t* tile_ent;
+  const uint16_t* tile_nbr;
+  int max_span;
 };
 
 // ---------------------------------------------------------------------------
@@ -500,6 +504,245 @@ static int v2_tile_n(const KnnParams& p) {
   return 0;
 }
 
+// ---------------------------------------------------------------------------
+// bf16 MFMA path with the tile's input rows staged in LDS
+// ---------------------------------------------------------------------------
+// Same tile shape and MFMA core as v2. The inputs of a 256-point tile form a
+// contiguous index range (six rings for a two-ring tile on the log-polar
+// lattice), copied into LDS one 32-channel chunk at a time (S, row stride 64
+// bytes) with coalesced loads; the next chunk's rows are loaded into
+// registers a whole channel chunk ahead and written when S is free. Each
+// (slot, chunk) A tile is then assembled LDS -> LDS from S through the
+// tile's uint16 CSR tables (neighbour sums in fp32, one RNE rounding via
+// v_cvt_pk_bf16_f32), one iteration ahead of the MFMAs that consume it. The
+// only global loads inside the reduction loop are the weight tiles.
+// Iterations run channel chunk outer, slot inner.
+constexpr int V3_MT = 256;
+constexpr int V3_CC = 32;
+
+size_t v3_lds_bytes(int nt, int64_t V, int64_t K, int max_span) {
+  return static_cast<size_t>(max_span) * V3_CC * 2 + 2 * V3_MT * V3_CC * 2 + 2 * nt * V3_CC * 2 +
+         static_cast<size_t>(V3_MT) * static_cast<size_t>(V + K) * 2;
+}
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
+  const f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2v));
+}
+
+template <int NT, int SV, typename OutT>
+__global__ __launch_bounds__(512, 1) void knnconv_bf16_v3_kernel(KnnParams p, int64_t tiles_per_b,
+                                                                 int64_t n_tiles_n, int64_t total_tiles,
+                                                                 int64_t padded_tiles) {
+  constexpr int WN = NT / 2;
+  constexpr int CB = WN / 32;
+  constexpr int B_VECS = (NT * V3_CC / 8 + 511) / 512;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint16_t* As = reinterpret_cast<uint16_t*>(smem);                     // [2][256*32]
+  uint16_t* Bs = As + 2 * V3_MT * V3_CC;                                // [2][NT*32]
+  uint16_t* ent = Bs + 2 * NT * V3_CC;                                  // [256][V]
+  uint16_t* nbl = ent + V3_MT * p.V;                                    // [256][K]
+  uint16_t* S = nbl + V3_MT * p.K;                                      // [max_span][32]
+  S = reinterpret_cast<uint16_t*>((reinterpret_cast<uintptr_t>(S) + 15) & ~uintptr_t(15));
+
+  const int64_t tile = xcd_tile(blockIdx.x, padded_tiles);
+  if (tile >= total_tiles) return;
+  const int64_t mt = tile / n_tiles_n;
+  const int64_t o0 = (tile % n_tiles_n) * NT;
+  const int64_t b = mt / tiles_per_b;
+  const int64_t pt = mt % tiles_per_b;          // point tile within the batch row
+  const int64_t n0 = pt * V3_MT;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 3, wn = wave >> 2;
+  const int V = static_cast<int>(p.V), K = static_cast<int>(p.K);
+  const int64_t lo = p.tile_lo[pt];
+  const int span = static_cast<int>(min(static_cast<int64_t>(p.max_span), p.Nin - lo));
+
+  for (int i = tid; i < V3_MT * V; i += 512) ent[i] = p.tile_ent[n0 * p.V + i];
+  for (int i = tid; i < V3_MT * K; i += 512) nbl[i] = p.tile_nbr[n0 * p.K + i];
+
+  const uint16_t* xb = static_cast<const uint16_t*>(p.x) + b * p.xs0;
+  const uint16_t* wp = static_cast<const uint16_t*>(p.w);
+  const int ncc = static_cast<int>(p.C / V3_CC);
+  const int nit = ncc * V;
+  const int part = tid & 3;
+  const int row0 = tid >> 2;
+
+  Raw16 rs[SV], rb[B_VECS];
+  auto load_s = [&](int cc) {
+#pragma unroll
+    for (int j = 0; j < SV; ++j) {
+      const int q = tid + 512 * j;
+      const int r = q >> 2;
+      rs[j] = (r < span) ? *reinterpret_cast<const Raw16*>(xb + (lo + r) * p.xs2 + cc * V3_CC + (q & 3) * 8)
+                         : Raw16{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_s = [&]() {
+#pragma unroll
+    for (int j = 0; j < SV; ++j) {
+      const int q = tid + 512 * j;
+      if ((q >> 2) < span) *reinterpret_cast<Raw16*>(&S[q * 8]) = rs[j];
+    }
+  };
+  auto load_w = [&](int it) {
+    const int cc = it / V, v = it - cc * V;
+    const int64_t k0 = static_cast<int64_t>(v) * p.C + cc * V3_CC;
+#pragma unroll
+    for (int i = 0; i < B_VECS; ++i) {
+      const int q = tid + 512 * i;
+      const int64_t o = o0 + (q >> 2);
+      rb[i] = (q < NT * 4 && o < p.Cout)
+                  ? *reinterpret_cast<const Raw16*>(wp + o * p.Kpad + k0 + (q & 3) * 8)
+                  : Raw16{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_w = [&](int buf) {
+    uint16_t* bsm = Bs + buf * NT * V3_CC;
+#pragma unroll
+    for (int i = 0; i < B_VECS; ++i) {
+      const int q = tid + 512 * i;
+      if (q < NT * 4) *reinterpret_cast<Raw16*>(&bsm[swz32(q >> 2, q & 3)]) = rb[i];
+    }
+  };
+  auto build_a = [&](int it, int buf) {
+    const int v = it % V;
+    uint16_t* a = As + buf * V3_MT * V3_CC;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int row = row0 + 128 * i;
+      const int e = ent[row * V + v];
+      const int cnt = e >> 8;
+      const uint16_t* nb = nbl + row * K + (e & 0xff);
+      Raw16 r{0u, 0u, 0u, 0u};
+      if (cnt == 1) {
+        r = *reinterpret_cast<const Raw16*>(&S[nb[0] * V3_CC + part * 8]);
+      } else if (cnt > 1) {
+        float s8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < cnt; ++j) add_bf16x8(s8, *reinterpret_cast<const Raw16*>(&S[nb[j] * V3_CC + part * 8]));
+        r = Raw16{cvt_pk_bf16(s8[0], s8[1]), cvt_pk_bf16(s8[2], s8[3]), cvt_pk_bf16(s8[4], s8[5]),
+                  cvt_pk_bf16(s8[6], s8[7])};
+      }
+      *reinterpret_cast<Raw16*>(&a[swz32(row, part)]) = r;
+    }
+  };
+
+  f32x16 acc[2][CB];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < CB; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  // prologue: S(0), W(0), A(0); S(1) in flight
+  load_s(0);
+  load_w(0);
+  store_s();
+  store_w(0);
+  if (ncc > 1) load_s(1);
+  __syncthreads();
+  build_a(0, 0);
+  __syncthreads();
+
+  for (int it = 0; it < nit; ++it) {
+    const int cur = it & 1;
+    const int nx = it + 1;
+    if (nx < nit) {
+      load_w(nx);
+      const int cc1 = nx / V, v1 = nx - cc1 * V;
+      if (v1 == 0) {            // next iteration starts channel chunk cc1: refresh S
+        store_s();
+        __syncthreads();
+        if (cc1 + 1 < ncc) load_s(cc1 + 1);
+      }
+      build_a(nx, cur ^ 1);
+    }
+    const uint16_t* a = As + cur * V3_MT * V3_CC;
+    const uint16_t* bsm = Bs + cur * NT * V3_CC;
+#pragma unroll
+    for (int ks = 0; ks < V3_CC / 16; ++ks) {
+      const int q = ks * 2 + (lane >> 5);
+      bf16x8 af[2], bfr[CB];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        af[i] = *reinterpret_cast<const bf16x8*>(&a[swz32(wm * 64 + i * 32 + (lane & 31), q)]);
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+        bfr[j] = *reinterpret_cast<const bf16x8*>(&bsm[swz32(wn * WN + j * 32 + (lane & 31), q)]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < CB; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+    if (nx < nit) store_w(cur ^ 1);
+    __syncthreads();
+  }
+
+  OutT* y = static_cast<OutT*>(p.y) + b * p.ys0;
+#pragma unroll
+  for (int j = 0; j < CB; ++j) {
+    const int64_t o = o0 + wn * WN + j * 32 + (lane & 31);
+    if (o >= p.Cout) continue;
+    const float bo = p.bias ? p.bias[o] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t n = n0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (n < p.Nout) Elem<OutT>::store(y + o * p.ys1 + n * p.ys2, acc[i][j][r] + bo);
+      }
+  }
+}
+
+template <int NT, int SV>
+static void launch_bf16_v3_sv(const KnnParams& p, int out_t, hipStream_t s) {
+  const int64_t tiles_per_b = (p.Nout + V3_MT - 1) / V3_MT;
+  const int64_t n_tiles_n = (p.Cout + NT - 1) / NT;
+  const int64_t total = p.B * tiles_per_b * n_tiles_n;
+  const int64_t padded = (total + 7) / 8 * 8;
+  const size_t lds = v3_lds_bytes(NT, p.V, p.K, p.max_span) + 16;
+  dim3 grid(static_cast<unsigned>(padded));
+  if (out_t == FOVI_BF16) {
+    hipFuncSetAttribute(reinterpret_cast<const void*>(&knnconv_bf16_v3_kernel<NT, SV, uint16_t>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    hipLaunchKernelGGL((knnconv_bf16_v3_kernel<NT, SV, uint16_t>), grid, dim3(512), lds, s, p, tiles_per_b,
+                       n_tiles_n, total, padded);
+  } else {
+    hipFuncSetAttribute(reinterpret_cast<const void*>(&knnconv_bf16_v3_kernel<NT, SV, float>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    hipLaunchKernelGGL((knnconv_bf16_v3_kernel<NT, SV, float>), grid, dim3(512), lds, s, p, tiles_per_b,
+                       n_tiles_n, total, padded);
+  }
+}
+
+template <int NT>
+static bool launch_bf16_v3(const KnnParams& p, int out_t, hipStream_t s) {
+  const int sv = (p.max_span * 4 + 511) / 512;
+  if (sv <= 2) launch_bf16_v3_sv<NT, 2>(p, out_t, s);
+  else if (sv <= 4) launch_bf16_v3_sv<NT, 4>(p, out_t, s);
+  else if (sv <= 6) launch_bf16_v3_sv<NT, 6>(p, out_t, s);
+  else if (sv <= 8) launch_bf16_v3_sv<NT, 8>(p, out_t, s);
+  else return false;
+  return true;
+}
+
+// Widest channel tile whose LDS footprint fits with the staged rows; 0 if none.
+static int v3_tile_n(const KnnParams& p) {
+  if (p.max_span <= 0 || p.max_span > 1024) return 0;
+  const int cands[4] = {256, 192, 128, 64};
+  for (int nt : cands) {
+    if (nt > 64 && p.Cout <= nt / 2) continue;
+    if (v3_lds_bytes(nt, p.V, p.K, p.max_span) + 16 <= 160 * 1024) return nt;
+  }
+  return 0;
+}
+
 template <int NT, bool VEC>
 static void launch_bf16(const KnnParams& p, int out_t, hipStream_t s) {
   const int64_t tiles_per_b = (p.Nout + MM_MT - 1) / MM_MT;
@@ -607,6 +850,11 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
   p.Nout = a->n_out; p.K = a->k; p.V = a->n_ref; p.slot_ptr = a->slot_ptr; p.nbr = a->nbr_sorted;
   p.w = a->w; p.Cout = a->c_out; p.Kpad = a->k_pad; p.bias = a->bias; p.w_scale = a->w_scale;
   p.x_scale = a->x_scale; p.y = a->y; p.ys0 = a->y_stride[0]; p.ys1 = a->y_stride[1]; p.ys2 = a->y_stride[2];
+  p.tile_lo = a->tile_lo; p.tile_ent = a->tile_ent; p.tile_nbr = a->tile_nbr; p.max_span = a->max_span;
+  if (a->tile_lo && (a->tile_points != V3_MT || !a->tile_span || a->max_span <= 0)) {
+    set_error("fovi_knnconv_fwd: tile tables need tile_points=%d, tile_span and max_span > 0", V3_MT);
+    return 1;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
 
   if (a->x_dtype == FOVI_F32 && a->w_dtype == FOVI_F32) {
@@ -624,6 +872,16 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
   if (a->x_dtype == FOVI_BF16 && a->w_dtype == FOVI_BF16) {
     const uintptr_t xa = reinterpret_cast<uintptr_t>(a->x);
     const bool rows16 = p.xs1 == 1 && p.xs2 % 8 == 0 && p.xs0 % 8 == 0 && (xa % 16) == 0;
+    if (rows16 && p.C % V3_CC == 0 && a->tile_lo && a->tile_ent && a->tile_nbr &&
+        a->tile_points == V3_MT && p.K <= 255) {
+      const int nt = v3_tile_n(p);
+      bool ok = false;
+      if (nt == 256) ok = launch_bf16_v3<256>(p, a->y_dtype, s);
+      else if (nt == 192) ok = launch_bf16_v3<192>(p, a->y_dtype, s);
+      else if (nt == 128) ok = launch_bf16_v3<128>(p, a->y_dtype, s);
+      else if (nt == 64) ok = launch_bf16_v3<64>(p, a->y_dtype, s);
+      if (ok) return check_launch("fovi_knnconv_fwd(bf16 v3)");
+    }
     if (rows16 && p.C % V2_CC == 0) {
       const int nt = v2_tile_n(p);
       int rc = -1;

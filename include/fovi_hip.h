@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 1
+#define FOVI_ABI_VERSION 2
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -96,6 +96,14 @@ int fovi_sampler_fwd(const fovi_sampler_args* args, void* stream);
  *
  * x_dtype/w_dtype: F32/F32 (fp32 parity path) or BF16/BF16 (MFMA path) or
  * F8E4M3/F8E4M3 (MFMA path; y = x_scale * w_scale[o] * sum(q_x * q_w) + bias).
+ *
+ * Optional tile tables (all NULL to leave them out) select the kernel that
+ * copies each tile's input rows into LDS: output points are cut into tiles
+ * of tile_points (256) consecutive points; tile t reads only input points
+ * tile_lo[t] .. tile_lo[t] + tile_span[t] - 1 (max_span = max tile_span);
+ * tile_ent[n * n_ref + v] = (count << 8) | begin and
+ * tile_nbr[n * k + begin + i] = input index - tile_lo[t], same lists as the
+ * CSR tables. Used for channels-last bf16 input when the rows fit in LDS.
  */
 typedef struct fovi_knnconv_args {
   const void* x;
@@ -118,6 +126,12 @@ typedef struct fovi_knnconv_args {
   int32_t y_dtype;            /* F32 or BF16 */
   int32_t reserved3;
   int64_t y_stride[3];        /* batch, out channel, point */
+  const int32_t* tile_lo;     /* [n_tiles] or NULL */
+  const int32_t* tile_span;   /* [n_tiles] or NULL */
+  const uint16_t* tile_ent;   /* [n_tiles * tile_points, n_ref] or NULL */
+  const uint16_t* tile_nbr;   /* [n_tiles * tile_points, k] or NULL */
+  int32_t tile_points;
+  int32_t max_span;
 } fovi_knnconv_args;
 
 int fovi_knnconv_fwd(const fovi_knnconv_args* args, void* stream);

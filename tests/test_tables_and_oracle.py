@@ -183,3 +183,19 @@ def test_transform_sampling_grid_closed_form():
     # +x edge: 384 + 64 = 448 -> 0.75 ; -y edge (grid y=-1): 64 - 32 = 32 -> -0.75
     assert g[1].tolist() == [0.75, -0.5]
     assert g[2].tolist() == [0.5, -0.75]
+
+
+@pytest.mark.parametrize("res_in,res_out,k", [(32, 32, 25), (32, 16, 25), (64, 32, 49), (16, 16, 9)])
+def test_tile_tables_are_the_csr_lists_relative_to_tile_lo(res_in, res_out, k):
+    t = layer_tables(res_in, res_out, k)
+    lo, span, ent, nbr = (x.numpy().astype(np.int64) for x in
+                          T.tile_tables(t["idx"], t["slots"], t["n_in"], t["V"], tile=256))
+    ptr, gnbr = t["ptr"].numpy(), t["nbr"].numpy()
+    for n in range(t["n_out"]):
+        tt = n // 256
+        for v in range(t["V"]):
+            cnt, beg = ent[n, v] >> 8, ent[n, v] & 0xFF
+            assert cnt == (ptr[n, v] & 0xFFFF) and beg == (ptr[n, v] >> 16)
+            got = nbr[n, beg:beg + cnt] + lo[tt]
+            assert list(got) == list(gnbr[n, beg:beg + cnt])
+            assert np.all(nbr[n, beg:beg + cnt] < span[tt])
