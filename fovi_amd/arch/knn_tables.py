@@ -179,8 +179,9 @@ def tile_tables(knn_idx, slots, n_in, n_ref, tile=TILE_POINTS):
     inputs any point of a tile reads lie in one contiguous index range
     ``[lo, lo + span)`` (on the ring-major log-polar lattice a tile of two
     rings reads about six rings), which the kernel copies into LDS. Returns
-    ``(lo [T] int32, span [T] int32, ent [T*tile, V] uint16,
-    nbr [T*tile, k] uint16)`` where ``ent = (count << 8) | begin`` and
+    ``(lo [T] int32, span [T] int32, ent [T*tile, V] int32,
+    nbr [T*tile, k] uint16)`` where ``ent = (first << 16) | (count << 8) |
+    begin`` (``first`` = the slot's first input, relative to ``lo``) and
     ``nbr`` holds input indices relative to ``lo`` in the CSR order of
     ``csr_tables``; or ``None`` when k > 255 or a span exceeds 65535.
     """
@@ -204,8 +205,11 @@ def tile_tables(knn_idx, slots, n_in, n_ref, tile=TILE_POINTS):
         lo[t] = blk[valid].min()
         span[t] = blk[valid].max() - lo[t] + 1
         nbr_loc[s:e] = np.where(valid, blk - lo[t], 0)
-        ent[s:e] = ((ptr[s:e] & 0xFFFF) << 8) | (ptr[s:e] >> 16)
+        beg = ptr[s:e] >> 16
+        first = np.take_along_axis(nbr_loc[s:e], np.minimum(beg, k - 1), axis=1)
+        first = np.where((ptr[s:e] & 0xFFFF) > 0, first, 0)
+        ent[s:e] = (first << 16) | ((ptr[s:e] & 0xFFFF) << 8) | beg
     if span.max() > 0xFFFF:
         return None
     return (torch.from_numpy(lo.astype(np.int32)), torch.from_numpy(span.astype(np.int32)),
-            torch.from_numpy(ent.astype(np.uint16)), torch.from_numpy(nbr_loc.astype(np.uint16)))
+            torch.from_numpy(ent.astype(np.uint32).view(np.int32)), torch.from_numpy(nbr_loc.astype(np.uint16)))

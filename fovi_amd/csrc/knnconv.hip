@@ -38,7 +38,7 @@ struct KnnParams {
   void* y;
   int64_t ys0, ys1, ys2;
   const int32_t* tile_lo;
-  const uint16_t* tile_ent;
+  const uint32_t* tile_ent;
   const uint16_t* tile_nbr;
   int max_span;
 };
@@ -318,13 +318,19 @@ __global__ __launch_bounds__(256, 2) void knnconv_bf16_kernel(KnnParams p, int64
 // 32-channel chunks of one slot: the chunk's gathered A tile (256 x 32) and
 // weight tile (NT x 32) are double buffered in LDS, with the next chunk's
 // global loads in flight in registers while the current chunk's MFMAs run.
-// LDS rows are 64 bytes (four 16-byte chunks); chunk q of row r is stored at
-// q ^ ((r >> 1) & 3), which makes every 8-lane group of a fragment read hit
-// eight distinct 16-byte bank groups.
+// LDS rows are 64 bytes (four 16-byte chunks), XOR-swizzled per row (swz32)
+// so that fragment reads and tile writes are bank-conflict free.
 constexpr int V2_MT = 256;
 constexpr int V2_CC = 32;
 
-__device__ __forceinline__ int swz32(int r, int q) { return r * V2_CC + ((q ^ ((r >> 1) & 3)) << 3); }
+// XOR pattern g(r) = (bit1(r) ^ bit3(r)) | bit2(r) << 1 keeps any 8 consecutive
+// rows of one chunk in distinct 16-byte slots of a 128-byte window and any 16
+// consecutive rows in distinct slots of a 256-byte window, so 16-byte reads
+// are conflict-free whether the LDS serves 8 or 16 lanes per cycle.
+__device__ __forceinline__ int swz32(int r, int q) {
+  const int g = (((r >> 1) ^ (r >> 3)) & 1) | ((r >> 1) & 2);
+  return r * V2_CC + ((q ^ g) << 3);
+}
 
 size_t v2_lds_bytes(int nt, int64_t V, int64_t K) {
   return static_cast<size_t>(2 * V2_MT * V2_CC * 2 + 2 * nt * V2_CC * 2) +
@@ -513,20 +519,37 @@ static int v2_tile_n(const KnnParams& p) {
 // bytes) with coalesced loads; the next chunk's rows are loaded into
 // registers a whole channel chunk ahead and written when S is free. Each
 // (slot, chunk) A tile is then assembled LDS -> LDS from S through the
-// tile's uint16 CSR tables (neighbour sums in fp32, one RNE rounding via
-// v_cvt_pk_bf16_f32), one iteration ahead of the MFMAs that consume it. The
-// only global loads inside the reduction loop are the weight tiles.
-// Iterations run channel chunk outer, slot inner.
+// tile's CSR words (first neighbour, count and list start in one 32-bit word
+// per (slot, point), stored slot-major so a slot's words are contiguous;
+// further neighbours from a uint16 list; sums in fp32 with one RNE rounding
+// via v_cvt_pk_bf16_f32), one iteration ahead of the MFMAs that consume it.
+// The only global loads inside the reduction loop are the weight tiles,
+// addressed as 32-bit per-lane offsets from uniform bases. Iterations run
+// channel chunk outer, slot inner.
 constexpr int V3_MT = 256;
 constexpr int V3_CC = 32;
 
 size_t v3_lds_bytes(int nt, int64_t V, int64_t K, int max_span) {
   return static_cast<size_t>(max_span) * V3_CC * 2 + 2 * V3_MT * V3_CC * 2 + 2 * nt * V3_CC * 2 +
-         static_cast<size_t>(V3_MT) * static_cast<size_t>(V + K) * 2;
+         static_cast<size_t>(V3_MT) * static_cast<size_t>(V) * 4 +
+         ((static_cast<size_t>(V3_MT) * static_cast<size_t>(K) + 7) & ~static_cast<size_t>(7)) * 2;
 }
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f32x8 unpack_bf16x8(u32x4 r) {
+  f32x8 f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(r[i] << 16);
+    f[2 * i + 1] = __uint_as_float(r[i] & 0xffff0000u);
+  }
+  return f;
+}
 
 __device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
   const f32x2 v = {a, b};
@@ -543,10 +566,9 @@ __global__ __launch_bounds__(512, 1) void knnconv_bf16_v3_kernel(KnnParams p, in
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint16_t* As = reinterpret_cast<uint16_t*>(smem);                     // [2][256*32]
   uint16_t* Bs = As + 2 * V3_MT * V3_CC;                                // [2][NT*32]
-  uint16_t* ent = Bs + 2 * NT * V3_CC;                                  // [256][V]
-  uint16_t* nbl = ent + V3_MT * p.V;                                    // [256][K]
-  uint16_t* S = nbl + V3_MT * p.K;                                      // [max_span][32]
-  S = reinterpret_cast<uint16_t*>((reinterpret_cast<uintptr_t>(S) + 15) & ~uintptr_t(15));
+  uint32_t* ent = reinterpret_cast<uint32_t*>(Bs + 2 * NT * V3_CC);     // [V][256] slot-major
+  uint16_t* nbl = reinterpret_cast<uint16_t*>(ent + V3_MT * p.V);       // [256][K]
+  uint16_t* S = nbl + ((V3_MT * p.K + 7) & ~static_cast<int64_t>(7));   // [max_span][32]
 
   const int64_t tile = xcd_tile(blockIdx.x, padded_tiles);
   if (tile >= total_tiles) return;
@@ -562,72 +584,80 @@ __global__ __launch_bounds__(512, 1) void knnconv_bf16_v3_kernel(KnnParams p, in
   const int64_t lo = p.tile_lo[pt];
   const int span = static_cast<int>(min(static_cast<int64_t>(p.max_span), p.Nin - lo));
 
-  for (int i = tid; i < V3_MT * V; i += 512) ent[i] = p.tile_ent[n0 * p.V + i];
+  // CSR words, transposed to slot-major so one slot's 256 rows are contiguous
+  for (int i = tid; i < V3_MT * V; i += 512) {
+    const int r = i / V, v = i - r * V;
+    ent[v * V3_MT + r] = p.tile_ent[n0 * p.V + i];
+  }
   for (int i = tid; i < V3_MT * K; i += 512) nbl[i] = p.tile_nbr[n0 * p.K + i];
 
-  const uint16_t* xb = static_cast<const uint16_t*>(p.x) + b * p.xs0;
-  const uint16_t* wp = static_cast<const uint16_t*>(p.w);
+  // per-lane 32-bit byte offsets against uniform bases
+  const char* xrows = reinterpret_cast<const char*>(static_cast<const uint16_t*>(p.x) + b * p.xs0 + lo * p.xs2);
+  const char* wbase = reinterpret_cast<const char*>(static_cast<const uint16_t*>(p.w) + o0 * p.Kpad);
+  uint32_t s_off[SV], w_off[B_VECS];
+  uint32_t s_ok = 0, w_ok = 0;   // bit j: vector j of this lane is in range
+#pragma unroll
+  for (int j = 0; j < SV; ++j) {
+    const int q = tid + 512 * j;
+    s_ok |= static_cast<uint32_t>((q >> 2) < span) << j;
+    s_off[j] = static_cast<uint32_t>(((q >> 2) * p.xs2 + (q & 3) * 8) * 2);
+  }
+#pragma unroll
+  for (int i = 0; i < B_VECS; ++i) {
+    const int q = tid + 512 * i;
+    w_ok |= static_cast<uint32_t>(q < NT * 4 && o0 + (q >> 2) < p.Cout) << i;
+    w_off[i] = static_cast<uint32_t>(((q >> 2) * p.Kpad + (q & 3) * 8) * 2);
+  }
   const int ncc = static_cast<int>(p.C / V3_CC);
   const int nit = ncc * V;
   const int part = tid & 3;
   const int row0 = tid >> 2;
 
-  Raw16 rs[SV], rb[B_VECS];
+  u32x4 rs[SV], rb[B_VECS];
   auto load_s = [&](int cc) {
+    const char* base = xrows + cc * V3_CC * 2;
 #pragma unroll
-    for (int j = 0; j < SV; ++j) {
-      const int q = tid + 512 * j;
-      const int r = q >> 2;
-      rs[j] = (r < span) ? *reinterpret_cast<const Raw16*>(xb + (lo + r) * p.xs2 + cc * V3_CC + (q & 3) * 8)
-                         : Raw16{0u, 0u, 0u, 0u};
-    }
+    for (int j = 0; j < SV; ++j)
+      rs[j] = ((s_ok >> j) & 1) ? *reinterpret_cast<const u32x4*>(base + s_off[j]) : u32x4{0u, 0u, 0u, 0u};
   };
   auto store_s = [&]() {
 #pragma unroll
-    for (int j = 0; j < SV; ++j) {
-      const int q = tid + 512 * j;
-      if ((q >> 2) < span) *reinterpret_cast<Raw16*>(&S[q * 8]) = rs[j];
-    }
+    for (int j = 0; j < SV; ++j)
+      if ((s_ok >> j) & 1) *reinterpret_cast<u32x4*>(&S[(tid + 512 * j) * 8]) = rs[j];
   };
-  auto load_w = [&](int it) {
-    const int cc = it / V, v = it - cc * V;
-    const int64_t k0 = static_cast<int64_t>(v) * p.C + cc * V3_CC;
+  auto load_w = [&](int cc, int v) {
+    const char* base = wbase + (static_cast<int64_t>(v) * p.C + cc * V3_CC) * 2;
 #pragma unroll
-    for (int i = 0; i < B_VECS; ++i) {
-      const int q = tid + 512 * i;
-      const int64_t o = o0 + (q >> 2);
-      rb[i] = (q < NT * 4 && o < p.Cout)
-                  ? *reinterpret_cast<const Raw16*>(wp + o * p.Kpad + k0 + (q & 3) * 8)
-                  : Raw16{0u, 0u, 0u, 0u};
-    }
+    for (int i = 0; i < B_VECS; ++i)
+      rb[i] = ((w_ok >> i) & 1) ? *reinterpret_cast<const u32x4*>(base + w_off[i]) : u32x4{0u, 0u, 0u, 0u};
   };
   auto store_w = [&](int buf) {
     uint16_t* bsm = Bs + buf * NT * V3_CC;
 #pragma unroll
     for (int i = 0; i < B_VECS; ++i) {
       const int q = tid + 512 * i;
-      if (q < NT * 4) *reinterpret_cast<Raw16*>(&bsm[swz32(q >> 2, q & 3)]) = rb[i];
+      if (q < NT * 4) *reinterpret_cast<u32x4*>(&bsm[swz32(q >> 2, q & 3)]) = rb[i];
     }
   };
-  auto build_a = [&](int it, int buf) {
-    const int v = it % V;
+  auto build_a = [&](int v, int buf) {
     uint16_t* a = As + buf * V3_MT * V3_CC;
+    const uint32_t* ev = ent + v * V3_MT;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int row = row0 + 128 * i;
-      const int e = ent[row * V + v];
-      const int cnt = e >> 8;
-      const uint16_t* nb = nbl + row * K + (e & 0xff);
-      Raw16 r{0u, 0u, 0u, 0u};
-      if (cnt == 1) {
-        r = *reinterpret_cast<const Raw16*>(&S[nb[0] * V3_CC + part * 8]);
+      const uint32_t e = ev[row];
+      const int cnt = (e >> 8) & 0xff;
+      u32x4 r = *reinterpret_cast<const u32x4*>(&S[(e >> 16) * V3_CC + part * 8]);
+      if (cnt == 0) {
+        r = u32x4{0u, 0u, 0u, 0u};
       } else if (cnt > 1) {
-        float s8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        for (int j = 0; j < cnt; ++j) add_bf16x8(s8, *reinterpret_cast<const Raw16*>(&S[nb[j] * V3_CC + part * 8]));
-        r = Raw16{cvt_pk_bf16(s8[0], s8[1]), cvt_pk_bf16(s8[2], s8[3]), cvt_pk_bf16(s8[4], s8[5]),
-                  cvt_pk_bf16(s8[6], s8[7])};
+        const uint16_t* nb = nbl + row * K + (e & 0xff);
+        f32x8 acc8 = unpack_bf16x8(r);
+        for (int j = 1; j < cnt; ++j) acc8 += unpack_bf16x8(*reinterpret_cast<const u32x4*>(&S[nb[j] * V3_CC + part * 8]));
+        r = u32x4{cvt_pk_bf16(acc8[0], acc8[1]), cvt_pk_bf16(acc8[2], acc8[3]), cvt_pk_bf16(acc8[4], acc8[5]),
+                  cvt_pk_bf16(acc8[6], acc8[7])};
       }
-      *reinterpret_cast<Raw16*>(&a[swz32(row, part)]) = r;
+      *reinterpret_cast<u32x4*>(&a[swz32(row, part)]) = r;
     }
   };
 
@@ -641,7 +671,7 @@ __global__ __launch_bounds__(512, 1) void knnconv_bf16_v3_kernel(KnnParams p, in
 
   // prologue: S(0), W(0), A(0); S(1) in flight
   load_s(0);
-  load_w(0);
+  load_w(0, 0);
   store_s();
   store_w(0);
   if (ncc > 1) load_s(1);
@@ -649,18 +679,19 @@ __global__ __launch_bounds__(512, 1) void knnconv_bf16_v3_kernel(KnnParams p, in
   build_a(0, 0);
   __syncthreads();
 
+  int cc1 = 0, v1 = 0;   // chunk and slot of iteration it + 1
   for (int it = 0; it < nit; ++it) {
     const int cur = it & 1;
-    const int nx = it + 1;
-    if (nx < nit) {
-      load_w(nx);
-      const int cc1 = nx / V, v1 = nx - cc1 * V;
+    if (++v1 == V) { v1 = 0; ++cc1; }
+    const bool more = it + 1 < nit;
+    if (more) {
+      load_w(cc1, v1);
       if (v1 == 0) {            // next iteration starts channel chunk cc1: refresh S
         store_s();
         __syncthreads();
         if (cc1 + 1 < ncc) load_s(cc1 + 1);
       }
-      build_a(nx, cur ^ 1);
+      build_a(v1, cur ^ 1);
     }
     const uint16_t* a = As + cur * V3_MT * V3_CC;
     const uint16_t* bsm = Bs + cur * NT * V3_CC;
@@ -680,7 +711,7 @@ __global__ __launch_bounds__(512, 1) void knnconv_bf16_v3_kernel(KnnParams p, in
         for (int j = 0; j < CB; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
     }
-    if (nx < nit) store_w(cur ^ 1);
+    if (more) store_w(cur ^ 1);
     __syncthreads();
   }
 
@@ -706,7 +737,7 @@ static void launch_bf16_v3_sv(const KnnParams& p, int out_t, hipStream_t s) {
   const int64_t n_tiles_n = (p.Cout + NT - 1) / NT;
   const int64_t total = p.B * tiles_per_b * n_tiles_n;
   const int64_t padded = (total + 7) / 8 * 8;
-  const size_t lds = v3_lds_bytes(NT, p.V, p.K, p.max_span) + 16;
+  const size_t lds = v3_lds_bytes(NT, p.V, p.K, p.max_span);
   dim3 grid(static_cast<unsigned>(padded));
   if (out_t == FOVI_BF16) {
     hipFuncSetAttribute(reinterpret_cast<const void*>(&knnconv_bf16_v3_kernel<NT, SV, uint16_t>),
@@ -738,7 +769,7 @@ static int v3_tile_n(const KnnParams& p) {
   const int cands[4] = {256, 192, 128, 64};
   for (int nt : cands) {
     if (nt > 64 && p.Cout <= nt / 2) continue;
-    if (v3_lds_bytes(nt, p.V, p.K, p.max_span) + 16 <= 160 * 1024) return nt;
+    if (v3_lds_bytes(nt, p.V, p.K, p.max_span) <= 160 * 1024) return nt;
   }
   return 0;
 }

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 2
+#define FOVI_ABI_VERSION 3
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -101,9 +101,10 @@ int fovi_sampler_fwd(const fovi_sampler_args* args, void* stream);
  * copies each tile's input rows into LDS: output points are cut into tiles
  * of tile_points (256) consecutive points; tile t reads only input points
  * tile_lo[t] .. tile_lo[t] + tile_span[t] - 1 (max_span = max tile_span);
- * tile_ent[n * n_ref + v] = (count << 8) | begin and
- * tile_nbr[n * k + begin + i] = input index - tile_lo[t], same lists as the
- * CSR tables. Used for channels-last bf16 input when the rows fit in LDS.
+ * tile_ent[n * n_ref + v] = (first << 16) | (count << 8) | begin and
+ * tile_nbr[n * k + begin + i] = input index - tile_lo[t] (first = the i = 0
+ * entry, or 0 when count is 0), same lists as the CSR tables. Used for
+ * channels-last bf16 input when the rows fit in LDS (k <= 255).
  */
 typedef struct fovi_knnconv_args {
   const void* x;
@@ -128,7 +129,7 @@ typedef struct fovi_knnconv_args {
   int64_t y_stride[3];        /* batch, out channel, point */
   const int32_t* tile_lo;     /* [n_tiles] or NULL */
   const int32_t* tile_span;   /* [n_tiles] or NULL */
-  const uint16_t* tile_ent;   /* [n_tiles * tile_points, n_ref] or NULL */
+  const uint32_t* tile_ent;   /* [n_tiles * tile_points, n_ref] or NULL */
   const uint16_t* tile_nbr;   /* [n_tiles * tile_points, k] or NULL */
   int32_t tile_points;
   int32_t max_span;

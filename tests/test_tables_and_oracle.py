@@ -190,12 +190,15 @@ def test_tile_tables_are_the_csr_lists_relative_to_tile_lo(res_in, res_out, k):
     t = layer_tables(res_in, res_out, k)
     lo, span, ent, nbr = (x.numpy().astype(np.int64) for x in
                           T.tile_tables(t["idx"], t["slots"], t["n_in"], t["V"], tile=256))
+    ent = ent & 0xFFFFFFFF
     ptr, gnbr = t["ptr"].numpy(), t["nbr"].numpy()
     for n in range(t["n_out"]):
         tt = n // 256
         for v in range(t["V"]):
-            cnt, beg = ent[n, v] >> 8, ent[n, v] & 0xFF
+            cnt, beg, first = (ent[n, v] >> 8) & 0xFF, ent[n, v] & 0xFF, ent[n, v] >> 16
             assert cnt == (ptr[n, v] & 0xFFFF) and beg == (ptr[n, v] >> 16)
+            if cnt:
+                assert first == nbr[n, beg]
             got = nbr[n, beg:beg + cnt] + lo[tt]
             assert list(got) == list(gnbr[n, beg:beg + cnt])
             assert np.all(nbr[n, beg:beg + cnt] < span[tt])
