@@ -14,7 +14,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 F32, BF16, F8E4M3 = 0, 1, 2
 NEAREST, BILINEAR = 0, 1
 PAD_ZEROS, PAD_BORDER = 0, 1
@@ -58,6 +58,8 @@ class KnnConvArgs(C.Structure):
         ("tile_lo", C.c_void_p), ("tile_span", C.c_void_p),
         ("tile_ent", C.c_void_p), ("tile_nbr", C.c_void_p),
         ("tile_points", C.c_int32), ("max_span", C.c_int32),
+        ("tile_coll", C.c_void_p), ("tile_coll_n", C.c_void_p),
+        ("zero_row", C.c_int32), ("reserved4", C.c_int32),
     ]
 
 

@@ -121,13 +121,15 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         self.knn_indices_pad_mask = self.knn_indices_pad_mask.to(device)
         self.register_buffer("slot_ptr", slot_ptr.to(device), persistent=False)
         self.register_buffer("nbr_sorted", nbr_sorted.to(device), persistent=False)
-        tiles = T.tile_tables(knn_indices, self.slots, n_in, n_ref)
+        tiles = T.direct_tables(knn_indices, self.slots, n_in, n_ref)
         self._max_span = 0
-        for name, t in zip(("tile_lo", "tile_span", "tile_ent", "tile_nbr"),
-                           tiles if tiles is not None else (None,) * 4):
+        self._zero_row = 0
+        for name, t in zip(("tile_lo", "tile_span", "tile_ent", "tile_nbr", "tile_coll", "tile_coll_n"),
+                           tiles[:6] if tiles is not None else (None,) * 6):
             self.register_buffer(name, None if t is None else t.to(device), persistent=False)
         if tiles is not None:
             self._max_span = int(tiles[1].max())
+            self._zero_row = tiles[6]
         self._packed = {}
 
     # -- setup ---------------------------------------------------------------
@@ -221,6 +223,8 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
             a.tile_lo = self.tile_lo.data_ptr(); a.tile_span = self.tile_span.data_ptr()
             a.tile_ent = self.tile_ent.data_ptr(); a.tile_nbr = self.tile_nbr.data_ptr()
             a.tile_points = T.TILE_POINTS; a.max_span = self._max_span
+            a.tile_coll = self.tile_coll.data_ptr(); a.tile_coll_n = self.tile_coll_n.data_ptr()
+            a.zero_row = self._zero_row
         lib = _lib.load()
         _lib.check(lib.fovi_knnconv_fwd(a, _lib.stream_handle(x.device)), "fovi_knnconv_fwd")
         return y.transpose(1, 2)

@@ -37,6 +37,7 @@ __all__ = [
     "slots_to_one_hot",
     "csr_tables",
     "tile_tables",
+    "direct_tables",
     "TILE_POINTS",
 ]
 
@@ -213,3 +214,40 @@ def tile_tables(knn_idx, slots, n_in, n_ref, tile=TILE_POINTS):
         return None
     return (torch.from_numpy(lo.astype(np.int32)), torch.from_numpy(span.astype(np.int32)),
             torch.from_numpy(ent.astype(np.uint32).view(np.int32)), torch.from_numpy(nbr_loc.astype(np.uint16)))
+
+
+def direct_tables(knn_idx, slots, n_in, n_ref, tile=TILE_POINTS):
+    """Tables of the kernel that reads single-neighbour slots straight from LDS.
+
+    Extends ``tile_tables``: the kernel keeps the staged input rows in LDS plus
+    one zero row at index ``zero_row = max span``; a slot with no neighbour
+    points at the zero row, a slot with one neighbour at that neighbour's row,
+    and only slots with two or more neighbours are summed into a separate
+    tile. Returns ``(lo, span, ent, nbr, coll, coll_n, zero_row)`` where
+    ``ent [T*tile, V] int32 = (first << 16) | (count << 8) | begin`` (first =
+    ``zero_row`` when count is 0), ``coll [T, V, tile] uint8`` lists, per tile
+    and slot, the tile rows with count >= 2 in decreasing count order, and
+    ``coll_n [T, V] int32`` their number; or ``None`` (see ``tile_tables``).
+    """
+    base = tile_tables(knn_idx, slots, n_in, n_ref, tile)
+    if base is None:
+        return None
+    lo, span, ent, nbr = base
+    zero_row = int(span.max())
+    if zero_row >= 0xFFFF:
+        return None
+    e = ent.numpy().view(np.uint32).astype(np.int64)
+    cnt = (e >> 8) & 0xFF
+    e = np.where(cnt == 0, (zero_row << 16) | (e & 0xFFFF), e)
+    n_tiles = lo.shape[0]
+    coll = np.zeros((n_tiles, n_ref, tile), np.uint8)
+    coll_n = np.zeros((n_tiles, n_ref), np.int32)
+    c3 = cnt.reshape(n_tiles, tile, n_ref)
+    for t in range(n_tiles):
+        for v in range(n_ref):
+            rows = np.nonzero(c3[t, :, v] >= 2)[0]
+            rows = rows[np.argsort(-c3[t, rows, v], kind="stable")]
+            coll[t, v, :len(rows)] = rows
+            coll_n[t, v] = len(rows)
+    return (lo, span, torch.from_numpy(e.astype(np.uint32).view(np.int32)), nbr,
+            torch.from_numpy(coll), torch.from_numpy(coll_n), zero_row)

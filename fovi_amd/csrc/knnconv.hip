@@ -41,6 +41,9 @@ struct KnnParams {
   const uint32_t* tile_ent;
   const uint16_t* tile_nbr;
   int max_span;
+  const uint8_t* tile_coll;
+  const int32_t* tile_coll_n;
+  int zero_row;
 };
 
 // ---------------------------------------------------------------------------
@@ -647,10 +650,9 @@ __global__ __launch_bounds__(512, 1) void knnconv_bf16_v3_kernel(KnnParams p, in
       const int row = row0 + 128 * i;
       const uint32_t e = ev[row];
       const int cnt = (e >> 8) & 0xff;
-      u32x4 r = *reinterpret_cast<const u32x4*>(&S[(e >> 16) * V3_CC + part * 8]);
-      if (cnt == 0) {
-        r = u32x4{0u, 0u, 0u, 0u};
-      } else if (cnt > 1) {
+      u32x4 r = u32x4{0u, 0u, 0u, 0u};
+      if (cnt != 0) r = *reinterpret_cast<const u32x4*>(&S[(e >> 16) * V3_CC + part * 8]);
+      if (cnt > 1) {
         const uint16_t* nb = nbl + row * K + (e & 0xff);
         f32x8 acc8 = unpack_bf16x8(r);
         for (int j = 1; j < cnt; ++j) acc8 += unpack_bf16x8(*reinterpret_cast<const u32x4*>(&S[nb[j] * V3_CC + part * 8]));
@@ -774,6 +776,282 @@ static int v3_tile_n(const KnnParams& p) {
   return 0;
 }
 
+// ---------------------------------------------------------------------------
+// bf16 MFMA path reading single-neighbour slots straight from the staged rows
+// ---------------------------------------------------------------------------
+// Same tile, staging (S, now XOR-swizzled like the tiles) and MFMA core as
+// above, but the A tile is no longer assembled for every slot: an MFMA lane
+// takes its 16-byte fragment from the S row of its point's only neighbour in
+// the slot, or from a zero row (index zero_row) when the slot is empty. Only
+// the points of a slot with two or more neighbours (about a quarter on the
+// log-polar lattice) are summed, into a small tile, driven by a per-(tile,
+// slot) row list sorted by count so that lanes of a wave loop about equally.
+// S may only be refreshed after the last MFMA of a channel chunk has read it,
+// so the refresh (and the first slot's sums) run between two extra barriers
+// once per chunk.
+__device__ __forceinline__ int swz_g(int r) { return (((r >> 1) ^ (r >> 3)) & 1) | ((r >> 1) & 2); }
+
+struct V4Layout {
+  int b_off, ent_off, colln_off, coll_off, nbl_off, s_off, total;  // bytes
+};
+
+__host__ __device__ inline V4Layout v4_layout(int nt, int V, int K, int zero_row) {
+  V4Layout l;
+  int o = 2 * 256 * 32 * 2;                       // A: two 256 x 32 bf16 tiles
+  l.b_off = o;      o += 2 * nt * 32 * 2;         // B: two NT x 32 tiles
+  l.ent_off = o;    o += 256 * V * 4;             // CSR words, slot-major
+  l.colln_off = o;  o += (V * 4 + 15) & ~15;      // collision row counts
+  l.coll_off = o;   o += V * 256;                 // collision row lists
+  l.nbl_off = o;    o += (256 * K * 2 + 15) & ~15;
+  l.s_off = o;      o += (zero_row + 1) * 32 * 2; // staged rows + zero row
+  l.total = o;
+  return l;
+}
+
+template <int NT, int SV, typename OutT>
+__global__ __launch_bounds__(512, 1) void knnconv_bf16_v4_kernel(KnnParams p, int64_t tiles_per_b,
+                                                                 int64_t n_tiles_n, int64_t total_tiles,
+                                                                 int64_t padded_tiles) {
+  constexpr int WN = NT / 2;
+  constexpr int CB = WN / 32;
+  constexpr int B_VECS = (NT * V3_CC / 8 + 511) / 512;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int V = static_cast<int>(p.V), K = static_cast<int>(p.K);
+  const int zr = p.zero_row;
+  const V4Layout L = v4_layout(NT, V, K, zr);
+  uint16_t* sm16 = reinterpret_cast<uint16_t*>(smem);
+  uint16_t* Bs = sm16 + L.b_off / 2;
+  uint32_t* ent = reinterpret_cast<uint32_t*>(smem + L.ent_off);
+  int32_t* colln = reinterpret_cast<int32_t*>(smem + L.colln_off);
+  uint8_t* coll = smem + L.coll_off;
+  uint16_t* nbl = sm16 + L.nbl_off / 2;
+  const int s16 = L.s_off / 2;                    // S offset in bf16 elements
+  uint16_t* S = sm16 + s16;
+
+  const int64_t tile = xcd_tile(blockIdx.x, padded_tiles);
+  if (tile >= total_tiles) return;
+  const int64_t mt = tile / n_tiles_n;
+  const int64_t o0 = (tile % n_tiles_n) * NT;
+  const int64_t b = mt / tiles_per_b;
+  const int64_t pt = mt % tiles_per_b;
+  const int64_t n0 = pt * V3_MT;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 3, wn = wave >> 2;
+  const int64_t lo = p.tile_lo[pt];
+  const int span = static_cast<int>(min(static_cast<int64_t>(zr), p.Nin - lo));
+
+  for (int i = tid; i < V3_MT * V; i += 512) {
+    const int r = i / V, v = i - r * V;
+    ent[v * V3_MT + r] = p.tile_ent[n0 * p.V + i];
+  }
+  for (int i = tid; i < V * 64; i += 512)
+    reinterpret_cast<uint32_t*>(coll)[i] = reinterpret_cast<const uint32_t*>(p.tile_coll)[pt * V * 64 + i];
+  for (int i = tid; i < V; i += 512) colln[i] = p.tile_coll_n[pt * V + i];
+  for (int i = tid; i < V3_MT * K; i += 512) nbl[i] = p.tile_nbr[n0 * p.K + i];
+  if (tid < 4) *reinterpret_cast<u32x4*>(&S[zr * V3_CC + tid * 8]) = u32x4{0u, 0u, 0u, 0u};
+
+  const char* xrows = reinterpret_cast<const char*>(static_cast<const uint16_t*>(p.x) + b * p.xs0 + lo * p.xs2);
+  const char* wbase = reinterpret_cast<const char*>(static_cast<const uint16_t*>(p.w) + o0 * p.Kpad);
+  uint32_t s_off[SV], w_off[B_VECS];
+  uint32_t s_ok = 0, w_ok = 0;
+#pragma unroll
+  for (int j = 0; j < SV; ++j) {
+    const int q = tid + 512 * j;
+    s_ok |= static_cast<uint32_t>((q >> 2) < span) << j;
+    s_off[j] = static_cast<uint32_t>(((q >> 2) * p.xs2 + (q & 3) * 8) * 2);
+  }
+#pragma unroll
+  for (int i = 0; i < B_VECS; ++i) {
+    const int q = tid + 512 * i;
+    w_ok |= static_cast<uint32_t>(q < NT * 4 && o0 + (q >> 2) < p.Cout) << i;
+    w_off[i] = static_cast<uint32_t>(((q >> 2) * p.Kpad + (q & 3) * 8) * 2);
+  }
+  const int ncc = static_cast<int>(p.C / V3_CC);
+  const int nit = ncc * V;
+
+  u32x4 rs[SV], rb[B_VECS];
+  auto load_s = [&](int cc) {
+    const char* base = xrows + cc * V3_CC * 2;
+#pragma unroll
+    for (int j = 0; j < SV; ++j)
+      rs[j] = ((s_ok >> j) & 1) ? *reinterpret_cast<const u32x4*>(base + s_off[j]) : u32x4{0u, 0u, 0u, 0u};
+  };
+  auto store_s = [&]() {
+#pragma unroll
+    for (int j = 0; j < SV; ++j) {
+      const int q = tid + 512 * j;
+      if ((s_ok >> j) & 1) *reinterpret_cast<u32x4*>(&S[swz32(q >> 2, q & 3)]) = rs[j];
+    }
+  };
+  auto load_w = [&](int cc, int v) {
+    const char* base = wbase + (static_cast<int64_t>(v) * p.C + cc * V3_CC) * 2;
+#pragma unroll
+    for (int i = 0; i < B_VECS; ++i)
+      rb[i] = ((w_ok >> i) & 1) ? *reinterpret_cast<const u32x4*>(base + w_off[i]) : u32x4{0u, 0u, 0u, 0u};
+  };
+  auto store_w = [&](int buf) {
+    uint16_t* bsm = Bs + buf * NT * V3_CC;
+#pragma unroll
+    for (int i = 0; i < B_VECS; ++i) {
+      const int q = tid + 512 * i;
+      if (q < NT * 4) *reinterpret_cast<u32x4*>(&bsm[swz32(q >> 2, q & 3)]) = rb[i];
+    }
+  };
+  // sums of the slots with two or more neighbours into A tile `buf`
+  auto build_coll = [&](int v, int buf) {
+    const int items = colln[v] * 4;
+    uint16_t* a = sm16 + buf * V3_MT * V3_CC;
+    for (int item = tid; item < items; item += 512) {
+      const int row = coll[v * V3_MT + (item >> 2)];
+      const int part = item & 3;
+      const uint32_t e = ent[v * V3_MT + row];
+      const int cnt = (e >> 8) & 0xff;
+      const uint16_t* nb = nbl + row * K + (e & 0xff);
+      f32x8 acc8 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < cnt; ++j) {
+        const int r = nb[j];
+        acc8 += unpack_bf16x8(*reinterpret_cast<const u32x4*>(&S[swz32(r, part)]));
+      }
+      *reinterpret_cast<u32x4*>(&a[swz32(row, part)]) =
+          u32x4{cvt_pk_bf16(acc8[0], acc8[1]), cvt_pk_bf16(acc8[2], acc8[3]), cvt_pk_bf16(acc8[4], acc8[5]),
+                cvt_pk_bf16(acc8[6], acc8[7])};
+    }
+  };
+
+  f32x16 acc[2][CB];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < CB; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  int rowm[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) rowm[i] = wm * 64 + i * 32 + (lane & 31);
+
+  load_s(0);
+  load_w(0, 0);
+  store_s();
+  store_w(0);
+  if (ncc > 1) load_s(1);
+  __syncthreads();
+  build_coll(0, 0);
+  uint32_t ecur[2], enxt[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) ecur[i] = ent[rowm[i]];
+  __syncthreads();
+
+  int cc1 = 0, v1 = 0;
+  for (int it = 0; it < nit; ++it) {
+    const int cur = it & 1;
+    if (++v1 == V) { v1 = 0; ++cc1; }
+    const bool more = it + 1 < nit;
+    if (more) {
+      load_w(cc1, v1);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) enxt[i] = ent[v1 * V3_MT + rowm[i]];
+      if (v1 != 0) build_coll(v1, cur ^ 1);
+    }
+    int a_base[2], s_row[2];
+    bool from_a[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      from_a[i] = ((ecur[i] >> 8) & 0xff) >= 2;
+      s_row[i] = static_cast<int>(ecur[i] >> 16);
+      a_base[i] = cur * V3_MT * V3_CC;
+    }
+    const uint16_t* bsm = Bs + cur * NT * V3_CC;
+#pragma unroll
+    for (int ks = 0; ks < V3_CC / 16; ++ks) {
+      const int q = ks * 2 + (lane >> 5);
+      bf16x8 af[2], bfr[CB];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int off = from_a[i] ? a_base[i] + swz32(rowm[i], q) : s16 + swz32(s_row[i], q);
+        af[i] = *reinterpret_cast<const bf16x8*>(&sm16[off]);
+      }
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+        bfr[j] = *reinterpret_cast<const bf16x8*>(&bsm[swz32(wn * WN + j * 32 + (lane & 31), q)]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < CB; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) store_w(cur ^ 1);
+    __syncthreads();
+    if (more && v1 == 0) {      // chunk boundary: every MFMA of chunk cc1-1 is done with S
+      store_s();
+      __syncthreads();
+      if (cc1 + 1 < ncc) load_s(cc1 + 1);
+      build_coll(0, cur ^ 1);
+      __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) ecur[i] = enxt[i];
+  }
+
+  OutT* y = static_cast<OutT*>(p.y) + b * p.ys0;
+#pragma unroll
+  for (int j = 0; j < CB; ++j) {
+    const int64_t o = o0 + wn * WN + j * 32 + (lane & 31);
+    if (o >= p.Cout) continue;
+    const float bo = p.bias ? p.bias[o] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t n = n0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (n < p.Nout) Elem<OutT>::store(y + o * p.ys1 + n * p.ys2, acc[i][j][r] + bo);
+      }
+  }
+}
+
+template <int NT, int SV>
+static void launch_bf16_v4_sv(const KnnParams& p, int out_t, hipStream_t s) {
+  const int64_t tiles_per_b = (p.Nout + V3_MT - 1) / V3_MT;
+  const int64_t n_tiles_n = (p.Cout + NT - 1) / NT;
+  const int64_t total = p.B * tiles_per_b * n_tiles_n;
+  const int64_t padded = (total + 7) / 8 * 8;
+  const size_t lds = v4_layout(NT, static_cast<int>(p.V), static_cast<int>(p.K), p.zero_row).total;
+  dim3 grid(static_cast<unsigned>(padded));
+  if (out_t == FOVI_BF16) {
+    hipFuncSetAttribute(reinterpret_cast<const void*>(&knnconv_bf16_v4_kernel<NT, SV, uint16_t>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    hipLaunchKernelGGL((knnconv_bf16_v4_kernel<NT, SV, uint16_t>), grid, dim3(512), lds, s, p, tiles_per_b,
+                       n_tiles_n, total, padded);
+  } else {
+    hipFuncSetAttribute(reinterpret_cast<const void*>(&knnconv_bf16_v4_kernel<NT, SV, float>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    hipLaunchKernelGGL((knnconv_bf16_v4_kernel<NT, SV, float>), grid, dim3(512), lds, s, p, tiles_per_b,
+                       n_tiles_n, total, padded);
+  }
+}
+
+template <int NT>
+static bool launch_bf16_v4(const KnnParams& p, int out_t, hipStream_t s) {
+  const int sv = (p.zero_row * 4 + 511) / 512;
+  if (sv <= 2) launch_bf16_v4_sv<NT, 2>(p, out_t, s);
+  else if (sv <= 4) launch_bf16_v4_sv<NT, 4>(p, out_t, s);
+  else if (sv <= 6) launch_bf16_v4_sv<NT, 6>(p, out_t, s);
+  else if (sv <= 8) launch_bf16_v4_sv<NT, 8>(p, out_t, s);
+  else return false;
+  return true;
+}
+
+static int v4_tile_n(const KnnParams& p) {
+  if (p.zero_row <= 0 || p.zero_row > 1024 || !p.tile_coll || !p.tile_coll_n) return 0;
+  const int cands[4] = {256, 192, 128, 64};
+  for (int nt : cands) {
+    if (nt > 64 && p.Cout <= nt / 2) continue;
+    if (v4_layout(nt, static_cast<int>(p.V), static_cast<int>(p.K), p.zero_row).total <= 160 * 1024) return nt;
+  }
+  return 0;
+}
+
 template <int NT, bool VEC>
 static void launch_bf16(const KnnParams& p, int out_t, hipStream_t s) {
   const int64_t tiles_per_b = (p.Nout + MM_MT - 1) / MM_MT;
@@ -882,6 +1160,7 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
   p.w = a->w; p.Cout = a->c_out; p.Kpad = a->k_pad; p.bias = a->bias; p.w_scale = a->w_scale;
   p.x_scale = a->x_scale; p.y = a->y; p.ys0 = a->y_stride[0]; p.ys1 = a->y_stride[1]; p.ys2 = a->y_stride[2];
   p.tile_lo = a->tile_lo; p.tile_ent = a->tile_ent; p.tile_nbr = a->tile_nbr; p.max_span = a->max_span;
+  p.tile_coll = a->tile_coll; p.tile_coll_n = a->tile_coll_n; p.zero_row = a->zero_row;
   if (a->tile_lo && (a->tile_points != V3_MT || !a->tile_span || a->max_span <= 0)) {
     set_error("fovi_knnconv_fwd: tile tables need tile_points=%d, tile_span and max_span > 0", V3_MT);
     return 1;
@@ -904,7 +1183,14 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
     const uintptr_t xa = reinterpret_cast<uintptr_t>(a->x);
     const bool rows16 = p.xs1 == 1 && p.xs2 % 8 == 0 && p.xs0 % 8 == 0 && (xa % 16) == 0;
     if (rows16 && p.C % V3_CC == 0 && a->tile_lo && a->tile_ent && a->tile_nbr &&
-        a->tile_points == V3_MT && p.K <= 255) {
+        a->tile_points == V3_MT && p.K <= 255 && p.V <= 255) {
+      const int nt4 = v4_tile_n(p);
+      bool ok4 = false;
+      if (nt4 == 256) ok4 = launch_bf16_v4<256>(p, a->y_dtype, s);
+      else if (nt4 == 192) ok4 = launch_bf16_v4<192>(p, a->y_dtype, s);
+      else if (nt4 == 128) ok4 = launch_bf16_v4<128>(p, a->y_dtype, s);
+      else if (nt4 == 64) ok4 = launch_bf16_v4<64>(p, a->y_dtype, s);
+      if (ok4) return check_launch("fovi_knnconv_fwd(bf16 v4)");
       const int nt = v3_tile_n(p);
       bool ok = false;
       if (nt == 256) ok = launch_bf16_v3<256>(p, a->y_dtype, s);

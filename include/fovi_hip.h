@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 3
+#define FOVI_ABI_VERSION 4
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -103,8 +103,13 @@ int fovi_sampler_fwd(const fovi_sampler_args* args, void* stream);
  * tile_lo[t] .. tile_lo[t] + tile_span[t] - 1 (max_span = max tile_span);
  * tile_ent[n * n_ref + v] = (first << 16) | (count << 8) | begin and
  * tile_nbr[n * k + begin + i] = input index - tile_lo[t] (first = the i = 0
- * entry, or 0 when count is 0), same lists as the CSR tables. Used for
+ * entry; zero_row when count is 0), same lists as the CSR tables. Used for
  * channels-last bf16 input when the rows fit in LDS (k <= 255).
+ * tile_coll[t * n_ref * tile_points + v * tile_points + i], i < tile_coll_n[t * n_ref + v],
+ * lists the tile rows whose slot v has two or more neighbours (decreasing
+ * count); zero_row (>= every tile_span) is the LDS row index standing for an
+ * empty slot. With these the kernel reads single-neighbour slots straight
+ * from the staged rows and only sums the listed ones.
  */
 typedef struct fovi_knnconv_args {
   const void* x;
@@ -133,6 +138,10 @@ typedef struct fovi_knnconv_args {
   const uint16_t* tile_nbr;   /* [n_tiles * tile_points, k] or NULL */
   int32_t tile_points;
   int32_t max_span;
+  const uint8_t* tile_coll;   /* [n_tiles, n_ref, tile_points] or NULL */
+  const int32_t* tile_coll_n; /* [n_tiles, n_ref] or NULL */
+  int32_t zero_row;
+  int32_t reserved4;
 } fovi_knnconv_args;
 
 int fovi_knnconv_fwd(const fovi_knnconv_args* args, void* stream);

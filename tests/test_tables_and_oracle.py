@@ -202,3 +202,22 @@ def test_tile_tables_are_the_csr_lists_relative_to_tile_lo(res_in, res_out, k):
             got = nbr[n, beg:beg + cnt] + lo[tt]
             assert list(got) == list(gnbr[n, beg:beg + cnt])
             assert np.all(nbr[n, beg:beg + cnt] < span[tt])
+
+
+@pytest.mark.parametrize("res_in,res_out,k", [(32, 32, 25), (64, 32, 49), (16, 16, 9)])
+def test_direct_tables_lists_and_zero_row(res_in, res_out, k):
+    t = layer_tables(res_in, res_out, k)
+    lo, span, ent, nbr, coll, coll_n, zr = T.direct_tables(t["idx"], t["slots"], t["n_in"], t["V"])
+    e = ent.numpy().view(np.uint32).astype(np.int64)
+    cnt, first = (e >> 8) & 0xFF, e >> 16
+    assert zr == int(span.max())
+    assert np.all(first[cnt == 0] == zr)
+    assert np.all(first[cnt > 0] < zr)
+    coll, coll_n = coll.numpy(), coll_n.numpy()
+    for tt in range(coll.shape[0]):
+        for v in range(t["V"]):
+            rows = coll[tt, v, :coll_n[tt, v]].astype(np.int64)
+            want = np.nonzero(cnt[tt * 256:(tt + 1) * 256, v] >= 2)[0]
+            assert sorted(rows.tolist()) == want.tolist()
+            c = cnt[tt * 256 + rows, v]
+            assert np.all(np.diff(c) <= 0)          # decreasing count order
