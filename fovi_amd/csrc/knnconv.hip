@@ -908,10 +908,22 @@ __global__ __launch_bounds__(512, 1) void knnconv_bf16_v4_kernel(KnnParams p, in
       const uint32_t e = ent[v * V3_MT + row];
       const int cnt = (e >> 8) & 0xff;
       const uint16_t* nb = nbl + row * K + (e & 0xff);
+      // groups of four neighbours: independent index reads, then independent
+      // row reads; missing neighbours read the zero row (adding exact zeros)
       f32x8 acc8 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int j = 0; j < cnt; ++j) {
-        const int r = nb[j];
-        acc8 += unpack_bf16x8(*reinterpret_cast<const u32x4*>(&S[swz32(r, part)]));
+      for (int j0 = 0; j0 < cnt; j0 += 4) {
+        const int r0 = j0 == 0 ? static_cast<int>(e >> 16) : nb[j0];
+        const int r1 = j0 + 1 < cnt ? nb[j0 + 1] : zr;
+        const int r2 = j0 + 2 < cnt ? nb[j0 + 2] : zr;
+        const int r3 = j0 + 3 < cnt ? nb[j0 + 3] : zr;
+        const u32x4 x0 = *reinterpret_cast<const u32x4*>(&S[swz32(r0, part)]);
+        const u32x4 x1 = *reinterpret_cast<const u32x4*>(&S[swz32(r1, part)]);
+        const u32x4 x2 = *reinterpret_cast<const u32x4*>(&S[swz32(r2, part)]);
+        const u32x4 x3 = *reinterpret_cast<const u32x4*>(&S[swz32(r3, part)]);
+        acc8 += unpack_bf16x8(x0);
+        acc8 += unpack_bf16x8(x1);
+        acc8 += unpack_bf16x8(x2);
+        acc8 += unpack_bf16x8(x3);
       }
       *reinterpret_cast<u32x4*>(&a[swz32(row, part)]) =
           u32x4{cvt_pk_bf16(acc8[0], acc8[1]), cvt_pk_bf16(acc8[2], acc8[3]), cvt_pk_bf16(acc8[4], acc8[5]),
