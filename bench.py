@@ -131,6 +131,92 @@ def bench_c4_sampler(steps, warmup, dev, mode="nearest"):
     return dict(ms=ms, bytes=nbytes, gbs=gbs, images_per_s=B / (ms * 1e-3))
 
 
+def _init_weights(layers, dev, seed):
+    import torch
+    g = torch.Generator(device=dev).manual_seed(seed)
+    with torch.no_grad():
+        for c in layers:
+            c.weight.copy_(torch.randn(c.weight.shape, generator=g, device=dev) * (1.0 / (c.in_channels * c._k)) ** 0.5)
+            if c.bias is not None:
+                c.bias.zero_()
+
+
+def bench_c2(steps, warmup, dev):
+    """C2: 256 images 3x224x224 fp32 -> bilinear sampler (4096 log-polar points, bf16 out) ->
+    5 kNN-conv layers 64/192/384/256/256, k=49/25/9/9/9, strides 2,2,1,1,1, ReLU between."""
+    import numpy as np
+    import torch
+    from fovi_amd.arch.knnalexnet import KNNAlexNet
+    from fovi_amd.sensing.samplers import GridSampler
+    B, S = 256, 224
+    t0 = time.time()
+    net = KNNAlexNet(64, 3, [64, 192, 384, 256, 256], [2, 2, 1, 1, 1], [], [49, 25, 9, 9, 9], style="logpolar",
+                     norm_type="none", fov=16, cmf_a=2.78, device=dev, final_activation=False)
+    _init_weights([blk.conv for blk in net.layers], dev, 3)
+    sampler = GridSampler(16, 2.78, 64, device=dev, mode="bilinear", style="logpolar")
+    log(f"[c2] model built in {time.time() - t0:.1f}s")
+    gi = torch.Generator(device=dev).manual_seed(0)
+    imgs = [torch.rand(B, 3, S, S, generator=gi, device=dev) for _ in range(2)]
+    views = sampler.prepare_views(torch.full((B, 2), 0.5), np.array([[S, S]] * B), B, dev)
+    feats = torch.empty(B, 3, 4096, device=dev, dtype=torch.bfloat16)
+    state = {"i": 0}
+
+    def step():
+        sampler.sample_views(imgs[state["i"] & 1], out=feats, views=views)
+        state["i"] += 1
+        return net(feats)
+
+    with torch.no_grad():
+        ms = time_steps(step, steps, warmup)
+    flops = 0.0
+    for blk in net.layers:
+        c = blk.conv
+        flops += 2.0 * B * c.out_coords.shape[0] * c.out_channels * c.in_channels * c.ref_coords.shape[0]
+    ips = B / (ms * 1e-3)
+    log(f"[c2] {ms:.3f} ms/step  {ips:.0f} images/s  ({flops / 1e9:.1f} GFLOP/batch, "
+        f"{flops / (ms * 1e-3) / 1e12:.1f} TFLOP/s)")
+    return dict(ms=ms, images_per_s=ips, gflop=flops / 1e9, tflops=flops / (ms * 1e-3) / 1e12)
+
+
+def bench_c4_frontend(steps, warmup, dev):
+    """C4: 128 images 3x512x512 bf16, 4 fixations each -> nearest sampler (16384 points) ->
+    kNN patch embedding 3 -> 384 (k=256, 16x16 ref grid) onto 256 tokens, bias."""
+    import numpy as np
+    import torch
+    from fovi_amd.arch.knnvit import KNNPatchEmbedding
+    from fovi_amd.sensing.samplers import GridSampler
+    B, Fx, S = 128, 4, 512
+    t0 = time.time()
+    pe = KNNPatchEmbedding(3, 384, 128, 16, 2.78, style="logpolar", auto_match_cart_resources=0,
+                           cart_patch_size=16, patch_overlap_factor=2, new_parameterization=True, transposed=True,
+                           sample_cortex=True, ref_frame_side_length=16, device=dev, bias=True)
+    _init_weights([pe], dev, 4)
+    sampler = GridSampler(16, 2.78, 128, device=dev, mode="nearest", style="logpolar")
+    log(f"[c4] model built in {time.time() - t0:.1f}s")
+    gi = torch.Generator(device=dev).manual_seed(0)
+    imgs = [torch.rand(B, 3, S, S, generator=gi, device=dev).bfloat16() for _ in range(2)]
+    gf = torch.Generator().manual_seed(2)
+    fix = 0.25 + 0.5 * torch.rand(B * Fx, 2, generator=gf)
+    views = sampler.prepare_views(fix, np.array([[S, S]] * (B * Fx)), B, dev,
+                                  view_image=torch.arange(B).repeat_interleave(Fx))
+    feats = torch.empty(B * Fx, 3, 16384, device=dev, dtype=torch.bfloat16)
+    state = {"i": 0}
+
+    def step():
+        sampler.sample_views(imgs[state["i"] & 1], out=feats, views=views)
+        state["i"] += 1
+        return pe(feats)
+
+    with torch.no_grad():
+        ms = time_steps(step, steps, warmup)
+        ms_pe = time_steps(lambda: pe(feats), steps, warmup)
+    flops = 2.0 * B * Fx * 256 * 384 * 3 * 256
+    log(f"[c4] {ms:.3f} ms/step  {B / (ms * 1e-3):.0f} images/s  (patch embed alone {ms_pe:.3f} ms = "
+        f"{flops / (ms_pe * 1e-3) / 1e12:.1f} TFLOP/s)")
+    return dict(ms=ms, images_per_s=B / (ms * 1e-3), ms_patch_embed=ms_pe,
+                patch_embed_tflops=flops / (ms_pe * 1e-3) / 1e12)
+
+
 def cpu_baseline_c3(c3, seconds_budget=25.0):
     """Oracle (torch CPU fp32 restatement of knn.py:484-557) on a B=2 slice of C3."""
     import torch
@@ -176,6 +262,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sampler", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the C2/C4 end-to-end legs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -186,6 +273,8 @@ def main():
     c3 = bench_c3(args.steps, args.warmup, dev)
     c4 = None if args.no_sampler else bench_c4_sampler(args.steps, args.warmup, dev, "nearest")
     c4b = None if args.no_sampler else bench_c4_sampler(args.steps, args.warmup, dev, "bilinear")
+    c2 = None if args.no_e2e else bench_c2(args.steps, args.warmup, dev)
+    c4e = None if args.no_e2e else bench_c4_frontend(args.steps, args.warmup, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline_c3(c3)
     line = {
         "metric": "kNN-conv fwd TFLOP/s + sampler GB/s (% of MI355X roofline); images/sec",
@@ -217,6 +306,17 @@ def main():
                          "ms": round(c4b["ms"], 4), "images/s": round(c4b["images_per_s"], 1)},
             "roofline": {"bound": "hbm", "peak": PEAK_HBM_GBS, "unit": "GB/s"},
         }
+    if c2 is not None:
+        line["c2_alexnet"] = {"workload": "C2: 256 images 3x224x224 -> bilinear sampler (4096 pts) -> 5 kNN-conv "
+                                          "layers 64/192/384/256/256, k=49/25/9/9/9, ReLU between, bf16",
+                              "images/s": round(c2["images_per_s"], 1), "ms": round(c2["ms"], 4),
+                              "GFLOP/batch": round(c2["gflop"], 2), "TFLOP/s": round(c2["tflops"], 1)}
+    if c4e is not None:
+        line["c4_frontend"] = {"workload": "C4: 128 images 3x512x512 bf16 x 4 fixations -> nearest sampler "
+                                           "(16384 pts) -> kNN patch embed 3->384, k=256, 256 tokens",
+                               "images/s": round(c4e["images_per_s"], 1), "ms": round(c4e["ms"], 4),
+                               "patch_embed_ms": round(c4e["ms_patch_embed"], 4),
+                               "patch_embed_TFLOP/s": round(c4e["patch_embed_tflops"], 1)}
     print(json.dumps(line), flush=True)
 
 

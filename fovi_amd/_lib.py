@@ -14,10 +14,11 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 F32, BF16, F8E4M3 = 0, 1, 2
 NEAREST, BILINEAR = 0, 1
 PAD_ZEROS, PAD_BORDER = 0, 1
+ACT_NONE, ACT_RELU = 0, 1
 
 _DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float8_e4m3fn: F8E4M3}
 
@@ -59,7 +60,7 @@ class KnnConvArgs(C.Structure):
         ("tile_ent", C.c_void_p), ("tile_nbr", C.c_void_p),
         ("tile_points", C.c_int32), ("max_span", C.c_int32),
         ("tile_coll", C.c_void_p), ("tile_coll_n", C.c_void_p),
-        ("zero_row", C.c_int32), ("reserved4", C.c_int32),
+        ("zero_row", C.c_int32), ("activation", C.c_int32),
     ]
 
 

@@ -62,11 +62,11 @@ class KNNBaseLayer:
 
 class _KnnConvFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, layer, weight, bias):
-        return layer._launch(x)
+    def forward(ctx, x, layer, weight, bias, activation=None):
+        return layer._launch(x, activation)
 
     @staticmethod
-    def backward(ctx, grad):
+    def backward(ctx, *grads):
         raise NotImplementedError("fovi_amd KNNConvLayer: backward is not implemented (forward-only "
                                   "HIP kernels)")
 
@@ -196,7 +196,7 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
             return torch.float32
         raise TypeError(f"KNNConvLayer: unsupported input dtype {x.dtype}")
 
-    def _launch(self, x):
+    def _launch(self, x, activation=None):
         _lib.require_device(x, self.weight)
         if x.dim() != 3 or x.shape[1] != self.in_channels or x.shape[2] != self.in_coords.shape[0]:
             raise ValueError(f"KNNConvLayer: expected [B, {self.in_channels}, {self.in_coords.shape[0]}], "
@@ -219,6 +219,9 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         a.bias = None if bias is None else bias.data_ptr()
         a.y = y.data_ptr(); a.y_dtype = _lib.dtype_code(dt)
         a.y_stride[:] = [y.stride(0), y.stride(2), y.stride(1)]
+        if activation not in (None, "relu"):
+            raise ValueError(f"activation must be None or 'relu', got {activation!r}")
+        a.activation = _lib.ACT_RELU if activation == "relu" else _lib.ACT_NONE
         if self.tile_lo is not None:
             a.tile_lo = self.tile_lo.data_ptr(); a.tile_span = self.tile_span.data_ptr()
             a.tile_ent = self.tile_ent.data_ptr(); a.tile_nbr = self.tile_nbr.data_ptr()
@@ -231,6 +234,10 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
 
     def forward(self, X_l):
         return _KnnConvFn.apply(X_l, self, self.weight, self.bias)
+
+    def forward_fused(self, X_l, activation="relu"):
+        """``activation(forward(X_l))`` with the activation applied in the kernel's store."""
+        return _KnnConvFn.apply(X_l, self, self.weight, self.bias, activation)
 
     # -- conv2d import (reference knn.py:649-715) -------------------------------
     def _load_conv_2d_weight(self, conv_weight, conv_bias, strict=False):

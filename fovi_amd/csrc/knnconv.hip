@@ -44,7 +44,12 @@ struct KnnParams {
   const uint8_t* tile_coll;
   const int32_t* tile_coll_n;
   int zero_row;
+  int relu;
 };
+
+// Output transform: optional ReLU fused into the store (the activation that
+// follows the conv in the reference blocks when no norm sits between them).
+__device__ __forceinline__ float epilogue(float v, int relu) { return relu ? fmaxf(v, 0.0f) : v; }
 
 // ---------------------------------------------------------------------------
 // fp32 path
@@ -120,7 +125,7 @@ __global__ __launch_bounds__(256) void knnconv_f32_kernel(KnnParams p, int64_t t
       if (o >= p.Cout) continue;
       float r = acc[i][j];
       if (p.bias) r += p.bias[o];
-      Elem<OutT>::store(y + o * p.ys1 + n * p.ys2, r);
+      Elem<OutT>::store(y + o * p.ys1 + n * p.ys2, epilogue(r, p.relu));
     }
   }
 }
@@ -305,7 +310,7 @@ __global__ __launch_bounds__(256, 2) void knnconv_bf16_kernel(KnnParams p, int64
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int64_t n = n0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (n < p.Nout) Elem<OutT>::store(y + o * p.ys1 + n * p.ys2, acc[i][j][r] + bo);
+        if (n < p.Nout) Elem<OutT>::store(y + o * p.ys1 + n * p.ys2, epilogue(acc[i][j][r] + bo, p.relu));
       }
   }
 }
@@ -476,7 +481,7 @@ __global__ __launch_bounds__(512, 1) void knnconv_bf16_v2_kernel(KnnParams p, in
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int64_t n = n0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (n < p.Nout) Elem<OutT>::store(y + o * p.ys1 + n * p.ys2, acc[i][j][r] + bo);
+        if (n < p.Nout) Elem<OutT>::store(y + o * p.ys1 + n * p.ys2, epilogue(acc[i][j][r] + bo, p.relu));
       }
   }
 }
@@ -728,7 +733,7 @@ __global__ __launch_bounds__(512, 1) void knnconv_bf16_v3_kernel(KnnParams p, in
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int64_t n = n0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (n < p.Nout) Elem<OutT>::store(y + o * p.ys1 + n * p.ys2, acc[i][j][r] + bo);
+        if (n < p.Nout) Elem<OutT>::store(y + o * p.ys1 + n * p.ys2, epilogue(acc[i][j][r] + bo, p.relu));
       }
   }
 }
@@ -1017,7 +1022,7 @@ __global__ __launch_bounds__(512, 1) void knnconv_bf16_v4_kernel(KnnParams p, in
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int64_t n = n0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (n < p.Nout) Elem<OutT>::store(y + o * p.ys1 + n * p.ys2, acc[i][j][r] + bo);
+        if (n < p.Nout) Elem<OutT>::store(y + o * p.ys1 + n * p.ys2, epilogue(acc[i][j][r] + bo, p.relu));
       }
   }
 }
@@ -1173,6 +1178,10 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
   p.x_scale = a->x_scale; p.y = a->y; p.ys0 = a->y_stride[0]; p.ys1 = a->y_stride[1]; p.ys2 = a->y_stride[2];
   p.tile_lo = a->tile_lo; p.tile_ent = a->tile_ent; p.tile_nbr = a->tile_nbr; p.max_span = a->max_span;
   p.tile_coll = a->tile_coll; p.tile_coll_n = a->tile_coll_n; p.zero_row = a->zero_row;
+  if (a->activation != FOVI_ACT_NONE && a->activation != FOVI_ACT_RELU) {
+    set_error("fovi_knnconv_fwd: bad activation %d", a->activation); return 1;
+  }
+  p.relu = a->activation == FOVI_ACT_RELU;
   if (a->tile_lo && (a->tile_points != V3_MT || !a->tile_span || a->max_span <= 0)) {
     set_error("fovi_knnconv_fwd: tile tables need tile_points=%d, tile_span and max_span > 0", V3_MT);
     return 1;

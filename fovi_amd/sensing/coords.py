@@ -169,6 +169,8 @@ class SamplingCoords:
     """
 
     def __init__(self, fov, cmf_a, res, device="cpu", style="logpolar", dtype=torch.float, max_val=1):
+        if isinstance(res, float) and res.is_integer():
+            res = int(res)
         self.fov = fov
         self.cmf_a = cmf_a
         self.resolution = res

@@ -23,11 +23,12 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 4
+#define FOVI_ABI_VERSION 5
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
 enum fovi_padding { FOVI_PAD_ZEROS = 0, FOVI_PAD_BORDER = 1 };
+enum fovi_activation { FOVI_ACT_NONE = 0, FOVI_ACT_RELU = 1 };
 
 /* Version of this header the library was built from (FOVI_ABI_VERSION). */
 int fovi_abi_version(void);
@@ -141,7 +142,7 @@ typedef struct fovi_knnconv_args {
   const uint8_t* tile_coll;   /* [n_tiles, n_ref, tile_points] or NULL */
   const int32_t* tile_coll_n; /* [n_tiles, n_ref] or NULL */
   int32_t zero_row;
-  int32_t reserved4;
+  int32_t activation;         /* fovi_activation applied to y (after bias) */
 } fovi_knnconv_args;
 
 int fovi_knnconv_fwd(const fovi_knnconv_args* args, void* stream);

@@ -142,3 +142,63 @@ def test_c3_large_layer_slice_and_batch_independence():
             assert torch.equal(y[b:b + 1], yb), f"row {b} differs from its B=1 launch"
     ref = _oracle(layer, x[:1], layer.weight.detach().cpu().bfloat16().float())
     assert_close_rel(y[:1].float().cpu(), ref, 1e-2, "C3 row 0")
+
+
+@pytest.mark.parametrize("c_in,channels_last,dt", [(64, True, torch.bfloat16), (5, False, torch.bfloat16),
+                                                   (8, False, torch.float32)])
+def test_fused_relu_equals_relu_of_output(c_in, channels_last, dt):
+    layer = _layer(32, 16, 25, c_in, 128, bias=True, seed=4)
+    x = torch.randn(2, c_in, 1024, generator=torch.Generator().manual_seed(10)).to(dt).cuda()
+    if channels_last:
+        x = x.transpose(1, 2).contiguous().transpose(1, 2)
+    with torch.no_grad():
+        y = layer(x)
+        yr = layer.forward_fused(x, "relu")
+    assert torch.equal(yr, torch.relu(y))
+
+
+def test_patch_embedding_c4_geometry():
+    """C4 patch embedding: 16384 log-polar points -> 256 tokens, k=256, 16x16 ref grid, 3 -> 384, bias."""
+    from fovi_amd.arch.knnvit import KNNPatchEmbedding
+    pe = KNNPatchEmbedding(3, 384, 128, 16, 2.78, style="logpolar", auto_match_cart_resources=0,
+                           cart_patch_size=16, patch_overlap_factor=2, new_parameterization=True, transposed=True,
+                           sample_cortex=True, ref_frame_side_length=16, device="cuda", bias=True)
+    assert pe._k == 256 and pe.ref_coords.shape[0] == 256 and pe.out_coords.shape[0] == 256
+    g = torch.Generator().manual_seed(12)
+    with torch.no_grad():
+        pe.weight.copy_(torch.randn(pe.weight.shape, generator=g) * (1.0 / 768) ** 0.5)
+        pe.bias.copy_(torch.randn(384, generator=g) * 0.1)
+    x = torch.rand(3, 3, 16384, generator=g).bfloat16()
+    with torch.no_grad():
+        y = pe(x.cuda())
+    assert y.shape == (3, 384, 256)
+    ref = _oracle(pe, x, pe.weight.detach().cpu().bfloat16().float())
+    assert_close_rel(y.float().cpu(), ref, 1e-2)
+    pe.transposed = False
+    with torch.no_grad():
+        assert pe(x.cuda()).shape == (3, 256, 384)
+
+
+def test_alexnet_chain_c2_geometry():
+    """C2 network (5 layers, 64/192/384/256/256, k=49/25/9/9/9, strides 2,2,1,1,1, ReLU between)
+    against the oracle chain with bf16 rounding between layers, as autocast does."""
+    from fovi_amd.arch.knnalexnet import KNNAlexNet
+    net = KNNAlexNet(64, 3, [64, 192, 384, 256, 256], [2, 2, 1, 1, 1], [], [49, 25, 9, 9, 9], style="logpolar",
+                     norm_type="none", fov=16, cmf_a=2.78, device="cuda", final_activation=False)
+    g = torch.Generator().manual_seed(13)
+    with torch.no_grad():
+        for blk in net.layers:
+            c = blk.conv
+            c.weight.copy_(torch.randn(c.weight.shape, generator=g) * (1.0 / (c.in_channels * c._k)) ** 0.5)
+    x = torch.rand(2, 3, 4096, generator=g).bfloat16()
+    with torch.no_grad():
+        y = net(x.cuda())
+    h = x
+    for i, blk in enumerate(net.layers):
+        c = blk.conv
+        h = _oracle(c, h.float(), c.weight.detach().cpu().bfloat16().float())
+        if i < 4:
+            h = torch.relu(h)
+        h = h.bfloat16()
+    assert y.shape == (2, 256, 256)
+    assert_close_rel(y.float().cpu(), h.float(), 2e-2)
