@@ -158,7 +158,8 @@ def bench_c2(steps, warmup, dev):
     gi = torch.Generator(device=dev).manual_seed(0)
     imgs = [torch.rand(B, 3, S, S, generator=gi, device=dev) for _ in range(2)]
     views = sampler.prepare_views(torch.full((B, 2), 0.5), np.array([[S, S]] * B), B, dev)
-    feats = torch.empty(B, 3, 4096, device=dev, dtype=torch.bfloat16)
+    # the sampler writes channels-last rows padded to 4 channels: the layout the first layer reads
+    _, feats = net.layers[0].conv.padded_input(B)
     state = {"i": 0}
 
     def step():
@@ -199,7 +200,7 @@ def bench_c4_frontend(steps, warmup, dev):
     fix = 0.25 + 0.5 * torch.rand(B * Fx, 2, generator=gf)
     views = sampler.prepare_views(fix, np.array([[S, S]] * (B * Fx)), B, dev,
                                   view_image=torch.arange(B).repeat_interleave(Fx))
-    feats = torch.empty(B * Fx, 3, 16384, device=dev, dtype=torch.bfloat16)
+    _, feats = pe.padded_input(B * Fx)
     state = {"i": 0}
 
     def step():

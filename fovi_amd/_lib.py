@@ -14,7 +14,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 F32, BF16, F8E4M3 = 0, 1, 2
 NEAREST, BILINEAR = 0, 1
 PAD_ZEROS, PAD_BORDER = 0, 1
@@ -61,6 +61,7 @@ class KnnConvArgs(C.Structure):
         ("tile_points", C.c_int32), ("max_span", C.c_int32),
         ("tile_coll", C.c_void_p), ("tile_coll_n", C.c_void_p),
         ("zero_row", C.c_int32), ("activation", C.c_int32),
+        ("w_c_slot", C.c_int32), ("reserved5", C.c_int32),
     ]
 
 
@@ -82,7 +83,7 @@ def load(path: str = LIB_PATH):
     lib.fovi_knnconv_fwd.argtypes = [C.POINTER(KnnConvArgs), C.c_void_p]
     lib.fovi_knnconv_fwd.restype = C.c_int
     lib.fovi_knnconv_pack_weight.argtypes = [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_void_p,
-                                             C.c_int32, C.c_int64, C.c_void_p, C.c_void_p]
+                                             C.c_int32, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p]
     lib.fovi_knnconv_pack_weight.restype = C.c_int
     got = lib.fovi_abi_version()
     if got != ABI_VERSION:

@@ -168,23 +168,42 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         return torch.einsum("dcv,nkv->ncdk", weights, self.local_rf)
 
     # -- weights -------------------------------------------------------------
-    def _packed_weight(self, dtype):
+    def _packed_weight(self, dtype, c_slot=None):
+        """Packed weight (slot-major, ``c_slot`` channels per slot), cached per weight version."""
+        c_slot = self.in_channels if c_slot is None else c_slot
         w = self.weight
-        key = (dtype, w._version, w.data_ptr())
-        hit = self._packed.get(dtype)
+        key = (dtype, c_slot, w._version, w.data_ptr())
+        hit = self._packed.get((dtype, c_slot))
         if hit is not None and hit[0] == key:
             return hit[1]
         n_ref = self.ref_coords.shape[0]
-        k_pad = -(-self.in_channels * n_ref // _KCHUNK) * _KCHUNK
+        k_pad = -(-c_slot * n_ref // _KCHUNK) * _KCHUNK
         src = w.detach().to(torch.float32).contiguous()
         out = torch.empty(self.out_channels, k_pad, dtype=dtype, device=w.device)
         lib = _lib.load()
         _lib.check(lib.fovi_knnconv_pack_weight(_lib.ptr(src), self.out_channels, self.in_channels, n_ref,
-                                                _lib.ptr(out), _lib.dtype_code(dtype), k_pad, None,
+                                                _lib.ptr(out), _lib.dtype_code(dtype), k_pad, c_slot, None,
                                                 _lib.stream_handle(w.device)),
                    "fovi_knnconv_pack_weight")
-        self._packed[dtype] = (key, out)
+        self._packed[(dtype, c_slot)] = (key, out)
         return out
+
+    @property
+    def padded_channels(self):
+        """Channels per input row the few-channel bf16 kernel reads (4 or 8), or None."""
+        c = self.in_channels
+        return 4 if c <= 4 else (8 if c <= 8 else None)
+
+    def padded_input(self, batch, device=None):
+        """A zeroed channels-last buffer ``[B, N_in, padded_channels]`` (bf16) and its
+        ``[B, C_in, N_in]`` view: a producer (e.g. the sampler) that writes into the view
+        hands this layer its preferred layout without a copy."""
+        cp = self.padded_channels
+        if cp is None:
+            raise ValueError("padded input rows are for layers with at most 8 input channels")
+        buf = torch.zeros(batch, self.in_coords.shape[0], cp, dtype=torch.bfloat16,
+                          device=device or self.weight.device)
+        return buf, buf.transpose(1, 2)[:, :self.in_channels]
 
     # -- forward -------------------------------------------------------------
     def _compute_dtype(self, x):
@@ -204,7 +223,16 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         dt = self._compute_dtype(x)
         if x.dtype != dt:
             x = x.to(dt)
-        w = self._packed_weight(dt)
+        c_slot = self.in_channels
+        cp = self.padded_channels if dt == torch.bfloat16 else None
+        if cp is not None:
+            c_slot = cp
+            if not (x.stride(1) == 1 and x.stride(2) == cp and x.stride(0) % cp == 0
+                    and x.data_ptr() % (2 * cp) == 0):
+                buf, view = self.padded_input(x.shape[0], x.device)
+                view.copy_(x)
+                x = view
+        w = self._packed_weight(dt, c_slot)
         bsz, n_out = x.shape[0], self.out_coords.shape[0]
         y = torch.empty(bsz, n_out, self.out_channels, dtype=dt, device=x.device)
         bias = None if self.bias is None else self.bias.detach().to(torch.float32).contiguous()
@@ -222,6 +250,7 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         if activation not in (None, "relu"):
             raise ValueError(f"activation must be None or 'relu', got {activation!r}")
         a.activation = _lib.ACT_RELU if activation == "relu" else _lib.ACT_NONE
+        a.w_c_slot = c_slot
         if self.tile_lo is not None:
             a.tile_lo = self.tile_lo.data_ptr(); a.tile_span = self.tile_span.data_ptr()
             a.tile_ent = self.tile_ent.data_ptr(); a.tile_nbr = self.tile_nbr.data_ptr()

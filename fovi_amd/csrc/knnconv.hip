@@ -45,6 +45,7 @@ struct KnnParams {
   const int32_t* tile_coll_n;
   int zero_row;
   int relu;
+  int w_c_slot;
 };
 
 // Output transform: optional ReLU fused into the store (the activation that
@@ -1069,6 +1070,227 @@ static int v4_tile_n(const KnnParams& p) {
   return 0;
 }
 
+// ---------------------------------------------------------------------------
+// bf16 MFMA path for few input channels (c_in <= CP, CP = 4 or 8)
+// ---------------------------------------------------------------------------
+// Input rows are channels-last and padded to CP channels (8 or 16 bytes), so
+// one load fetches a neighbour's whole feature vector; the packed weight has
+// CP channels per slot (zeros beyond c_in), and a 32-wide reduction chunk is
+// 32 / CP slots. Each thread assembles the slot sums of (point, slot) items
+// from the CSR lists (fp32 sums, one RNE rounding) into the chunk's A tile;
+// channels >= c_in of the input rows are masked to zero. Tile shape and MFMA
+// core are those of the large-channel kernels.
+template <int CP> struct RowVec;
+template <> struct RowVec<4> { typedef uint32_t __attribute__((ext_vector_type(2))) T; };
+template <> struct RowVec<8> { typedef u32x4 T; };
+
+template <int NT, int CP, typename OutT>
+__global__ __launch_bounds__(512, 1) void knnconv_bf16_smallc_kernel(KnnParams p, int64_t tiles_per_b,
+                                                                     int64_t n_tiles_n, int64_t total_tiles,
+                                                                     int64_t padded_tiles) {
+  typedef typename RowVec<CP>::T RowT;
+  constexpr int NW = CP / 2;               // 32-bit words per row
+  constexpr int SPC = 32 / CP;             // slots per chunk
+  constexpr int ITEMS = V3_MT * SPC / 512; // (point, slot) items per thread
+  constexpr int WN = NT / 2;
+  constexpr int CB = WN / 32;
+  constexpr int B_VECS = (NT * V3_CC / 8 + 511) / 512;
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][V3_MT * V3_CC];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][NT * V3_CC];
+
+  const int64_t tile = xcd_tile(blockIdx.x, padded_tiles);
+  if (tile >= total_tiles) return;
+  const int64_t mt = tile / n_tiles_n;
+  const int64_t o0 = (tile % n_tiles_n) * NT;
+  const int64_t b = mt / tiles_per_b;
+  const int64_t n0 = (mt % tiles_per_b) * V3_MT;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 3, wn = wave >> 2;
+  const uint16_t* xb = static_cast<const uint16_t*>(p.x) + b * p.xs0;
+  const char* wbase = reinterpret_cast<const char*>(static_cast<const uint16_t*>(p.w) + o0 * p.Kpad);
+  const int nk = static_cast<int>((p.V * CP + V3_CC - 1) / V3_CC);
+  // mask of the real channels within a padded row
+  uint32_t cmask[NW];
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const int c0 = 2 * w;
+    cmask[w] = (c0 < p.C ? 0x0000ffffu : 0u) | (c0 + 1 < p.C ? 0xffff0000u : 0u);
+  }
+
+  RowT ra[ITEMS];
+  u32x4 rb[B_VECS];
+  // All of a thread's (point, slot) items advance together through their
+  // neighbour lists in groups of four: the index loads of a group are issued
+  // together, then the row loads, so a list of length c costs about
+  // 2 * ceil(c / 4) memory round trips instead of 2 * c.
+  auto gather = [&](int kt) {
+    int cnt[ITEMS];
+    const int32_t* nb[ITEMS];
+    int most = 0;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int item = tid + 512 * i;
+      const int row = item / SPC, sl = item - row * SPC;
+      const int64_t n = n0 + row;
+      const int64_t v = static_cast<int64_t>(kt) * SPC + sl;
+      int32_t e = 0;
+      if (n < p.Nout && v < p.V) e = p.slot_ptr[n * p.V + v];
+      cnt[i] = e & 0xffff;
+      nb[i] = p.nbr + n * p.K + (e >> 16);
+      most = max(most, cnt[i]);
+    }
+    float acc[ITEMS][CP];
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+#pragma unroll
+      for (int c = 0; c < CP; ++c) acc[i][c] = 0.0f;
+    for (int j0 = 0; j0 < most; j0 += 4) {
+      int idx[ITEMS][4];
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) idx[i][u] = (j0 + u < cnt[i]) ? nb[i][j0 + u] : -1;
+      RowT r[ITEMS][4];
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          RowT z;
+#pragma unroll
+          for (int w = 0; w < NW; ++w) z[w] = 0u;
+          r[i][u] = idx[i][u] >= 0 ? *reinterpret_cast<const RowT*>(xb + static_cast<int64_t>(idx[i][u]) * p.xs2) : z;
+        }
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i)
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int w = 0; w < NW; ++w) {
+            const uint32_t bits = r[i][u][w] & cmask[w];
+            acc[i][2 * w] += __uint_as_float(bits << 16);
+            acc[i][2 * w + 1] += __uint_as_float(bits & 0xffff0000u);
+          }
+    }
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      RowT out;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) out[w] = cvt_pk_bf16(acc[i][2 * w], acc[i][2 * w + 1]);
+      ra[i] = out;
+    }
+  };
+  auto store_a = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const int item = tid + 512 * i;
+      const int row = item / SPC, sl = item - row * SPC;
+      const int byte = sl * CP * 2;                 // byte offset in the 64-byte row
+      const int q = byte >> 4;
+      uint16_t* dst = &As[buf][swz32(row, q) + ((byte & 15) >> 1)];
+      *reinterpret_cast<RowT*>(dst) = ra[i];
+    }
+  };
+  auto load_w = [&](int kt) {
+    const char* base = wbase + static_cast<int64_t>(kt) * V3_CC * 2;
+#pragma unroll
+    for (int i = 0; i < B_VECS; ++i) {
+      const int q = tid + 512 * i;
+      const bool ok = q < NT * 4 && o0 + (q >> 2) < p.Cout;
+      rb[i] = ok ? *reinterpret_cast<const u32x4*>(base + ((q >> 2) * p.Kpad + (q & 3) * 8) * 2)
+                 : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_w = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < B_VECS; ++i) {
+      const int q = tid + 512 * i;
+      if (q < NT * 4) *reinterpret_cast<u32x4*>(&Bs[buf][swz32(q >> 2, q & 3)]) = rb[i];
+    }
+  };
+
+  f32x16 acc[2][CB];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < CB; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  gather(0);
+  load_w(0);
+  store_a(0);
+  store_w(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < nk;
+    if (more) {
+      gather(kt + 1);
+      load_w(kt + 1);
+    }
+#pragma unroll
+    for (int ks = 0; ks < V3_CC / 16; ++ks) {
+      const int q = ks * 2 + (lane >> 5);
+      bf16x8 af[2], bfr[CB];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        af[i] = *reinterpret_cast<const bf16x8*>(&As[cur][swz32(wm * 64 + i * 32 + (lane & 31), q)]);
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+        bfr[j] = *reinterpret_cast<const bf16x8*>(&Bs[cur][swz32(wn * WN + j * 32 + (lane & 31), q)]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < CB; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) {
+      store_a(cur ^ 1);
+      store_w(cur ^ 1);
+    }
+    __syncthreads();
+  }
+
+  OutT* y = static_cast<OutT*>(p.y) + b * p.ys0;
+#pragma unroll
+  for (int j = 0; j < CB; ++j) {
+    const int64_t o = o0 + wn * WN + j * 32 + (lane & 31);
+    if (o >= p.Cout) continue;
+    const float bo = p.bias ? p.bias[o] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t n = n0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (n < p.Nout) Elem<OutT>::store(y + o * p.ys1 + n * p.ys2, epilogue(acc[i][j][r] + bo, p.relu));
+      }
+  }
+}
+
+template <int NT, int CP>
+static void launch_bf16_smallc(const KnnParams& p, int out_t, hipStream_t s) {
+  const int64_t tiles_per_b = (p.Nout + V3_MT - 1) / V3_MT;
+  const int64_t n_tiles_n = (p.Cout + NT - 1) / NT;
+  const int64_t total = p.B * tiles_per_b * n_tiles_n;
+  const int64_t padded = (total + 7) / 8 * 8;
+  dim3 grid(static_cast<unsigned>(padded));
+  if (out_t == FOVI_BF16)
+    hipLaunchKernelGGL((knnconv_bf16_smallc_kernel<NT, CP, uint16_t>), grid, dim3(512), 0, s, p, tiles_per_b,
+                       n_tiles_n, total, padded);
+  else
+    hipLaunchKernelGGL((knnconv_bf16_smallc_kernel<NT, CP, float>), grid, dim3(512), 0, s, p, tiles_per_b,
+                       n_tiles_n, total, padded);
+}
+
+template <int CP>
+static void launch_bf16_smallc_nt(const KnnParams& p, int out_t, hipStream_t s) {
+  if (p.Cout % 256 == 0) launch_bf16_smallc<256, CP>(p, out_t, s);
+  else if (p.Cout % 192 == 0) launch_bf16_smallc<192, CP>(p, out_t, s);
+  else if (p.Cout > 64) launch_bf16_smallc<128, CP>(p, out_t, s);
+  else launch_bf16_smallc<64, CP>(p, out_t, s);
+}
+
 template <int NT, bool VEC>
 static void launch_bf16(const KnnParams& p, int out_t, hipStream_t s) {
   const int64_t tiles_per_b = (p.Nout + MM_MT - 1) / MM_MT;
@@ -1114,15 +1336,12 @@ __device__ __forceinline__ uint8_t f32_to_e4m3(float f) {
 }
 
 __global__ void pack_weight_kernel(const float* w_ref, int64_t c_out, int64_t c_in, int64_t n_ref,
-                                   void* out, int dtype, int64_t k_pad, const float* w_scale) {
+                                   void* out, int dtype, int64_t k_pad, int64_t c_slot, const float* w_scale) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (idx >= c_out * k_pad) return;
   const int64_t o = idx / k_pad, kk = idx - o * k_pad;
-  float val = 0.0f;
-  if (kk < c_in * n_ref) {
-    const int64_t v = kk / c_in, c = kk - v * c_in;
-    val = w_ref[o * c_in * n_ref + c * n_ref + v];
-  }
+  const int64_t v = kk / c_slot, c = kk - v * c_slot;
+  const float val = (v < n_ref && c < c_in) ? w_ref[o * c_in * n_ref + c * n_ref + v] : 0.0f;
   if (dtype == FOVI_F32) static_cast<float*>(out)[idx] = val;
   else if (dtype == FOVI_BF16) static_cast<uint16_t*>(out)[idx] = f32_to_bf16_bits(val);
   else static_cast<uint8_t*>(out)[idx] = f32_to_e4m3(val / w_scale[o]);
@@ -1131,14 +1350,15 @@ __global__ void pack_weight_kernel(const float* w_ref, int64_t c_out, int64_t c_
 }  // namespace fovi
 
 extern "C" int fovi_knnconv_pack_weight(const float* w_ref, int64_t c_out, int64_t c_in, int64_t n_ref,
-                                        void* w_packed, int32_t out_dtype, int64_t k_pad,
+                                        void* w_packed, int32_t out_dtype, int64_t k_pad, int64_t c_slot,
                                         const float* w_scale, void* stream) {
   using namespace fovi;
   clear_error();
   if (!w_ref || !w_packed) { set_error("fovi_knnconv_pack_weight: null pointer"); return 1; }
-  if (c_out <= 0 || c_in <= 0 || n_ref <= 0 || k_pad < c_in * n_ref || k_pad % MM_KC != 0) {
-    set_error("fovi_knnconv_pack_weight: bad sizes c_out=%lld c_in=%lld n_ref=%lld k_pad=%lld",
-              (long long)c_out, (long long)c_in, (long long)n_ref, (long long)k_pad);
+  if (c_slot == 0) c_slot = c_in;
+  if (c_out <= 0 || c_in <= 0 || n_ref <= 0 || c_slot < c_in || k_pad < c_slot * n_ref || k_pad % MM_KC != 0) {
+    set_error("fovi_knnconv_pack_weight: bad sizes c_out=%lld c_in=%lld n_ref=%lld k_pad=%lld c_slot=%lld",
+              (long long)c_out, (long long)c_in, (long long)n_ref, (long long)k_pad, (long long)c_slot);
     return 1;
   }
   if (out_dtype != FOVI_F32 && out_dtype != FOVI_BF16 && out_dtype != FOVI_F8E4M3) {
@@ -1148,7 +1368,7 @@ extern "C" int fovi_knnconv_pack_weight(const float* w_ref, int64_t c_out, int64
   const int64_t n = c_out * k_pad;
   hipLaunchKernelGGL(pack_weight_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), w_ref, c_out, c_in, n_ref, w_packed, out_dtype, k_pad,
-                     w_scale);
+                     c_slot, w_scale);
   return check_launch("fovi_knnconv_pack_weight");
 }
 
@@ -1164,7 +1384,7 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
     set_error("fovi_knnconv_fwd: bad sizes"); return 1;
   }
   if (a->k > 65535) { set_error("fovi_knnconv_fwd: k=%lld exceeds 65535", (long long)a->k); return 1; }
-  if (a->k_pad < a->c_in * a->n_ref || a->k_pad % MM_KC != 0) {
+  if (a->k_pad % MM_KC != 0) {
     set_error("fovi_knnconv_fwd: k_pad=%lld must be a multiple of 64 >= c_in*n_ref=%lld",
               (long long)a->k_pad, (long long)(a->c_in * a->n_ref));
     return 1;
@@ -1182,6 +1402,11 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
     set_error("fovi_knnconv_fwd: bad activation %d", a->activation); return 1;
   }
   p.relu = a->activation == FOVI_ACT_RELU;
+  p.w_c_slot = a->w_c_slot > 0 ? a->w_c_slot : static_cast<int>(a->c_in);
+  if (p.w_c_slot < p.C || a->k_pad < p.w_c_slot * p.V) {
+    set_error("fovi_knnconv_fwd: w_c_slot=%d must be >= c_in and k_pad >= w_c_slot * n_ref", p.w_c_slot);
+    return 1;
+  }
   if (a->tile_lo && (a->tile_points != V3_MT || !a->tile_span || a->max_span <= 0)) {
     set_error("fovi_knnconv_fwd: tile tables need tile_points=%d, tile_span and max_span > 0", V3_MT);
     return 1;
@@ -1199,6 +1424,21 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
     else
       hipLaunchKernelGGL((knnconv_f32_kernel<uint16_t>), grid, dim3(256), 0, s, p, tiles_per_b);
     return check_launch("fovi_knnconv_fwd(f32)");
+  }
+  if (a->x_dtype == FOVI_BF16 && a->w_dtype == FOVI_BF16 && p.w_c_slot != p.C) {
+    // packed weight with padded slots: only the small-channel kernel reads it
+    const uintptr_t xa = reinterpret_cast<uintptr_t>(a->x);
+    const int cp = p.w_c_slot;
+    if ((cp == 4 || cp == 8) && p.xs1 == 1 && p.xs2 == cp && p.xs0 % cp == 0 && xa % (2 * cp) == 0) {
+      if (cp == 4) launch_bf16_smallc_nt<4>(p, a->y_dtype, s);
+      else launch_bf16_smallc_nt<8>(p, a->y_dtype, s);
+      return check_launch("fovi_knnconv_fwd(bf16 small-c)");
+    }
+    set_error("fovi_knnconv_fwd: w_c_slot=%d needs channels-last input rows padded to it", cp);
+    return 1;
+  }
+  if (p.w_c_slot != p.C) {
+    set_error("fovi_knnconv_fwd: w_c_slot != c_in is only supported for bf16"); return 1;
   }
   if (a->x_dtype == FOVI_BF16 && a->w_dtype == FOVI_BF16) {
     const uintptr_t xa = reinterpret_cast<uintptr_t>(a->x);

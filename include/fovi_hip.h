@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 5
+#define FOVI_ABI_VERSION 6
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -143,6 +143,10 @@ typedef struct fovi_knnconv_args {
   const int32_t* tile_coll_n; /* [n_tiles, n_ref] or NULL */
   int32_t zero_row;
   int32_t activation;         /* fovi_activation applied to y (after bias) */
+  int32_t w_c_slot;           /* channels per slot in the packed weight (0 = c_in); 4 or 8
+                                 with c_in <= w_c_slot selects the few-channel kernel, which
+                                 needs channels-last input rows padded to w_c_slot channels */
+  int32_t reserved5;
 } fovi_knnconv_args;
 
 int fovi_knnconv_fwd(const fovi_knnconv_args* args, void* stream);
@@ -152,12 +156,13 @@ int fovi_knnconv_fwd(const fovi_knnconv_args* args, void* stream);
  *
  * w_ref is KNNConvLayer.weight, fp32 [c_out, c_in * n_ref] with reduction
  * index c * n_ref + v (fovi/arch/knn.py:462,524). The packed output is
- * [c_out, k_pad] with index v * c_in + c, zero padded, in out_dtype. For
+ * [c_out, k_pad] with index v * c_slot + c (c_slot >= c_in channels per slot,
+ * 0 = c_in; channels >= c_in are zero), zero padded, in out_dtype. For
  * F8E4M3, row o is divided by w_scale[o] and rounded to OCP e4m3 (RNE,
  * saturating to +-448).
  */
 int fovi_knnconv_pack_weight(const float* w_ref, int64_t c_out, int64_t c_in, int64_t n_ref,
-                             void* w_packed, int32_t out_dtype, int64_t k_pad,
+                             void* w_packed, int32_t out_dtype, int64_t k_pad, int64_t c_slot,
                              const float* w_scale, void* stream);
 
 #ifdef __cplusplus

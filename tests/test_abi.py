@@ -46,7 +46,7 @@ def test_argument_validation_without_gpu():
     s = _lib.SamplerArgs()
     assert lib.fovi_sampler_fwd(s, None) != 0
     assert b"null pointer" in lib.fovi_last_error()
-    assert lib.fovi_knnconv_pack_weight(None, 1, 1, 1, None, 0, 64, None, None) != 0
+    assert lib.fovi_knnconv_pack_weight(None, 1, 1, 1, None, 0, 64, 0, None, None) != 0
 
 
 def _c_layout(struct, fields, tmp_path):

@@ -202,3 +202,20 @@ def test_alexnet_chain_c2_geometry():
         h = h.bfloat16()
     assert y.shape == (2, 256, 256)
     assert_close_rel(y.float().cpu(), h.float(), 2e-2)
+
+
+@pytest.mark.parametrize("c_in,k,side", [(3, 49, None), (1, 9, None), (4, 25, None), (6, 25, None), (3, 256, 16)])
+def test_bf16_few_channels_padded_rows(c_in, k, side):
+    """Few-channel kernel: rows padded to 4/8 channels by the producer (no copy) or by the layer."""
+    res_out = 4 if k == 256 else 16
+    layer = _layer(32, res_out, k, c_in, 96, side, bias=True, seed=7)
+    x = torch.randn(2, c_in, 1024, generator=torch.Generator().manual_seed(11)).bfloat16()
+    buf, view = layer.padded_input(2)
+    view.copy_(x.cuda())
+    buf[..., c_in:] = torch.nan          # padding channels must not leak into the result
+    with torch.no_grad():
+        y_view = layer(view)
+        y_copy = layer(x.cuda())
+    ref = _oracle(layer, x, layer.weight.detach().cpu().bfloat16().float())
+    assert_close_rel(y_view.float().cpu(), ref, 1e-2)
+    assert torch.equal(y_view, y_copy)
