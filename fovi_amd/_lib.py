@@ -14,7 +14,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 F32, BF16, F8E4M3 = 0, 1, 2
 NEAREST, BILINEAR = 0, 1
 PAD_ZEROS, PAD_BORDER = 0, 1
@@ -62,6 +62,7 @@ class KnnConvArgs(C.Structure):
         ("tile_coll", C.c_void_p), ("tile_coll_n", C.c_void_p),
         ("zero_row", C.c_int32), ("activation", C.c_int32),
         ("w_c_slot", C.c_int32), ("reserved5", C.c_int32),
+        ("workspace", C.c_void_p), ("workspace_bytes", C.c_int64),
     ]
 
 

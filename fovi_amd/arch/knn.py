@@ -131,6 +131,9 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
             self._max_span = int(tiles[1].max())
             self._zero_row = tiles[6]
         self._packed = {}
+        # few-channel bf16 layers: slot sums through a workspace, then a dense GEMM
+        # (False: the single fused kernel, which needs no workspace)
+        self.two_pass_few_channels = True
 
     # -- setup ---------------------------------------------------------------
     def _init_conv_like(self):
@@ -251,6 +254,11 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
             raise ValueError(f"activation must be None or 'relu', got {activation!r}")
         a.activation = _lib.ACT_RELU if activation == "relu" else _lib.ACT_NONE
         a.w_c_slot = c_slot
+        ws = None
+        if cp is not None and self.two_pass_few_channels:
+            # slot-sum rows for the two-pass few-channel path (caller-owned scratch)
+            ws = torch.empty(bsz * n_out * w.shape[1], dtype=torch.bfloat16, device=x.device)
+            a.workspace = ws.data_ptr(); a.workspace_bytes = ws.numel() * 2
         if self.tile_lo is not None:
             a.tile_lo = self.tile_lo.data_ptr(); a.tile_span = self.tile_span.data_ptr()
             a.tile_ent = self.tile_ent.data_ptr(); a.tile_nbr = self.tile_nbr.data_ptr()

@@ -509,6 +509,20 @@ static int launch_bf16_v2(const KnnParams& p, int out_t, hipStream_t s) {
   return 0;
 }
 
+// Channel-tile width: the widest candidate that divides c_out and fits the
+// LDS budget (no wasted MFMA columns); otherwise the widest that fits.
+template <typename Fits>
+static int pick_tile_n(int64_t cout, Fits fits) {
+  const int cands[4] = {256, 192, 128, 64};
+  for (int nt : cands)
+    if (cout % nt == 0 && fits(nt)) return nt;
+  for (int nt : cands) {
+    if (nt > 64 && cout <= nt / 2) continue;
+    if (fits(nt)) return nt;
+  }
+  return 0;
+}
+
 // Picks the widest channel tile whose LDS footprint fits; 0 if none does.
 static int v2_tile_n(const KnnParams& p) {
   const int cands[4] = {256, 192, 128, 64};
@@ -774,12 +788,7 @@ static bool launch_bf16_v3(const KnnParams& p, int out_t, hipStream_t s) {
 // Widest channel tile whose LDS footprint fits with the staged rows; 0 if none.
 static int v3_tile_n(const KnnParams& p) {
   if (p.max_span <= 0 || p.max_span > 1024) return 0;
-  const int cands[4] = {256, 192, 128, 64};
-  for (int nt : cands) {
-    if (nt > 64 && p.Cout <= nt / 2) continue;
-    if (v3_lds_bytes(nt, p.V, p.K, p.max_span) <= 160 * 1024) return nt;
-  }
-  return 0;
+  return pick_tile_n(p.Cout, [&](int nt) { return v3_lds_bytes(nt, p.V, p.K, p.max_span) <= 160 * 1024; });
 }
 
 // ---------------------------------------------------------------------------
@@ -1062,12 +1071,9 @@ static bool launch_bf16_v4(const KnnParams& p, int out_t, hipStream_t s) {
 
 static int v4_tile_n(const KnnParams& p) {
   if (p.zero_row <= 0 || p.zero_row > 1024 || !p.tile_coll || !p.tile_coll_n) return 0;
-  const int cands[4] = {256, 192, 128, 64};
-  for (int nt : cands) {
-    if (nt > 64 && p.Cout <= nt / 2) continue;
-    if (v4_layout(nt, static_cast<int>(p.V), static_cast<int>(p.K), p.zero_row).total <= 160 * 1024) return nt;
-  }
-  return 0;
+  return pick_tile_n(p.Cout, [&](int nt) {
+    return v4_layout(nt, static_cast<int>(p.V), static_cast<int>(p.K), p.zero_row).total <= 160 * 1024;
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -1291,6 +1297,201 @@ static void launch_bf16_smallc_nt(const KnnParams& p, int out_t, hipStream_t s) 
   else launch_bf16_smallc<64, CP>(p, out_t, s);
 }
 
+// ---------------------------------------------------------------------------
+// Few-channel layers with many slots, two passes through a workspace
+// ---------------------------------------------------------------------------
+// Pass 1 (slotsum_kernel): one wave per output point, lanes over slots; each
+// lane walks its slots' neighbour lists (index loads, then row loads, four
+// at a time) and writes the point's slot-major reduction row
+// A[b, n, v * CP + c] in bf16 (fp32 sums, one RNE rounding), zero padded to
+// k_pad. Few registers, many waves in flight: the neighbour-list latency is
+// hidden by occupancy, which the MFMA kernels (one 8-wave workgroup per CU)
+// cannot do. Pass 2 (dense_gemm_kernel): the MFMA tile core of the kernels
+// above with A rows read contiguously from the workspace.
+template <int CP>
+__global__ __launch_bounds__(256) void slotsum_kernel(KnnParams p, uint16_t* A, int64_t rows) {
+  typedef typename RowVec<CP>::T RowT;
+  constexpr int NW = CP / 2;
+  const int lane = threadIdx.x & 63;
+  const int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);   // output row (b, n)
+  if (m >= rows) return;
+  const int64_t b = m / p.Nout, n = m - b * p.Nout;
+  const uint16_t* xb = static_cast<const uint16_t*>(p.x) + b * p.xs0;
+  uint16_t* arow = A + m * p.Kpad;
+  uint32_t cmask[NW];
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const int c0 = 2 * w;
+    cmask[w] = (c0 < p.C ? 0x0000ffffu : 0u) | (c0 + 1 < p.C ? 0xffff0000u : 0u);
+  }
+  const int64_t nslots = p.Kpad / CP;
+  for (int64_t v = lane; v < nslots; v += 64) {
+    float acc[CP];
+#pragma unroll
+    for (int c = 0; c < CP; ++c) acc[c] = 0.0f;
+    if (v < p.V) {
+      const int32_t e = p.slot_ptr[n * p.V + v];
+      const int cnt = e & 0xffff;
+      const int32_t* nb = p.nbr + n * p.K + (e >> 16);
+      for (int j0 = 0; j0 < cnt; j0 += 4) {
+        int idx[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) idx[u] = j0 + u < cnt ? nb[j0 + u] : -1;
+        RowT r[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          RowT z;
+#pragma unroll
+          for (int w = 0; w < NW; ++w) z[w] = 0u;
+          r[u] = idx[u] >= 0 ? *reinterpret_cast<const RowT*>(xb + static_cast<int64_t>(idx[u]) * p.xs2) : z;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int w = 0; w < NW; ++w) {
+            const uint32_t bits = r[u][w] & cmask[w];
+            acc[2 * w] += __uint_as_float(bits << 16);
+            acc[2 * w + 1] += __uint_as_float(bits & 0xffff0000u);
+          }
+      }
+    }
+    RowT out;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) out[w] = cvt_pk_bf16(acc[2 * w], acc[2 * w + 1]);
+    *reinterpret_cast<RowT*>(arow + v * CP) = out;
+  }
+}
+
+// Y[b, n, o] = sum_k A[(b, n), k] * W[o, k] (+ bias, activation), A in the workspace.
+template <int NT, typename OutT>
+__global__ __launch_bounds__(512, 1) void dense_gemm_kernel(KnnParams p, const uint16_t* A, int64_t tiles_per_b,
+                                                            int64_t n_tiles_n, int64_t total_tiles,
+                                                            int64_t padded_tiles) {
+  constexpr int WN = NT / 2;
+  constexpr int CB = WN / 32;
+  constexpr int B_VECS = (NT * V3_CC / 8 + 511) / 512;
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][V3_MT * V3_CC];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][NT * V3_CC];
+  const int64_t tile = xcd_tile(blockIdx.x, padded_tiles);
+  if (tile >= total_tiles) return;
+  const int64_t mt = tile / n_tiles_n;
+  const int64_t o0 = (tile % n_tiles_n) * NT;
+  const int64_t b = mt / tiles_per_b;
+  const int64_t n0 = (mt % tiles_per_b) * V3_MT;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 3, wn = wave >> 2;
+  const uint16_t* ab = A + (b * p.Nout + n0) * p.Kpad;
+  const char* wbase = reinterpret_cast<const char*>(static_cast<const uint16_t*>(p.w) + o0 * p.Kpad);
+  const int nk = static_cast<int>(p.Kpad / V3_CC);
+  u32x4 ra[2], rb[B_VECS];
+  auto load = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int q = tid + 512 * i;
+      const int row = q >> 2;
+      ra[i] = n0 + row < p.Nout
+                  ? *reinterpret_cast<const u32x4*>(ab + static_cast<int64_t>(row) * p.Kpad + kt * V3_CC + (q & 3) * 8)
+                  : u32x4{0u, 0u, 0u, 0u};
+    }
+    const char* base = wbase + static_cast<int64_t>(kt) * V3_CC * 2;
+#pragma unroll
+    for (int i = 0; i < B_VECS; ++i) {
+      const int q = tid + 512 * i;
+      const bool ok = q < NT * 4 && o0 + (q >> 2) < p.Cout;
+      rb[i] = ok ? *reinterpret_cast<const u32x4*>(base + ((q >> 2) * p.Kpad + (q & 3) * 8) * 2)
+                 : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int q = tid + 512 * i;
+      *reinterpret_cast<u32x4*>(&As[buf][swz32(q >> 2, q & 3)]) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_VECS; ++i) {
+      const int q = tid + 512 * i;
+      if (q < NT * 4) *reinterpret_cast<u32x4*>(&Bs[buf][swz32(q >> 2, q & 3)]) = rb[i];
+    }
+  };
+  f32x16 acc[2][CB];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < CB; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < nk;
+    if (more) load(kt + 1);
+#pragma unroll
+    for (int ks = 0; ks < V3_CC / 16; ++ks) {
+      const int q = ks * 2 + (lane >> 5);
+      bf16x8 af[2], bfr[CB];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        af[i] = *reinterpret_cast<const bf16x8*>(&As[cur][swz32(wm * 64 + i * 32 + (lane & 31), q)]);
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+        bfr[j] = *reinterpret_cast<const bf16x8*>(&Bs[cur][swz32(wn * WN + j * 32 + (lane & 31), q)]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < CB; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) store(cur ^ 1);
+    __syncthreads();
+  }
+  OutT* y = static_cast<OutT*>(p.y) + b * p.ys0;
+#pragma unroll
+  for (int j = 0; j < CB; ++j) {
+    const int64_t o = o0 + wn * WN + j * 32 + (lane & 31);
+    if (o >= p.Cout) continue;
+    const float bo = p.bias ? p.bias[o] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t n = n0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (n < p.Nout) Elem<OutT>::store(y + o * p.ys1 + n * p.ys2, epilogue(acc[i][j][r] + bo, p.relu));
+      }
+  }
+}
+
+template <int NT>
+static void launch_dense(const KnnParams& p, const uint16_t* A, int out_t, hipStream_t s) {
+  const int64_t tiles_per_b = (p.Nout + V3_MT - 1) / V3_MT;
+  const int64_t n_tiles_n = (p.Cout + NT - 1) / NT;
+  const int64_t total = p.B * tiles_per_b * n_tiles_n;
+  const int64_t padded = (total + 7) / 8 * 8;
+  dim3 grid(static_cast<unsigned>(padded));
+  if (out_t == FOVI_BF16)
+    hipLaunchKernelGGL((dense_gemm_kernel<NT, uint16_t>), grid, dim3(512), 0, s, p, A, tiles_per_b, n_tiles_n,
+                       total, padded);
+  else
+    hipLaunchKernelGGL((dense_gemm_kernel<NT, float>), grid, dim3(512), 0, s, p, A, tiles_per_b, n_tiles_n,
+                       total, padded);
+}
+
+static int launch_two_pass(const KnnParams& p, int cp, uint16_t* A, int out_t, hipStream_t s) {
+  const int64_t rows = p.B * p.Nout;
+  dim3 g1(static_cast<unsigned>((rows + 3) / 4));
+  if (cp == 4) hipLaunchKernelGGL((slotsum_kernel<4>), g1, dim3(256), 0, s, p, A, rows);
+  else hipLaunchKernelGGL((slotsum_kernel<8>), g1, dim3(256), 0, s, p, A, rows);
+  if (check_launch("fovi_knnconv_fwd(slot sums)")) return 1;
+  if (p.Cout % 256 == 0) launch_dense<256>(p, A, out_t, s);
+  else if (p.Cout % 192 == 0) launch_dense<192>(p, A, out_t, s);
+  else if (p.Cout > 64) launch_dense<128>(p, A, out_t, s);
+  else launch_dense<64>(p, A, out_t, s);
+  return check_launch("fovi_knnconv_fwd(dense gemm)");
+}
+
 template <int NT, bool VEC>
 static void launch_bf16(const KnnParams& p, int out_t, hipStream_t s) {
   const int64_t tiles_per_b = (p.Nout + MM_MT - 1) / MM_MT;
@@ -1430,6 +1631,11 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
     const uintptr_t xa = reinterpret_cast<uintptr_t>(a->x);
     const int cp = p.w_c_slot;
     if ((cp == 4 || cp == 8) && p.xs1 == 1 && p.xs2 == cp && p.xs0 % cp == 0 && xa % (2 * cp) == 0) {
+      const uint64_t need = static_cast<uint64_t>(p.B) * static_cast<uint64_t>(p.Nout) *
+                            static_cast<uint64_t>(p.Kpad) * 2u;
+      if (a->workspace && static_cast<uint64_t>(a->workspace_bytes) >= need &&
+          reinterpret_cast<uintptr_t>(a->workspace) % 16 == 0)
+        return launch_two_pass(p, cp, static_cast<uint16_t*>(a->workspace), a->y_dtype, s);
       if (cp == 4) launch_bf16_smallc_nt<4>(p, a->y_dtype, s);
       else launch_bf16_smallc_nt<8>(p, a->y_dtype, s);
       return check_launch("fovi_knnconv_fwd(bf16 small-c)");

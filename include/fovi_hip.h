@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 6
+#define FOVI_ABI_VERSION 7
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -144,9 +144,13 @@ typedef struct fovi_knnconv_args {
   int32_t zero_row;
   int32_t activation;         /* fovi_activation applied to y (after bias) */
   int32_t w_c_slot;           /* channels per slot in the packed weight (0 = c_in); 4 or 8
-                                 with c_in <= w_c_slot selects the few-channel kernel, which
-                                 needs channels-last input rows padded to w_c_slot channels */
+                                 with c_in <= w_c_slot selects the few-channel kernels, which
+                                 need channels-last input rows padded to w_c_slot channels */
   int32_t reserved5;
+  void* workspace;            /* optional caller-owned device scratch (16-byte aligned); with
+                                 >= batch * n_out * k_pad * 2 bytes the few-channel path runs
+                                 in two passes (slot sums into it, then a dense GEMM) */
+  int64_t workspace_bytes;
 } fovi_knnconv_args;
 
 int fovi_knnconv_fwd(const fovi_knnconv_args* args, void* stream);

@@ -216,6 +216,9 @@ def test_bf16_few_channels_padded_rows(c_in, k, side):
     with torch.no_grad():
         y_view = layer(view)
         y_copy = layer(x.cuda())
+        layer.two_pass_few_channels = False      # single fused kernel, no workspace
+        y_fused = layer(view)
     ref = _oracle(layer, x, layer.weight.detach().cpu().bfloat16().float())
     assert_close_rel(y_view.float().cpu(), ref, 1e-2)
     assert torch.equal(y_view, y_copy)
+    assert_close_rel(y_fused.float().cpu(), ref, 1e-2)
