@@ -73,6 +73,26 @@ def bench_c3(steps, warmup, dev):
     return dict(ms=ms, flops=flops, tflops=tflops, layer=layer, x=x)
 
 
+def bench_c5(c3, steps, warmup):
+    """C5: the C3 layer with e4m3 activations (per-tensor scale) and weights
+    (per-output-channel scales), fp32 accumulation, bf16 output. The input is
+    quantized once before timing (the layer's producer would emit e4m3); the
+    quantizer is timed on its own."""
+    import torch
+    layer, x = c3["layer"], c3["x"]
+    with torch.no_grad():
+        xq = layer.quantize_input(x)
+        ms = time_steps(lambda: layer(xq), steps, warmup)
+        ms_q = time_steps(lambda: layer.quantize_input(x), steps, warmup)
+    tflops = c3["flops"] / (ms * 1e-3) / 1e12
+    # quantizer: amax pass reads x, quantize pass reads x and writes e4m3
+    q_bytes = 2 * x.numel() * x.element_size() + x.numel()
+    q_gbs = q_bytes / (ms_q * 1e-3) / 1e9
+    log(f"[c5] {ms:.3f} ms/step  {tflops:.1f} TFLOP/s  ({100 * tflops / PEAK_FP8_TFLOPS:.1f}% of fp8 peak); "
+        f"quantize {ms_q:.3f} ms ({q_gbs:.0f} GB/s)")
+    return dict(ms=ms, tflops=tflops, ms_q=ms_q, q_gbs=q_gbs)
+
+
 def sampler_algorithmic_bytes(sampler, img, fix, sizes, vmap, mode):
     """Output bytes + sum over views of distinct in-bounds tap pixels x C x element size."""
     import torch
@@ -264,6 +284,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sampler", action="store_true")
     ap.add_argument("--no-e2e", action="store_true", help="skip the C2/C4 end-to-end legs")
+    ap.add_argument("--no-fp8", action="store_true", help="skip the C5 fp8 leg")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -272,6 +293,7 @@ def main():
     import torch
     dev = torch.device("cuda:0")
     c3 = bench_c3(args.steps, args.warmup, dev)
+    c5 = None if args.no_fp8 else bench_c5(c3, args.steps, args.warmup)
     c4 = None if args.no_sampler else bench_c4_sampler(args.steps, args.warmup, dev, "nearest")
     c4b = None if args.no_sampler else bench_c4_sampler(args.steps, args.warmup, dev, "bilinear")
     c2 = None if args.no_e2e else bench_c2(args.steps, args.warmup, dev)
@@ -297,6 +319,13 @@ def main():
                      "unit": "TFLOP/s", "frac": round(c3["tflops"] / PEAK_BF16_TFLOPS, 4), "traffic": None},
         "cpu_baseline": cpu,
     }
+    if c5 is not None:
+        line["c5_fp8"] = {"workload": "C5: C3 layer with OCP e4m3 activations (per-tensor scale) and weights "
+                                      "(per-output-channel scales), fp32 accumulate, bf16 out",
+                          "TFLOP/s": round(c5["tflops"], 2), "ms": round(c5["ms"], 4),
+                          "roofline": {"bound": "mfma", "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
+                                       "frac": round(c5["tflops"] / PEAK_FP8_TFLOPS, 4)},
+                          "quantize_ms": round(c5["ms_q"], 4), "quantize_GB/s": round(c5["q_gbs"], 1)}
     if c4 is not None:
         line["sampler_c4"] = {
             "workload": "C4 sampler: 128 images 3x512x512 bf16, 4 fixations each (512 views), "

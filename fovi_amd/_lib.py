@@ -14,7 +14,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 F32, BF16, F8E4M3 = 0, 1, 2
 NEAREST, BILINEAR = 0, 1
 PAD_ZEROS, PAD_BORDER = 0, 1
@@ -24,7 +24,7 @@ _DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float8_e4m3fn: F8
 
 # Every symbol include/fovi_hip.h declares.
 EXPORTED = ("fovi_abi_version", "fovi_last_error", "fovi_sampler_fwd", "fovi_knnconv_fwd",
-            "fovi_knnconv_pack_weight")
+            "fovi_knnconv_pack_weight", "fovi_quantize_e4m3")
 
 
 class SamplerArgs(C.Structure):
@@ -63,6 +63,18 @@ class KnnConvArgs(C.Structure):
         ("zero_row", C.c_int32), ("activation", C.c_int32),
         ("w_c_slot", C.c_int32), ("reserved5", C.c_int32),
         ("workspace", C.c_void_p), ("workspace_bytes", C.c_int64),
+        ("x_scale_dev", C.c_void_p),
+    ]
+
+
+class QuantizeArgs(C.Structure):
+    _fields_ = [
+        ("x", C.c_void_p), ("x_dtype", C.c_int32), ("reserved0", C.c_int32),
+        ("batch", C.c_int64), ("channels", C.c_int64), ("points", C.c_int64),
+        ("x_stride", C.c_int64 * 3),
+        ("q", C.c_void_p), ("q_stride", C.c_int64 * 3),
+        ("headroom", C.c_float), ("reserved1", C.c_int32),
+        ("scale_in", C.c_void_p), ("scale_out", C.c_void_p), ("amax_work", C.c_void_p),
     ]
 
 
@@ -86,6 +98,8 @@ def load(path: str = LIB_PATH):
     lib.fovi_knnconv_pack_weight.argtypes = [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_void_p,
                                              C.c_int32, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p]
     lib.fovi_knnconv_pack_weight.restype = C.c_int
+    lib.fovi_quantize_e4m3.argtypes = [C.POINTER(QuantizeArgs), C.c_void_p]
+    lib.fovi_quantize_e4m3.restype = C.c_int
     got = lib.fovi_abi_version()
     if got != ABI_VERSION:
         raise RuntimeError(f"{path}: ABI version {got}, expected {ABI_VERSION}")

@@ -16,7 +16,11 @@ also what the reference returns (``F.linear(...).transpose(1,2)``,
 Compute dtype: bf16 inputs, or any input under ``torch.autocast('cuda',
 dtype=torch.bfloat16)``, run the bf16 MFMA kernel with fp32 accumulation and
 return bf16 (the reference's autocast behaviour); fp32 inputs run the fp32
-kernel. Backward is not built: calling it raises.
+kernel. ``Fp8Activations`` inputs (``layer.quantize_input``), or any input
+when ``layer.fp8`` is set, run the e4m3 MFMA kernel (per-tensor activation
+scale, per-output-channel weight scale ``amax|W[o]|/448``, fp32 accumulation,
+bf16 output); the reference has no fp8 path. Backward is not built: calling
+it raises.
 """
 from __future__ import annotations
 
@@ -29,6 +33,7 @@ from einops import rearrange
 from .. import _lib
 from ..sensing.coords import SamplingCoords
 from . import knn_tables as T
+from .fp8 import Fp8Activations, headroom_for, quantize_e4m3
 
 __all__ = [
     "KNNBaseLayer",
@@ -131,6 +136,10 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
             self._max_span = int(tiles[1].max())
             self._zero_row = tiles[6]
         self._packed = {}
+        # slot-sum headroom of the fp8 path: the largest neighbour count of a slot
+        self._max_slot_count = int((slot_ptr & 0xFFFF).max()) if slot_ptr.numel() else 1
+        # quantize every input to e4m3 and run the fp8 kernel
+        self.fp8 = False
         # few-channel bf16 layers: slot sums through a workspace, then a dense GEMM
         # (False: the single fused kernel, which needs no workspace)
         self.two_pass_few_channels = True
@@ -183,13 +192,20 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         k_pad = -(-c_slot * n_ref // _KCHUNK) * _KCHUNK
         src = w.detach().to(torch.float32).contiguous()
         out = torch.empty(self.out_channels, k_pad, dtype=dtype, device=w.device)
+        w_scale = None
+        if dtype == torch.float8_e4m3fn:
+            # per-output-channel scale amax|W[o, :]| / 448 (1 for an all-zero row), divided on
+            # the host: torch's device kernel divides by a scalar via its reciprocal
+            amax = src.abs().amax(1).cpu()
+            w_scale = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax)).to(w.device)
         lib = _lib.load()
         _lib.check(lib.fovi_knnconv_pack_weight(_lib.ptr(src), self.out_channels, self.in_channels, n_ref,
-                                                _lib.ptr(out), _lib.dtype_code(dtype), k_pad, c_slot, None,
-                                                _lib.stream_handle(w.device)),
+                                                _lib.ptr(out), _lib.dtype_code(dtype), k_pad, c_slot,
+                                                _lib.ptr(w_scale), _lib.stream_handle(w.device)),
                    "fovi_knnconv_pack_weight")
-        self._packed[(dtype, c_slot)] = (key, out)
-        return out
+        packed = out if w_scale is None else (out, w_scale)
+        self._packed[(dtype, c_slot)] = (key, packed)
+        return packed
 
     @property
     def padded_channels(self):
@@ -269,11 +285,68 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         _lib.check(lib.fovi_knnconv_fwd(a, _lib.stream_handle(x.device)), "fovi_knnconv_fwd")
         return y.transpose(1, 2)
 
+    # -- fp8 ----------------------------------------------------------------
+    @property
+    def fp8_headroom(self):
+        """Power of two >= the largest slot neighbour count: the activation scale
+        ``amax * headroom / 448`` keeps every slot sum of quantized values <= 448."""
+        return headroom_for(self._max_slot_count)
+
+    def quantize_input(self, x, scale=None):
+        """e4m3 activations for this layer (``Fp8Activations``; channels-last)."""
+        if isinstance(x, Fp8Activations):
+            return x
+        return quantize_e4m3(x, self.fp8_headroom, scale)
+
+    def _launch_fp8(self, xq, activation=None):
+        x, scale = xq.data, xq.scale
+        _lib.require_device(x, scale, self.weight)
+        if x.dtype != torch.float8_e4m3fn:
+            raise TypeError(f"Fp8Activations.data must be float8_e4m3fn, got {x.dtype}")
+        if x.dim() != 3 or x.shape[1] != self.in_channels or x.shape[2] != self.in_coords.shape[0]:
+            raise ValueError(f"KNNConvLayer: expected [B, {self.in_channels}, {self.in_coords.shape[0]}], "
+                             f"got {tuple(x.shape)}")
+        if self.tile_lo is None:
+            raise NotImplementedError("fp8 kNN-conv needs the tile tables (k <= 255, tile spans <= 65535)")
+        w, w_scale = self._packed_weight(torch.float8_e4m3fn)
+        bsz, n_out = x.shape[0], self.out_coords.shape[0]
+        y = torch.empty(bsz, n_out, self.out_channels, dtype=torch.bfloat16, device=x.device)
+        bias = None if self.bias is None else self.bias.detach().to(torch.float32).contiguous()
+        scale = scale.to(torch.float32).reshape(1).contiguous()
+        a = _lib.KnnConvArgs()
+        a.x = x.data_ptr(); a.x_dtype = _lib.F8E4M3
+        a.batch, a.c_in, a.n_in = bsz, self.in_channels, x.shape[2]
+        a.x_stride[:] = list(x.stride())
+        a.n_out, a.k, a.n_ref = n_out, self._k, self.ref_coords.shape[0]
+        a.slot_ptr = self.slot_ptr.data_ptr(); a.nbr_sorted = self.nbr_sorted.data_ptr()
+        a.w = w.data_ptr(); a.w_dtype = _lib.F8E4M3
+        a.c_out, a.k_pad = self.out_channels, w.shape[1]
+        a.bias = None if bias is None else bias.data_ptr()
+        a.w_scale = w_scale.data_ptr(); a.x_scale_dev = scale.data_ptr()
+        a.y = y.data_ptr(); a.y_dtype = _lib.BF16
+        a.y_stride[:] = [y.stride(0), y.stride(2), y.stride(1)]
+        if activation not in (None, "relu"):
+            raise ValueError(f"activation must be None or 'relu', got {activation!r}")
+        a.activation = _lib.ACT_RELU if activation == "relu" else _lib.ACT_NONE
+        a.w_c_slot = self.in_channels
+        a.tile_lo = self.tile_lo.data_ptr(); a.tile_span = self.tile_span.data_ptr()
+        a.tile_ent = self.tile_ent.data_ptr(); a.tile_nbr = self.tile_nbr.data_ptr()
+        a.tile_points = T.TILE_POINTS; a.max_span = self._max_span
+        a.tile_coll = self.tile_coll.data_ptr(); a.tile_coll_n = self.tile_coll_n.data_ptr()
+        a.zero_row = self._zero_row
+        lib = _lib.load()
+        _lib.check(lib.fovi_knnconv_fwd(a, _lib.stream_handle(x.device)), "fovi_knnconv_fwd(fp8)")
+        return y.transpose(1, 2)
+
     def forward(self, X_l):
+        if isinstance(X_l, Fp8Activations) or self.fp8:
+            return self._launch_fp8(self.quantize_input(X_l))
         return _KnnConvFn.apply(X_l, self, self.weight, self.bias)
 
     def forward_fused(self, X_l, activation="relu"):
         """``activation(forward(X_l))`` with the activation applied in the kernel's store."""
+        if isinstance(X_l, Fp8Activations) or self.fp8:
+            return self._launch_fp8(self.quantize_input(X_l), activation)
         return _KnnConvFn.apply(X_l, self, self.weight, self.bias, activation)
 
     # -- conv2d import (reference knn.py:649-715) -------------------------------

@@ -19,38 +19,9 @@
 //    gather issued into registers before the current chunk's MFMAs.
 //    VEC loader: channels-last rows and c_in % 64 == 0, one 16-byte load per
 //    (row, 8 channels). Generic loader: any strides / c_in, element gathers.
-#include "common.h"
+#include "knnconv_internal.h"
 
 namespace fovi {
-
-struct KnnParams {
-  const void* x;
-  int64_t B, C, Nin;
-  int64_t xs0, xs1, xs2;
-  int64_t Nout, K, V;
-  const int32_t* slot_ptr;
-  const int32_t* nbr;
-  const void* w;
-  int64_t Cout, Kpad;
-  const float* bias;
-  const float* w_scale;
-  float x_scale;
-  void* y;
-  int64_t ys0, ys1, ys2;
-  const int32_t* tile_lo;
-  const uint32_t* tile_ent;
-  const uint16_t* tile_nbr;
-  int max_span;
-  const uint8_t* tile_coll;
-  const int32_t* tile_coll_n;
-  int zero_row;
-  int relu;
-  int w_c_slot;
-};
-
-// Output transform: optional ReLU fused into the store (the activation that
-// follows the conv in the reference blocks when no norm sits between them).
-__device__ __forceinline__ float epilogue(float v, int relu) { return relu ? fmaxf(v, 0.0f) : v; }
 
 // ---------------------------------------------------------------------------
 // fp32 path
@@ -330,16 +301,6 @@ __global__ __launch_bounds__(256, 2) void knnconv_bf16_kernel(KnnParams p, int64
 // LDS rows are 64 bytes (four 16-byte chunks), XOR-swizzled per row (swz32)
 // so that fragment reads and tile writes are bank-conflict free.
 constexpr int V2_MT = 256;
-constexpr int V2_CC = 32;
-
-// XOR pattern g(r) = (bit1(r) ^ bit3(r)) | bit2(r) << 1 keeps any 8 consecutive
-// rows of one chunk in distinct 16-byte slots of a 128-byte window and any 16
-// consecutive rows in distinct slots of a 256-byte window, so 16-byte reads
-// are conflict-free whether the LDS serves 8 or 16 lanes per cycle.
-__device__ __forceinline__ int swz32(int r, int q) {
-  const int g = (((r >> 1) ^ (r >> 3)) & 1) | ((r >> 1) & 2);
-  return r * V2_CC + ((q ^ g) << 3);
-}
 
 size_t v2_lds_bytes(int nt, int64_t V, int64_t K) {
   return static_cast<size_t>(2 * V2_MT * V2_CC * 2 + 2 * nt * V2_CC * 2) +
@@ -509,20 +470,6 @@ static int launch_bf16_v2(const KnnParams& p, int out_t, hipStream_t s) {
   return 0;
 }
 
-// Channel-tile width: the widest candidate that divides c_out and fits the
-// LDS budget (no wasted MFMA columns); otherwise the widest that fits.
-template <typename Fits>
-static int pick_tile_n(int64_t cout, Fits fits) {
-  const int cands[4] = {256, 192, 128, 64};
-  for (int nt : cands)
-    if (cout % nt == 0 && fits(nt)) return nt;
-  for (int nt : cands) {
-    if (nt > 64 && cout <= nt / 2) continue;
-    if (fits(nt)) return nt;
-  }
-  return 0;
-}
-
 // Picks the widest channel tile whose LDS footprint fits; 0 if none does.
 static int v2_tile_n(const KnnParams& p) {
   const int cands[4] = {256, 192, 128, 64};
@@ -561,7 +508,6 @@ size_t v3_lds_bytes(int nt, int64_t V, int64_t K, int max_span) {
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ f32x8 unpack_bf16x8(u32x4 r) {
@@ -1510,32 +1456,6 @@ static void launch_bf16(const KnnParams& p, int out_t, hipStream_t s) {
 // ---------------------------------------------------------------------------
 // weight packing
 // ---------------------------------------------------------------------------
-// float -> OCP fp8 e4m3 (bias 7, max finite 448, no infinities), round to
-// nearest even, saturating to +-448; NaN -> 0x7f.
-__device__ __forceinline__ uint8_t f32_to_e4m3(float f) {
-  const uint32_t u = __float_as_uint(f);
-  const uint8_t sign = static_cast<uint8_t>((u >> 24) & 0x80u);
-  float a = fabsf(f);
-  if (!(a == a)) return 0x7f;
-  if (a >= 464.0f) return sign | 0x7e;  // rounds past the largest finite value
-  if (a < 0.0009765625f) {              // below 2^-10: rounds to zero or the smallest subnormal
-    if (a <= 0.0009765625f * 0.5f) return sign;
-    return sign | 0x01;
-  }
-  int e;
-  float m = frexpf(a, &e);              // a = m * 2^e, m in [0.5, 1)
-  int exp = e - 1 + 7;                  // biased exponent of 1.xxx form
-  if (exp <= 0) {                       // subnormal: value = mant * 2^-9
-    const float q = __builtin_rintf(a * 512.0f);
-    return sign | static_cast<uint8_t>(q);  // q == 8 rolls into the first normal
-  }
-  float frac = m * 2.0f - 1.0f;         // [0, 1)
-  float q = __builtin_rintf(frac * 8.0f);
-  if (q == 8.0f) { q = 0.0f; ++exp; }
-  if (exp > 15 || (exp == 15 && q > 6.0f)) return sign | 0x7e;
-  return sign | static_cast<uint8_t>((exp << 3) | static_cast<int>(q));
-}
-
 __global__ void pack_weight_kernel(const float* w_ref, int64_t c_out, int64_t c_in, int64_t n_ref,
                                    void* out, int dtype, int64_t k_pad, int64_t c_slot, const float* w_scale) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -1596,7 +1516,7 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
   p.xs0 = a->x_stride[0]; p.xs1 = a->x_stride[1]; p.xs2 = a->x_stride[2];
   p.Nout = a->n_out; p.K = a->k; p.V = a->n_ref; p.slot_ptr = a->slot_ptr; p.nbr = a->nbr_sorted;
   p.w = a->w; p.Cout = a->c_out; p.Kpad = a->k_pad; p.bias = a->bias; p.w_scale = a->w_scale;
-  p.x_scale = a->x_scale; p.y = a->y; p.ys0 = a->y_stride[0]; p.ys1 = a->y_stride[1]; p.ys2 = a->y_stride[2];
+  p.x_scale = a->x_scale; p.x_scale_dev = a->x_scale_dev; p.y = a->y; p.ys0 = a->y_stride[0]; p.ys1 = a->y_stride[1]; p.ys2 = a->y_stride[2];
   p.tile_lo = a->tile_lo; p.tile_ent = a->tile_ent; p.tile_nbr = a->tile_nbr; p.max_span = a->max_span;
   p.tile_coll = a->tile_coll; p.tile_coll_n = a->tile_coll_n; p.zero_row = a->zero_row;
   if (a->activation != FOVI_ACT_NONE && a->activation != FOVI_ACT_RELU) {
@@ -1625,6 +1545,10 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
     else
       hipLaunchKernelGGL((knnconv_f32_kernel<uint16_t>), grid, dim3(256), 0, s, p, tiles_per_b);
     return check_launch("fovi_knnconv_fwd(f32)");
+  }
+  if (a->x_dtype == FOVI_F8E4M3 && a->w_dtype == FOVI_F8E4M3) {
+    if (p.w_c_slot != p.C) { set_error("fovi_knnconv_fwd(fp8): w_c_slot must equal c_in"); return 1; }
+    return launch_knnconv_fp8(p, a->y_dtype, s);
   }
   if (a->x_dtype == FOVI_BF16 && a->w_dtype == FOVI_BF16 && p.w_c_slot != p.C) {
     // packed weight with padded slots: only the small-channel kernel reads it

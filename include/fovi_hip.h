@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 7
+#define FOVI_ABI_VERSION 8
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -97,6 +97,12 @@ int fovi_sampler_fwd(const fovi_sampler_args* args, void* stream);
  *
  * x_dtype/w_dtype: F32/F32 (fp32 parity path) or BF16/BF16 (MFMA path) or
  * F8E4M3/F8E4M3 (MFMA path; y = x_scale * w_scale[o] * sum(q_x * q_w) + bias).
+ * The fp8 path has no counterpart in the reference. It needs channels-last
+ * input rows (x_stride[1] == 1, 16-byte aligned), c_in % 64 == 0 and the tile
+ * tables. Each slot with two or more neighbours is summed in fp32 and rounded
+ * once more to e4m3 (round to nearest even) before the MFMA, so the activation
+ * scale must keep sums of up to max(count) quantized values below 448 (the
+ * headroom argument of fovi_quantize_e4m3).
  *
  * Optional tile tables (all NULL to leave them out) select the kernel that
  * copies each tile's input rows into LDS: output points are cut into tiles
@@ -151,6 +157,8 @@ typedef struct fovi_knnconv_args {
                                  >= batch * n_out * k_pad * 2 bytes the few-channel path runs
                                  in two passes (slot sums into it, then a dense GEMM) */
   int64_t workspace_bytes;
+  const float* x_scale_dev;   /* (F8E4M3 only) device copy of the activation scale, e.g. the one
+                                 fovi_quantize_e4m3 writes; used instead of x_scale when non-NULL */
 } fovi_knnconv_args;
 
 int fovi_knnconv_fwd(const fovi_knnconv_args* args, void* stream);
@@ -168,6 +176,40 @@ int fovi_knnconv_fwd(const fovi_knnconv_args* args, void* stream);
 int fovi_knnconv_pack_weight(const float* w_ref, int64_t c_out, int64_t c_in, int64_t n_ref,
                              void* w_packed, int32_t out_dtype, int64_t k_pad, int64_t c_slot,
                              const float* w_scale, void* stream);
+
+/*
+ * Per-tensor OCP e4m3 quantization of activations for the fp8 kNN-conv path
+ * (no counterpart in the reference, which has no fp8 path; callers are
+ * quantized inference pipelines feeding fovi_knnconv_fwd with F8E4M3 input).
+ *
+ *   amax  = max |x| over the [batch, channels, points] view
+ *   scale = amax * headroom / 448 in fp32 (1 when amax is 0)
+ *   q[b, c, n] = e4m3(x[b, c, n] / scale)   (fp32 division, round to nearest
+ *                                            even, saturating to +-448)
+ *
+ * headroom (>= 1, a power of two) leaves room below 448 for sums of up to
+ * `headroom` quantized values. scale_out[0] receives the scale (device
+ * memory). With scale_in non-NULL the amax pass is skipped and *scale_in (a
+ * calibrated device scale) is used; scale_out may then be NULL. amax_work is
+ * one float of caller device memory, overwritten. Strides are in elements of
+ * the [batch, channel, point] views of x and q.
+ */
+typedef struct fovi_quantize_args {
+  const void* x;
+  int32_t x_dtype;            /* F32 or BF16 */
+  int32_t reserved0;
+  int64_t batch, channels, points;
+  int64_t x_stride[3];
+  uint8_t* q;                 /* e4m3 bytes */
+  int64_t q_stride[3];
+  float headroom;
+  int32_t reserved1;
+  const float* scale_in;      /* optional */
+  float* scale_out;
+  float* amax_work;
+} fovi_quantize_args;
+
+int fovi_quantize_e4m3(const fovi_quantize_args* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -47,6 +47,15 @@ def test_argument_validation_without_gpu():
     assert lib.fovi_sampler_fwd(s, None) != 0
     assert b"null pointer" in lib.fovi_last_error()
     assert lib.fovi_knnconv_pack_weight(None, 1, 1, 1, None, 0, 64, 0, None, None) != 0
+    q = _lib.QuantizeArgs()
+    assert lib.fovi_quantize_e4m3(q, None) != 0
+    assert b"null argument" in lib.fovi_last_error()
+    q.x, q.q, q.x_dtype, q.headroom = 16, 16, _lib.BF16, 8.0
+    assert lib.fovi_quantize_e4m3(q, None) != 0           # no scale_in and no amax/scale buffers
+    assert b"amax_work" in lib.fovi_last_error()
+    q.scale_in, q.headroom = 16, 0.5
+    assert lib.fovi_quantize_e4m3(q, None) != 0
+    assert b"headroom" in lib.fovi_last_error()
 
 
 def _c_layout(struct, fields, tmp_path):
@@ -64,7 +73,8 @@ def _c_layout(struct, fields, tmp_path):
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
-@pytest.mark.parametrize("py,c", [(_lib.SamplerArgs, "fovi_sampler_args"), (_lib.KnnConvArgs, "fovi_knnconv_args")])
+@pytest.mark.parametrize("py,c", [(_lib.SamplerArgs, "fovi_sampler_args"), (_lib.KnnConvArgs, "fovi_knnconv_args"),
+                                  (_lib.QuantizeArgs, "fovi_quantize_args")])
 def test_struct_layout_matches_header(py, c, tmp_path):
     fields = [f for f, _ in py._fields_]
     size, offs = _c_layout(c, fields, tmp_path)

@@ -1,0 +1,146 @@
+"""GPU tests of the fp8 (OCP e4m3) path: quantizer, weight packing, kNN-conv.
+
+The reference has no fp8 path. Bars: quantized bytes and scales bit-exact
+against torch's float8_e4m3fn cast of ``x / scale`` (scale computed in fp32 as
+``amax * headroom / 448``); kNN-conv output (bf16) within 1e-2 relative and
+cosine >= 0.9999 of the fp8 oracle (dequantized operands, multi-neighbour
+slot sums re-rounded to e4m3), and cosine >= 0.995 of the unquantized fp32
+oracle, per layer.
+"""
+import pytest
+import torch
+
+from fovi_amd.arch.fp8 import quantize_e4m3
+from fovi_amd.arch.knn import KNNConvLayer
+from fovi_amd.sensing.coords import SamplingCoords
+from oracle import knnconv_ref
+from tests.helpers import assert_close_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def _cos(a, b):
+    a, b = a.double().flatten(), b.double().flatten()
+    return (a @ b / (a.norm() * b.norm())).item()
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("layout", ["channel_major", "channels_last", "strided"])
+@pytest.mark.parametrize("headroom", [1.0, 32.0])
+def test_quantize_matches_torch_cast(dt, layout, headroom):
+    g = torch.Generator().manual_seed(3)
+    x = (torch.randn(3, 64, 999, generator=g) * 3).to(dt)
+    x[0, 0, :8] = torch.tensor([0.0, -0.0, 1e-6, -1e-6, 2.0 ** -12, 5.0, -7.5, 0.3])
+    xd = x.cuda()
+    if layout == "channels_last":
+        xd = xd.transpose(1, 2).contiguous().transpose(1, 2)
+    elif layout == "strided":
+        xd = torch.zeros(3, 64, 2 * 999, dtype=dt, device="cuda")[:, :, ::2]
+        xd.copy_(x.cuda())
+    q = quantize_e4m3(xd, headroom)
+    xf = x.float()
+    s = xf.abs().amax() * headroom / 448.0
+    assert q.scale.cpu().view(torch.int32).item() == s.view(torch.int32).item()
+    want = (xf / s).to(torch.float8_e4m3fn)
+    assert q.data.shape == x.shape and q.data.stride(1) == 1
+    assert torch.equal(q.data.cpu().view(torch.uint8), want.view(torch.uint8))
+
+
+def test_quantize_given_scale_saturates_and_zero_tensor():
+    x = torch.tensor([[[0.0, 1.0, -1.0, 500.0, -1e4, 0.017]]]).cuda()
+    scale = torch.tensor([0.5], device="cuda")
+    q = quantize_e4m3(x, scale=scale)
+    want = (x.cpu() / 0.5).clamp(-448, 448).to(torch.float8_e4m3fn)
+    assert torch.equal(q.data.cpu().view(torch.uint8), want.view(torch.uint8))
+    z = quantize_e4m3(torch.zeros(2, 64, 10, device="cuda"), 8.0)
+    assert z.scale.item() == 1.0 and not z.data.cpu().view(torch.uint8).any()
+
+
+def _layer(res_in, res_out, k, c_in, c_out, bias=False, seed=1):
+    cin = SamplingCoords(16, 2.78, res_in, style="logpolar")
+    cout = SamplingCoords(16, 2.78, res_out, style="logpolar")
+    layer = KNNConvLayer(c_in, c_out, k, cin, cout, device="cuda", bias=bias)
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        layer.weight.copy_(torch.randn(layer.weight.shape, generator=g) * (1.0 / (c_in * layer._k)) ** 0.5)
+        if bias:
+            layer.bias.copy_(torch.randn(c_out, generator=g) * 0.1)
+    return layer
+
+
+def test_pack_weight_fp8_bytes():
+    layer = _layer(32, 16, 25, 64, 96, seed=2)
+    w_packed, w_scale = layer._packed_weight(torch.float8_e4m3fn)
+    w = layer.weight.detach().cpu()
+    s = w.abs().amax(1) / 448.0
+    assert torch.equal(w_scale.cpu(), s)
+    q = (w / s[:, None]).to(torch.float8_e4m3fn).view(torch.uint8)             # [C_out, C*V], index c*V+v
+    q = q.reshape(96, 64, 25).transpose(1, 2).reshape(96, -1)                  # slot-major v*C+c
+    got = w_packed.cpu().view(torch.uint8)
+    assert torch.equal(got[:, :q.shape[1]], q) and not got[:, q.shape[1]:].any()
+
+
+def _fp8_oracle(layer, xq, rows=None):
+    w_packed, w_scale = layer._packed_weight(torch.float8_e4m3fn)
+    wq = knnconv_ref.quantize_e4m3(layer.weight.detach().cpu(), w_scale.cpu()[:, None])
+    b = None if layer.bias is None else layer.bias.detach().cpu()
+    x = xq.data.float().cpu()
+    if rows is not None:
+        x = x[rows]
+    return knnconv_ref.knnconv_fp8_forward(x, xq.scale.item(), layer.knn_indices.cpu(), layer.in_coords.shape[0],
+                                           layer.local_rf.cpu(), wq, w_scale.cpu(), b)
+
+
+def _fp32_oracle(layer, x):
+    b = None if layer.bias is None else layer.bias.detach().cpu()
+    return knnconv_ref.knnconv_forward(x.float().cpu(), layer.knn_indices.cpu(), layer.in_coords.shape[0],
+                                       layer.local_rf.cpu(), layer.weight.detach().cpu(), b)
+
+
+@pytest.mark.parametrize("res_in,res_out,k,c_in,c_out,bias", [
+    (32, 16, 25, 64, 128, True),      # C2 layer-2 geometry, 64 channels
+    (16, 16, 9, 192, 384, False),     # C2 layer 3
+    (64, 64, 25, 128, 256, True),     # C3 neighbourhood, smaller lattice
+    (24, 12, 30, 64, 40, True),       # ragged: non-square k, partial channel tile
+])
+def test_fp8_knnconv_vs_oracles(res_in, res_out, k, c_in, c_out, bias):
+    layer = _layer(res_in, res_out, k, c_in, c_out, bias, seed=5)
+    x = torch.randn(2, c_in, res_in * res_in, generator=torch.Generator().manual_seed(6)).bfloat16()
+    xq = layer.quantize_input(x.cuda())
+    assert xq.scale.item() == pytest.approx(x.float().abs().max().item() * layer.fp8_headroom / 448, rel=1e-6)
+    with torch.no_grad():
+        y = layer(xq)
+    assert y.dtype == torch.bfloat16 and y.shape == (2, c_out, res_out * res_out)
+    ref = _fp8_oracle(layer, xq)
+    assert_close_rel(y.float().cpu(), ref, 1e-2, "fp8 vs fp8 oracle")
+    assert _cos(y.float().cpu(), ref) >= 0.9999
+    assert _cos(y.float().cpu(), _fp32_oracle(layer, x)) >= 0.995
+    with torch.no_grad():
+        layer.fp8 = True                                           # quantize inside forward
+        assert torch.equal(layer(x.cuda()), y)
+        assert torch.equal(layer.forward_fused(x.cuda(), "relu"), torch.relu(y))
+
+
+def test_fp8_c5_geometry_slice_and_batch_independence():
+    """C5: C3 tensors in e4m3 (16384 points, k=25, 256 -> 256). Oracle on batch row 0;
+    rows of a B=8 launch equal their B=1 launches bit for bit."""
+    layer = _layer(128, 128, 25, 256, 256, seed=11)
+    x = torch.randn(8, 256, 16384, generator=torch.Generator().manual_seed(0)).bfloat16()
+    xd = x.cuda().transpose(1, 2).contiguous().transpose(1, 2)
+    xq = layer.quantize_input(xd)
+    with torch.no_grad():
+        y = layer(xq)
+        for b in (0, 5):
+            yb = layer(type(xq)(xq.data[b:b + 1], xq.scale))
+            assert torch.equal(y[b:b + 1], yb), f"row {b} differs from its B=1 launch"
+    ref = _fp8_oracle(layer, xq, rows=slice(0, 1))
+    assert_close_rel(y[:1].float().cpu(), ref, 1e-2, "C5 row 0")
+    assert _cos(y[:1].float().cpu(), ref) >= 0.9999
+    assert _cos(y[:1].float().cpu(), _fp32_oracle(layer, x[:1])) >= 0.995
+
+
+def test_fp8_rejects_unsupported_shapes():
+    layer = _layer(16, 16, 9, 32, 64)
+    xq = quantize_e4m3(torch.randn(1, 32, 256, device="cuda"))
+    with pytest.raises(RuntimeError, match="multiple of 64"):
+        layer(xq)
