@@ -9,14 +9,21 @@ does, and has no CPU fallback.
 Pinning (what checks each function beyond retyping its formula):
   * sampler_ref.transform_sampling_grid: closed-form fixation mapping
     (centre -> pixel centre, window edge -> window edge), exact fp32 values
-    on power-of-two inputs; golden fixtures from the reference.
+    on power-of-two inputs.
   * sampler_ref.grid_sample_views: torch.nn.functional.grid_sample (library
     routine) and the textbook bilinear/nearest formulas on tiny images
     (sampler_ref.bilinear_numpy, brute force).
   * knnconv_ref.knnconv_forward: brute-force triple loop
     (knnconv_ref.knnconv_bruteforce) in float64, linearity, a one-hot
-    weight that selects a single (slot, channel); golden fixtures.
-  * geometry_ref: closed forms (point counts, ring radii, lattice
-    neighbourhoods) and golden fixtures written by the reference itself
-    (tests/golden/make_golden.py).
+    weight that selects a single (slot, channel).
+  * knnconv_ref.knnconv_fp8_forward / quantize_e4m3 (no reference
+    counterpart): exhaustive nearest-value search over the e4m3 grid
+    (e4m3_round_bruteforce), a closed form for constant inputs (slot sums =
+    neighbour counts, rounded to e4m3 above 16), equality with
+    knnconv_forward where every slot holds at most one neighbour.
+  * The host tables the oracle consumes (sensor coordinates, kNN indices,
+    ref slots; built by fovi_amd, not by this package) are pinned bit for bit
+    by vectors the reference itself wrote (tests/golden/tables.npz, from
+    tests/golden/make_golden.py), by closed forms (point counts, ring radii,
+    lattice neighbourhoods) and by brute-force argsort on small grids.
 """

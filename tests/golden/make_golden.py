@@ -1,0 +1,109 @@
+"""Writes tests/golden/tables.npz: sensor coordinates, neighbour indices and ref-slot
+assignments computed by the reference itself (nblauch/fovi, read from
+/root/reference), for the log-polar layer geometries of the benchmark configs.
+
+Run only in the build container, where the reference checkout exists:
+
+    python tests/golden/make_golden.py
+
+The reference is loaded by file path under a synthetic package name; the two
+modules it imports that are absent here and unused on this path (trimesh in
+fovi/sensing/manifold.py:3, skimage in fovi/utils/__init__.py:10) are replaced
+by empty stand-in modules, and fovi/__init__.py (training-stack imports) is
+bypassed. These vectors pin what no closed form does: the tie order of topk at
+the log-polar angle seam (fovi/arch/knn.py:137-146) and the argmin of
+near-equidistant ref slots (knn.py:637-642). The GPU box never runs this file.
+"""
+import hashlib
+import importlib.util
+import os
+import sys
+import types
+
+import numpy as np
+import torch
+
+REF = "/root/reference/fovi"
+OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tables.npz")
+
+# name -> (res_in, res_out, k, ref_frame_side_length); fov 16, cmf_a 2.78 (SURVEY configs)
+CONFIGS = {
+    "c1": (64, 64, 9, None),
+    "c2_l1": (64, 32, 49, None),
+    "c2_l2": (32, 16, 25, None),
+    "c2_l3": (16, 16, 9, None),
+    "ragged": (24, 12, 30, None),
+    "c4_patch": (128, 16, 256, 16),
+    "c3": (128, 128, 25, None),     # stored as digests plus the seam columns
+}
+FULL_LIMIT = 60_000                  # k * n_out above this: digest + seam subset only
+
+
+def _load(name, path, package):
+    spec = importlib.util.spec_from_file_location(name, path, submodule_search_locations=package)
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def load_reference():
+    for stub in ("trimesh", "skimage", "skimage.measure"):
+        sys.modules.setdefault(stub, types.ModuleType(stub))
+    sys.modules["skimage.measure"].EllipseModel = object
+    root = types.ModuleType("fovi_ref")
+    root.__path__ = []
+    sys.modules["fovi_ref"] = root
+    _load("fovi_ref.utils", os.path.join(REF, "utils", "__init__.py"), [os.path.join(REF, "utils")])
+    for pkg in ("sensing", "arch"):
+        m = types.ModuleType(f"fovi_ref.{pkg}")
+        m.__path__ = []
+        sys.modules[f"fovi_ref.{pkg}"] = m
+    _load("fovi_ref.sensing.manifold", os.path.join(REF, "sensing", "manifold.py"), None)
+    coords = _load("fovi_ref.sensing.coords", os.path.join(REF, "sensing", "coords.py"), None)
+    knn = _load("fovi_ref.arch.knn", os.path.join(REF, "arch", "knn.py"), None)
+    return coords, knn
+
+
+def digest(a):
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def main():
+    coords_mod, knn_mod = load_reference()
+    torch.manual_seed(0)
+    out = {"torch_version": np.array(torch.__version__)}
+    for name, (r_in, r_out, k, side) in CONFIGS.items():
+        cin = coords_mod.SamplingCoords(16, 2.78, r_in, device="cpu", style="logpolar")
+        cout = coords_mod.SamplingCoords(16, 2.78, r_out, device="cpu", style="logpolar")
+        layer = knn_mod.KNNConvLayer(1, 1, k, cin, cout, device="cpu", ref_frame_side_length=side)
+        idx = layer.knn_indices.numpy().astype(np.int32)                  # [k, n_out]
+        rf = layer.local_rf.numpy()                                       # [n_out, k, V] one-hot
+        assert np.all(rf.sum(2) == 1), "every neighbour has exactly one slot"
+        slots = rf.argmax(2).astype(np.uint8)                             # [n_out, k]
+        out[f"{name}__in_cartesian"] = cin.cartesian.numpy()
+        out[f"{name}__in_cortical"] = cin.cortical.numpy()
+        out[f"{name}__out_cortical"] = cout.cortical.numpy()
+        out[f"{name}__ref_coords"] = layer.ref_coords.numpy()
+        out[f"{name}__idx_sha256"] = np.array(digest(idx))
+        out[f"{name}__slots_sha256"] = np.array(digest(slots))
+        if cin.cartesian.shape[0] > 4096:        # large point sets: coordinates as digests
+            for key in ("in_cartesian", "in_cortical"):
+                out[f"{name}__{key}"] = np.array(digest(out[f"{name}__{key}"]))
+        if idx.size <= FULL_LIMIT:
+            out[f"{name}__idx"] = idx.astype(np.int16)
+            out[f"{name}__slots"] = slots
+        else:
+            ang = np.arange(r_out * r_out) % r_out
+            cols = np.flatnonzero((ang <= 1) | (ang >= r_out - 2))       # both sides of the angle seam
+            out[f"{name}__seam_cols"] = cols.astype(np.int32)
+            out[f"{name}__idx_seam"] = idx[:, cols].astype(np.int16)
+            out[f"{name}__slots_seam"] = slots[cols]
+            out[f"{name}__out_cortical"] = np.array(digest(out[f"{name}__out_cortical"]))
+        print(f"{name}: k={k} n_out={idx.shape[1]} V={rf.shape[2]}", flush=True)
+    np.savez_compressed(OUT, **out)
+    print(f"wrote {OUT} ({os.path.getsize(OUT) / 1024:.0f} KiB)")
+
+
+if __name__ == "__main__":
+    main()
