@@ -285,20 +285,37 @@ def main():
     ap.add_argument("--no-sampler", action="store_true")
     ap.add_argument("--no-e2e", action="store_true", help="skip the C2/C4 end-to-end legs")
     ap.add_argument("--no-fp8", action="store_true", help="skip the C5 fp8 leg")
+    ap.add_argument("--only", default="", help="comma list of legs to run (c3,c5,sampler,c2,c4,cpu); "
+                                                "for profiling runs, the JSON line then holds only those legs")
     args = ap.parse_args()
+    if args.only:
+        legs = set(args.only.split(","))
+        unknown = legs - {"c3", "c5", "sampler", "c2", "c4", "cpu"}
+        if unknown:
+            ap.error(f"unknown legs {sorted(unknown)}")
+        if legs & {"c5", "cpu"}:
+            legs.add("c3")
+        args.no_fp8 = "c5" not in legs
+        args.no_sampler = "sampler" not in legs
+        args.no_e2e = not (legs & {"c2", "c4"})
+        args.no_cpu_baseline = "cpu" not in legs
+    else:
+        legs = {"c3", "c5", "sampler", "c2", "c4", "cpu"}
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               f"(the forward shards over batch with no communication, see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
     import torch
     dev = torch.device("cuda:0")
-    c3 = bench_c3(args.steps, args.warmup, dev)
+    c3 = bench_c3(args.steps, args.warmup, dev) if "c3" in legs else None
     c5 = None if args.no_fp8 else bench_c5(c3, args.steps, args.warmup)
     c4 = None if args.no_sampler else bench_c4_sampler(args.steps, args.warmup, dev, "nearest")
     c4b = None if args.no_sampler else bench_c4_sampler(args.steps, args.warmup, dev, "bilinear")
-    c2 = None if args.no_e2e else bench_c2(args.steps, args.warmup, dev)
-    c4e = None if args.no_e2e else bench_c4_frontend(args.steps, args.warmup, dev)
+    c2 = None if args.no_e2e or "c2" not in legs else bench_c2(args.steps, args.warmup, dev)
+    c4e = None if args.no_e2e or "c4" not in legs else bench_c4_frontend(args.steps, args.warmup, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline_c3(c3)
+    if c3 is None:
+        c3 = {"tflops": float("nan"), "ms": float("nan")}
     line = {
         "metric": "kNN-conv fwd TFLOP/s + sampler GB/s (% of MI355X roofline); images/sec",
         "value": round(c3["tflops"], 2),

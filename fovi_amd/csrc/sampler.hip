@@ -37,10 +37,48 @@ struct SamplerParams {
   float* grid_out;
 };
 
-template <typename InT, typename OutT, int MODE, int PAD>
-__global__ __launch_bounds__(256) void sampler_kernel(SamplerParams p) {
-  const int64_t v = blockIdx.y;
-  const int64_t pt = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+// Two horizontally adjacent pixels (cx, cx + 1) of one row with one load.
+// Only used when 0 <= cx and the loaded words stay inside the row (checked
+// by the caller): bf16 reads the 4-byte-aligned words covering cx and cx + 1
+// (8 bytes at the even pixel at or below cx), fp32 reads the 8 bytes at cx.
+template <typename T> struct PixelPair;
+template <> struct PixelPair<uint16_t> {
+  typedef uint32_t u32x2a4 __attribute__((ext_vector_type(2), aligned(4)));
+  // row is 4-byte aligned (checked on the host); pairs need cx & ~1 + 4 <= W
+  static __device__ __forceinline__ bool fits(int64_t cx, int64_t W) { return cx >= 0 && (cx & ~int64_t(1)) + 4 <= W; }
+  static __device__ __forceinline__ void load(const uint16_t* row, int64_t cx, float& a, float& b) {
+    const u32x2a4 w = *reinterpret_cast<const u32x2a4*>(row + (cx & ~int64_t(1)));
+    const uint32_t lo = (cx & 1) ? (w[0] >> 16) | (w[1] << 16) : w[0];
+    a = __uint_as_float(lo << 16);
+    b = __uint_as_float(lo & 0xffff0000u);
+  }
+};
+template <> struct PixelPair<float> {
+  typedef float f32x2a4 __attribute__((ext_vector_type(2), aligned(4)));
+  static __device__ __forceinline__ bool fits(int64_t cx, int64_t W) { return cx >= 0 && cx + 1 < W; }
+  static __device__ __forceinline__ void load(const float* row, int64_t cx, float& a, float& b) {
+    const f32x2a4 w = *reinterpret_cast<const f32x2a4*>(row + cx);
+    a = w[0];
+    b = w[1];
+  }
+};
+
+// One thread per (view, sensor point). Blocks are numbered view-major
+// (blocks_per_view blocks of 256 points per view) and mapped XCD-aware: each
+// of the 8 XCDs takes one contiguous range of views, so the views of one
+// image (adjacent when views are ordered image by image, as the fused
+// fixation loop orders them) are sampled by one XCD and share its L2: at
+// 128-byte line granularity the fixation views of an image together touch
+// most of the image, which is then fetched from HBM about once.
+// PAIRS: image rows are unit-stride and 4-byte aligned, so the two pixels of
+// a bilinear row are fetched with one load.
+template <typename InT, typename OutT, int MODE, int PAD, bool PAIRS>
+__global__ __launch_bounds__(256) void sampler_kernel(SamplerParams p, int64_t blocks_per_view, int64_t total_blocks,
+                                                      int64_t padded_blocks) {
+  const int64_t lb = xcd_tile(blockIdx.x, padded_blocks);
+  if (lb >= total_blocks) return;
+  const int64_t v = lb / blocks_per_view;
+  const int64_t pt = (lb - v * blocks_per_view) * 256 + threadIdx.x;
   if (pt >= p.N) return;
 
   const float W = static_cast<float>(p.W);
@@ -105,6 +143,20 @@ __global__ __launch_bounds__(256) void sampler_kernel(SamplerParams p) {
   const bool x0 = fx >= 0.0f && fx < W, x1 = fx + 1.0f >= 0.0f && fx + 1.0f < W;
   const bool y0 = fy >= 0.0f && fy < H, y1 = fy + 1.0f >= 0.0f && fy + 1.0f < H;
   const int64_t cx = static_cast<int64_t>(fx), cy = static_cast<int64_t>(fy);
+  if (PAIRS && PixelPair<InT>::fits(cx, p.W)) {
+    // both columns inside the image; rows checked per row
+    const int64_t o_n = y0 ? cy * p.is2 : 0;
+    const int64_t o_s = y1 ? (cy + 1) * p.is2 : 0;
+    for (int64_t c = 0; c < p.C; ++c) {
+      const InT* s = src + c * p.is1;
+      float v_nw = 0.0f, v_ne = 0.0f, v_sw = 0.0f, v_se = 0.0f;
+      if (y0) PixelPair<InT>::load(s + o_n, cx, v_nw, v_ne);
+      if (y1) PixelPair<InT>::load(s + o_s, cx, v_sw, v_se);
+      const float val = __builtin_fmaf(v_se, w_se, __builtin_fmaf(v_sw, w_sw, __builtin_fmaf(v_ne, w_ne, v_nw * w_nw)));
+      Elem<OutT>::store(out + c * p.os1, val);
+    }
+    return;
+  }
   const bool b_nw = y0 && x0, b_ne = y0 && x1, b_sw = y1 && x0, b_se = y1 && x1;
   const int64_t o_nw = b_nw ? cy * p.is2 + cx * p.is3 : 0;
   const int64_t o_ne = b_ne ? cy * p.is2 + (cx + 1) * p.is3 : 0;
@@ -121,19 +173,29 @@ __global__ __launch_bounds__(256) void sampler_kernel(SamplerParams p) {
   }
 }
 
+template <typename InT, typename OutT, int MODE, int PAD>
+static void launch_mode(const SamplerParams& p, int64_t n_views, bool pairs, hipStream_t s) {
+  const int64_t bpv = (p.N + 255) / 256;
+  const int64_t total = bpv * n_views;
+  const int64_t padded = (total + 7) / 8 * 8;
+  dim3 grid(static_cast<unsigned>(padded));
+  if (MODE == FOVI_BILINEAR && pairs)
+    hipLaunchKernelGGL((sampler_kernel<InT, OutT, MODE, PAD, true>), grid, dim3(256), 0, s, p, bpv, total, padded);
+  else
+    hipLaunchKernelGGL((sampler_kernel<InT, OutT, MODE, PAD, false>), grid, dim3(256), 0, s, p, bpv, total, padded);
+}
+
 template <typename InT, typename OutT>
 static void launch_typed(const SamplerParams& p, int mode, int pad, int64_t n_views, hipStream_t s) {
-  dim3 grid(static_cast<unsigned>((p.N + 255) / 256), static_cast<unsigned>(n_views));
+  // pixel pairs need unit-stride rows whose starts are 4-byte aligned
+  const bool pairs = p.is3 == 1 && (reinterpret_cast<uintptr_t>(p.img) & 3) == 0 &&
+                     (sizeof(InT) == 4 || ((p.is0 | p.is1 | p.is2) & 1) == 0);
   if (mode == FOVI_NEAREST) {
-    if (pad == FOVI_PAD_ZEROS)
-      hipLaunchKernelGGL((sampler_kernel<InT, OutT, FOVI_NEAREST, FOVI_PAD_ZEROS>), grid, dim3(256), 0, s, p);
-    else
-      hipLaunchKernelGGL((sampler_kernel<InT, OutT, FOVI_NEAREST, FOVI_PAD_BORDER>), grid, dim3(256), 0, s, p);
+    if (pad == FOVI_PAD_ZEROS) launch_mode<InT, OutT, FOVI_NEAREST, FOVI_PAD_ZEROS>(p, n_views, pairs, s);
+    else launch_mode<InT, OutT, FOVI_NEAREST, FOVI_PAD_BORDER>(p, n_views, pairs, s);
   } else {
-    if (pad == FOVI_PAD_ZEROS)
-      hipLaunchKernelGGL((sampler_kernel<InT, OutT, FOVI_BILINEAR, FOVI_PAD_ZEROS>), grid, dim3(256), 0, s, p);
-    else
-      hipLaunchKernelGGL((sampler_kernel<InT, OutT, FOVI_BILINEAR, FOVI_PAD_BORDER>), grid, dim3(256), 0, s, p);
+    if (pad == FOVI_PAD_ZEROS) launch_mode<InT, OutT, FOVI_BILINEAR, FOVI_PAD_ZEROS>(p, n_views, pairs, s);
+    else launch_mode<InT, OutT, FOVI_BILINEAR, FOVI_PAD_BORDER>(p, n_views, pairs, s);
   }
 }
 
@@ -153,7 +215,11 @@ extern "C" int fovi_sampler_fwd(const fovi_sampler_args* a, void* stream) {
               (long long)a->n_points, (long long)a->n_views);
     return 1;
   }
-  if (a->n_views > 65535) { set_error("fovi_sampler_fwd: n_views %lld > 65535", (long long)a->n_views); return 1; }
+  if ((a->n_points + 255) / 256 * a->n_views > (int64_t(1) << 31) - 8) {
+    set_error("fovi_sampler_fwd: %lld views x %lld points exceed one launch", (long long)a->n_views,
+              (long long)a->n_points);
+    return 1;
+  }
   if (!a->view_image && a->n_views > a->n_img) {
     set_error("fovi_sampler_fwd: %lld views but %lld images and no view_image map",
               (long long)a->n_views, (long long)a->n_img);
