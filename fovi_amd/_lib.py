@@ -14,7 +14,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 F32, BF16, F8E4M3 = 0, 1, 2
 NEAREST, BILINEAR = 0, 1
 PAD_ZEROS, PAD_BORDER = 0, 1
@@ -34,7 +34,7 @@ class SamplerArgs(C.Structure):
         ("img_stride", C.c_int64 * 4),
         ("grid", C.c_void_p), ("n_points", C.c_int64), ("n_views", C.c_int64),
         ("fix_loc", C.c_void_p), ("fix_half", C.c_void_p),
-        ("fix_half_wide", C.c_int32), ("reserved1", C.c_int32),
+        ("fix_half_wide", C.c_int32), ("ring_len", C.c_int32),
         ("view_image", C.c_void_p),
         ("mode", C.c_int32), ("padding", C.c_int32),
         ("out", C.c_void_p), ("out_dtype", C.c_int32), ("reserved2", C.c_int32),

@@ -35,6 +35,7 @@ struct SamplerParams {
   void* out;
   int64_t os0, os1, os2;
   float* grid_out;
+  int64_t ring_len;
 };
 
 // Two horizontally adjacent pixels (cx, cx + 1) of one row with one load.
@@ -45,9 +46,11 @@ template <typename T> struct PixelPair;
 template <> struct PixelPair<uint16_t> {
   typedef uint32_t u32x2a4 __attribute__((ext_vector_type(2), aligned(4)));
   // row is 4-byte aligned (checked on the host); pairs need cx & ~1 + 4 <= W
-  static __device__ __forceinline__ bool fits(int64_t cx, int64_t W) { return cx >= 0 && (cx & ~int64_t(1)) + 4 <= W; }
-  static __device__ __forceinline__ void load(const uint16_t* row, int64_t cx, float& a, float& b) {
-    const u32x2a4 w = *reinterpret_cast<const u32x2a4*>(row + (cx & ~int64_t(1)));
+  template <typename Off>
+  static __device__ __forceinline__ bool fits(Off cx, Off W) { return cx >= 0 && (cx & ~Off(1)) + 4 <= W; }
+  template <typename Off>
+  static __device__ __forceinline__ void load(const uint16_t* row, Off cx, float& a, float& b) {
+    const u32x2a4 w = *reinterpret_cast<const u32x2a4*>(row + (cx & ~Off(1)));
     const uint32_t lo = (cx & 1) ? (w[0] >> 16) | (w[1] << 16) : w[0];
     a = __uint_as_float(lo << 16);
     b = __uint_as_float(lo & 0xffff0000u);
@@ -55,20 +58,113 @@ template <> struct PixelPair<uint16_t> {
 };
 template <> struct PixelPair<float> {
   typedef float f32x2a4 __attribute__((ext_vector_type(2), aligned(4)));
-  static __device__ __forceinline__ bool fits(int64_t cx, int64_t W) { return cx >= 0 && cx + 1 < W; }
-  static __device__ __forceinline__ void load(const float* row, int64_t cx, float& a, float& b) {
+  template <typename Off>
+  static __device__ __forceinline__ bool fits(Off cx, Off W) { return cx >= 0 && cx + 1 < W; }
+  template <typename Off>
+  static __device__ __forceinline__ void load(const float* row, Off cx, float& a, float& b) {
     const f32x2a4 w = *reinterpret_cast<const f32x2a4*>(row + cx);
     a = w[0];
     b = w[1];
   }
 };
 
-// One thread per (view, sensor point). Blocks are numbered view-major
-// (blocks_per_view blocks of 256 points per view) and mapped XCD-aware: each
-// of the 8 XCDs takes one contiguous range of views, so the views of one
-// image (adjacent when views are ordered image by image, as the fused
-// fixation loop orders them) are sampled by one XCD and share its L2: at
-// 128-byte line granularity the fixation views of an image together touch
+// Sampling set-up of one (view, sensor point): fixation transform, tap
+// coordinates and weights; value() then samples one channel plane.
+template <typename InT, int MODE, int PAD, bool PAIRS, typename Off = int64_t>
+struct Taps {
+  bool inb, y0, y1, pair;
+  bool b_nw, b_ne, b_sw, b_se;
+  Off off, o_nw, o_ne, o_sw, o_se;
+  Off cx;
+  float w_nw, w_ne, w_sw, w_se;
+
+  __device__ __forceinline__ Taps(const SamplerParams& p, int64_t v, int64_t pt) {
+    // (v, pt) index the small per-view / per-point tables
+    const float W = static_cast<float>(p.W);
+    const float H = static_cast<float>(p.H);
+    const float g0 = p.grid[2 * pt];
+    const float g1 = p.grid[2 * pt + 1];
+    const double half_h = p.fix_half[2 * v];
+    const double half_w = p.fix_half[2 * v + 1];
+    float x, y;
+    if (p.wide) {
+      x = static_cast<float>(static_cast<double>(g0) * half_w);
+      y = static_cast<float>(static_cast<double>(g1) * half_h);
+    } else {
+      x = g0 * static_cast<float>(half_w);
+      y = g1 * static_cast<float>(half_h);
+    }
+    const float centre_h = p.fix_loc[2 * v] * H;
+    const float centre_w = p.fix_loc[2 * v + 1] * W;
+    x = x + centre_w;
+    y = y + centre_h;
+    const float gx = (2.0f * x) / W - 1.0f;
+    const float gy = (2.0f * y) / H - 1.0f;
+    if (p.grid_out) {
+      p.grid_out[(v * p.N + pt) * 2] = gx;
+      p.grid_out[(v * p.N + pt) * 2 + 1] = gy;
+    }
+    float ix = __builtin_fmaf(gx + 1.0f, W * 0.5f, -0.5f);
+    float iy = __builtin_fmaf(gy + 1.0f, H * 0.5f, -0.5f);
+    if (PAD == FOVI_PAD_BORDER) {
+      ix = fminf(fmaxf(ix, 0.0f), W - 1.0f);
+      iy = fminf(fmaxf(iy, 0.0f), H - 1.0f);
+    }
+    if (MODE == FOVI_NEAREST) {
+      const float rx = __builtin_rintf(ix);
+      const float ry = __builtin_rintf(iy);
+      inb = rx >= 0.0f && rx < W && ry >= 0.0f && ry < H;
+      off = inb ? static_cast<Off>(ry) * static_cast<Off>(p.is2) + static_cast<Off>(rx) * static_cast<Off>(p.is3) : 0;
+      return;
+    }
+    const float fx = floorf(ix);
+    const float fy = floorf(iy);
+    const float we = ix - fx;          // weight of the east column
+    const float ww = 1.0f - we;
+    const float ws = iy - fy;          // weight of the south row
+    const float wn = 1.0f - ws;
+    w_nw = wn * ww; w_ne = wn * we; w_sw = ws * ww; w_se = ws * we;
+    const bool x0 = fx >= 0.0f && fx < W, x1 = fx + 1.0f >= 0.0f && fx + 1.0f < W;
+    y0 = fy >= 0.0f && fy < H;
+    y1 = fy + 1.0f >= 0.0f && fy + 1.0f < H;
+    cx = static_cast<Off>(fx);
+    const Off cy = static_cast<Off>(fy);
+    const Off is2 = static_cast<Off>(p.is2), is3 = static_cast<Off>(p.is3);
+    pair = PAIRS && PixelPair<InT>::fits(cx, static_cast<Off>(p.W));
+    if (pair) {  // both columns inside the image; rows checked per row
+      o_nw = y0 ? cy * is2 : 0;
+      o_sw = y1 ? (cy + 1) * is2 : 0;
+      return;
+    }
+    b_nw = y0 && x0; b_ne = y0 && x1; b_sw = y1 && x0; b_se = y1 && x1;
+    o_nw = b_nw ? cy * is2 + cx * is3 : 0;
+    o_ne = b_ne ? cy * is2 + (cx + 1) * is3 : 0;
+    o_sw = b_sw ? (cy + 1) * is2 + cx * is3 : 0;
+    o_se = b_se ? (cy + 1) * is2 + (cx + 1) * is3 : 0;
+  }
+
+  __device__ __forceinline__ float value(const InT* s) const {
+    if (MODE == FOVI_NEAREST) return inb ? Elem<InT>::load(s + off) : 0.0f;
+    float v_nw = 0.0f, v_ne = 0.0f, v_sw = 0.0f, v_se = 0.0f;
+    if (pair) {
+      if (y0) PixelPair<InT>::load(s + o_nw, cx, v_nw, v_ne);
+      if (y1) PixelPair<InT>::load(s + o_sw, cx, v_sw, v_se);
+    } else {
+      v_nw = b_nw ? Elem<InT>::load(s + o_nw) : 0.0f;
+      v_ne = b_ne ? Elem<InT>::load(s + o_ne) : 0.0f;
+      v_sw = b_sw ? Elem<InT>::load(s + o_sw) : 0.0f;
+      v_se = b_se ? Elem<InT>::load(s + o_se) : 0.0f;
+    }
+    return __builtin_fmaf(v_se, w_se, __builtin_fmaf(v_sw, w_sw, __builtin_fmaf(v_ne, w_ne, v_nw * w_nw)));
+  }
+};
+
+// Linear path: one thread per (view, sensor point). Blocks are numbered
+// view-major (blocks_per_view blocks of 256 points per view) and mapped
+// XCD-aware: each of the 8 XCDs takes one contiguous range of views, so the
+// views of one image (adjacent when views are ordered image by image, as the
+// fused fixation loop orders them) are sampled by one XCD and share its L2:
+// at 128-byte line granularity the fixation views of an image together touch
 // most of the image, which is then fetched from HBM about once.
 // PAIRS: image rows are unit-stride and 4-byte aligned, so the two pixels of
 // a bilinear row are fetched with one load.
@@ -80,32 +176,7 @@ __global__ __launch_bounds__(256) void sampler_kernel(SamplerParams p, int64_t b
   const int64_t v = lb / blocks_per_view;
   const int64_t pt = (lb - v * blocks_per_view) * 256 + threadIdx.x;
   if (pt >= p.N) return;
-
-  const float W = static_cast<float>(p.W);
-  const float H = static_cast<float>(p.H);
-  const float g0 = p.grid[2 * pt];
-  const float g1 = p.grid[2 * pt + 1];
-  const double half_h = p.fix_half[2 * v];
-  const double half_w = p.fix_half[2 * v + 1];
-  float x, y;
-  if (p.wide) {
-    x = static_cast<float>(static_cast<double>(g0) * half_w);
-    y = static_cast<float>(static_cast<double>(g1) * half_h);
-  } else {
-    x = g0 * static_cast<float>(half_w);
-    y = g1 * static_cast<float>(half_h);
-  }
-  const float centre_h = p.fix_loc[2 * v] * H;
-  const float centre_w = p.fix_loc[2 * v + 1] * W;
-  x = x + centre_w;
-  y = y + centre_h;
-  const float gx = (2.0f * x) / W - 1.0f;
-  const float gy = (2.0f * y) / H - 1.0f;
-  if (p.grid_out) {
-    p.grid_out[(v * p.N + pt) * 2] = gx;
-    p.grid_out[(v * p.N + pt) * 2 + 1] = gy;
-  }
-
+  const Taps<InT, MODE, PAD, PAIRS> t(p, v, pt);
   OutT* out = static_cast<OutT*>(p.out) + v * p.os0 + pt * p.os2;
   const int64_t img = p.view_image ? static_cast<int64_t>(p.view_image[v]) : v;
   if (img < 0 || img >= p.n_img) {
@@ -113,64 +184,85 @@ __global__ __launch_bounds__(256) void sampler_kernel(SamplerParams p, int64_t b
     return;
   }
   const InT* src = static_cast<const InT*>(p.img) + img * p.is0;
+  for (int64_t c = 0; c < p.C; ++c) Elem<OutT>::store(out + c * p.os1, t.value(src + c * p.is1));
+}
 
-  float ix = __builtin_fmaf(gx + 1.0f, W * 0.5f, -0.5f);
-  float iy = __builtin_fmaf(gy + 1.0f, H * 0.5f, -0.5f);
-  if (PAD == FOVI_PAD_BORDER) {
-    ix = fminf(fmaxf(ix, 0.0f), W - 1.0f);
-    iy = fminf(fmaxf(iy, 0.0f), H - 1.0f);
+// Blocked path for grids of whole rings (point = ring * ring_len + angle,
+// ring_len % 32 == 0, rings % 8 == 0) and at most 4 channels (NC, or 0 for a
+// run-time count <= 4). A block takes 8 rings x 32 angles of one view, each
+// wave 8 rings x 8 angles: on the log-polar sensor these points are
+// neighbours in the image, so the lanes of one gather share cache lines
+// (about 1.75x fewer distinct lines per load than a wave along one ring). The
+// block's samples are staged in LDS and written back along the rings (64-byte
+// runs per channel plane). The grid is only a processing order: every point
+// of the view is sampled exactly once whatever the geometry, so results do
+// not depend on it. Block indices and in-image / in-view offsets are 32-bit
+// (the host checks the extents).
+template <typename InT, typename OutT, int MODE, int PAD, bool PAIRS, int NC>
+__global__ __launch_bounds__(256) void sampler_rings_kernel(SamplerParams p, uint32_t blocks_per_view,
+                                                            uint32_t total_blocks, uint32_t padded_blocks) {
+  __shared__ float st[4][256];
+  const uint32_t per = padded_blocks >> 3;
+  const uint32_t lb = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  if (lb >= total_blocks) return;
+  const uint32_t v = lb / blocks_per_view;
+  const uint32_t b = lb - v * blocks_per_view;
+  const uint32_t ring_len = static_cast<uint32_t>(p.ring_len);
+  const uint32_t segs = ring_len >> 5;              // 32-angle segments per ring
+  const uint32_t band = b / segs;
+  const uint32_t ring0 = band * 8, ang0 = (b - band * segs) * 32;
+  const int tid = threadIdx.x;
+  const uint32_t r_in = (tid & 63) >> 3, a_in = (tid >> 6) * 8 + (tid & 7);
+  const uint32_t pt = (ring0 + r_in) * ring_len + ang0 + a_in;
+  const int C = NC > 0 ? NC : static_cast<int>(p.C);
+  const int64_t img = p.view_image ? static_cast<int64_t>(p.view_image[v]) : static_cast<int64_t>(v);
+  const Taps<InT, MODE, PAD, PAIRS, int32_t> t(p, v, pt);
+  float val[4];
+  if (img >= 0 && img < p.n_img) {
+    const InT* src = static_cast<const InT*>(p.img) + img * p.is0;
+    const int32_t is1 = static_cast<int32_t>(p.is1);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) val[c] = c < C ? t.value(src + c * is1) : 0.0f;
+  } else {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) val[c] = 0.0f;
   }
+  const int li = r_in * 32 + a_in;
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    if (c < C) st[c][li] = val[c];
+  __syncthreads();
+  const uint32_t pw = (ring0 + (tid >> 5)) * ring_len + ang0 + (tid & 31);
+  OutT* out = static_cast<OutT*>(p.out) + static_cast<int64_t>(v) * p.os0;
+  const int32_t o = static_cast<int32_t>(pw) * static_cast<int32_t>(p.os2);
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    if (c < C) Elem<OutT>::store(out + o + c * static_cast<int32_t>(p.os1), st[c][tid]);
+}
 
-  if (MODE == FOVI_NEAREST) {
-    const float rx = __builtin_rintf(ix);
-    const float ry = __builtin_rintf(iy);
-    const bool inb = rx >= 0.0f && rx < W && ry >= 0.0f && ry < H;
-    const int64_t off = inb ? static_cast<int64_t>(ry) * p.is2 + static_cast<int64_t>(rx) * p.is3 : 0;
-    for (int64_t c = 0; c < p.C; ++c) {
-      const float val = inb ? Elem<InT>::load(src + c * p.is1 + off) : 0.0f;
-      Elem<OutT>::store(out + c * p.os1, val);
-    }
-    return;
-  }
+// Whether the blocked path applies (see sampler_rings_kernel).
+static bool rings_path(const SamplerParams& p, int64_t n_views) {
+  if (!(p.ring_len > 0 && p.ring_len % 32 == 0 && p.N % (8 * p.ring_len) == 0 && p.C <= 4)) return false;
+  // 32-bit block ids, in-image tap offsets and in-view output offsets
+  const int64_t lim = (int64_t(1) << 31) - 1;
+  if (p.is1 < 0 || p.is2 < 0 || p.is3 < 0 || p.os1 < 0 || p.os2 < 0) return false;
+  const int64_t img_ext = (p.C - 1) * p.is1 + (p.H + 1) * p.is2 + (p.W + 1) * p.is3;
+  const int64_t out_ext = (p.C - 1) * p.os1 + p.N * p.os2;
+  return img_ext < lim && out_ext < lim && (p.N / 256) * n_views + 8 < lim;
+}
 
-  const float fx = floorf(ix);
-  const float fy = floorf(iy);
-  const float we = ix - fx;          // weight of the east column
-  const float ww = 1.0f - we;
-  const float ws = iy - fy;          // weight of the south row
-  const float wn = 1.0f - ws;
-  const float w_nw = wn * ww, w_ne = wn * we, w_sw = ws * ww, w_se = ws * we;
-  const bool x0 = fx >= 0.0f && fx < W, x1 = fx + 1.0f >= 0.0f && fx + 1.0f < W;
-  const bool y0 = fy >= 0.0f && fy < H, y1 = fy + 1.0f >= 0.0f && fy + 1.0f < H;
-  const int64_t cx = static_cast<int64_t>(fx), cy = static_cast<int64_t>(fy);
-  if (PAIRS && PixelPair<InT>::fits(cx, p.W)) {
-    // both columns inside the image; rows checked per row
-    const int64_t o_n = y0 ? cy * p.is2 : 0;
-    const int64_t o_s = y1 ? (cy + 1) * p.is2 : 0;
-    for (int64_t c = 0; c < p.C; ++c) {
-      const InT* s = src + c * p.is1;
-      float v_nw = 0.0f, v_ne = 0.0f, v_sw = 0.0f, v_se = 0.0f;
-      if (y0) PixelPair<InT>::load(s + o_n, cx, v_nw, v_ne);
-      if (y1) PixelPair<InT>::load(s + o_s, cx, v_sw, v_se);
-      const float val = __builtin_fmaf(v_se, w_se, __builtin_fmaf(v_sw, w_sw, __builtin_fmaf(v_ne, w_ne, v_nw * w_nw)));
-      Elem<OutT>::store(out + c * p.os1, val);
-    }
-    return;
-  }
-  const bool b_nw = y0 && x0, b_ne = y0 && x1, b_sw = y1 && x0, b_se = y1 && x1;
-  const int64_t o_nw = b_nw ? cy * p.is2 + cx * p.is3 : 0;
-  const int64_t o_ne = b_ne ? cy * p.is2 + (cx + 1) * p.is3 : 0;
-  const int64_t o_sw = b_sw ? (cy + 1) * p.is2 + cx * p.is3 : 0;
-  const int64_t o_se = b_se ? (cy + 1) * p.is2 + (cx + 1) * p.is3 : 0;
-  for (int64_t c = 0; c < p.C; ++c) {
-    const InT* s = src + c * p.is1;
-    const float v_nw = b_nw ? Elem<InT>::load(s + o_nw) : 0.0f;
-    const float v_ne = b_ne ? Elem<InT>::load(s + o_ne) : 0.0f;
-    const float v_sw = b_sw ? Elem<InT>::load(s + o_sw) : 0.0f;
-    const float v_se = b_se ? Elem<InT>::load(s + o_se) : 0.0f;
-    const float val = __builtin_fmaf(v_se, w_se, __builtin_fmaf(v_sw, w_sw, __builtin_fmaf(v_ne, w_ne, v_nw * w_nw)));
-    Elem<OutT>::store(out + c * p.os1, val);
-  }
+template <typename InT, typename OutT, int MODE, int PAD, bool PAIRS>
+static void launch_rings(const SamplerParams& p, uint32_t bpv, uint32_t total, uint32_t padded, hipStream_t s) {
+  dim3 grid(padded);
+  if (p.C == 3)
+    hipLaunchKernelGGL((sampler_rings_kernel<InT, OutT, MODE, PAD, PAIRS, 3>), grid, dim3(256), 0, s, p, bpv, total,
+                       padded);
+  else if (p.C == 1)
+    hipLaunchKernelGGL((sampler_rings_kernel<InT, OutT, MODE, PAD, PAIRS, 1>), grid, dim3(256), 0, s, p, bpv, total,
+                       padded);
+  else
+    hipLaunchKernelGGL((sampler_rings_kernel<InT, OutT, MODE, PAD, PAIRS, 0>), grid, dim3(256), 0, s, p, bpv, total,
+                       padded);
 }
 
 template <typename InT, typename OutT, int MODE, int PAD>
@@ -179,6 +271,15 @@ static void launch_mode(const SamplerParams& p, int64_t n_views, bool pairs, hip
   const int64_t total = bpv * n_views;
   const int64_t padded = (total + 7) / 8 * 8;
   dim3 grid(static_cast<unsigned>(padded));
+  if (rings_path(p, n_views)) {
+    if (MODE == FOVI_BILINEAR && pairs)
+      launch_rings<InT, OutT, MODE, PAD, true>(p, static_cast<uint32_t>(bpv), static_cast<uint32_t>(total),
+                                               static_cast<uint32_t>(padded), s);
+    else
+      launch_rings<InT, OutT, MODE, PAD, false>(p, static_cast<uint32_t>(bpv), static_cast<uint32_t>(total),
+                                                static_cast<uint32_t>(padded), s);
+    return;
+  }
   if (MODE == FOVI_BILINEAR && pairs)
     hipLaunchKernelGGL((sampler_kernel<InT, OutT, MODE, PAD, true>), grid, dim3(256), 0, s, p, bpv, total, padded);
   else
@@ -236,6 +337,7 @@ extern "C" int fovi_sampler_fwd(const fovi_sampler_args* a, void* stream) {
   p.grid = a->grid; p.N = a->n_points; p.fix_loc = a->fix_loc; p.fix_half = a->fix_half;
   p.wide = a->fix_half_wide ? 1 : 0; p.view_image = a->view_image; p.out = a->out;
   p.os0 = a->out_stride[0]; p.os1 = a->out_stride[1]; p.os2 = a->out_stride[2]; p.grid_out = a->grid_out;
+  p.ring_len = a->ring_len > 0 ? a->ring_len : 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int in_t = a->img_dtype, out_t = a->out_dtype;
   if (in_t == FOVI_F32 && out_t == FOVI_F32) launch_typed<float, float>(p, a->mode, a->padding, a->n_views, s);

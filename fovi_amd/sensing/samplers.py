@@ -77,6 +77,7 @@ class GridSampler(BaseGridSampler):
         self.fov = fov
         self.cmf_a = cmf_a
         self.resolution = resolution
+        self.ring_order = True
         self.device = device
         self.dtype = dtype
         self.mode = mode
@@ -155,6 +156,11 @@ class GridSampler(BaseGridSampler):
         a.out = out.data_ptr(); a.out_dtype = _lib.dtype_code(out.dtype)
         a.out_stride[:] = list(out.stride())
         a.grid_out = None if g_out is None else g_out.data_ptr()
+        # ring-major grids (index = ring * res + angle) are sampled in 8-ring x 32-angle blocks;
+        # the order changes no result (ring_order=False samples point by point)
+        res = getattr(self.coords, "resolution", 0)
+        res = int(res) if isinstance(res, (int, float)) else 0
+        a.ring_len = res if self.ring_order and res > 0 and res * res == n_pts else 0
         lib = _lib.load()
         _lib.check(lib.fovi_sampler_fwd(a, _lib.stream_handle(dev)), "fovi_sampler_fwd")
         return (out, g_out) if return_grid else out

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 8
+#define FOVI_ABI_VERSION 9
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -64,7 +64,9 @@ typedef struct fovi_sampler_args {
   const float* fix_loc;       /* [n_views, 2] (h, w) fixation centre in [0, 1] */
   const double* fix_half;     /* [n_views, 2] (h, w) half fixation size in pixels */
   int32_t fix_half_wide;      /* 0: half size is used as fp32; 1: fp64 multiply */
-  int32_t reserved1;
+  int32_t ring_len;           /* processing-order hint: points per ring when the grid is
+                                 ring-major (point = ring * ring_len + angle), else 0;
+                                 results do not depend on it */
   const int32_t* view_image;  /* [n_views] or NULL */
   int32_t mode;               /* fovi_interp */
   int32_t padding;            /* fovi_padding */

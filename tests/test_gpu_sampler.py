@@ -142,3 +142,32 @@ def test_full_size_c4_views_match_per_view_and_are_deterministic():
     ref, _ = sampler_ref.sampler_forward(img[vmap[5]:vmap[5] + 1].float().cpu(), s.sampling_grid.cpu(),
                                          fix[5:6], sizes[:1], mode="nearest")
     assert torch.equal(out[5:6].float().cpu(), ref)
+
+
+@pytest.mark.parametrize("mode", ["bilinear", "nearest"])
+@pytest.mark.parametrize("pad", ["zeros", "border"])
+@pytest.mark.parametrize("dt,channels", [(torch.float32, 3), (torch.bfloat16, 3), (torch.bfloat16, 1),
+                                         (torch.float32, 4)])
+def test_ring_blocked_order_equals_point_order(mode, pad, dt, channels):
+    """The 8-ring x 32-angle processing order of ring-major grids changes no result.
+
+    Fixations near the corners put part of the sensor outside the image, and
+    an odd image width sends some rows to the per-pixel bilinear loads.
+    """
+    g = torch.Generator().manual_seed(11)
+    img = torch.rand(3, channels, 150, 173, generator=g).to(dt).cuda()
+    fix = torch.tensor([[0.5, 0.5], [0.05, 0.95], [0.9, 0.1], [0.3, 0.7], [0.6, 0.4], [0.99, 0.99]])
+    sizes = np.array([[150, 173]] * 6)
+    vmap = torch.tensor([0, 0, 1, 1, 2, 2])
+    s = GridSampler(16, 2.78, 64, device="cuda", mode=mode, style="logpolar", padding_mode=pad)
+    blocked, g1 = s.sample_views(img, fix, sizes, view_image=vmap, return_grid=True)
+    out_cl = torch.empty(6, 4096, channels, device="cuda", dtype=dt).transpose(1, 2)
+    s.sample_views(img, fix, sizes, view_image=vmap, out=out_cl)
+    s.ring_order = False
+    linear, g2 = s.sample_views(img, fix, sizes, view_image=vmap, return_grid=True)
+    assert torch.equal(g1, g2)
+    assert torch.equal(blocked, linear)
+    assert torch.equal(out_cl, linear)
+    ref, _ = sampler_ref.sampler_forward(img[1:2].float().cpu(), s.sampling_grid.cpu(), fix[2:3], sizes[:1],
+                                         mode, pad)
+    assert_close_rel(blocked[2:3].float().cpu(), ref, 1e-5 if dt == torch.float32 else 1e-2)
