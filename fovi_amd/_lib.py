@@ -14,17 +14,19 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
 
-ABI_VERSION = 9
+ABI_VERSION = 11
 F32, BF16, F8E4M3 = 0, 1, 2
 NEAREST, BILINEAR = 0, 1
 PAD_ZEROS, PAD_BORDER = 0, 1
 ACT_NONE, ACT_RELU = 0, 1
+W_ROWS, W_MFMA = 0, 1
 
 _DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float8_e4m3fn: F8E4M3}
 
 # Every symbol include/fovi_hip.h declares.
 EXPORTED = ("fovi_abi_version", "fovi_last_error", "fovi_sampler_fwd", "fovi_knnconv_fwd",
-            "fovi_knnconv_pack_weight", "fovi_quantize_e4m3")
+            "fovi_knnconv_pack_weight", "fovi_knnconv_weight_mfma_elems", "fovi_knnconv_pack_weight_mfma",
+            "fovi_quantize_e4m3")
 
 
 class SamplerArgs(C.Structure):
@@ -50,7 +52,7 @@ class KnnConvArgs(C.Structure):
         ("x_stride", C.c_int64 * 3),
         ("n_out", C.c_int64), ("k", C.c_int64), ("n_ref", C.c_int64),
         ("slot_ptr", C.c_void_p), ("nbr_sorted", C.c_void_p),
-        ("w", C.c_void_p), ("w_dtype", C.c_int32), ("reserved1", C.c_int32),
+        ("w", C.c_void_p), ("w_dtype", C.c_int32), ("w_layout", C.c_int32),
         ("c_out", C.c_int64), ("k_pad", C.c_int64),
         ("bias", C.c_void_p), ("w_scale", C.c_void_p),
         ("x_scale", C.c_float), ("reserved2", C.c_int32),
@@ -64,6 +66,8 @@ class KnnConvArgs(C.Structure):
         ("w_c_slot", C.c_int32), ("reserved5", C.c_int32),
         ("workspace", C.c_void_p), ("workspace_bytes", C.c_int64),
         ("x_scale_dev", C.c_void_p),
+        ("tile_src", C.c_void_p), ("tile_coll_off", C.c_void_p), ("tile_coll4", C.c_void_p),
+        ("coll_off_stride", C.c_int32), ("coll4_stride", C.c_int32),
     ]
 
 
@@ -98,6 +102,11 @@ def load(path: str = LIB_PATH):
     lib.fovi_knnconv_pack_weight.argtypes = [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_void_p,
                                              C.c_int32, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p]
     lib.fovi_knnconv_pack_weight.restype = C.c_int
+    lib.fovi_knnconv_weight_mfma_elems.argtypes = [C.c_int64, C.c_int64, C.c_int64]
+    lib.fovi_knnconv_weight_mfma_elems.restype = C.c_int64
+    lib.fovi_knnconv_pack_weight_mfma.argtypes = [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_void_p,
+                                                  C.c_int32, C.c_void_p]
+    lib.fovi_knnconv_pack_weight_mfma.restype = C.c_int
     lib.fovi_quantize_e4m3.argtypes = [C.POINTER(QuantizeArgs), C.c_void_p]
     lib.fovi_quantize_e4m3.restype = C.c_int
     got = lib.fovi_abi_version()

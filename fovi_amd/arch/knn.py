@@ -135,6 +135,15 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         if tiles is not None:
             self._max_span = int(tiles[1].max())
             self._zero_row = tiles[6]
+        # tables of the wide-layer (fragment-order weight) kernel
+        wide = T.wide_tables(tiles, self._k) if tiles is not None else None
+        self._coll4_stride = 0
+        self._coll_off_stride = 0
+        for name, t in zip(("tile_src", "tile_coll4", "tile_coll_off"), wide[:3] if wide is not None else (None,) * 3):
+            self.register_buffer(name, None if t is None else t.to(device), persistent=False)
+        if wide is not None:
+            self._coll4_stride = wide[3]
+            self._coll_off_stride = int(wide[2].shape[1])
         self._packed = {}
         # slot-sum headroom of the fp8 path: the largest neighbour count of a slot
         self._max_slot_count = int((slot_ptr & 0xFFFF).max()) if slot_ptr.numel() else 1
@@ -143,6 +152,9 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         # few-channel bf16 layers: slot sums through a workspace, then a dense GEMM
         # (False: the single fused kernel, which needs no workspace)
         self.two_pass_few_channels = True
+        # wide bf16 layers (c_in % 32 == 0, c_out % 256 == 0): weights in MFMA-fragment order
+        # for the 256 x 256-tile kernel (False: the row-packed kernels)
+        self.mfma_weights = False
 
     # -- setup ---------------------------------------------------------------
     def _init_conv_like(self):
@@ -207,6 +219,44 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         self._packed[(dtype, c_slot)] = (key, packed)
         return packed
 
+    def _packed_weight_mfma(self):
+        """bf16 weight in MFMA-fragment order (``fovi_knnconv_pack_weight_mfma``), cached per version."""
+        w = self.weight
+        key = ("mfma", w._version, w.data_ptr())
+        hit = self._packed.get("mfma")
+        if hit is not None and hit[0] == key:
+            return hit[1]
+        n_ref = self.ref_coords.shape[0]
+        lib = _lib.load()
+        n = lib.fovi_knnconv_weight_mfma_elems(self.out_channels, self.in_channels, n_ref)
+        if n <= 0:
+            raise ValueError("fragment-order weights need in_channels % 32 == 0")
+        src = w.detach().to(torch.float32).contiguous()
+        out = torch.empty(n, dtype=torch.bfloat16, device=w.device)
+        _lib.check(lib.fovi_knnconv_pack_weight_mfma(_lib.ptr(src), self.out_channels, self.in_channels, n_ref,
+                                                     _lib.ptr(out), _lib.BF16, _lib.stream_handle(w.device)),
+                   "fovi_knnconv_pack_weight_mfma")
+        self._packed["mfma"] = (key, out)
+        return out
+
+    def _mfma_lds_bytes(self):
+        """LDS bytes of the fragment-order kernel's tile (its ``v5_layout``): two 256 x 32 bf16
+        collision tiles and a trash row, per-(slot, row) sources, per-slot entry offsets, packed
+        collision entries, neighbour lists, 128-byte alignment, then the staged rows plus the
+        zero row (64 bytes each)."""
+        v, k = self.ref_coords.shape[0], self._k
+        o = (2 * 256 + 1) * 32 * 2 + v * 256 * 2 + self._coll_off_stride * 4 + self._coll4_stride * 8 + 256 * k * 2
+        o = (o + 127) & ~127
+        return o + (self._zero_row + 1) * 64
+
+    def _mfma_path(self, x, dt):
+        """Whether this call runs the fragment-order kernel (see ``mfma_weights``)."""
+        return (self.mfma_weights and dt == torch.bfloat16 and self.in_channels % 32 == 0
+                and self._mfma_lds_bytes() <= 160 * 1024
+                and self.out_channels % 256 == 0 and self.tile_src is not None and 0 < self._zero_row <= 1023
+                and self._k <= 255 and x.stride(1) == 1 and x.stride(2) % 8 == 0 and x.stride(0) % 8 == 0
+                and x.data_ptr() % 16 == 0)
+
     @property
     def padded_channels(self):
         """Channels per input row the few-channel bf16 kernel reads (4 or 8), or None."""
@@ -251,7 +301,9 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
                 buf, view = self.padded_input(x.shape[0], x.device)
                 view.copy_(x)
                 x = view
-        w = self._packed_weight(dt, c_slot)
+        mfma = cp is None and self._mfma_path(x, dt)
+        self.last_weight_layout = "mfma" if mfma else "rows"
+        w = self._packed_weight_mfma() if mfma else self._packed_weight(dt, c_slot)
         bsz, n_out = x.shape[0], self.out_coords.shape[0]
         y = torch.empty(bsz, n_out, self.out_channels, dtype=dt, device=x.device)
         bias = None if self.bias is None else self.bias.detach().to(torch.float32).contiguous()
@@ -262,7 +314,9 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         a.n_out, a.k, a.n_ref = n_out, self._k, self.ref_coords.shape[0]
         a.slot_ptr = self.slot_ptr.data_ptr(); a.nbr_sorted = self.nbr_sorted.data_ptr()
         a.w = w.data_ptr(); a.w_dtype = _lib.dtype_code(dt)
-        a.c_out, a.k_pad = self.out_channels, w.shape[1]
+        a.w_layout = _lib.W_MFMA if mfma else _lib.W_ROWS
+        a.c_out = self.out_channels
+        a.k_pad = self.in_channels * self.ref_coords.shape[0] if mfma else w.shape[1]
         a.bias = None if bias is None else bias.data_ptr()
         a.y = y.data_ptr(); a.y_dtype = _lib.dtype_code(dt)
         a.y_stride[:] = [y.stride(0), y.stride(2), y.stride(1)]
@@ -281,6 +335,10 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
             a.tile_points = T.TILE_POINTS; a.max_span = self._max_span
             a.tile_coll = self.tile_coll.data_ptr(); a.tile_coll_n = self.tile_coll_n.data_ptr()
             a.zero_row = self._zero_row
+        if mfma:
+            a.tile_src = self.tile_src.data_ptr(); a.tile_coll_off = self.tile_coll_off.data_ptr()
+            a.tile_coll4 = self.tile_coll4.data_ptr()
+            a.coll_off_stride = self._coll_off_stride; a.coll4_stride = self._coll4_stride
         lib = _lib.load()
         _lib.check(lib.fovi_knnconv_fwd(a, _lib.stream_handle(x.device)), "fovi_knnconv_fwd")
         return y.transpose(1, 2)

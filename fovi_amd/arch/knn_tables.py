@@ -251,3 +251,60 @@ def direct_tables(knn_idx, slots, n_in, n_ref, tile=TILE_POINTS):
             coll_n[t, v] = len(rows)
     return (lo, span, torch.from_numpy(e.astype(np.uint32).view(np.int32)), nbr,
             torch.from_numpy(coll), torch.from_numpy(coll_n), zero_row)
+
+
+def wide_tables(direct, k):
+    """Tables of the wide-layer (fragment-order) kernel, derived from ``direct_tables``.
+
+    Laid out in the kernel's LDS order so that the kernel copies them with
+    16-byte loads:
+
+    * ``src [T, V, tile] uint16``: per (slot, row) the staged-row index the
+      MFMA lanes read for that slot (the neighbour's row when the slot holds
+      one neighbour, ``zero_row`` when it holds none) or, with bit 15 set,
+      the row's own collision sum (two or more neighbours);
+    * ``coll4 [T, stride] uint64``: one entry per (slot, collision row),
+      grouped by slot and within a slot by decreasing count: bits 0-7 row,
+      8-15 count, 16-23 begin (in the ``tile_nbr`` list of the row), then the
+      staged-row indices of the first four neighbours in 10-bit fields at
+      bits 24, 34, 44 and 54 (``zero_row`` past the count);
+    * ``coll_off [T, V + 1 rounded up to 4] int32``: slot v's entries are
+      ``coll4[t, coll_off[t, v]:coll_off[t, v + 1]]``.
+
+    Returns ``(src, coll4, coll_off, stride)`` or ``None`` when zero_row does
+    not fit 10 bits or k exceeds 255.
+    """
+    lo, span, ent, nbr, coll, coll_n, zero_row = direct
+    if zero_row > 1023 or k > 255:
+        return None
+    e = ent.numpy().view(np.uint32).astype(np.int64)          # [T*tile, V]
+    n_tiles, n_ref, tile = coll.shape
+    first = e >> 16
+    cnt = (e >> 8) & 0xFF
+    beg = e & 0xFF
+    src = np.where(cnt >= 2, 0x8000, first).astype(np.uint16)
+    src = src.reshape(n_tiles, tile, n_ref).transpose(0, 2, 1).copy()
+    nb = nbr.numpy().astype(np.int64).reshape(n_tiles, tile, k)
+    cn = coll_n.numpy().astype(np.int64)
+    counts = cn.sum(axis=1)
+    stride = int(max(2, -(-int(counts.max()) // 2) * 2)) if n_tiles else 2
+    voff = -(-(n_ref + 1) // 4) * 4
+    coll4 = np.zeros((n_tiles, stride), np.uint64)
+    coll_off = np.zeros((n_tiles, voff), np.int32)
+    cl = coll.numpy().astype(np.int64)
+    for t in range(n_tiles):
+        off = np.concatenate([[0], np.cumsum(cn[t])])
+        coll_off[t, :n_ref + 1] = off
+        if off[-1] == 0:
+            continue
+        rows = np.concatenate([cl[t, v, :cn[t, v]] for v in range(n_ref)])
+        slot = np.repeat(np.arange(n_ref), cn[t])
+        eb = e.reshape(n_tiles, tile, n_ref)[t, rows, slot]
+        c = (eb >> 8) & 0xFF
+        b = eb & 0xFF
+        word = rows | (c << 8) | (b << 16) | ((eb >> 16) << 24)
+        for j in range(1, 4):
+            r = np.where(j < c, nb[t, rows, np.minimum(b + j, k - 1)], zero_row)
+            word |= r << (24 + 10 * j)
+        coll4[t, :off[-1]] = word.astype(np.uint64)
+    return (torch.from_numpy(src), torch.from_numpy(coll4.view(np.int64)), torch.from_numpy(coll_off), stride)

@@ -505,25 +505,6 @@ size_t v3_lds_bytes(int nt, int64_t V, int64_t K, int max_span) {
          ((static_cast<size_t>(V3_MT) * static_cast<size_t>(K) + 7) & ~static_cast<size_t>(7)) * 2;
 }
 
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
-
-typedef float f32x8 __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ f32x8 unpack_bf16x8(u32x4 r) {
-  f32x8 f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f[2 * i] = __uint_as_float(r[i] << 16);
-    f[2 * i + 1] = __uint_as_float(r[i] & 0xffff0000u);
-  }
-  return f;
-}
-
-__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
-  const f32x2 v = {a, b};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2v));
-}
 
 template <int NT, int SV, typename OutT>
 __global__ __launch_bounds__(512, 1) void knnconv_bf16_v3_kernel(KnnParams p, int64_t tiles_per_b,
@@ -1505,7 +1486,7 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
     set_error("fovi_knnconv_fwd: bad sizes"); return 1;
   }
   if (a->k > 65535) { set_error("fovi_knnconv_fwd: k=%lld exceeds 65535", (long long)a->k); return 1; }
-  if (a->k_pad % MM_KC != 0) {
+  if (a->w_layout == FOVI_W_ROWS && a->k_pad % MM_KC != 0) {
     set_error("fovi_knnconv_fwd: k_pad=%lld must be a multiple of 64 >= c_in*n_ref=%lld",
               (long long)a->k_pad, (long long)(a->c_in * a->n_ref));
     return 1;
@@ -1523,6 +1504,9 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
     set_error("fovi_knnconv_fwd: bad activation %d", a->activation); return 1;
   }
   p.relu = a->activation == FOVI_ACT_RELU;
+  p.w_layout = a->w_layout;
+  p.tile_src = a->tile_src; p.tile_coll_off = a->tile_coll_off; p.tile_coll4 = a->tile_coll4;
+  p.coll_off_stride = a->coll_off_stride; p.coll4_stride = a->coll4_stride;
   p.w_c_slot = a->w_c_slot > 0 ? a->w_c_slot : static_cast<int>(a->c_in);
   if (p.w_c_slot < p.C || a->k_pad < p.w_c_slot * p.V) {
     set_error("fovi_knnconv_fwd: w_c_slot=%d must be >= c_in and k_pad >= w_c_slot * n_ref", p.w_c_slot);
@@ -1533,6 +1517,23 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
     return 1;
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
+
+  if (a->w_layout != FOVI_W_ROWS) {
+    if (a->w_layout != FOVI_W_MFMA || a->x_dtype != FOVI_BF16 || a->w_dtype != FOVI_BF16 || p.w_c_slot != p.C) {
+      set_error("fovi_knnconv_fwd: w_layout=%d needs BF16 input and weight", a->w_layout);
+      return 1;
+    }
+    if (!v5_applies(p)) {
+      set_error("fovi_knnconv_fwd: fragment-order weights need c_in %% 32 == 0, channels-last 16-byte input "
+                "rows, the tile tables with zero_row <= 1024 and k <= 255");
+      return 1;
+    }
+    if (launch_knnconv_bf16_v5(p, a->y_dtype, s) != 0) {
+      set_error("fovi_knnconv_fwd: tile span too large for the fragment-order kernel");
+      return 1;
+    }
+    return check_launch("fovi_knnconv_fwd(bf16 v5)");
+  }
 
   if (a->x_dtype == FOVI_F32 && a->w_dtype == FOVI_F32) {
     const int64_t tiles_per_b = (p.Nout + F32_TM - 1) / F32_TM;

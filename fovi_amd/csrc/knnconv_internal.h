@@ -31,7 +31,34 @@ struct KnnParams {
   int zero_row;
   int relu;
   int w_c_slot;
+  int w_layout;   // FOVI_W_ROWS or FOVI_W_MFMA
+  const uint16_t* tile_src;
+  const int32_t* tile_coll_off;
+  const uint64_t* tile_coll4;
+  int coll_off_stride;
+  int coll4_stride;
 };
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+
+// Eight bf16 values (one 16-byte row part) widened to fp32.
+__device__ __forceinline__ f32x8 unpack_bf16x8(u32x4 r) {
+  f32x8 f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(r[i] << 16);
+    f[2 * i + 1] = __uint_as_float(r[i] & 0xffff0000u);
+  }
+  return f;
+}
+
+// Two floats -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
+  const f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2v));
+}
 
 // Output transform: optional ReLU fused into the store (the activation that
 // follows the conv in the reference blocks when no norm sits between them).
@@ -78,5 +105,8 @@ static int pick_tile_n(int64_t cout, Fits fits) {
 }
 
 int launch_knnconv_fp8(const KnnParams& p, int out_t, hipStream_t s);
+// 1 if the fragment-order kernel takes this call (see knnconv_v5.hip), 0 if not.
+int v5_applies(const KnnParams& p);
+int launch_knnconv_bf16_v5(const KnnParams& p, int out_t, hipStream_t s);
 
 }  // namespace fovi

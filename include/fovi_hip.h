@@ -23,12 +23,13 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 9
+#define FOVI_ABI_VERSION 11
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
 enum fovi_padding { FOVI_PAD_ZEROS = 0, FOVI_PAD_BORDER = 1 };
 enum fovi_activation { FOVI_ACT_NONE = 0, FOVI_ACT_RELU = 1 };
+enum fovi_weight_layout { FOVI_W_ROWS = 0, FOVI_W_MFMA = 1 };
 
 /* Version of this header the library was built from (FOVI_ABI_VERSION). */
 int fovi_abi_version(void);
@@ -129,9 +130,11 @@ typedef struct fovi_knnconv_args {
   int64_t n_out, k, n_ref;
   const int32_t* slot_ptr;    /* [n_out, n_ref] */
   const int32_t* nbr_sorted;  /* [n_out, k] */
-  const void* w;              /* packed [c_out, k_pad] */
+  const void* w;              /* packed [c_out, k_pad] (FOVI_W_ROWS) or fragment order (FOVI_W_MFMA) */
   int32_t w_dtype;
-  int32_t reserved1;
+  int32_t w_layout;           /* fovi_weight_layout: FOVI_W_MFMA (from fovi_knnconv_pack_weight_mfma)
+                                 selects the wide-layer bf16 kernel and needs c_in % 32 == 0,
+                                 channels-last 16-byte input rows and the tile tables */
   int64_t c_out, k_pad;
   const float* bias;          /* [c_out] or NULL */
   const float* w_scale;       /* [c_out] (F8E4M3 only) */
@@ -161,6 +164,20 @@ typedef struct fovi_knnconv_args {
   int64_t workspace_bytes;
   const float* x_scale_dev;   /* (F8E4M3 only) device copy of the activation scale, e.g. the one
                                  fovi_quantize_e4m3 writes; used instead of x_scale when non-NULL */
+  /* Tables of the wide-layer kernel (w_layout = FOVI_W_MFMA), in its LDS order:
+   *   tile_src[(t * n_ref + v) * tile_points + r]: staged row (relative to tile_lo[t]) the MFMA
+   *     reads for slot v of row r (the neighbour's, or zero_row for an empty slot), or 0x8000
+   *     when the slot holds two or more neighbours (summed by the kernel);
+   *   tile_coll4[t * coll4_stride + i], i in [tile_coll_off[t * coll_off_stride + v],
+   *     tile_coll_off[t * coll_off_stride + v + 1]): one entry per (slot v, row with two or more
+   *     neighbours): bits 0-7 row, 8-15 count, 16-23 begin in tile_nbr, then the staged rows of
+   *     the first four neighbours in 10-bit fields at bits 24, 34, 44, 54 (zero_row past the
+   *     count). zero_row must be below 1024. */
+  const uint16_t* tile_src;
+  const int32_t* tile_coll_off;
+  const uint64_t* tile_coll4;
+  int32_t coll_off_stride;    /* multiple of 4, > n_ref */
+  int32_t coll4_stride;       /* even */
 } fovi_knnconv_args;
 
 int fovi_knnconv_fwd(const fovi_knnconv_args* args, void* stream);
@@ -178,6 +195,20 @@ int fovi_knnconv_fwd(const fovi_knnconv_args* args, void* stream);
 int fovi_knnconv_pack_weight(const float* w_ref, int64_t c_out, int64_t c_in, int64_t n_ref,
                              void* w_packed, int32_t out_dtype, int64_t k_pad, int64_t c_slot,
                              const float* w_scale, void* stream);
+
+/*
+ * Weight in MFMA-fragment order for the wide-layer bf16 kernel (w_layout =
+ * FOVI_W_MFMA). Same source as fovi_knnconv_pack_weight (w_ref = KNNConvLayer.weight,
+ * fp32 [c_out, c_in * n_ref], index c * n_ref + v, fovi/arch/knn.py:462,524);
+ * the output is fovi_knnconv_weight_mfma_elems(c_out, c_in, n_ref) bf16
+ * values: 1 KB fragments f = ((it * ncb + cb) * 2 + ks), it = (c / 32) * n_ref + v,
+ * ncb = 8 * ceil(c_out / 256); lane l of fragment f holds, at 8 * l + e,
+ * w_ref[o = 32 * cb + l % 32][c * n_ref + v] with c % 32 = 16 * ks + 8 * (l / 32) + e
+ * (zero for o >= c_out). c_in must be a multiple of 32; only BF16 output.
+ */
+int64_t fovi_knnconv_weight_mfma_elems(int64_t c_out, int64_t c_in, int64_t n_ref);
+int fovi_knnconv_pack_weight_mfma(const float* w_ref, int64_t c_out, int64_t c_in, int64_t n_ref,
+                                  void* w_frag, int32_t out_dtype, void* stream);
 
 /*
  * Per-tensor OCP e4m3 quantization of activations for the fp8 kNN-conv path

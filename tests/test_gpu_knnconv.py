@@ -222,3 +222,44 @@ def test_bf16_few_channels_padded_rows(c_in, k, side):
     assert_close_rel(y_view.float().cpu(), ref, 1e-2)
     assert torch.equal(y_view, y_copy)
     assert_close_rel(y_fused.float().cpu(), ref, 1e-2)
+
+
+@pytest.mark.parametrize("res_in,res_out,k,c_in,c_out,bias,act,batch", [
+    (16, 16, 9, 32, 256, True, None, 3),      # one channel chunk
+    (16, 16, 9, 96, 512, False, "relu", 2),   # three chunks, two channel tiles
+    (24, 12, 25, 64, 256, True, None, 3),     # strided: 144 outputs (one partial point tile)
+    (16, 16, 25, 64, 256, False, None, 2),    # k = 25 on a small lattice (seam-heavy tiles)
+    (128, 128, 25, 256, 256, False, None, 2), # C3 geometry
+])
+def test_fragment_order_kernel(res_in, res_out, k, c_in, c_out, bias, act, batch):
+    """Wide bf16 layers take the fragment-order (256 x 256 tile) kernel; it matches the oracle
+    and the row-packed kernel."""
+    layer = _layer(res_in, res_out, k, c_in, c_out, bias=bias, seed=12)
+    layer.mfma_weights = True
+    x = torch.randn(batch, c_in, res_in * res_in, generator=torch.Generator().manual_seed(13)).bfloat16()
+    xd = x.cuda().transpose(1, 2).contiguous().transpose(1, 2)
+    with torch.no_grad():
+        y = layer.forward_fused(xd, act) if act else layer(xd)
+        assert layer.last_weight_layout == "mfma"
+        layer.mfma_weights = False
+        y_rows = layer.forward_fused(xd, act) if act else layer(xd)
+        assert layer.last_weight_layout == "rows"
+    ref = _oracle(layer, x, layer.weight.detach().cpu().bfloat16().float())
+    if act:
+        ref = torch.relu(ref)
+    assert_close_rel(y.float().cpu(), ref, 1e-2, "fragment-order kernel vs oracle")
+    assert_close_rel(y.float().cpu(), y_rows.float().cpu(), 1e-2, "fragment-order vs row-packed kernel")
+
+
+def test_fragment_order_kernel_falls_back_when_tables_exceed_lds():
+    """k = 49 (7x7 ref grid): the tile's tables do not fit the fragment-order kernel's LDS, so the
+    layer keeps the row-packed kernel."""
+    layer = _layer(32, 16, 49, 64, 256, seed=14)
+    layer.mfma_weights = True
+    x = torch.randn(2, 64, 1024, generator=torch.Generator().manual_seed(15)).bfloat16()
+    xd = x.cuda().transpose(1, 2).contiguous().transpose(1, 2)
+    with torch.no_grad():
+        y = layer(xd)
+    assert layer.last_weight_layout == "rows"
+    ref = _oracle(layer, x, layer.weight.detach().cpu().bfloat16().float())
+    assert_close_rel(y.float().cpu(), ref, 1e-2)

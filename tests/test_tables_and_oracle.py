@@ -221,3 +221,44 @@ def test_direct_tables_lists_and_zero_row(res_in, res_out, k):
             assert sorted(rows.tolist()) == want.tolist()
             c = cnt[tt * 256 + rows, v]
             assert np.all(np.diff(c) <= 0)          # decreasing count order
+
+
+@pytest.mark.parametrize("res_in,res_out,k", [(32, 32, 25), (64, 32, 49), (16, 16, 9), (128, 128, 25)])
+def test_wide_tables_decode_to_the_csr_lists(res_in, res_out, k):
+    """Fragment-order kernel tables: every (slot, row) source and every packed collision entry
+    decodes back to the slot-major CSR lists (global input index = staged row + tile_lo)."""
+    t = layer_tables(res_in, res_out, k)
+    direct = T.direct_tables(t["idx"], t["slots"], t["n_in"], t["V"])
+    lo, span, ent, nbr, coll, coll_n, zr = direct
+    wide = T.wide_tables(direct, t["k"])
+    if wide is None:                      # staged-row indices need 10 bits
+        assert zr > 1023
+        return
+    src, coll4, coll_off, stride = wide
+    src, coll4, coll_off = src.numpy().astype(np.int64), coll4.numpy().view(np.uint64), coll_off.numpy()
+    ptr, gnbr = t["ptr"].numpy(), t["nbr"].numpy()
+    lo = lo.numpy().astype(np.int64)
+    n_tiles, V = src.shape[0], t["V"]
+    assert coll4.shape == (n_tiles, stride) and stride % 2 == 0
+    for tt in range(n_tiles):
+        seen = set()
+        for v in range(V):
+            for ei in range(coll_off[tt, v], coll_off[tt, v + 1]):
+                w = int(coll4[tt, ei])
+                row, cnt, beg = w & 0xFF, (w >> 8) & 0xFF, (w >> 16) & 0xFF
+                n = tt * 256 + row
+                assert cnt >= 2 and cnt == (ptr[n, v] & 0xFFFF) and beg == (ptr[n, v] >> 16)
+                rs = [(w >> (24 + 10 * j)) & 0x3FF for j in range(4)]
+                want = list(gnbr[n, beg:beg + min(cnt, 4)])
+                assert [r + lo[tt] for r in rs[:len(want)]] == want
+                assert all(r == zr for r in rs[len(want):])
+                assert src[tt, v, row] == 0x8000
+                seen.add((v, row))
+        for v in range(V):
+            for row in range(256):
+                n = tt * 256 + row
+                if n >= t["n_out"] or (v, row) in seen:
+                    continue
+                cnt = ptr[n, v] & 0xFFFF
+                assert cnt <= 1
+                assert src[tt, v, row] == (gnbr[n, ptr[n, v] >> 16] - lo[tt] if cnt == 1 else zr)
