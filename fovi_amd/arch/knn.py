@@ -137,12 +137,12 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
             self._zero_row = tiles[6]
         # tables of the wide-layer (fragment-order weight) kernel
         wide = T.wide_tables(tiles, self._k) if tiles is not None else None
-        self._coll4_stride = 0
+        self._cent_stride = 0
         self._coll_off_stride = 0
-        for name, t in zip(("tile_src", "tile_coll4", "tile_coll_off"), wide[:3] if wide is not None else (None,) * 3):
+        for name, t in zip(("tile_src", "tile_cent", "tile_coll_off"), wide[:3] if wide is not None else (None,) * 3):
             self.register_buffer(name, None if t is None else t.to(device), persistent=False)
         if wide is not None:
-            self._coll4_stride = wide[3]
+            self._cent_stride = wide[3]
             self._coll_off_stride = int(wide[2].shape[1])
         self._packed = {}
         # slot-sum headroom of the fp8 path: the largest neighbour count of a slot
@@ -154,7 +154,7 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         self.two_pass_few_channels = True
         # wide bf16 layers (c_in % 32 == 0, c_out % 256 == 0): weights in MFMA-fragment order
         # for the 256 x 256-tile kernel (False: the row-packed kernels)
-        self.mfma_weights = False
+        self.mfma_weights = True
 
     # -- setup ---------------------------------------------------------------
     def _init_conv_like(self):
@@ -240,14 +240,13 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         return out
 
     def _mfma_lds_bytes(self):
-        """LDS bytes of the fragment-order kernel's tile (its ``v5_layout``): two 256 x 32 bf16
-        collision tiles and a trash row, per-(slot, row) sources, per-slot entry offsets, packed
-        collision entries, neighbour lists, 128-byte alignment, then the staged rows plus the
-        zero row (64 bytes each)."""
+        """LDS bytes of the fragment-order kernel's tile (its ``v5_layout``): the staged rows plus
+        the zero row (64 bytes each), 128-byte alignment, two 256 x 32 bf16 collision tiles and a
+        trash row, per-(slot, row) sources, per-slot entry offsets, 16-byte collision entries,
+        neighbour lists."""
         v, k = self.ref_coords.shape[0], self._k
-        o = (2 * 256 + 1) * 32 * 2 + v * 256 * 2 + self._coll_off_stride * 4 + self._coll4_stride * 8 + 256 * k * 2
-        o = (o + 127) & ~127
-        return o + (self._zero_row + 1) * 64
+        o = ((self._zero_row + 1) * 64 + 127) & ~127
+        return o + (2 * 256 + 1) * 32 * 2 + v * 256 * 2 + self._coll_off_stride * 4 + self._cent_stride * 16 + 256 * k * 2
 
     def _mfma_path(self, x, dt):
         """Whether this call runs the fragment-order kernel (see ``mfma_weights``)."""
@@ -337,8 +336,8 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
             a.zero_row = self._zero_row
         if mfma:
             a.tile_src = self.tile_src.data_ptr(); a.tile_coll_off = self.tile_coll_off.data_ptr()
-            a.tile_coll4 = self.tile_coll4.data_ptr()
-            a.coll_off_stride = self._coll_off_stride; a.coll4_stride = self._coll4_stride
+            a.tile_cent = self.tile_cent.data_ptr()
+            a.coll_off_stride = self._coll_off_stride; a.cent_stride = self._cent_stride
         lib = _lib.load()
         _lib.check(lib.fovi_knnconv_fwd(a, _lib.stream_handle(x.device)), "fovi_knnconv_fwd")
         return y.transpose(1, 2)

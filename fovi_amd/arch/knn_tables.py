@@ -253,26 +253,38 @@ def direct_tables(knn_idx, slots, n_in, n_ref, tile=TILE_POINTS):
             torch.from_numpy(coll), torch.from_numpy(coll_n), zero_row)
 
 
+def _row_offset(r):
+    """Byte offset in the kernel's LDS of 16-byte part 0 of staged row ``r``: rows are 64
+    bytes, and part q of row r sits at ``(64 r + 16 g(r)) ^ 16 q`` with
+    g(r) = (bit1(r) ^ bit3(r)) | bit2(r) << 1 (the XOR swizzle that keeps 8 or 16
+    consecutive rows of one part on distinct LDS banks)."""
+    r = np.asarray(r, np.int64)
+    g = (((r >> 1) ^ (r >> 3)) & 1) | ((r >> 1) & 2)
+    return r * 64 + (g << 4)
+
+
 def wide_tables(direct, k):
     """Tables of the wide-layer (fragment-order) kernel, derived from ``direct_tables``.
 
-    Laid out in the kernel's LDS order so that the kernel copies them with
-    16-byte loads:
+    Laid out in the kernel's LDS order (16-byte copies) and holding swizzled
+    LDS byte offsets (``_row_offset``) rather than row numbers, so the kernel
+    forms every address with one XOR:
 
-    * ``src [T, V, tile] uint16``: per (slot, row) the staged-row index the
-      MFMA lanes read for that slot (the neighbour's row when the slot holds
-      one neighbour, ``zero_row`` when it holds none) or, with bit 15 set,
-      the row's own collision sum (two or more neighbours);
-    * ``coll4 [T, stride] uint64``: one entry per (slot, collision row),
-      grouped by slot and within a slot by decreasing count: bits 0-7 row,
-      8-15 count, 16-23 begin (in the ``tile_nbr`` list of the row), then the
-      staged-row indices of the first four neighbours in 10-bit fields at
-      bits 24, 34, 44 and 54 (``zero_row`` past the count);
+    * ``src [T, V, tile] uint16``: per (slot, row) the offset of the staged row
+      the MFMA lanes read for that slot (the neighbour's row when the slot
+      holds one neighbour, the zero row when it holds none), or 0xFFFF when
+      the slot holds two or more neighbours (the row's own collision sum);
+    * ``coll [T, stride, 4] uint32``: one 16-byte entry per (slot, collision
+      row), grouped by slot and within a slot by decreasing count. Word 0:
+      bits 0-15 the row's offset in a collision tile, 16-23 count, 24-31
+      begin (in the ``tile_nbr`` list of the row); words 1-2: offsets of the
+      first four neighbours' staged rows, two per word (low half first; the
+      zero row past the count); word 3: the row;
     * ``coll_off [T, V + 1 rounded up to 4] int32``: slot v's entries are
-      ``coll4[t, coll_off[t, v]:coll_off[t, v + 1]]``.
+      ``coll[t, coll_off[t, v]:coll_off[t, v + 1]]``.
 
-    Returns ``(src, coll4, coll_off, stride)`` or ``None`` when zero_row does
-    not fit 10 bits or k exceeds 255.
+    Returns ``(src, coll, coll_off, stride)`` or ``None`` when zero_row does
+    not fit the 16-bit offsets (above 1023) or k exceeds 255.
     """
     lo, span, ent, nbr, coll, coll_n, zero_row = direct
     if zero_row > 1023 or k > 255:
@@ -281,17 +293,17 @@ def wide_tables(direct, k):
     n_tiles, n_ref, tile = coll.shape
     first = e >> 16
     cnt = (e >> 8) & 0xFF
-    beg = e & 0xFF
-    src = np.where(cnt >= 2, 0x8000, first).astype(np.uint16)
+    src = np.where(cnt >= 2, 0xFFFF, _row_offset(first)).astype(np.uint16)
     src = src.reshape(n_tiles, tile, n_ref).transpose(0, 2, 1).copy()
     nb = nbr.numpy().astype(np.int64).reshape(n_tiles, tile, k)
     cn = coll_n.numpy().astype(np.int64)
     counts = cn.sum(axis=1)
-    stride = int(max(2, -(-int(counts.max()) // 2) * 2)) if n_tiles else 2
+    stride = int(max(1, int(counts.max()))) if n_tiles else 1
     voff = -(-(n_ref + 1) // 4) * 4
-    coll4 = np.zeros((n_tiles, stride), np.uint64)
+    out = np.zeros((n_tiles, stride, 4), np.uint32)
     coll_off = np.zeros((n_tiles, voff), np.int32)
     cl = coll.numpy().astype(np.int64)
+    zoff = int(_row_offset(zero_row))
     for t in range(n_tiles):
         off = np.concatenate([[0], np.cumsum(cn[t])])
         coll_off[t, :n_ref + 1] = off
@@ -302,9 +314,13 @@ def wide_tables(direct, k):
         eb = e.reshape(n_tiles, tile, n_ref)[t, rows, slot]
         c = (eb >> 8) & 0xFF
         b = eb & 0xFF
-        word = rows | (c << 8) | (b << 16) | ((eb >> 16) << 24)
+        nbo = [_row_offset(eb >> 16)]
         for j in range(1, 4):
-            r = np.where(j < c, nb[t, rows, np.minimum(b + j, k - 1)], zero_row)
-            word |= r << (24 + 10 * j)
-        coll4[t, :off[-1]] = word.astype(np.uint64)
-    return (torch.from_numpy(src), torch.from_numpy(coll4.view(np.int64)), torch.from_numpy(coll_off), stride)
+            r = nb[t, rows, np.minimum(b + j, k - 1)]
+            nbo.append(np.where(j < c, _row_offset(r), zoff))
+        n_e = off[-1]
+        out[t, :n_e, 0] = (_row_offset(rows) | (c << 16) | (b << 24)).astype(np.uint32)
+        out[t, :n_e, 1] = (nbo[0] | (nbo[1] << 16)).astype(np.uint32)
+        out[t, :n_e, 2] = (nbo[2] | (nbo[3] << 16)).astype(np.uint32)
+        out[t, :n_e, 3] = rows.astype(np.uint32)
+    return (torch.from_numpy(src), torch.from_numpy(out.view(np.int32)), torch.from_numpy(coll_off), stride)

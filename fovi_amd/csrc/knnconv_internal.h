@@ -34,9 +34,9 @@ struct KnnParams {
   int w_layout;   // FOVI_W_ROWS or FOVI_W_MFMA
   const uint16_t* tile_src;
   const int32_t* tile_coll_off;
-  const uint64_t* tile_coll4;
+  const uint32_t* tile_cent;
   int coll_off_stride;
-  int coll4_stride;
+  int cent_stride;
 };
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));

@@ -29,22 +29,43 @@ constexpr int V5_MT = 256;   // output points per tile
 constexpr int V5_NT = 256;   // output channels per tile
 constexpr int V5_CC = 32;    // channels per reduction chunk (one 64-byte LDS row)
 
+// LDS byte layout of a tile. The staged rows S come first, at offset 0, so
+// the host tables can hold absolute LDS byte offsets of staged rows.
 struct V5Layout {
-  int acol_off, src_off, coff_off, coll4_off, nbl_off, s_off, total;  // bytes
+  int acol_off, src_off, coff_off, cent_off, nbl_off, total;  // bytes
 };
 
-__host__ __device__ inline V5Layout v5_layout(int V, int K, int zero_row, int coff_stride, int coll4_stride) {
+__host__ __device__ inline V5Layout v5_layout(int V, int K, int zero_row, int coff_stride, int cent_stride) {
   V5Layout l;
-  int o = 0;
+  int o = (zero_row + 1) * V5_CC * 2;               // staged rows + zero row
+  o = (o + 127) & ~127;
   l.acol_off = o;   o += (2 * V5_MT + 1) * V5_CC * 2; // two 256 x 32 bf16 collision tiles + a trash row
-  l.src_off = o;    o += V * V5_MT * 2;             // per (slot, row) source row, slot-major
+  l.src_off = o;    o += V * V5_MT * 2;             // per (slot, row) A source, slot-major
   l.coff_off = o;   o += coff_stride * 4;           // per-slot collision entry offsets
-  l.coll4_off = o;  o += coll4_stride * 8;          // packed collision entries
+  l.cent_off = o;   o += cent_stride * 16;          // collision entries
   l.nbl_off = o;    o += V5_MT * K * 2;             // neighbour lists (rows with > 4 neighbours)
-  o = (o + 127) & ~127;                             // rows 128-byte aligned (fragment offsets are XORed)
-  l.s_off = o;      o += (zero_row + 1) * V5_CC * 2; // staged rows + zero row
   l.total = o;
   return l;
+}
+
+constexpr uint32_t V5_TILE_BYTES = V5_MT * V5_CC * 2;   // one collision tile
+
+// Byte offset of 16-byte part 0 of 64-byte row r under the swz32 XOR swizzle;
+// part q of the row is at row_off(r) ^ (q << 4).
+__device__ __forceinline__ uint32_t row_off(int r) {
+  const int g = (((r >> 1) ^ (r >> 3)) & 1) | ((r >> 1) & 2);
+  return static_cast<uint32_t>(r * 64 + (g << 4));
+}
+
+__device__ __forceinline__ u32x4 lds16(const uint8_t* smem, uint32_t off) {
+  return *reinterpret_cast<const u32x4*>(smem + off);
+}
+
+// a += the 8 bf16 values of x (widened to fp32; fp32 adds in order).
+__device__ __forceinline__ void acc_bf16x8(f32x8& a, u32x4 x) { a += unpack_bf16x8(x); }
+
+__device__ __forceinline__ u32x4 pack_bf16x8(const f32x8& a) {
+  return u32x4{cvt_pk_bf16(a[0], a[1]), cvt_pk_bf16(a[2], a[3]), cvt_pk_bf16(a[4], a[5]), cvt_pk_bf16(a[6], a[7])};
 }
 
 // Index of the 1 KB weight fragment (iteration it, 32-column block cb,
@@ -53,9 +74,6 @@ __host__ __device__ inline int64_t v5_frag(int64_t it, int64_t ncb, int64_t cb, 
   return (it * ncb + cb) * 2 + ks;
 }
 
-// Staged-row index of neighbour j (< 4) of a packed collision entry.
-__device__ __forceinline__ int coll4_row(uint64_t w, int j) { return static_cast<int>((w >> (24 + 10 * j)) & 0x3ff); }
-
 template <int SV, typename OutT>
 __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, int ncb, int64_t tiles_per_b,
                                                                  int64_t n_tiles_n, int64_t total_tiles,
@@ -63,14 +81,14 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int V = static_cast<int>(p.V), K = static_cast<int>(p.K);
   const int zr = p.zero_row;
-  const V5Layout L = v5_layout(V, K, zr, p.coll_off_stride, p.coll4_stride);
-  uint16_t* sm16 = reinterpret_cast<uint16_t*>(smem);
+  const V5Layout L = v5_layout(V, K, zr, p.coll_off_stride, p.cent_stride);
+  uint16_t* S = reinterpret_cast<uint16_t*>(smem);
   const uint16_t* srcs = reinterpret_cast<const uint16_t*>(smem + L.src_off);
   const int32_t* coff = reinterpret_cast<const int32_t*>(smem + L.coff_off);
-  const uint64_t* coll4 = reinterpret_cast<const uint64_t*>(smem + L.coll4_off);
+  const u32x4* cent = reinterpret_cast<const u32x4*>(smem + L.cent_off);
   const uint16_t* nbl = reinterpret_cast<const uint16_t*>(smem + L.nbl_off);
-  const int s16 = L.s_off / 2;                    // S offset in bf16 elements
-  uint16_t* S = sm16 + s16;
+  const uint32_t acol = static_cast<uint32_t>(L.acol_off);
+  const uint32_t trash = acol + 2 * V5_TILE_BYTES;
 
   const int64_t tile = xcd_tile(blockIdx.x, padded_tiles);
   if (tile >= total_tiles) return;
@@ -81,7 +99,8 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
   const int64_t pt = mt % tiles_per_b;
   const int64_t n0 = pt * V5_MT;
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
   const int wm = wave & 1, wn = wave >> 1;
   const int64_t lo = p.tile_lo[pt];
   const int span = static_cast<int>(min(static_cast<int64_t>(zr), p.Nin - lo));
@@ -97,8 +116,8 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
   }
   const int ncc = static_cast<int>(p.C / V5_CC);
   const int nit = ncc * V;
-  // this wave's weight fragments: column blocks cb0 .. cb0 + 3, lane-contiguous
-  const u32x4* wq = reinterpret_cast<const u32x4*>(p.w) + lane;
+  // this wave's weight fragments: column blocks cb0 .. cb0 + 3; the base of
+  // an iteration's fragments is wave-uniform, the lane adds 16 bytes
   const int64_t cb0 = tn * (V5_NT / 32) + wn * 4;
 
   u32x4 rs[SV];
@@ -116,10 +135,11 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
     }
   };
   auto load_w = [&](int it, u32x4 (&dst)[8]) {
+    const u32x4* wb = reinterpret_cast<const u32x4*>(p.w) + v5_frag(it, ncb, cb0, 0) * 64;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) dst[j * 2 + ks] = wq[v5_frag(it, ncb, cb0 + j, ks) * 64];
+      for (int ks = 0; ks < 2; ++ks) dst[j * 2 + ks] = wb[(j * 2 + ks) * 64 + lane];
   };
 
   // Prologue: the first chunk's rows and the tile's tables, all loads in
@@ -128,16 +148,16 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
   load_s(0);
   {
     const int n_src = V * V5_MT * 2 / 16, n_coff = p.coll_off_stride * 4 / 16;
-    const int n_c4 = p.coll4_stride * 8 / 16, n_nbl = V5_MT * K * 2 / 16;
+    const int n_ce = p.cent_stride, n_nbl = V5_MT * K * 2 / 16;
     const u32x4* g_src = reinterpret_cast<const u32x4*>(p.tile_src + pt * V * V5_MT);
     const u32x4* g_coff = reinterpret_cast<const u32x4*>(p.tile_coll_off + pt * p.coll_off_stride);
-    const u32x4* g_c4 = reinterpret_cast<const u32x4*>(p.tile_coll4 + pt * p.coll4_stride);
+    const u32x4* g_ce = reinterpret_cast<const u32x4*>(p.tile_cent) + pt * p.cent_stride;
     const u32x4* g_nbl = reinterpret_cast<const u32x4*>(p.tile_nbr + n0 * p.K);
     u32x4* d_src = reinterpret_cast<u32x4*>(smem + L.src_off);
     u32x4* d_coff = reinterpret_cast<u32x4*>(smem + L.coff_off);
-    u32x4* d_c4 = reinterpret_cast<u32x4*>(smem + L.coll4_off);
+    u32x4* d_ce = reinterpret_cast<u32x4*>(smem + L.cent_off);
     u32x4* d_nbl = reinterpret_cast<u32x4*>(smem + L.nbl_off);
-    const int total = n_src + n_coff + n_c4 + n_nbl;
+    const int total = n_src + n_coff + n_ce + n_nbl;
     for (int base = 0; base < total; base += 8 * 256) {
       u32x4 t[8];
       u32x4* dst[8];
@@ -149,8 +169,8 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
         i -= n_src;
         if (i < n_coff) { t[u] = g_coff[i]; dst[u] = d_coff + i; continue; }
         i -= n_coff;
-        if (i < n_c4) { t[u] = g_c4[i]; dst[u] = d_c4 + i; continue; }
-        i -= n_c4;
+        if (i < n_ce) { t[u] = g_ce[i]; dst[u] = d_ce + i; continue; }
+        i -= n_ce;
         if (i < n_nbl) { t[u] = g_nbl[i]; dst[u] = d_nbl + i; }
       }
 #pragma unroll
@@ -160,24 +180,35 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
   }
   if (tid < 4) *reinterpret_cast<u32x4*>(&S[zr * V5_CC + tid * 8]) = u32x4{0u, 0u, 0u, 0u};
 
-  // Full sums of slot v's collision rows into tile `buf` (all neighbours; used
-  // at chunk boundaries and for lists longer than the in-loop straight-line part).
-  auto coll_item = [&](int v, int buf, int item) {
-    const uint64_t w = coll4[coff[v] + (item >> 2)];
-    const int part = item & 3;
-    const int row = static_cast<int>(w & 0xff), cnt = static_cast<int>((w >> 8) & 0xff);
-    f32x8 acc8 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc8 += unpack_bf16x8(*reinterpret_cast<const u32x4*>(&S[swz32(coll4_row(w, j), part)]));
-    const uint16_t* nb = nbl + row * K + ((w >> 16) & 0xff);
-    for (int j = 4; j < cnt; ++j) acc8 += unpack_bf16x8(*reinterpret_cast<const u32x4*>(&S[swz32(nb[j], part)]));
-    *reinterpret_cast<u32x4*>(&sm16[buf * V5_MT * V5_CC + swz32(row, part)]) =
-        u32x4{cvt_pk_bf16(acc8[0], acc8[1]), cvt_pk_bf16(acc8[2], acc8[3]), cvt_pk_bf16(acc8[4], acc8[5]),
-              cvt_pk_bf16(acc8[6], acc8[7])};
+  // Collision sums. A unit is (entry, 16-byte part): entry = unit / 4. Its
+  // first four neighbours are summed from the entry's offsets (missing ones
+  // are the zero row); neighbours 5.. come from the row's neighbour list.
+  auto unit_sum4 = [&](const u32x4 ce, uint32_t pq) {
+    f32x8 a = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    acc_bf16x8(a, lds16(smem, (ce[1] & 0xffffu) ^ pq));
+    acc_bf16x8(a, lds16(smem, (ce[1] >> 16) ^ pq));
+    acc_bf16x8(a, lds16(smem, (ce[2] & 0xffffu) ^ pq));
+    acc_bf16x8(a, lds16(smem, (ce[2] >> 16) ^ pq));
+    return a;
   };
-  auto build_coll = [&](int v, int buf) {
-    const int items = (coff[v + 1] - coff[v]) * 4;
-    for (int item = tid; item < items; item += 256) coll_item(v, buf, item);
+  auto unit_rest = [&](f32x8& a, const u32x4 ce, uint32_t pq) {
+    const int cnt = static_cast<int>((ce[0] >> 16) & 0xff);
+    if (cnt > 4) {
+      const uint16_t* nb = nbl + static_cast<int>(ce[3]) * K + static_cast<int>(ce[0] >> 24);
+      for (int j = 4; j < cnt; ++j) acc_bf16x8(a, lds16(smem, row_off(nb[j]) ^ pq));
+    }
+  };
+  // every unit of slot v's list, into collision tile buf (chunk boundaries and
+  // the tail of long lists)
+  auto build_units = [&](int v, int buf, int first) {
+    const int c0 = coff[v], units = (coff[v + 1] - c0) * 4;
+    for (int u = first + tid; u < units; u += 256) {
+      const u32x4 ce = cent[c0 + (u >> 2)];
+      const uint32_t pq = static_cast<uint32_t>(u & 3) << 4;
+      f32x8 a = unit_sum4(ce, pq);
+      unit_rest(a, ce, pq);
+      *reinterpret_cast<u32x4*>(smem + acol + buf * V5_TILE_BYTES + ((ce[0] & 0xffffu) ^ pq)) = pack_bf16x8(a);
+    }
   };
 
   f32x16 acc[4][4];
@@ -188,30 +219,32 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
+  // this lane's rows of the A tile and their offsets in a collision tile
+  uint32_t rowm_off[4];
   int rowm[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) rowm[i] = wm * 128 + i * 32 + (lane & 31);
+  for (int i = 0; i < 4; ++i) {
+    rowm[i] = wm * 128 + i * 32 + (lane & 31);
+    rowm_off[i] = acol + row_off(rowm[i]);
+  }
+  const uint32_t qx = static_cast<uint32_t>(lane >> 5) << 4;   // 16-byte part of ks = 0
 
   u32x4 bcur[8], bnxt[8];
   load_w(0, bcur);
   store_s();
   if (ncc > 1) load_s(1);
   __syncthreads();
-  build_coll(0, 0);
+  build_units(0, 0, 0);
   uint32_t ecur[4], enxt[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) ecur[i] = srcs[rowm[i]];
   __syncthreads();
 
-  // In-loop collision sums for the next iteration, written as straight-line
-  // code so that they interleave with this iteration's MFMAs: each thread owns
-  // items tid and tid + 256 (item = collision entry * 4 + 16-byte part) and
-  // sums the entry's first four neighbours (missing ones are the zero row);
-  // masked items write a trash row. Entries with more than four neighbours
-  // (the head of each slot's list, which is sorted by count) finish in a
-  // short loop after the MFMAs, and lists longer than 128 entries in the
-  // generic loop.
-  const int trash = 2 * V5_MT * V5_CC;
+  // The next iteration's collision sums are straight-line code interleaved
+  // with this iteration's MFMAs: units tid and tid + 256 (entries 0 .. 127 of
+  // the slot's list); masked units write a trash row; entries with more than
+  // four neighbours (the head of the list, sorted by count) finish after the
+  // MFMAs, and lists longer than 128 entries in build_units.
   int cc1 = 0, v1 = 0;
   for (int it = 0; it < nit; ++it) {
     const int cur = it & 1;
@@ -220,41 +253,29 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
     const int itn = more ? it + 1 : it;
     const int vn = v1;   // slot of the next iteration (chunk boundaries build after the S refresh)
     const int c0 = coff[vn];
-    const int items = (more && v1 != 0) ? (coff[vn + 1] - c0) * 4 : 0;
+    const int units = (more && v1 != 0) ? (coff[vn + 1] - c0) * 4 : 0;
 
-    int src[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      src[i] = (ecur[i] & 0x8000u) ? cur * V5_MT * V5_CC + swz32(rowm[i], 0)
-                                   : s16 + swz32(static_cast<int>(ecur[i]), 0);
     bf16x8 af[2][4];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        // swz32(r, q) = swz32(r, 0) ^ (q << 3) within the row (XOR of the 16-byte part)
-        af[ks][i] = *reinterpret_cast<const bf16x8*>(&sm16[src[i] ^ ((ks * 2 + (lane >> 5)) << 3)]);
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t a = ecur[i] == 0xffffu ? rowm_off[i] + cur * V5_TILE_BYTES : ecur[i];
+      af[0][i] = __builtin_bit_cast(bf16x8, lds16(smem, a ^ qx));
+      af[1][i] = __builtin_bit_cast(bf16x8, lds16(smem, a ^ qx ^ 32u));
+    }
 
     load_w(itn, bnxt);
 #pragma unroll
     for (int i = 0; i < 4; ++i) enxt[i] = srcs[v1 * V5_MT + rowm[i]];
 
-    uint64_t w_k[2];
-    int part_k[2];
+    u32x4 ce_k[2];
     f32x8 sum_k[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      const int item = tid + 256 * k;
-      const bool valid = item < items;
-      const uint64_t w = coll4[valid ? c0 + (item >> 2) : 0];
-      const int part = item & 3;
-      f32x8 acc8 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc8 += unpack_bf16x8(*reinterpret_cast<const u32x4*>(&S[swz32(coll4_row(w, j), part)]));
-      w_k[k] = valid ? w : 0;      // count 0: nothing left to add, written to the trash row
-      part_k[k] = part;
-      sum_k[k] = acc8;
+      const int u = tid + 256 * k;
+      u32x4 ce = cent[u < units ? c0 + (u >> 2) : 0];
+      if (u >= units) ce[0] = 0;   // count 0: written to the trash row
+      ce_k[k] = ce;
+      sum_k[k] = unit_sum4(ce, static_cast<uint32_t>(tid & 3) << 4);
     }
 
 #pragma unroll
@@ -268,26 +289,19 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
 
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      const uint64_t w = w_k[k];
-      const int cnt = static_cast<int>((w >> 8) & 0xff), row = static_cast<int>(w & 0xff);
-      if (cnt > 4) {                      // neighbours 5 .. count, in order
-        const uint16_t* nb = nbl + row * K + ((w >> 16) & 0xff);
-        for (int j = 4; j < cnt; ++j)
-          sum_k[k] += unpack_bf16x8(*reinterpret_cast<const u32x4*>(&S[swz32(nb[j], part_k[k])]));
-      }
-      const f32x8 a8 = sum_k[k];
-      const int dst = cnt > 0 ? (cur ^ 1) * V5_MT * V5_CC + swz32(row, part_k[k]) : trash;
-      *reinterpret_cast<u32x4*>(&sm16[dst]) =
-          u32x4{cvt_pk_bf16(a8[0], a8[1]), cvt_pk_bf16(a8[2], a8[3]), cvt_pk_bf16(a8[4], a8[5]),
-                cvt_pk_bf16(a8[6], a8[7])};
+      const uint32_t pq = static_cast<uint32_t>(tid & 3) << 4;
+      unit_rest(sum_k[k], ce_k[k], pq);
+      const uint32_t dst = ((ce_k[k][0] >> 16) & 0xff) ? acol + (cur ^ 1) * V5_TILE_BYTES + ((ce_k[k][0] & 0xffffu) ^ pq)
+                                                       : trash;
+      *reinterpret_cast<u32x4*>(smem + dst) = pack_bf16x8(sum_k[k]);
     }
-    for (int item = tid + 512; item < items; item += 256) coll_item(vn, cur ^ 1, item);
+    if (units > 512) build_units(vn, cur ^ 1, 512);
     __syncthreads();
     if (more && v1 == 0) {      // chunk boundary: every MFMA of chunk cc1-1 is done with S
       store_s();
       __syncthreads();
       if (cc1 + 1 < ncc) load_s(cc1 + 1);
-      build_coll(0, cur ^ 1);
+      build_units(0, cur ^ 1, 0);
       __syncthreads();
     }
 #pragma unroll
@@ -307,7 +321,7 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
     // bf16 channels-last output: each wave transposes its 32-row blocks
     // through LDS (the collision tiles, free now) and stores 16-byte pieces,
     // four 256-byte row runs per store instruction
-    uint16_t* E = sm16 + wave * 32 * 128;
+    uint16_t* E = reinterpret_cast<uint16_t*>(smem + acol) + wave * 32 * 128;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -356,7 +370,7 @@ static void launch_v5_sv(const KnnParams& p, int out_t, hipStream_t s) {
   const int64_t padded = (total + 7) / 8 * 8;
   const int ncb = static_cast<int>(n_tiles_n * (V5_NT / 32));
   const size_t lds = v5_layout(static_cast<int>(p.V), static_cast<int>(p.K), p.zero_row, p.coll_off_stride,
-                               p.coll4_stride).total;
+                               p.cent_stride).total;
   // 16-byte channels-last bf16 stores: unit channel stride, rows and base 16-byte aligned
   const int vec_out = out_t == FOVI_BF16 && p.ys1 == 1 && p.ys2 % 8 == 0 && p.ys0 % 8 == 0 && p.Cout % 8 == 0 &&
                       reinterpret_cast<uintptr_t>(p.y) % 16 == 0;
@@ -377,15 +391,15 @@ static void launch_v5_sv(const KnnParams& p, int out_t, hipStream_t s) {
 int v5_applies(const KnnParams& p) {
   if (p.w_layout != FOVI_W_MFMA) return 0;
   if (p.C % V5_CC != 0 || p.zero_row <= 0 || p.zero_row > 1023 || !p.tile_lo || !p.tile_nbr || !p.tile_src ||
-      !p.tile_coll_off || !p.tile_coll4 || p.K > 255 || p.V > 255)
+      !p.tile_coll_off || !p.tile_cent || p.K > 255 || p.V > 255)
     return 0;
-  if (p.coll_off_stride <= p.V || p.coll_off_stride % 4 != 0 || p.coll4_stride < 2 || p.coll4_stride % 2 != 0) return 0;
+  if (p.coll_off_stride <= p.V || p.coll_off_stride % 4 != 0 || p.cent_stride < 1) return 0;
   if ((reinterpret_cast<uintptr_t>(p.tile_src) | reinterpret_cast<uintptr_t>(p.tile_coll_off) |
-       reinterpret_cast<uintptr_t>(p.tile_coll4) | reinterpret_cast<uintptr_t>(p.tile_nbr)) % 16 != 0)
+       reinterpret_cast<uintptr_t>(p.tile_cent) | reinterpret_cast<uintptr_t>(p.tile_nbr)) % 16 != 0)
     return 0;
   if (p.xs1 != 1 || p.xs2 % 8 != 0 || p.xs0 % 8 != 0 || reinterpret_cast<uintptr_t>(p.x) % 16 != 0) return 0;
   if (reinterpret_cast<uintptr_t>(p.w) % 16 != 0) return 0;
-  return v5_layout(static_cast<int>(p.V), static_cast<int>(p.K), p.zero_row, p.coll_off_stride, p.coll4_stride)
+  return v5_layout(static_cast<int>(p.V), static_cast<int>(p.K), p.zero_row, p.coll_off_stride, p.cent_stride)
              .total <= 160 * 1024;
 }
 

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 11
+#define FOVI_ABI_VERSION 12
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -164,20 +164,22 @@ typedef struct fovi_knnconv_args {
   int64_t workspace_bytes;
   const float* x_scale_dev;   /* (F8E4M3 only) device copy of the activation scale, e.g. the one
                                  fovi_quantize_e4m3 writes; used instead of x_scale when non-NULL */
-  /* Tables of the wide-layer kernel (w_layout = FOVI_W_MFMA), in its LDS order:
-   *   tile_src[(t * n_ref + v) * tile_points + r]: staged row (relative to tile_lo[t]) the MFMA
-   *     reads for slot v of row r (the neighbour's, or zero_row for an empty slot), or 0x8000
-   *     when the slot holds two or more neighbours (summed by the kernel);
-   *   tile_coll4[t * coll4_stride + i], i in [tile_coll_off[t * coll_off_stride + v],
-   *     tile_coll_off[t * coll_off_stride + v + 1]): one entry per (slot v, row with two or more
-   *     neighbours): bits 0-7 row, 8-15 count, 16-23 begin in tile_nbr, then the staged rows of
-   *     the first four neighbours in 10-bit fields at bits 24, 34, 44, 54 (zero_row past the
-   *     count). zero_row must be below 1024. */
+  /* Tables of the wide-layer kernel (w_layout = FOVI_W_MFMA), in its LDS order. Staged rows
+   * are named by LDS byte offsets off(r) = 64 r + 16 g(r), g(r) = (bit1(r) ^ bit3(r)) | bit2(r) << 1
+   * (16-byte part q of row r is at off(r) ^ 16 q); zero_row must be below 1024.
+   *   tile_src[(t * n_ref + v) * tile_points + r]: off() of the staged row (relative to
+   *     tile_lo[t]) the MFMA reads for slot v of row r (the neighbour's, or the zero row for an
+   *     empty slot), or 0xFFFF when the slot holds two or more neighbours (summed by the kernel);
+   *   tile_cent[(t * cent_stride + i) * 4 + 0..3], i in [tile_coll_off[t * coll_off_stride + v],
+   *     tile_coll_off[t * coll_off_stride + v + 1]): one 16-byte entry per (slot v, row with two
+   *     or more neighbours), decreasing count within a slot: word 0 = off(row) | count << 16 |
+   *     begin in tile_nbr << 24; words 1, 2 = off() of the first four neighbours' staged rows,
+   *     two 16-bit halves each (the zero row past the count); word 3 = row. */
   const uint16_t* tile_src;
   const int32_t* tile_coll_off;
-  const uint64_t* tile_coll4;
+  const uint32_t* tile_cent;
   int32_t coll_off_stride;    /* multiple of 4, > n_ref */
-  int32_t coll4_stride;       /* even */
+  int32_t cent_stride;        /* entries per tile, >= 1 */
 } fovi_knnconv_args;
 
 int fovi_knnconv_fwd(const fovi_knnconv_args* args, void* stream);

@@ -225,34 +225,38 @@ def test_direct_tables_lists_and_zero_row(res_in, res_out, k):
 
 @pytest.mark.parametrize("res_in,res_out,k", [(32, 32, 25), (64, 32, 49), (16, 16, 9), (128, 128, 25)])
 def test_wide_tables_decode_to_the_csr_lists(res_in, res_out, k):
-    """Fragment-order kernel tables: every (slot, row) source and every packed collision entry
+    """Fragment-order kernel tables: every (slot, row) source and every collision entry
     decodes back to the slot-major CSR lists (global input index = staged row + tile_lo)."""
     t = layer_tables(res_in, res_out, k)
     direct = T.direct_tables(t["idx"], t["slots"], t["n_in"], t["V"])
     lo, span, ent, nbr, coll, coll_n, zr = direct
     wide = T.wide_tables(direct, t["k"])
-    if wide is None:                      # staged-row indices need 10 bits
+    if wide is None:                      # staged-row offsets need 16 bits
         assert zr > 1023
         return
-    src, coll4, coll_off, stride = wide
-    src, coll4, coll_off = src.numpy().astype(np.int64), coll4.numpy().view(np.uint64), coll_off.numpy()
+    src, cent, coll_off, stride = wide
+    src, cent, coll_off = src.numpy().astype(np.int64), cent.numpy().view(np.uint32), coll_off.numpy()
+    # offset -> row: 64-byte rows, swizzle bits only in bits 4-5
+    row_of = {int(T._row_offset(r)): r for r in range(zr + 1)}
+    assert len(row_of) == zr + 1 and all(o & 15 == 0 for o in row_of)
     ptr, gnbr = t["ptr"].numpy(), t["nbr"].numpy()
     lo = lo.numpy().astype(np.int64)
     n_tiles, V = src.shape[0], t["V"]
-    assert coll4.shape == (n_tiles, stride) and stride % 2 == 0
+    assert cent.shape == (n_tiles, stride, 4)
     for tt in range(n_tiles):
         seen = set()
         for v in range(V):
             for ei in range(coll_off[tt, v], coll_off[tt, v + 1]):
-                w = int(coll4[tt, ei])
-                row, cnt, beg = w & 0xFF, (w >> 8) & 0xFF, (w >> 16) & 0xFF
+                w0, w1, w2, row = (int(x) for x in cent[tt, ei])
+                cnt, beg = (w0 >> 16) & 0xFF, w0 >> 24
+                assert row_of[w0 & 0xFFFF] == row
                 n = tt * 256 + row
                 assert cnt >= 2 and cnt == (ptr[n, v] & 0xFFFF) and beg == (ptr[n, v] >> 16)
-                rs = [(w >> (24 + 10 * j)) & 0x3FF for j in range(4)]
+                rs = [row_of[o] for o in (w1 & 0xFFFF, w1 >> 16, w2 & 0xFFFF, w2 >> 16)]
                 want = list(gnbr[n, beg:beg + min(cnt, 4)])
                 assert [r + lo[tt] for r in rs[:len(want)]] == want
                 assert all(r == zr for r in rs[len(want):])
-                assert src[tt, v, row] == 0x8000
+                assert src[tt, v, row] == 0xFFFF
                 seen.add((v, row))
         for v in range(V):
             for row in range(256):
@@ -261,4 +265,5 @@ def test_wide_tables_decode_to_the_csr_lists(res_in, res_out, k):
                     continue
                 cnt = ptr[n, v] & 0xFFFF
                 assert cnt <= 1
-                assert src[tt, v, row] == (gnbr[n, ptr[n, v] >> 16] - lo[tt] if cnt == 1 else zr)
+                want = gnbr[n, ptr[n, v] >> 16] - lo[tt] if cnt == 1 else zr
+                assert row_of[src[tt, v, row]] == want
