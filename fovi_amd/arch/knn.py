@@ -241,12 +241,12 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
 
     def _mfma_lds_bytes(self):
         """LDS bytes of the fragment-order kernel's tile (its ``v5_layout``): the staged rows plus
-        the zero row (64 bytes each), 128-byte alignment, two 256 x 32 bf16 collision tiles and a
-        trash row, per-(slot, row) sources, per-slot entry offsets, 16-byte collision entries,
-        neighbour lists."""
+        the zero row (64 bytes each), 128-byte alignment, three 256 x 32 bf16 collision tiles
+        and a trash row, per-(slot, row) sources, per-slot entry offsets, 16-byte collision
+        entries, neighbour lists."""
         v, k = self.ref_coords.shape[0], self._k
         o = ((self._zero_row + 1) * 64 + 127) & ~127
-        return o + (2 * 256 + 1) * 32 * 2 + v * 256 * 2 + self._coll_off_stride * 4 + self._cent_stride * 16 + 256 * k * 2
+        return o + (3 * 256 + 1) * 32 * 2 + v * 256 * 2 + self._coll_off_stride * 4 + self._cent_stride * 16 + 256 * k * 2
 
     def _mfma_path(self, x, dt):
         """Whether this call runs the fragment-order kernel (see ``mfma_weights``)."""

@@ -279,7 +279,7 @@ def wide_tables(direct, k):
       bits 0-15 the row's offset in a collision tile, 16-23 count, 24-31
       begin (in the ``tile_nbr`` list of the row); words 1-2: offsets of the
       first four neighbours' staged rows, two per word (low half first; the
-      zero row past the count); word 3: the row;
+      zero row past the count); word 3: the row, and the slot at bits 8-15;
     * ``coll_off [T, V + 1 rounded up to 4] int32``: slot v's entries are
       ``coll[t, coll_off[t, v]:coll_off[t, v + 1]]``.
 
@@ -322,5 +322,5 @@ def wide_tables(direct, k):
         out[t, :n_e, 0] = (_row_offset(rows) | (c << 16) | (b << 24)).astype(np.uint32)
         out[t, :n_e, 1] = (nbo[0] | (nbo[1] << 16)).astype(np.uint32)
         out[t, :n_e, 2] = (nbo[2] | (nbo[3] << 16)).astype(np.uint32)
-        out[t, :n_e, 3] = rows.astype(np.uint32)
+        out[t, :n_e, 3] = (rows | (slot << 8)).astype(np.uint32)
     return (torch.from_numpy(src), torch.from_numpy(out.view(np.int32)), torch.from_numpy(coll_off), stride)

@@ -12,8 +12,9 @@
 //    chunk at a time (S); the next chunk is loaded into registers while the
 //    current one is consumed. MFMA lanes read single-neighbour slots straight
 //    from S (an LDS zero row serves empty slots); slots with two or more
-//    neighbours are summed in fp32 (one RNE rounding) into a double-buffered
-//    collision tile one iteration ahead, from per-(tile, slot) row lists.
+//    neighbours are summed in fp32 (one RNE rounding) into a ring of three
+//    collision tiles, up to two slots ahead, as a stream over the tile's
+//    collision entries that advances a fixed 256 units per iteration.
 //  * Weights are not staged in LDS: fovi_knnconv_pack_weight_mfma stores
 //    them in the order the MFMA B operand is consumed, so each lane loads its
 //    16-byte fragment with one coalesced load (1 KB per wave and fragment)
@@ -28,6 +29,7 @@ namespace fovi {
 constexpr int V5_MT = 256;   // output points per tile
 constexpr int V5_NT = 256;   // output channels per tile
 constexpr int V5_CC = 32;    // channels per reduction chunk (one 64-byte LDS row)
+constexpr int V5_NB = 3;     // collision tiles: slot v uses tile v % 3, so sums run up to two slots ahead
 
 // LDS byte layout of a tile. The staged rows S come first, at offset 0, so
 // the host tables can hold absolute LDS byte offsets of staged rows.
@@ -39,7 +41,7 @@ __host__ __device__ inline V5Layout v5_layout(int V, int K, int zero_row, int co
   V5Layout l;
   int o = (zero_row + 1) * V5_CC * 2;               // staged rows + zero row
   o = (o + 127) & ~127;
-  l.acol_off = o;   o += (2 * V5_MT + 1) * V5_CC * 2; // two 256 x 32 bf16 collision tiles + a trash row
+  l.acol_off = o;   o += (V5_NB * V5_MT + 1) * V5_CC * 2; // V5_NB 256 x 32 bf16 collision tiles + a trash row
   l.src_off = o;    o += V * V5_MT * 2;             // per (slot, row) A source, slot-major
   l.coff_off = o;   o += coff_stride * 4;           // per-slot collision entry offsets
   l.cent_off = o;   o += cent_stride * 16;          // collision entries
@@ -88,7 +90,7 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
   const u32x4* cent = reinterpret_cast<const u32x4*>(smem + L.cent_off);
   const uint16_t* nbl = reinterpret_cast<const uint16_t*>(smem + L.nbl_off);
   const uint32_t acol = static_cast<uint32_t>(L.acol_off);
-  const uint32_t trash = acol + 2 * V5_TILE_BYTES;
+  const uint32_t trash = acol + V5_NB * V5_TILE_BYTES;
 
   const int64_t tile = xcd_tile(blockIdx.x, padded_tiles);
   if (tile >= total_tiles) return;
@@ -194,20 +196,24 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
   auto unit_rest = [&](f32x8& a, const u32x4 ce, uint32_t pq) {
     const int cnt = static_cast<int>((ce[0] >> 16) & 0xff);
     if (cnt > 4) {
-      const uint16_t* nb = nbl + static_cast<int>(ce[3]) * K + static_cast<int>(ce[0] >> 24);
+      const uint16_t* nb = nbl + static_cast<int>(ce[3] & 0xffu) * K + static_cast<int>(ce[0] >> 24);
       for (int j = 4; j < cnt; ++j) acc_bf16x8(a, lds16(smem, row_off(nb[j]) ^ pq));
     }
   };
-  // every unit of slot v's list, into collision tile buf (chunk boundaries and
-  // the tail of long lists)
-  auto build_units = [&](int v, int buf, int first) {
-    const int c0 = coff[v], units = (coff[v + 1] - c0) * 4;
-    for (int u = first + tid; u < units; u += 256) {
-      const u32x4 ce = cent[c0 + (u >> 2)];
+  // collision tile offset of a unit: tile slot % 3 (slot in entry word 3)
+  auto unit_dst = [&](const u32x4 ce, uint32_t pq) {
+    const uint32_t slot = (ce[3] >> 8) & 0xffu;
+    return acol + (slot % V5_NB) * V5_TILE_BYTES + ((ce[0] & 0xffffu) ^ pq);
+  };
+  // units [from, to) of the tile's unit stream (the entry list in slot order,
+  // four 16-byte parts per entry), complete sums; from % 4 == 0
+  auto build_range = [&](int from, int to) {
+    for (int u = from + tid; u < to; u += 256) {
+      const u32x4 ce = cent[u >> 2];
       const uint32_t pq = static_cast<uint32_t>(u & 3) << 4;
       f32x8 a = unit_sum4(ce, pq);
       unit_rest(a, ce, pq);
-      *reinterpret_cast<u32x4*>(smem + acol + buf * V5_TILE_BYTES + ((ce[0] & 0xffffu) ^ pq)) = pack_bf16x8(a);
+      *reinterpret_cast<u32x4*>(smem + unit_dst(ce, pq)) = pack_bf16x8(a);
     }
   };
 
@@ -229,54 +235,56 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
   }
   const uint32_t qx = static_cast<uint32_t>(lane >> 5) << 4;   // 16-byte part of ks = 0
 
-  u32x4 bcur[8], bnxt[8];
-  load_w(0, bcur);
+  u32x4 wa[8], wb[8];
+  load_w(0, wa);
   store_s();
   if (ncc > 1) load_s(1);
   __syncthreads();
-  build_units(0, 0, 0);
+  // Collision sums run as a stream over the tile's entry list (units in slot
+  // order): every iteration takes the next 256 units (one per thread,
+  // straight-line code interleaved with its MFMAs) of slots up to two ahead
+  // of the one it consumes, so heavy and light slots even out. A chunk starts
+  // with its slot 0 built; a slot not yet complete when its turn comes is
+  // finished first (uniform branch). Masked units write a trash row; entries
+  // with more than four neighbours finish after the MFMAs.
+  int bpos = 4 * coff[1];
+  build_range(0, bpos);
   uint32_t ecur[4], enxt[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) ecur[i] = srcs[rowm[i]];
   __syncthreads();
 
-  // The next iteration's collision sums are straight-line code interleaved
-  // with this iteration's MFMAs: units tid and tid + 256 (entries 0 .. 127 of
-  // the slot's list); masked units write a trash row; entries with more than
-  // four neighbours (the head of the list, sorted by count) finish after the
-  // MFMAs, and lists longer than 128 entries in build_units.
-  int cc1 = 0, v1 = 0;
+  int v = 0, cc = 0;
+  uint32_t vb = 0;   // v % V5_NB
   for (int it = 0; it < nit; ++it) {
-    const int cur = it & 1;
-    if (++v1 == V) { v1 = 0; ++cc1; }
+    u32x4(&bc)[8] = wa;   // this iteration's weight fragments
+    u32x4(&bn)[8] = wb;   // the next iteration's
+    const int need = 4 * coff[v + 1];
+    if (bpos < need) {            // slot v incomplete: finish it
+      build_range(bpos, need);
+      bpos = need;
+      __syncthreads();
+    }
+    const int lim = 4 * coff[min(v + V5_NB, V)];
     const bool more = it + 1 < nit;
-    const int itn = more ? it + 1 : it;
-    const int vn = v1;   // slot of the next iteration (chunk boundaries build after the S refresh)
-    const int c0 = coff[vn];
-    const int units = (more && v1 != 0) ? (coff[vn + 1] - c0) * 4 : 0;
+    const int vn = v + 1 == V ? 0 : v + 1;
 
     bf16x8 af[2][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t a = ecur[i] == 0xffffu ? rowm_off[i] + cur * V5_TILE_BYTES : ecur[i];
+      const uint32_t a = ecur[i] == 0xffffu ? rowm_off[i] + vb * V5_TILE_BYTES : ecur[i];
       af[0][i] = __builtin_bit_cast(bf16x8, lds16(smem, a ^ qx));
       af[1][i] = __builtin_bit_cast(bf16x8, lds16(smem, a ^ qx ^ 32u));
     }
-
-    load_w(itn, bnxt);
+    load_w(more ? it + 1 : it, bn);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) enxt[i] = srcs[v1 * V5_MT + rowm[i]];
+    for (int i = 0; i < 4; ++i) enxt[i] = srcs[vn * V5_MT + rowm[i]];
 
-    u32x4 ce_k[2];
-    f32x8 sum_k[2];
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int u = tid + 256 * k;
-      u32x4 ce = cent[u < units ? c0 + (u >> 2) : 0];
-      if (u >= units) ce[0] = 0;   // count 0: written to the trash row
-      ce_k[k] = ce;
-      sum_k[k] = unit_sum4(ce, static_cast<uint32_t>(tid & 3) << 4);
-    }
+    const int u = bpos + tid;
+    const uint32_t pq = static_cast<uint32_t>(tid & 3) << 4;
+    u32x4 ce = cent[u < lim ? (u >> 2) : 0];
+    if (u >= lim) ce[0] = 0;      // count 0: written to the trash row
+    f32x8 sum = unit_sum4(ce, pq);
 
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
@@ -284,30 +292,31 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks][i], __builtin_bit_cast(bf16x8, bcur[j * 2 + ks]),
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks][i], __builtin_bit_cast(bf16x8, bc[j * 2 + ks]),
                                                               acc[i][j], 0, 0, 0);
 
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const uint32_t pq = static_cast<uint32_t>(tid & 3) << 4;
-      unit_rest(sum_k[k], ce_k[k], pq);
-      const uint32_t dst = ((ce_k[k][0] >> 16) & 0xff) ? acol + (cur ^ 1) * V5_TILE_BYTES + ((ce_k[k][0] & 0xffffu) ^ pq)
-                                                       : trash;
-      *reinterpret_cast<u32x4*>(smem + dst) = pack_bf16x8(sum_k[k]);
-    }
-    if (units > 512) build_units(vn, cur ^ 1, 512);
+    unit_rest(sum, ce, pq);
+    *reinterpret_cast<u32x4*>(smem + (((ce[0] >> 16) & 0xffu) ? unit_dst(ce, pq) : trash)) = pack_bf16x8(sum);
+    bpos = min(bpos + 256, lim);
     __syncthreads();
-    if (more && v1 == 0) {      // chunk boundary: every MFMA of chunk cc1-1 is done with S
-      store_s();
-      __syncthreads();
-      if (cc1 + 1 < ncc) load_s(cc1 + 1);
-      build_units(0, cur ^ 1, 0);
-      __syncthreads();
+    v = vn;
+    vb = vb + 1 == V5_NB ? 0 : vb + 1;
+    if (v == 0) {                 // chunk boundary
+      vb = 0;
+      ++cc;
+      if (more) {                 // every MFMA of the finished chunk is done with S
+        store_s();
+        __syncthreads();
+        if (cc + 1 < ncc) load_s(cc + 1);
+        bpos = 4 * coff[1];
+        build_range(0, bpos);
+        __syncthreads();
+      }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) ecur[i] = enxt[i];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) bcur[k] = bnxt[k];
+    for (int k = 0; k < 8; ++k) wa[k] = wb[k];
   }
 
   OutT* y = static_cast<OutT*>(p.y) + b * p.ys0;

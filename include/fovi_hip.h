@@ -174,7 +174,7 @@ typedef struct fovi_knnconv_args {
    *     tile_coll_off[t * coll_off_stride + v + 1]): one 16-byte entry per (slot v, row with two
    *     or more neighbours), decreasing count within a slot: word 0 = off(row) | count << 16 |
    *     begin in tile_nbr << 24; words 1, 2 = off() of the first four neighbours' staged rows,
-   *     two 16-bit halves each (the zero row past the count); word 3 = row. */
+   *     two 16-bit halves each (the zero row past the count); word 3 = row | slot << 8. */
   const uint16_t* tile_src;
   const int32_t* tile_coll_off;
   const uint32_t* tile_cent;

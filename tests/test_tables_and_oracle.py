@@ -247,7 +247,9 @@ def test_wide_tables_decode_to_the_csr_lists(res_in, res_out, k):
         seen = set()
         for v in range(V):
             for ei in range(coll_off[tt, v], coll_off[tt, v + 1]):
-                w0, w1, w2, row = (int(x) for x in cent[tt, ei])
+                w0, w1, w2, w3 = (int(x) for x in cent[tt, ei])
+                row = w3 & 0xFF
+                assert w3 >> 8 == v
                 cnt, beg = (w0 >> 16) & 0xFF, w0 >> 24
                 assert row_of[w0 & 0xFFFF] == row
                 n = tt * 256 + row
