@@ -238,6 +238,31 @@ def bench_c4_frontend(steps, warmup, dev):
                 patch_embed_tflops=flops / (ms_pe * 1e-3) / 1e12)
 
 
+def copy_probe(dev, mib=256, reps=3):
+    """A plain device copy of known size (``mib`` MiB read + written per launch):
+    the calibration kernel for rocprofv3 FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+    x = torch.empty(mib << 20, dtype=torch.uint8, device=dev)
+    y = torch.empty_like(x)
+    for _ in range(reps):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    log(f"[copy] {reps} copies of {mib} MiB")
+
+
+def measured_traffic(kernel_prefix):
+    """HBM bytes per launch of the named kernel from the committed rocprofv3
+    counter summary (profiles/hbm_traffic.json), or None."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    k = rec.get("kernels", {}).get(kernel_prefix)
+    return None if k is None else int(k["fetch_bytes"] + k["write_bytes"])
+
+
 def cpu_baseline_c3(c3, seconds_budget=25.0):
     """Oracle (torch CPU fp32 restatement of knn.py:484-557) on a B=2 slice of C3."""
     import torch
@@ -285,12 +310,12 @@ def main():
     ap.add_argument("--no-sampler", action="store_true")
     ap.add_argument("--no-e2e", action="store_true", help="skip the C2/C4 end-to-end legs")
     ap.add_argument("--no-fp8", action="store_true", help="skip the C5 fp8 leg")
-    ap.add_argument("--only", default="", help="comma list of legs to run (c3,c5,sampler,c2,c4,cpu); "
+    ap.add_argument("--only", default="", help="comma list of legs to run (c3,c5,sampler,c2,c4,cpu,copy); "
                                                 "for profiling runs, the JSON line then holds only those legs")
     args = ap.parse_args()
     if args.only:
         legs = set(args.only.split(","))
-        unknown = legs - {"c3", "c5", "sampler", "c2", "c4", "cpu"}
+        unknown = legs - {"c3", "c5", "sampler", "c2", "c4", "cpu", "copy"}
         if unknown:
             ap.error(f"unknown legs {sorted(unknown)}")
         if legs & {"c5", "cpu"}:
@@ -303,7 +328,7 @@ def main():
         legs = {"c3", "c5", "sampler", "c2", "c4", "cpu"}
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              f"(the forward shards over batch with no communication, see DESIGN.md)", file=sys.stderr)
+              f"(the forward would shard over the batch with no communication)", file=sys.stderr)
         sys.exit(2)
     import torch
     dev = torch.device("cuda:0")
@@ -314,6 +339,8 @@ def main():
     c2 = None if args.no_e2e or "c2" not in legs else bench_c2(args.steps, args.warmup, dev)
     c4e = None if args.no_e2e or "c4" not in legs else bench_c4_frontend(args.steps, args.warmup, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline_c3(c3)
+    if "copy" in legs and args.only:
+        copy_probe(dev)
     if c3 is None:
         c3 = {"tflops": float("nan"), "ms": float("nan")}
     line = {
@@ -333,7 +360,8 @@ def main():
                                "k=25, V=25, C_in=C_out=256, bf16 in/out, fp32 accumulate",
                    "batch": 64, "points": 16384, "k": 25, "c_in": 256, "c_out": 256},
         "roofline": {"bound": "mfma", "achieved": round(c3["tflops"], 2), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(c3["tflops"] / PEAK_BF16_TFLOPS, 4), "traffic": None},
+                     "unit": "TFLOP/s", "frac": round(c3["tflops"] / PEAK_BF16_TFLOPS, 4),
+                     "traffic": measured_traffic("knnconv_bf16_v5_kernel")},
         "cpu_baseline": cpu,
     }
     if c5 is not None:
@@ -351,7 +379,9 @@ def main():
                         "ms": round(c4["ms"], 4), "images/s": round(c4["images_per_s"], 1)},
             "bilinear": {"GB/s": round(c4b["gbs"], 1), "frac": round(c4b["gbs"] / PEAK_HBM_GBS, 4),
                          "ms": round(c4b["ms"], 4), "images/s": round(c4b["images_per_s"], 1)},
-            "roofline": {"bound": "hbm", "peak": PEAK_HBM_GBS, "unit": "GB/s"},
+            "roofline": {"bound": "hbm", "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "traffic": {"nearest": measured_traffic("sampler_rings_kernel<bf16,nearest>"),
+                                     "bilinear": measured_traffic("sampler_rings_kernel<bf16,bilinear>")}},
         }
     if c2 is not None:
         line["c2_alexnet"] = {"workload": "C2: 256 images 3x224x224 -> bilinear sampler (4096 pts) -> 5 kNN-conv "
