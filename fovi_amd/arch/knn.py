@@ -135,16 +135,14 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         if tiles is not None:
             self._max_span = int(tiles[1].max())
             self._zero_row = tiles[6]
-        # tables of the wide-layer (fragment-order weight) kernel
-        wide = T.wide_tables(tiles, self._k) if tiles is not None else None
-        self._cent_stride = 0
-        self._coll_off_stride = 0
-        for name, t in zip(("tile_src", "tile_cent", "tile_coll_off"), wide[:3] if wide is not None else (None,) * 3):
-            self.register_buffer(name, None if t is None else t.to(device), persistent=False)
-        if wide is not None:
-            self._cent_stride = wide[3]
-            self._coll_off_stride = int(wide[2].shape[1])
+        # tables of the wide-layer (fragment-order weight) kernel, in a slot-visit order
+        # that spreads the heavy slots' collision sums over the stream
+        self._direct_tables = tiles
         self._packed = {}
+        order = None
+        if tiles is not None:
+            order = T.stream_slot_order(4 * tiles[5].numpy().astype(np.int64))
+        self.set_slot_order(order)
         # slot-sum headroom of the fp8 path: the largest neighbour count of a slot
         self._max_slot_count = int((slot_ptr & 0xFFFF).max()) if slot_ptr.numel() else 1
         # quantize every input to e4m3 and run the fp8 kernel
@@ -219,8 +217,28 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         self._packed[(dtype, c_slot)] = (key, packed)
         return packed
 
+    def set_slot_order(self, order=None):
+        """Order in which the wide-layer kernel visits the slots of a channel chunk (a
+        permutation of range(V); None = 0, 1, ...). The sum over slots does not depend on it;
+        the order 0, 1, ... gives results bit-identical to the row-packed kernels."""
+        tiles = self._direct_tables
+        wide = T.wide_tables(tiles, self._k, order) if tiles is not None else None
+        self._cent_stride = 0
+        self._coll_off_stride = 0
+        dev = self.weight.device
+        for name, t in zip(("tile_src", "tile_cent", "tile_coll_off"), wide[:3] if wide is not None else (None,) * 3):
+            self.register_buffer(name, None if t is None else t.to(dev), persistent=False)
+        if wide is not None:
+            self._cent_stride = wide[3]
+            self._coll_off_stride = int(wide[2].shape[1])
+        self.slot_order = None if order is None else [int(v) for v in order]
+        self._slot_order_dev = None if order is None else torch.tensor(self.slot_order, dtype=torch.int32,
+                                                                          device=dev)
+        self._packed.pop("mfma", None)
+
     def _packed_weight_mfma(self):
-        """bf16 weight in MFMA-fragment order (``fovi_knnconv_pack_weight_mfma``), cached per version."""
+        """bf16 weight in MFMA-fragment order (``fovi_knnconv_pack_weight_mfma``) for the current
+        slot order, cached per weight version."""
         w = self.weight
         key = ("mfma", w._version, w.data_ptr())
         hit = self._packed.get("mfma")
@@ -234,7 +252,8 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         src = w.detach().to(torch.float32).contiguous()
         out = torch.empty(n, dtype=torch.bfloat16, device=w.device)
         _lib.check(lib.fovi_knnconv_pack_weight_mfma(_lib.ptr(src), self.out_channels, self.in_channels, n_ref,
-                                                     _lib.ptr(out), _lib.BF16, _lib.stream_handle(w.device)),
+                                                     _lib.ptr(out), _lib.BF16, _lib.ptr(self._slot_order_dev),
+                                                     _lib.stream_handle(w.device)),
                    "fovi_knnconv_pack_weight_mfma")
         self._packed["mfma"] = (key, out)
         return out

@@ -263,7 +263,7 @@ def _row_offset(r):
     return r * 64 + (g << 4)
 
 
-def wide_tables(direct, k):
+def wide_tables(direct, k, order=None):
     """Tables of the wide-layer (fragment-order) kernel, derived from ``direct_tables``.
 
     Laid out in the kernel's LDS order (16-byte copies) and holding swizzled
@@ -283,6 +283,10 @@ def wide_tables(direct, k):
     * ``coll_off [T, V + 1 rounded up to 4] int32``: slot v's entries are
       ``coll[t, coll_off[t, v]:coll_off[t, v + 1]]``.
 
+    ``order`` (default: slot order) is the order in which the kernel visits
+    the slots (``stream_slot_order``): the tables are laid out by position p
+    in that order, slot ``order[p]``, and an entry's slot field holds p.
+
     Returns ``(src, coll, coll_off, stride)`` or ``None`` when zero_row does
     not fit the 16-bit offsets (above 1023) or k exceeds 255.
     """
@@ -293,10 +297,13 @@ def wide_tables(direct, k):
     n_tiles, n_ref, tile = coll.shape
     first = e >> 16
     cnt = (e >> 8) & 0xFF
+    order = np.arange(n_ref) if order is None else np.asarray(order, np.int64)
+    if sorted(order.tolist()) != list(range(n_ref)):
+        raise ValueError("order must be a permutation of the slots")
     src = np.where(cnt >= 2, 0xFFFF, _row_offset(first)).astype(np.uint16)
-    src = src.reshape(n_tiles, tile, n_ref).transpose(0, 2, 1).copy()
+    src = src.reshape(n_tiles, tile, n_ref).transpose(0, 2, 1)[:, order].copy()
     nb = nbr.numpy().astype(np.int64).reshape(n_tiles, tile, k)
-    cn = coll_n.numpy().astype(np.int64)
+    cn = coll_n.numpy().astype(np.int64)[:, order]
     counts = cn.sum(axis=1)
     stride = int(max(1, int(counts.max()))) if n_tiles else 1
     voff = -(-(n_ref + 1) // 4) * 4
@@ -309,9 +316,9 @@ def wide_tables(direct, k):
         coll_off[t, :n_ref + 1] = off
         if off[-1] == 0:
             continue
-        rows = np.concatenate([cl[t, v, :cn[t, v]] for v in range(n_ref)])
-        slot = np.repeat(np.arange(n_ref), cn[t])
-        eb = e.reshape(n_tiles, tile, n_ref)[t, rows, slot]
+        rows = np.concatenate([cl[t, order[q], :cn[t, q]] for q in range(n_ref)])
+        pos = np.repeat(np.arange(n_ref), cn[t])
+        eb = e.reshape(n_tiles, tile, n_ref)[t, rows, order[pos]]
         c = (eb >> 8) & 0xFF
         b = eb & 0xFF
         nbo = [_row_offset(eb >> 16)]
@@ -322,5 +329,53 @@ def wide_tables(direct, k):
         out[t, :n_e, 0] = (_row_offset(rows) | (c << 16) | (b << 24)).astype(np.uint32)
         out[t, :n_e, 1] = (nbo[0] | (nbo[1] << 16)).astype(np.uint32)
         out[t, :n_e, 2] = (nbo[2] | (nbo[3] << 16)).astype(np.uint32)
-        out[t, :n_e, 3] = (rows | (slot << 8)).astype(np.uint32)
+        out[t, :n_e, 3] = (rows | (pos << 8)).astype(np.uint32)
     return (torch.from_numpy(src), torch.from_numpy(out.view(np.int32)), torch.from_numpy(coll_off), stride)
+
+
+def stream_slot_order(units_per_slot, rate=256, ahead=3, iters=600, seed=0):
+    """Order in which the wide-layer kernel visits the slots of a channel chunk.
+
+    The kernel forms collision sums as a stream that advances ``rate`` units
+    per slot visit, up to ``ahead - 1`` slots ahead of the slot being
+    consumed; a slot not complete at its turn is finished serially, and the
+    first slot of a chunk is always built serially. ``units_per_slot [T, V]``
+    is the stream demand of each (tile, slot). Heavy and light slots are
+    interleaved (light first), then refined by pairwise swaps that lower the
+    mean serialized work over the tiles. The sum over slots does not depend
+    on the order. Returns a list of V slot indices.
+    """
+    units = np.asarray(units_per_slot, np.int64)
+    n_tiles, n_ref = units.shape
+    if n_ref <= 2:
+        return list(range(n_ref))
+
+    def cost(order):
+        u = units[:, order]
+        off = np.concatenate([np.zeros((n_tiles, 1), np.int64), np.cumsum(u, axis=1)], axis=1)
+        bpos = off[:, 1].copy()
+        serial = off[:, 1].astype(np.float64)
+        for v in range(n_ref):
+            need = off[:, v + 1]
+            serial += np.maximum(need - bpos, 0)
+            bpos = np.minimum(np.maximum(bpos, need) + rate, off[:, min(v + ahead, n_ref)])
+        return float(serial.mean())
+
+    by_load = list(np.argsort(-units.mean(axis=0), kind="stable"))
+    order, lo, hi = [], 0, n_ref - 1
+    while lo <= hi:
+        order.append(int(by_load[hi])); hi -= 1          # light
+        if lo <= hi:
+            order.append(int(by_load[lo])); lo += 1      # heavy
+    best = cost(order)
+    rng = np.random.default_rng(seed)
+    for _ in range(iters):
+        a, b = rng.integers(0, n_ref, 2)
+        if a == b:
+            continue
+        cand = order[:]
+        cand[a], cand[b] = cand[b], cand[a]
+        c = cost(cand)
+        if c <= best:
+            order, best = cand, c
+    return order

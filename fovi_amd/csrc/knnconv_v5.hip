@@ -423,10 +423,11 @@ int launch_knnconv_bf16_v5(const KnnParams& p, int out_t, hipStream_t s) {
 }
 
 // Fragment-order weight: fragment (it, cb, ks) holds, for lane l and e < 8,
-// w[o = cb * 32 + l % 32][c * n_ref + v] with it = (c / 32) * n_ref + v and
-// c % 32 = ks * 16 + (l / 32) * 8 + e (zero for o >= c_out).
+// w[o = cb * 32 + l % 32][c * n_ref + v] with it = (c / 32) * n_ref + p, slot
+// v = order[p] (v = p without an order) and c % 32 = ks * 16 + (l / 32) * 8 + e
+// (zero for o >= c_out).
 __global__ void pack_weight_mfma_kernel(const float* w_ref, int64_t c_out, int64_t c_in, int64_t n_ref,
-                                        uint16_t* out, int64_t ncb, int64_t total) {
+                                        uint16_t* out, int64_t ncb, int64_t total, const int32_t* order) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (idx >= total) return;
   const int e = static_cast<int>(idx & 7);
@@ -435,7 +436,8 @@ __global__ void pack_weight_mfma_kernel(const float* w_ref, int64_t c_out, int64
   const int ks = static_cast<int>(frag & 1);
   const int64_t cb = (frag >> 1) % ncb;
   const int64_t it = (frag >> 1) / ncb;
-  const int64_t v = it % n_ref, cc = it / n_ref;
+  const int64_t pos = it % n_ref, cc = it / n_ref;
+  const int64_t v = order ? order[pos] : pos;
   const int64_t o = cb * 32 + (l & 31);
   const int64_t c = cc * V5_CC + ks * 16 + (l >> 5) * 8 + e;
   const float val = o < c_out ? w_ref[o * c_in * n_ref + c * n_ref + v] : 0.0f;
@@ -452,7 +454,8 @@ extern "C" int64_t fovi_knnconv_weight_mfma_elems(int64_t c_out, int64_t c_in, i
 }
 
 extern "C" int fovi_knnconv_pack_weight_mfma(const float* w_ref, int64_t c_out, int64_t c_in, int64_t n_ref,
-                                             void* w_frag, int32_t out_dtype, void* stream) {
+                                             void* w_frag, int32_t out_dtype, const int32_t* slot_order,
+                                             void* stream) {
   using namespace fovi;
   clear_error();
   if (!w_ref || !w_frag) { set_error("fovi_knnconv_pack_weight_mfma: null pointer"); return 1; }
@@ -466,6 +469,6 @@ extern "C" int fovi_knnconv_pack_weight_mfma(const float* w_ref, int64_t c_out, 
   const int64_t ncb = (c_out + V5_NT - 1) / V5_NT * (V5_NT / 32);
   hipLaunchKernelGGL(pack_weight_mfma_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), w_ref, c_out, c_in, n_ref, static_cast<uint16_t*>(w_frag),
-                     ncb, total);
+                     ncb, total, slot_order);
   return check_launch("fovi_knnconv_pack_weight_mfma");
 }

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 12
+#define FOVI_ABI_VERSION 13
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -207,10 +207,15 @@ int fovi_knnconv_pack_weight(const float* w_ref, int64_t c_out, int64_t c_in, in
  * ncb = 8 * ceil(c_out / 256); lane l of fragment f holds, at 8 * l + e,
  * w_ref[o = 32 * cb + l % 32][c * n_ref + v] with c % 32 = 16 * ks + 8 * (l / 32) + e
  * (zero for o >= c_out). c_in must be a multiple of 32; only BF16 output.
+ * slot_order (device int32 [n_ref], or NULL for 0, 1, ...) is the order in
+ * which the kernel visits the slots of a channel chunk: position p of
+ * iteration it = (c / 32) * n_ref + p holds slot v = slot_order[p]. The
+ * wide-layer tables (tile_src, tile_cent, tile_coll_off) must be laid out in
+ * the same order, their slot fields holding positions.
  */
 int64_t fovi_knnconv_weight_mfma_elems(int64_t c_out, int64_t c_in, int64_t n_ref);
 int fovi_knnconv_pack_weight_mfma(const float* w_ref, int64_t c_out, int64_t c_in, int64_t n_ref,
-                                  void* w_frag, int32_t out_dtype, void* stream);
+                                  void* w_frag, int32_t out_dtype, const int32_t* slot_order, void* stream);
 
 /*
  * Per-tensor OCP e4m3 quantization of activations for the fp8 kNN-conv path

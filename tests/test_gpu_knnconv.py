@@ -248,8 +248,15 @@ def test_fragment_order_kernel(res_in, res_out, k, c_in, c_out, bias, act, batch
     if act:
         ref = torch.relu(ref)
     assert_close_rel(y.float().cpu(), ref, 1e-2, "fragment-order kernel vs oracle")
-    # same fp32 slot sums (in list order, one rounding) and the same MFMA accumulation order
-    assert torch.equal(y, y_rows), "fragment-order and row-packed kernels differ"
+    assert_close_rel(y.float().cpu(), y_rows.float().cpu(), 1e-2, "fragment-order vs row-packed kernel")
+    # visiting the slots in order 0, 1, ...: the same fp32 slot sums (in list order, one
+    # rounding) and the same MFMA accumulation order as the row-packed kernel, bit for bit
+    layer.mfma_weights = True
+    layer.set_slot_order(None)
+    with torch.no_grad():
+        y_plain = layer.forward_fused(xd, act) if act else layer(xd)
+    assert layer.last_weight_layout == "mfma"
+    assert torch.equal(y_plain, y_rows), "fragment-order (plain slot order) and row-packed kernels differ"
 
 
 def test_fragment_order_kernel_falls_back_when_tables_exceed_lds():

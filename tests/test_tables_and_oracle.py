@@ -223,14 +223,16 @@ def test_direct_tables_lists_and_zero_row(res_in, res_out, k):
             assert np.all(np.diff(c) <= 0)          # decreasing count order
 
 
-@pytest.mark.parametrize("res_in,res_out,k", [(32, 32, 25), (64, 32, 49), (16, 16, 9), (128, 128, 25)])
-def test_wide_tables_decode_to_the_csr_lists(res_in, res_out, k):
+@pytest.mark.parametrize("res_in,res_out,k,permute", [(32, 32, 25, False), (64, 32, 49, False), (16, 16, 9, False),
+                                                      (128, 128, 25, False), (32, 32, 25, True)])
+def test_wide_tables_decode_to_the_csr_lists(res_in, res_out, k, permute):
     """Fragment-order kernel tables: every (slot, row) source and every collision entry
     decodes back to the slot-major CSR lists (global input index = staged row + tile_lo)."""
     t = layer_tables(res_in, res_out, k)
     direct = T.direct_tables(t["idx"], t["slots"], t["n_in"], t["V"])
     lo, span, ent, nbr, coll, coll_n, zr = direct
-    wide = T.wide_tables(direct, t["k"])
+    order = list(np.random.default_rng(3).permutation(t["V"])) if permute else list(range(t["V"]))
+    wide = T.wide_tables(direct, t["k"], order if permute else None)
     if wide is None:                      # staged-row offsets need 16 bits
         assert zr > 1023
         return
@@ -245,11 +247,12 @@ def test_wide_tables_decode_to_the_csr_lists(res_in, res_out, k):
     assert cent.shape == (n_tiles, stride, 4)
     for tt in range(n_tiles):
         seen = set()
-        for v in range(V):
-            for ei in range(coll_off[tt, v], coll_off[tt, v + 1]):
+        for pos in range(V):
+            v = order[pos]
+            for ei in range(coll_off[tt, pos], coll_off[tt, pos + 1]):
                 w0, w1, w2, w3 = (int(x) for x in cent[tt, ei])
                 row = w3 & 0xFF
-                assert w3 >> 8 == v
+                assert w3 >> 8 == pos
                 cnt, beg = (w0 >> 16) & 0xFF, w0 >> 24
                 assert row_of[w0 & 0xFFFF] == row
                 n = tt * 256 + row
@@ -258,9 +261,10 @@ def test_wide_tables_decode_to_the_csr_lists(res_in, res_out, k):
                 want = list(gnbr[n, beg:beg + min(cnt, 4)])
                 assert [r + lo[tt] for r in rs[:len(want)]] == want
                 assert all(r == zr for r in rs[len(want):])
-                assert src[tt, v, row] == 0xFFFF
+                assert src[tt, pos, row] == 0xFFFF
                 seen.add((v, row))
-        for v in range(V):
+        for pos in range(V):
+            v = order[pos]
             for row in range(256):
                 n = tt * 256 + row
                 if n >= t["n_out"] or (v, row) in seen:
@@ -268,4 +272,24 @@ def test_wide_tables_decode_to_the_csr_lists(res_in, res_out, k):
                 cnt = ptr[n, v] & 0xFFFF
                 assert cnt <= 1
                 want = gnbr[n, ptr[n, v] >> 16] - lo[tt] if cnt == 1 else zr
-                assert row_of[src[tt, v, row]] == want
+                assert row_of[src[tt, pos, row]] == want
+
+
+def test_stream_slot_order_is_a_permutation_that_lowers_serial_work():
+    """The slot-visit order search returns a permutation, light slots first, and on the C3
+    lattice it leaves less serialized collision work than the plain order."""
+    t = layer_tables(128, 128, 25)
+    direct = T.direct_tables(t["idx"], t["slots"], t["n_in"], t["V"])
+    units = 4 * direct[5].numpy().astype(np.int64)
+    order = T.stream_slot_order(units)
+    assert sorted(order) == list(range(t["V"]))
+
+    def serial(order, rate=256, ahead=3):
+        u = units[:, order]
+        off = np.concatenate([np.zeros((u.shape[0], 1), np.int64), np.cumsum(u, axis=1)], axis=1)
+        bpos, tot = off[:, 1].copy(), off[:, 1].sum()
+        for v in range(u.shape[1]):
+            tot += np.maximum(off[:, v + 1] - bpos, 0).sum()
+            bpos = np.minimum(np.maximum(bpos, off[:, v + 1]) + rate, off[:, min(v + ahead, u.shape[1])])
+        return tot
+    assert serial(order) < 0.5 * serial(list(range(t["V"])))
