@@ -14,7 +14,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
 
-ABI_VERSION = 13
+ABI_VERSION = 14
 F32, BF16, F8E4M3 = 0, 1, 2
 NEAREST, BILINEAR = 0, 1
 PAD_ZEROS, PAD_BORDER = 0, 1
@@ -68,6 +68,8 @@ class KnnConvArgs(C.Structure):
         ("x_scale_dev", C.c_void_p),
         ("tile_src", C.c_void_p), ("tile_coll_off", C.c_void_p), ("tile_cent", C.c_void_p),
         ("coll_off_stride", C.c_int32), ("cent_stride", C.c_int32),
+        ("tile_heavy", C.c_void_p), ("tile_hlist", C.c_void_p), ("heavy_stride", C.c_int32),
+        ("hlist_stride", C.c_int32),
     ]
 
 

@@ -141,7 +141,7 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         self._packed = {}
         order = None
         if tiles is not None:
-            order = T.stream_slot_order(4 * tiles[5].numpy().astype(np.int64))
+            order = T.stream_slot_order(T.slot_stream_units(tiles))
         self.set_slot_order(order)
         # slot-sum headroom of the fp8 path: the largest neighbour count of a slot
         self._max_slot_count = int((slot_ptr & 0xFFFF).max()) if slot_ptr.numel() else 1
@@ -223,14 +223,17 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         the order 0, 1, ... gives results bit-identical to the row-packed kernels."""
         tiles = self._direct_tables
         wide = T.wide_tables(tiles, self._k, order) if tiles is not None else None
-        self._cent_stride = 0
-        self._coll_off_stride = 0
+        self._cent_stride = self._coll_off_stride = self._heavy_stride = self._hlist_stride = 0
         dev = self.weight.device
-        for name, t in zip(("tile_src", "tile_cent", "tile_coll_off"), wide[:3] if wide is not None else (None,) * 3):
+        for name, field in (("tile_src", "src"), ("tile_cent", "coll"), ("tile_coll_off", "coll_off"),
+                            ("tile_heavy", "heavy"), ("tile_hlist", "hlist")):
+            t = None if wide is None else getattr(wide, field)
             self.register_buffer(name, None if t is None else t.to(dev), persistent=False)
         if wide is not None:
-            self._cent_stride = wide[3]
-            self._coll_off_stride = int(wide[2].shape[1])
+            self._cent_stride = wide.stride
+            self._coll_off_stride = int(wide.coll_off.shape[1])
+            self._heavy_stride = wide.heavy_stride
+            self._hlist_stride = wide.hlist_stride
         self.slot_order = None if order is None else [int(v) for v in order]
         self._slot_order_dev = None if order is None else torch.tensor(self.slot_order, dtype=torch.int32,
                                                                           device=dev)
@@ -260,12 +263,13 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
 
     def _mfma_lds_bytes(self):
         """LDS bytes of the fragment-order kernel's tile (its ``v5_layout``): the staged rows plus
-        the zero row (64 bytes each), 128-byte alignment, three 256 x 32 bf16 collision tiles
-        and a trash row, per-(slot, row) sources, per-slot entry offsets, 16-byte collision
-        entries, neighbour lists."""
-        v, k = self.ref_coords.shape[0], self._k
-        o = ((self._zero_row + 1) * 64 + 127) & ~127
-        return o + (3 * 256 + 1) * 32 * 2 + v * 256 * 2 + self._coll_off_stride * 4 + self._cent_stride * 16 + 256 * k * 2
+        the zero row and the heavy-sum rows (64 bytes each), 128-byte alignment, three 256 x 32
+        bf16 collision tiles and a trash row, per-(slot, row) sources, per-slot entry offsets,
+        16-byte stream entries, 8-byte heavy entries, the heavy entries' neighbour offsets."""
+        v = self.ref_coords.shape[0]
+        o = ((self._zero_row + 1 + self._heavy_stride) * 64 + 127) & ~127
+        return (o + (3 * 256 + 1) * 32 * 2 + v * 256 * 2 + self._coll_off_stride * 4 + self._cent_stride * 16
+                + self._heavy_stride * 8 + self._hlist_stride * 2)
 
     def _mfma_path(self, x, dt):
         """Whether this call runs the fragment-order kernel (see ``mfma_weights``)."""
@@ -357,6 +361,8 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
             a.tile_src = self.tile_src.data_ptr(); a.tile_coll_off = self.tile_coll_off.data_ptr()
             a.tile_cent = self.tile_cent.data_ptr()
             a.coll_off_stride = self._coll_off_stride; a.cent_stride = self._cent_stride
+            a.tile_heavy = self.tile_heavy.data_ptr(); a.tile_hlist = self.tile_hlist.data_ptr()
+            a.heavy_stride = self._heavy_stride; a.hlist_stride = self._hlist_stride
         lib = _lib.load()
         _lib.check(lib.fovi_knnconv_fwd(a, _lib.stream_handle(x.device)), "fovi_knnconv_fwd")
         return y.transpose(1, 2)

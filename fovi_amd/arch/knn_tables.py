@@ -26,6 +26,8 @@ cannot represent the operator.
 """
 from __future__ import annotations
 
+from typing import NamedTuple
+
 import numpy as np
 import torch
 
@@ -263,74 +265,156 @@ def _row_offset(r):
     return r * 64 + (g << 4)
 
 
+# Collision entries of the wide-layer kernel's stream hold at most this many
+# neighbours; rows whose slot holds more ("heavy") are summed once per channel
+# chunk into their own LDS rows.
+STREAM_MAX_COUNT = 6
+# LDS bytes of one collision tile of the wide-layer kernel (256 rows x 64 bytes)
+WIDE_TILE_BYTES = 256 * 64
+WIDE_TILES = 3
+
+
+class WideTables(NamedTuple):
+    src: torch.Tensor        # [T, V, tile] uint16
+    coll: torch.Tensor       # [T, stride, 4] int32 (uint32 words)
+    coll_off: torch.Tensor   # [T, V + 1 rounded up to 4] int32
+    stride: int
+    heavy: torch.Tensor      # [T, heavy_stride, 2] int32 (uint32 words)
+    heavy_stride: int
+    hlist: torch.Tensor      # [T, hlist_stride] int16 (uint16 offsets)
+    hlist_stride: int
+
+
 def wide_tables(direct, k, order=None):
     """Tables of the wide-layer (fragment-order) kernel, derived from ``direct_tables``.
 
     Laid out in the kernel's LDS order (16-byte copies) and holding swizzled
     LDS byte offsets (``_row_offset``) rather than row numbers, so the kernel
-    forms every address with one XOR:
+    forms every address with one XOR. The kernel's LDS starts with the staged
+    rows and the zero row (``zero_row + 1`` rows of 64 bytes), followed by
+    ``heavy_stride`` rows of heavy sums.
 
-    * ``src [T, V, tile] uint16``: per (slot, row) the offset of the staged row
-      the MFMA lanes read for that slot (the neighbour's row when the slot
-      holds one neighbour, the zero row when it holds none), or 0xFFFF when
-      the slot holds two or more neighbours (the row's own collision sum);
-    * ``coll [T, stride, 4] uint32``: one 16-byte entry per (slot, collision
-      row), grouped by slot and within a slot by decreasing count. Word 0:
-      bits 0-15 the row's offset in a collision tile, 16-23 count, 24-31
-      begin (in the ``tile_nbr`` list of the row); words 1-2: offsets of the
-      first four neighbours' staged rows, two per word (low half first; the
-      zero row past the count); word 3: the row, and the slot at bits 8-15;
-    * ``coll_off [T, V + 1 rounded up to 4] int32``: slot v's entries are
-      ``coll[t, coll_off[t, v]:coll_off[t, v + 1]]``.
+    * ``src [T, V, tile] uint16``: per (slot, row) the offset of the 64-byte
+      row the MFMA lanes read for that slot: the neighbour's staged row when
+      the slot holds one neighbour, the zero row when it holds none, the row's
+      heavy sum when it holds more than ``STREAM_MAX_COUNT``; 0xFFFF when it
+      holds 2 .. ``STREAM_MAX_COUNT`` (the row's sum in a collision tile).
+    * ``coll [T, stride, 4] uint32``: one 16-byte stream entry per (slot,
+      collision row with 2 .. ``STREAM_MAX_COUNT`` neighbours), grouped by slot
+      position and within a slot by decreasing count. Word 0: bits 0-15 the
+      destination, relative to the first collision tile (tile ``p % 3`` of slot
+      position p, then the row's offset), bits 16-23 the count; words 1-3:
+      offsets of the staged rows of neighbours 1-6, two per word (low half
+      first; the zero row past the count).
+    * ``coll_off [T, V + 1 rounded up to 4] int32``: slot position p's entries
+      are ``coll[t, coll_off[t, p]:coll_off[t, p + 1]]``.
+    * ``heavy [T, heavy_stride, 2] uint32``: one entry per heavy (slot, row):
+      word 0 bits 0-15 the offset of its heavy-sum row, bits 16-23 the count
+      (0 = padding); word 1 the index of its first neighbour in ``hlist``.
+    * ``hlist [T, hlist_stride] uint16``: the heavy entries' neighbour offsets,
+      in list order.
 
     ``order`` (default: slot order) is the order in which the kernel visits
     the slots (``stream_slot_order``): the tables are laid out by position p
-    in that order, slot ``order[p]``, and an entry's slot field holds p.
+    in that order, slot ``order[p]``.
 
-    Returns ``(src, coll, coll_off, stride)`` or ``None`` when zero_row does
-    not fit the 16-bit offsets (above 1023) or k exceeds 255.
+    Returns a ``WideTables``, or ``None`` when the offsets do not fit 16 bits
+    (more than 1023 staged rows, or heavy rows past 64 KB) or k exceeds 255.
     """
     lo, span, ent, nbr, coll, coll_n, zero_row = direct
     if zero_row > 1023 or k > 255:
         return None
     e = ent.numpy().view(np.uint32).astype(np.int64)          # [T*tile, V]
     n_tiles, n_ref, tile = coll.shape
-    first = e >> 16
-    cnt = (e >> 8) & 0xFF
     order = np.arange(n_ref) if order is None else np.asarray(order, np.int64)
     if sorted(order.tolist()) != list(range(n_ref)):
         raise ValueError("order must be a permutation of the slots")
-    src = np.where(cnt >= 2, 0xFFFF, _row_offset(first)).astype(np.uint16)
-    src = src.reshape(n_tiles, tile, n_ref).transpose(0, 2, 1)[:, order].copy()
+    e3 = e.reshape(n_tiles, tile, n_ref)
+    first, cnt, begin = e3 >> 16, (e3 >> 8) & 0xFF, e3 & 0xFF
+    heavy_mask = cnt > STREAM_MAX_COUNT                        # [T, tile, V]
+    n_heavy = heavy_mask.sum(axis=(1, 2))
+    heavy_stride = max(2, -(-int(n_heavy.max(initial=0)) // 2) * 2)
+    heavy_base = (zero_row + 1) * 64
+    if heavy_base + heavy_stride * 64 > 0xFFFF:
+        return None
     nb = nbr.numpy().astype(np.int64).reshape(n_tiles, tile, k)
-    cn = coll_n.numpy().astype(np.int64)[:, order]
-    counts = cn.sum(axis=1)
-    stride = int(max(1, int(counts.max()))) if n_tiles else 1
+    zoff = int(_row_offset(zero_row))
+
+    # heavy entries: in (slot, row) order of each tile
+    heavy_row = np.full((n_tiles, tile, n_ref), -1, np.int64)
+    n_list = np.zeros(n_tiles, np.int64)
+    hent = []
+    for t in range(n_tiles):
+        rr, vv = np.nonzero(heavy_mask[t])
+        ordv = np.lexsort((rr, vv))
+        rr, vv = rr[ordv], vv[ordv]
+        heavy_row[t, rr, vv] = np.arange(len(rr))
+        hent.append((rr, vv))
+        n_list[t] = cnt[t, rr, vv].sum()
+    hlist_stride = max(8, -(-int(n_list.max(initial=0)) // 8) * 8)
+    heavy = np.zeros((n_tiles, heavy_stride, 2), np.uint32)
+    hlist = np.zeros((n_tiles, hlist_stride), np.uint16)
+    for t in range(n_tiles):
+        rr, vv = hent[t]
+        pos = 0
+        for h, (r, v) in enumerate(zip(rr, vv)):
+            c, b0 = int(cnt[t, r, v]), int(begin[t, r, v])
+            heavy[t, h, 0] = (heavy_base + 64 * h) | (c << 16)
+            heavy[t, h, 1] = pos
+            hlist[t, pos:pos + c] = _row_offset(nb[t, r, b0:b0 + c])
+            pos += c
+
+    src = np.where(cnt >= 2, 0xFFFF, _row_offset(first))
+    src = np.where(heavy_mask, heavy_base + 64 * heavy_row, src).astype(np.uint16)
+    src = src.transpose(0, 2, 1)[:, order].copy()              # [T, V (position), tile]
+
+    # stream entries: collision rows of each slot with 2 .. STREAM_MAX_COUNT neighbours
+    cl = coll.numpy().astype(np.int64)
+    cn = coll_n.numpy().astype(np.int64)
+    lists = [[None] * n_ref for _ in range(n_tiles)]
+    light_n = np.zeros((n_tiles, n_ref), np.int64)
+    for t in range(n_tiles):
+        for q in range(n_ref):
+            v = order[q]
+            rows = cl[t, v, :cn[t, v]]
+            rows = rows[cnt[t, rows, v] <= STREAM_MAX_COUNT]
+            lists[t][q] = rows
+            light_n[t, q] = len(rows)
+    stride = int(max(1, int(light_n.sum(axis=1).max(initial=0))))
     voff = -(-(n_ref + 1) // 4) * 4
     out = np.zeros((n_tiles, stride, 4), np.uint32)
     coll_off = np.zeros((n_tiles, voff), np.int32)
-    cl = coll.numpy().astype(np.int64)
-    zoff = int(_row_offset(zero_row))
     for t in range(n_tiles):
-        off = np.concatenate([[0], np.cumsum(cn[t])])
+        off = np.concatenate([[0], np.cumsum(light_n[t])])
         coll_off[t, :n_ref + 1] = off
         if off[-1] == 0:
             continue
-        rows = np.concatenate([cl[t, order[q], :cn[t, q]] for q in range(n_ref)])
-        pos = np.repeat(np.arange(n_ref), cn[t])
-        eb = e.reshape(n_tiles, tile, n_ref)[t, rows, order[pos]]
-        c = (eb >> 8) & 0xFF
-        b = eb & 0xFF
-        nbo = [_row_offset(eb >> 16)]
-        for j in range(1, 4):
-            r = nb[t, rows, np.minimum(b + j, k - 1)]
+        rows = np.concatenate(lists[t])
+        pos = np.repeat(np.arange(n_ref), light_n[t])
+        v = order[pos]
+        c, b0 = cnt[t, rows, v], begin[t, rows, v]
+        nbo = []
+        for j in range(STREAM_MAX_COUNT):
+            r = nb[t, rows, np.minimum(b0 + j, k - 1)]
             nbo.append(np.where(j < c, _row_offset(r), zoff))
         n_e = off[-1]
-        out[t, :n_e, 0] = (_row_offset(rows) | (c << 16) | (b << 24)).astype(np.uint32)
-        out[t, :n_e, 1] = (nbo[0] | (nbo[1] << 16)).astype(np.uint32)
-        out[t, :n_e, 2] = (nbo[2] | (nbo[3] << 16)).astype(np.uint32)
-        out[t, :n_e, 3] = (rows | (pos << 8)).astype(np.uint32)
-    return (torch.from_numpy(src), torch.from_numpy(out.view(np.int32)), torch.from_numpy(coll_off), stride)
+        dst = (pos % WIDE_TILES) * WIDE_TILE_BYTES + _row_offset(rows)
+        out[t, :n_e, 0] = (dst | (c << 16)).astype(np.uint32)
+        for w in range(3):
+            out[t, :n_e, 1 + w] = (nbo[2 * w] | (nbo[2 * w + 1] << 16)).astype(np.uint32)
+    return WideTables(torch.from_numpy(src), torch.from_numpy(out.view(np.int32)), torch.from_numpy(coll_off),
+                      stride, torch.from_numpy(heavy.view(np.int32)), heavy_stride,
+                      torch.from_numpy(hlist.view(np.int16)), hlist_stride)
+
+
+def slot_stream_units(direct):
+    """Stream demand of each (tile, slot) in the wide-layer kernel: four units (16-byte parts)
+    per collision row with 2 .. ``STREAM_MAX_COUNT`` neighbours. ``[T, V] int64``."""
+    ent = direct[2]
+    n_tiles, n_ref, tile = direct[4].shape
+    cnt = (ent.numpy().view(np.uint32).astype(np.int64) >> 8) & 0xFF
+    light = (cnt >= 2) & (cnt <= STREAM_MAX_COUNT)
+    return 4 * light.reshape(n_tiles, tile, n_ref).sum(axis=1)
 
 
 def stream_slot_order(units_per_slot, rate=256, ahead=3, iters=600, seed=0):

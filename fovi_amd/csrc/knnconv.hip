@@ -1507,6 +1507,8 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
   p.w_layout = a->w_layout;
   p.tile_src = a->tile_src; p.tile_coll_off = a->tile_coll_off; p.tile_cent = a->tile_cent;
   p.coll_off_stride = a->coll_off_stride; p.cent_stride = a->cent_stride;
+  p.tile_heavy = a->tile_heavy; p.tile_hlist = a->tile_hlist;
+  p.heavy_stride = a->heavy_stride; p.hlist_stride = a->hlist_stride;
   p.w_c_slot = a->w_c_slot > 0 ? a->w_c_slot : static_cast<int>(a->c_in);
   if (p.w_c_slot < p.C || a->k_pad < p.w_c_slot * p.V) {
     set_error("fovi_knnconv_fwd: w_c_slot=%d must be >= c_in and k_pad >= w_c_slot * n_ref", p.w_c_slot);

@@ -37,6 +37,10 @@ struct KnnParams {
   const uint32_t* tile_cent;
   int coll_off_stride;
   int cent_stride;
+  const uint32_t* tile_heavy;
+  const uint16_t* tile_hlist;
+  int heavy_stride;
+  int hlist_stride;
 };
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));

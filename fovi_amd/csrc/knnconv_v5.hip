@@ -11,10 +11,12 @@
 //    two-ring tile of the log-polar lattice) are staged in LDS one 32-channel
 //    chunk at a time (S); the next chunk is loaded into registers while the
 //    current one is consumed. MFMA lanes read single-neighbour slots straight
-//    from S (an LDS zero row serves empty slots); slots with two or more
+//    from S (an LDS zero row serves empty slots); slots with 2 to 6
 //    neighbours are summed in fp32 (one RNE rounding) into a ring of three
 //    collision tiles, up to two slots ahead, as a stream over the tile's
-//    collision entries that advances a fixed 256 units per iteration.
+//    collision entries that advances a fixed 256 units per iteration; the few
+//    slots with more neighbours are summed once per chunk into rows of their
+//    own, which the MFMA lanes read like staged rows.
 //  * Weights are not staged in LDS: fovi_knnconv_pack_weight_mfma stores
 //    them in the order the MFMA B operand is consumed, so each lane loads its
 //    16-byte fragment with one coalesced load (1 KB per wave and fragment)
@@ -31,21 +33,27 @@ constexpr int V5_NT = 256;   // output channels per tile
 constexpr int V5_CC = 32;    // channels per reduction chunk (one 64-byte LDS row)
 constexpr int V5_NB = 3;     // collision tiles: slot v uses tile v % 3, so sums run up to two slots ahead
 
-// LDS byte layout of a tile. The staged rows S come first, at offset 0, so
-// the host tables can hold absolute LDS byte offsets of staged rows.
+constexpr int V5_STREAM_MAX = 6;   // neighbours of a stream entry; more: a heavy entry
+
+// LDS byte layout of a tile. The staged rows S come first, at offset 0, then
+// the heavy-sum rows, so the host tables can hold absolute LDS byte offsets
+// (16 bits) of every row an MFMA lane reads.
 struct V5Layout {
-  int acol_off, src_off, coff_off, cent_off, nbl_off, total;  // bytes
+  int heavy_rows, acol_off, src_off, coff_off, cent_off, heavy_off, hlist_off, total;  // bytes
 };
 
-__host__ __device__ inline V5Layout v5_layout(int V, int K, int zero_row, int coff_stride, int cent_stride) {
+__host__ __device__ inline V5Layout v5_layout(int V, int zero_row, int coff_stride, int cent_stride,
+                                              int heavy_stride, int hlist_stride) {
   V5Layout l;
   int o = (zero_row + 1) * V5_CC * 2;               // staged rows + zero row
+  l.heavy_rows = o; o += heavy_stride * V5_CC * 2;  // heavy sums, one 64-byte row per heavy entry
   o = (o + 127) & ~127;
   l.acol_off = o;   o += (V5_NB * V5_MT + 1) * V5_CC * 2; // V5_NB 256 x 32 bf16 collision tiles + a trash row
   l.src_off = o;    o += V * V5_MT * 2;             // per (slot, row) A source, slot-major
   l.coff_off = o;   o += coff_stride * 4;           // per-slot collision entry offsets
   l.cent_off = o;   o += cent_stride * 16;          // collision entries
-  l.nbl_off = o;    o += V5_MT * K * 2;             // neighbour lists (rows with > 4 neighbours)
+  l.heavy_off = o;  o += heavy_stride * 8;          // heavy entries
+  l.hlist_off = o;  o += hlist_stride * 2;          // heavy entries' neighbour offsets
   l.total = o;
   return l;
 }
@@ -81,14 +89,15 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
                                                                  int64_t n_tiles_n, int64_t total_tiles,
                                                                  int64_t padded_tiles, int vec_out) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const int V = static_cast<int>(p.V), K = static_cast<int>(p.K);
+  const int V = static_cast<int>(p.V);
   const int zr = p.zero_row;
-  const V5Layout L = v5_layout(V, K, zr, p.coll_off_stride, p.cent_stride);
+  const V5Layout L = v5_layout(V, zr, p.coll_off_stride, p.cent_stride, p.heavy_stride, p.hlist_stride);
   uint16_t* S = reinterpret_cast<uint16_t*>(smem);
   const uint16_t* srcs = reinterpret_cast<const uint16_t*>(smem + L.src_off);
   const int32_t* coff = reinterpret_cast<const int32_t*>(smem + L.coff_off);
   const u32x4* cent = reinterpret_cast<const u32x4*>(smem + L.cent_off);
-  const uint16_t* nbl = reinterpret_cast<const uint16_t*>(smem + L.nbl_off);
+  const uint32_t* heavy = reinterpret_cast<const uint32_t*>(smem + L.heavy_off);
+  const uint16_t* hlist = reinterpret_cast<const uint16_t*>(smem + L.hlist_off);
   const uint32_t acol = static_cast<uint32_t>(L.acol_off);
   const uint32_t trash = acol + V5_NB * V5_TILE_BYTES;
 
@@ -150,16 +159,17 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
   load_s(0);
   {
     const int n_src = V * V5_MT * 2 / 16, n_coff = p.coll_off_stride * 4 / 16;
-    const int n_ce = p.cent_stride, n_nbl = V5_MT * K * 2 / 16;
+    const int n_ce = p.cent_stride, n_hv = p.heavy_stride * 8 / 16, n_hl = p.hlist_stride * 2 / 16;
     const u32x4* g_src = reinterpret_cast<const u32x4*>(p.tile_src + pt * V * V5_MT);
     const u32x4* g_coff = reinterpret_cast<const u32x4*>(p.tile_coll_off + pt * p.coll_off_stride);
     const u32x4* g_ce = reinterpret_cast<const u32x4*>(p.tile_cent) + pt * p.cent_stride;
-    const u32x4* g_nbl = reinterpret_cast<const u32x4*>(p.tile_nbr + n0 * p.K);
+    const u32x4* g_hv = reinterpret_cast<const u32x4*>(p.tile_heavy + pt * p.heavy_stride * 2);
+    const u32x4* g_hl = reinterpret_cast<const u32x4*>(p.tile_hlist + pt * p.hlist_stride);
     u32x4* d_src = reinterpret_cast<u32x4*>(smem + L.src_off);
     u32x4* d_coff = reinterpret_cast<u32x4*>(smem + L.coff_off);
     u32x4* d_ce = reinterpret_cast<u32x4*>(smem + L.cent_off);
-    u32x4* d_nbl = reinterpret_cast<u32x4*>(smem + L.nbl_off);
-    const int total = n_src + n_coff + n_ce + n_nbl;
+    u32x4* d_hv = reinterpret_cast<u32x4*>(smem + L.heavy_off);
+    const int total = n_src + n_coff + n_ce + n_hv + n_hl;
     for (int base = 0; base < total; base += 8 * 256) {
       u32x4 t[8];
       u32x4* dst[8];
@@ -173,7 +183,9 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
         i -= n_coff;
         if (i < n_ce) { t[u] = g_ce[i]; dst[u] = d_ce + i; continue; }
         i -= n_ce;
-        if (i < n_nbl) { t[u] = g_nbl[i]; dst[u] = d_nbl + i; }
+        if (i < n_hv) { t[u] = g_hv[i]; dst[u] = d_hv + i; continue; }
+        i -= n_hv;
+        if (i < n_hl) { t[u] = g_hl[i]; dst[u] = d_hv + n_hv + i; }
       }
 #pragma unroll
       for (int u = 0; u < 8; ++u)
@@ -183,8 +195,8 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
   if (tid < 4) *reinterpret_cast<u32x4*>(&S[zr * V5_CC + tid * 8]) = u32x4{0u, 0u, 0u, 0u};
 
   // Collision sums. A unit is (entry, 16-byte part): entry = unit / 4. Its
-  // first four neighbours are summed from the entry's offsets (missing ones
-  // are the zero row); neighbours 5.. come from the row's neighbour list.
+  // first four neighbours are summed from the entry's words 1-2, neighbours 5
+  // and 6 from word 3 (missing ones are the zero row).
   auto unit_sum4 = [&](const u32x4 ce, uint32_t pq) {
     f32x8 a = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     acc_bf16x8(a, lds16(smem, (ce[1] & 0xffffu) ^ pq));
@@ -194,16 +206,33 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
     return a;
   };
   auto unit_rest = [&](f32x8& a, const u32x4 ce, uint32_t pq) {
-    const int cnt = static_cast<int>((ce[0] >> 16) & 0xff);
-    if (cnt > 4) {
-      const uint16_t* nb = nbl + static_cast<int>(ce[3] & 0xffu) * K + static_cast<int>(ce[0] >> 24);
-      for (int j = 4; j < cnt; ++j) acc_bf16x8(a, lds16(smem, row_off(nb[j]) ^ pq));
+    if (((ce[0] >> 16) & 0xffu) > 4) {
+      acc_bf16x8(a, lds16(smem, (ce[3] & 0xffffu) ^ pq));
+      acc_bf16x8(a, lds16(smem, (ce[3] >> 16) ^ pq));
     }
   };
-  // collision tile offset of a unit: tile slot % 3 (slot in entry word 3)
-  auto unit_dst = [&](const u32x4 ce, uint32_t pq) {
-    const uint32_t slot = (ce[3] >> 8) & 0xffu;
-    return acol + (slot % V5_NB) * V5_TILE_BYTES + ((ce[0] & 0xffffu) ^ pq);
+  // collision tile offset of a unit (the entry holds tile and row)
+  auto unit_dst = [&](const u32x4 ce, uint32_t pq) { return acol + ((ce[0] & 0xffffu) ^ pq); };
+  // Heavy sums of the current chunk: one unit per (heavy entry, 16-byte part),
+  // neighbours in list order, four reads in flight (the zero row past the
+  // count: +0 leaves an fp32 sum that started at +0 unchanged).
+  const uint32_t zoff = row_off(zr);
+  auto build_heavy = [&]() {
+    for (int u = tid; u < p.heavy_stride * 4; u += 256) {
+      const uint32_t w0 = heavy[(u >> 2) * 2], w1 = heavy[(u >> 2) * 2 + 1];
+      const int cnt = static_cast<int>((w0 >> 16) & 0xffu);
+      if (cnt == 0) continue;
+      const uint32_t pq = static_cast<uint32_t>(u & 3) << 4;
+      f32x8 a = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < cnt; j += 4) {
+        uint32_t r[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) r[q] = j + q < cnt ? hlist[w1 + j + q] : zoff;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc_bf16x8(a, lds16(smem, r[q] ^ pq));
+      }
+      *reinterpret_cast<u32x4*>(smem + ((w0 & 0xffffu) ^ pq)) = pack_bf16x8(a);
+    }
   };
   // units [from, to) of the tile's unit stream (the entry list in slot order,
   // four 16-byte parts per entry), complete sums; from % 4 == 0
@@ -248,6 +277,7 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
   // finished first (uniform branch). Masked units write a trash row; entries
   // with more than four neighbours finish after the MFMAs.
   int bpos = 4 * coff[1];
+  build_heavy();
   build_range(0, bpos);
   uint32_t ecur[4], enxt[4];
 #pragma unroll
@@ -256,18 +286,19 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
 
   int v = 0, cc = 0;
   uint32_t vb = 0;   // v % V5_NB
+  // stream bounds of the current slot, read one iteration ahead
+  int need = bpos, lim = 4 * coff[min(V5_NB, V)];
   for (int it = 0; it < nit; ++it) {
     u32x4(&bc)[8] = wa;   // this iteration's weight fragments
     u32x4(&bn)[8] = wb;   // the next iteration's
-    const int need = 4 * coff[v + 1];
     if (bpos < need) {            // slot v incomplete: finish it
       build_range(bpos, need);
       bpos = need;
       __syncthreads();
     }
-    const int lim = 4 * coff[min(v + V5_NB, V)];
     const bool more = it + 1 < nit;
     const int vn = v + 1 == V ? 0 : v + 1;
+    const int need_n = 4 * coff[vn + 1], lim_n = 4 * coff[min(vn + V5_NB, V)];
 
     bf16x8 af[2][4];
 #pragma unroll
@@ -301,6 +332,8 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
     __syncthreads();
     v = vn;
     vb = vb + 1 == V5_NB ? 0 : vb + 1;
+    need = need_n;
+    lim = lim_n;
     if (v == 0) {                 // chunk boundary
       vb = 0;
       ++cc;
@@ -309,6 +342,7 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
         __syncthreads();
         if (cc + 1 < ncc) load_s(cc + 1);
         bpos = 4 * coff[1];
+        build_heavy();
         build_range(0, bpos);
         __syncthreads();
       }
@@ -378,8 +412,8 @@ static void launch_v5_sv(const KnnParams& p, int out_t, hipStream_t s) {
   const int64_t total = p.B * tiles_per_b * n_tiles_n;
   const int64_t padded = (total + 7) / 8 * 8;
   const int ncb = static_cast<int>(n_tiles_n * (V5_NT / 32));
-  const size_t lds = v5_layout(static_cast<int>(p.V), static_cast<int>(p.K), p.zero_row, p.coll_off_stride,
-                               p.cent_stride).total;
+  const size_t lds = v5_layout(static_cast<int>(p.V), p.zero_row, p.coll_off_stride, p.cent_stride,
+                               p.heavy_stride, p.hlist_stride).total;
   // 16-byte channels-last bf16 stores: unit channel stride, rows and base 16-byte aligned
   const int vec_out = out_t == FOVI_BF16 && p.ys1 == 1 && p.ys2 % 8 == 0 && p.ys0 % 8 == 0 && p.Cout % 8 == 0 &&
                       reinterpret_cast<uintptr_t>(p.y) % 16 == 0;
@@ -399,17 +433,20 @@ static void launch_v5_sv(const KnnParams& p, int out_t, hipStream_t s) {
 
 int v5_applies(const KnnParams& p) {
   if (p.w_layout != FOVI_W_MFMA) return 0;
-  if (p.C % V5_CC != 0 || p.zero_row <= 0 || p.zero_row > 1023 || !p.tile_lo || !p.tile_nbr || !p.tile_src ||
-      !p.tile_coll_off || !p.tile_cent || p.K > 255 || p.V > 255)
+  if (p.C % V5_CC != 0 || p.zero_row <= 0 || p.zero_row > 1023 || !p.tile_lo || !p.tile_src ||
+      !p.tile_coll_off || !p.tile_cent || !p.tile_heavy || !p.tile_hlist || p.V > 255)
     return 0;
   if (p.coll_off_stride <= p.V || p.coll_off_stride % 4 != 0 || p.cent_stride < 1) return 0;
+  if (p.heavy_stride < 2 || p.heavy_stride % 2 != 0 || p.hlist_stride < 8 || p.hlist_stride % 8 != 0) return 0;
+  if ((p.zero_row + 1 + p.heavy_stride) * V5_CC * 2 > 0xffff) return 0;   // 16-bit row offsets
   if ((reinterpret_cast<uintptr_t>(p.tile_src) | reinterpret_cast<uintptr_t>(p.tile_coll_off) |
-       reinterpret_cast<uintptr_t>(p.tile_cent) | reinterpret_cast<uintptr_t>(p.tile_nbr)) % 16 != 0)
+       reinterpret_cast<uintptr_t>(p.tile_cent) | reinterpret_cast<uintptr_t>(p.tile_heavy) |
+       reinterpret_cast<uintptr_t>(p.tile_hlist)) % 16 != 0)
     return 0;
   if (p.xs1 != 1 || p.xs2 % 8 != 0 || p.xs0 % 8 != 0 || reinterpret_cast<uintptr_t>(p.x) % 16 != 0) return 0;
   if (reinterpret_cast<uintptr_t>(p.w) % 16 != 0) return 0;
-  return v5_layout(static_cast<int>(p.V), static_cast<int>(p.K), p.zero_row, p.coll_off_stride, p.cent_stride)
-             .total <= 160 * 1024;
+  return v5_layout(static_cast<int>(p.V), p.zero_row, p.coll_off_stride, p.cent_stride, p.heavy_stride,
+                   p.hlist_stride).total <= 160 * 1024;
 }
 
 int launch_knnconv_bf16_v5(const KnnParams& p, int out_t, hipStream_t s) {

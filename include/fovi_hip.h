@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 13
+#define FOVI_ABI_VERSION 14
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -164,22 +164,32 @@ typedef struct fovi_knnconv_args {
   int64_t workspace_bytes;
   const float* x_scale_dev;   /* (F8E4M3 only) device copy of the activation scale, e.g. the one
                                  fovi_quantize_e4m3 writes; used instead of x_scale when non-NULL */
-  /* Tables of the wide-layer kernel (w_layout = FOVI_W_MFMA), in its LDS order. Staged rows
-   * are named by LDS byte offsets off(r) = 64 r + 16 g(r), g(r) = (bit1(r) ^ bit3(r)) | bit2(r) << 1
-   * (16-byte part q of row r is at off(r) ^ 16 q); zero_row must be below 1024.
-   *   tile_src[(t * n_ref + v) * tile_points + r]: off() of the staged row (relative to
-   *     tile_lo[t]) the MFMA reads for slot v of row r (the neighbour's, or the zero row for an
-   *     empty slot), or 0xFFFF when the slot holds two or more neighbours (summed by the kernel);
-   *   tile_cent[(t * cent_stride + i) * 4 + 0..3], i in [tile_coll_off[t * coll_off_stride + v],
-   *     tile_coll_off[t * coll_off_stride + v + 1]): one 16-byte entry per (slot v, row with two
-   *     or more neighbours), decreasing count within a slot: word 0 = off(row) | count << 16 |
-   *     begin in tile_nbr << 24; words 1, 2 = off() of the first four neighbours' staged rows,
-   *     two 16-bit halves each (the zero row past the count); word 3 = row | slot << 8. */
+  /* Tables of the wide-layer kernel (w_layout = FOVI_W_MFMA), in its LDS order and in the
+   * slot visit order (position p visits slot slot_order[p], see fovi_knnconv_pack_weight_mfma).
+   * 64-byte rows are named by LDS byte offsets; staged row r (relative to tile_lo[t]) is at
+   * off(r) = 64 r + 16 g(r), g(r) = (bit1(r) ^ bit3(r)) | bit2(r) << 1 (16-byte part q at
+   * off(r) ^ 16 q); zero_row must be below 1024. Heavy-sum row h is at 64 (zero_row + 1 + h).
+   *   tile_src[(t * n_ref + p) * tile_points + r]: the row the MFMA reads for position p of
+   *     output row r: the neighbour's staged row (one neighbour), the zero row (none), the
+   *     row's heavy sum (more than 6), or 0xFFFF (2 to 6: summed by the kernel's stream);
+   *   tile_cent[(t * cent_stride + i) * 4 + 0..3], i in [tile_coll_off[t * coll_off_stride + p],
+   *     tile_coll_off[t * coll_off_stride + p + 1]): one 16-byte entry per (position p, row
+   *     with 2 to 6 neighbours), decreasing count within a position: word 0 = destination
+   *     ((p % 3) * 16384 + off(row)) | count << 16; words 1-3 = off() of the staged rows of
+   *     neighbours 1-6 in list order, two 16-bit halves each (the zero row past the count);
+   *   tile_heavy[(t * heavy_stride + h) * 2 + 0..1]: heavy entry h (more than 6 neighbours):
+   *     word 0 = its heavy-sum row's offset | count << 16 (count 0: padding); word 1 = the
+   *     index of its first neighbour in tile_hlist[t * hlist_stride ...] (off() values, in
+   *     list order). */
   const uint16_t* tile_src;
   const int32_t* tile_coll_off;
   const uint32_t* tile_cent;
   int32_t coll_off_stride;    /* multiple of 4, > n_ref */
   int32_t cent_stride;        /* entries per tile, >= 1 */
+  const uint32_t* tile_heavy;
+  const uint16_t* tile_hlist;
+  int32_t heavy_stride;       /* heavy entries per tile, even, >= 2 */
+  int32_t hlist_stride;       /* multiple of 8, >= 8 */
 } fovi_knnconv_args;
 
 int fovi_knnconv_fwd(const fovi_knnconv_args* args, void* stream);
@@ -211,7 +221,7 @@ int fovi_knnconv_pack_weight(const float* w_ref, int64_t c_out, int64_t c_in, in
  * which the kernel visits the slots of a channel chunk: position p of
  * iteration it = (c / 32) * n_ref + p holds slot v = slot_order[p]. The
  * wide-layer tables (tile_src, tile_cent, tile_coll_off) must be laid out in
- * the same order, their slot fields holding positions.
+ * the same order.
  */
 int64_t fovi_knnconv_weight_mfma_elems(int64_t c_out, int64_t c_in, int64_t n_ref);
 int fovi_knnconv_pack_weight_mfma(const float* w_ref, int64_t c_out, int64_t c_in, int64_t n_ref,

@@ -226,7 +226,7 @@ def test_direct_tables_lists_and_zero_row(res_in, res_out, k):
 @pytest.mark.parametrize("res_in,res_out,k,permute", [(32, 32, 25, False), (64, 32, 49, False), (16, 16, 9, False),
                                                       (128, 128, 25, False), (32, 32, 25, True)])
 def test_wide_tables_decode_to_the_csr_lists(res_in, res_out, k, permute):
-    """Fragment-order kernel tables: every (slot, row) source and every collision entry
+    """Fragment-order kernel tables: every (slot, row) source, stream entry and heavy entry
     decodes back to the slot-major CSR lists (global input index = staged row + tile_lo)."""
     t = layer_tables(res_in, res_out, k)
     direct = T.direct_tables(t["idx"], t["slots"], t["n_in"], t["V"])
@@ -236,33 +236,40 @@ def test_wide_tables_decode_to_the_csr_lists(res_in, res_out, k, permute):
     if wide is None:                      # staged-row offsets need 16 bits
         assert zr > 1023
         return
-    src, cent, coll_off, stride = wide
-    src, cent, coll_off = src.numpy().astype(np.int64), cent.numpy().view(np.uint32), coll_off.numpy()
+    src, cent, coll_off = wide.src.numpy().astype(np.int64), wide.coll.numpy().view(np.uint32), wide.coll_off.numpy()
+    heavy, hlist = wide.heavy.numpy().view(np.uint32), wide.hlist.numpy().view(np.uint16)
     # offset -> row: 64-byte rows, swizzle bits only in bits 4-5
     row_of = {int(T._row_offset(r)): r for r in range(zr + 1)}
     assert len(row_of) == zr + 1 and all(o & 15 == 0 for o in row_of)
+    heavy_base = (zr + 1) * 64
     ptr, gnbr = t["ptr"].numpy(), t["nbr"].numpy()
     lo = lo.numpy().astype(np.int64)
     n_tiles, V = src.shape[0], t["V"]
-    assert cent.shape == (n_tiles, stride, 4)
+    assert cent.shape == (n_tiles, wide.stride, 4)
+    assert heavy.shape == (n_tiles, wide.heavy_stride, 2) and wide.heavy_stride % 2 == 0
+    assert hlist.shape == (n_tiles, wide.hlist_stride) and wide.hlist_stride % 8 == 0
+    n_heavy = 0
     for tt in range(n_tiles):
         seen = set()
         for pos in range(V):
             v = order[pos]
             for ei in range(coll_off[tt, pos], coll_off[tt, pos + 1]):
                 w0, w1, w2, w3 = (int(x) for x in cent[tt, ei])
-                row = w3 & 0xFF
-                assert w3 >> 8 == pos
-                cnt, beg = (w0 >> 16) & 0xFF, w0 >> 24
-                assert row_of[w0 & 0xFFFF] == row
+                dst, cnt = w0 & 0xFFFF, (w0 >> 16) & 0xFF
+                assert w0 >> 24 == 0
+                assert dst // T.WIDE_TILE_BYTES == pos % T.WIDE_TILES
+                row = row_of[dst % T.WIDE_TILE_BYTES]
                 n = tt * 256 + row
-                assert cnt >= 2 and cnt == (ptr[n, v] & 0xFFFF) and beg == (ptr[n, v] >> 16)
-                rs = [row_of[o] for o in (w1 & 0xFFFF, w1 >> 16, w2 & 0xFFFF, w2 >> 16)]
-                want = list(gnbr[n, beg:beg + min(cnt, 4)])
-                assert [r + lo[tt] for r in rs[:len(want)]] == want
-                assert all(r == zr for r in rs[len(want):])
+                assert 2 <= cnt <= T.STREAM_MAX_COUNT and cnt == (ptr[n, v] & 0xFFFF)
+                beg = ptr[n, v] >> 16
+                rs = [row_of[o] for o in (w1 & 0xFFFF, w1 >> 16, w2 & 0xFFFF, w2 >> 16, w3 & 0xFFFF, w3 >> 16)]
+                want = list(gnbr[n, beg:beg + cnt])
+                assert [r + lo[tt] for r in rs[:cnt]] == want
+                assert all(r == zr for r in rs[cnt:])
                 assert src[tt, pos, row] == 0xFFFF
+                assert (v, row) not in seen
                 seen.add((v, row))
+        used = 0
         for pos in range(V):
             v = order[pos]
             for row in range(256):
@@ -270,9 +277,24 @@ def test_wide_tables_decode_to_the_csr_lists(res_in, res_out, k, permute):
                 if n >= t["n_out"] or (v, row) in seen:
                     continue
                 cnt = ptr[n, v] & 0xFFFF
+                if cnt > T.STREAM_MAX_COUNT:       # heavy: its own row, summed once per chunk
+                    h, r = divmod(int(src[tt, pos, row]) - heavy_base, 64)
+                    assert r == 0 and 0 <= h < wide.heavy_stride
+                    w0, w1 = (int(x) for x in heavy[tt, h])
+                    assert w0 & 0xFFFF == src[tt, pos, row] and (w0 >> 16) & 0xFF == cnt
+                    beg = ptr[n, v] >> 16
+                    got = [row_of[int(o)] + lo[tt] for o in hlist[tt, w1:w1 + cnt]]
+                    assert got == list(gnbr[n, beg:beg + cnt])
+                    used += 1
+                    continue
                 assert cnt <= 1
                 want = gnbr[n, ptr[n, v] >> 16] - lo[tt] if cnt == 1 else zr
                 assert row_of[src[tt, pos, row]] == want
+        # every non-padding heavy entry is one (slot, row) of this tile
+        assert used == int((((heavy[tt, :, 0] >> 16) & 0xFF) > 0).sum())
+        n_heavy += used
+    if (res_in, res_out, k) == (128, 128, 25):
+        assert n_heavy > 0                 # the C3 lattice has slots with more than six neighbours
 
 
 def test_stream_slot_order_is_a_permutation_that_lowers_serial_work():
@@ -280,7 +302,7 @@ def test_stream_slot_order_is_a_permutation_that_lowers_serial_work():
     lattice it leaves less serialized collision work than the plain order."""
     t = layer_tables(128, 128, 25)
     direct = T.direct_tables(t["idx"], t["slots"], t["n_in"], t["V"])
-    units = 4 * direct[5].numpy().astype(np.int64)
+    units = T.slot_stream_units(direct)
     order = T.stream_slot_order(units)
     assert sorted(order) == list(range(t["V"]))
 
