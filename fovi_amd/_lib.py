@@ -14,7 +14,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
 
-ABI_VERSION = 14
+ABI_VERSION = 15
 F32, BF16, F8E4M3 = 0, 1, 2
 NEAREST, BILINEAR = 0, 1
 PAD_ZEROS, PAD_BORDER = 0, 1
@@ -107,7 +107,7 @@ def load(path: str = LIB_PATH):
     lib.fovi_knnconv_weight_mfma_elems.argtypes = [C.c_int64, C.c_int64, C.c_int64]
     lib.fovi_knnconv_weight_mfma_elems.restype = C.c_int64
     lib.fovi_knnconv_pack_weight_mfma.argtypes = [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_void_p,
-                                                  C.c_int32, C.c_void_p, C.c_void_p]
+                                                  C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p]
     lib.fovi_knnconv_pack_weight_mfma.restype = C.c_int
     lib.fovi_quantize_e4m3.argtypes = [C.POINTER(QuantizeArgs), C.c_void_p]
     lib.fovi_quantize_e4m3.restype = C.c_int

@@ -202,12 +202,7 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         k_pad = -(-c_slot * n_ref // _KCHUNK) * _KCHUNK
         src = w.detach().to(torch.float32).contiguous()
         out = torch.empty(self.out_channels, k_pad, dtype=dtype, device=w.device)
-        w_scale = None
-        if dtype == torch.float8_e4m3fn:
-            # per-output-channel scale amax|W[o, :]| / 448 (1 for an all-zero row), divided on
-            # the host: torch's device kernel divides by a scalar via its reciprocal
-            amax = src.abs().amax(1).cpu()
-            w_scale = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax)).to(w.device)
+        w_scale = self._fp8_weight_scale(src) if dtype == torch.float8_e4m3fn else None
         lib = _lib.load()
         _lib.check(lib.fovi_knnconv_pack_weight(_lib.ptr(src), self.out_channels, self.in_channels, n_ref,
                                                 _lib.ptr(out), _lib.dtype_code(dtype), k_pad, c_slot,
@@ -216,6 +211,13 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         packed = out if w_scale is None else (out, w_scale)
         self._packed[(dtype, c_slot)] = (key, packed)
         return packed
+
+    @staticmethod
+    def _fp8_weight_scale(src):
+        """Per-output-channel e4m3 weight scale amax|W[o, :]| / 448 (1 for an all-zero row),
+        divided on the host: torch's device kernel divides by a scalar via its reciprocal."""
+        amax = src.abs().amax(1).cpu()
+        return torch.where(amax > 0, amax / 448.0, torch.ones_like(amax)).to(src.device)
 
     def set_slot_order(self, order=None):
         """Order in which the wide-layer kernel visits the slots of a channel chunk (a
@@ -237,14 +239,15 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         self.slot_order = None if order is None else [int(v) for v in order]
         self._slot_order_dev = None if order is None else torch.tensor(self.slot_order, dtype=torch.int32,
                                                                           device=dev)
-        self._packed.pop("mfma", None)
+        self._packed.pop(("mfma", torch.bfloat16), None)
+        self._packed.pop(("mfma", torch.float8_e4m3fn), None)
 
-    def _packed_weight_mfma(self):
-        """bf16 weight in MFMA-fragment order (``fovi_knnconv_pack_weight_mfma``) for the current
-        slot order, cached per weight version."""
+    def _packed_weight_mfma(self, dtype=torch.bfloat16):
+        """Weight in MFMA-fragment order (``fovi_knnconv_pack_weight_mfma``) for the current slot
+        order, cached per weight version: bf16, or (e4m3, per-output-channel scale)."""
         w = self.weight
-        key = ("mfma", w._version, w.data_ptr())
-        hit = self._packed.get("mfma")
+        key = ("mfma", dtype, w._version, w.data_ptr())
+        hit = self._packed.get(("mfma", dtype))
         if hit is not None and hit[0] == key:
             return hit[1]
         n_ref = self.ref_coords.shape[0]
@@ -253,13 +256,16 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         if n <= 0:
             raise ValueError("fragment-order weights need in_channels % 32 == 0")
         src = w.detach().to(torch.float32).contiguous()
-        out = torch.empty(n, dtype=torch.bfloat16, device=w.device)
+        out = torch.empty(n, dtype=dtype, device=w.device)
+        w_scale = self._fp8_weight_scale(src) if dtype == torch.float8_e4m3fn else None
         _lib.check(lib.fovi_knnconv_pack_weight_mfma(_lib.ptr(src), self.out_channels, self.in_channels, n_ref,
-                                                     _lib.ptr(out), _lib.BF16, _lib.ptr(self._slot_order_dev),
+                                                     _lib.ptr(out), _lib.dtype_code(dtype),
+                                                     _lib.ptr(self._slot_order_dev), _lib.ptr(w_scale),
                                                      _lib.stream_handle(w.device)),
                    "fovi_knnconv_pack_weight_mfma")
-        self._packed["mfma"] = (key, out)
-        return out
+        packed = out if w_scale is None else (out, w_scale)
+        self._packed[("mfma", dtype)] = (key, packed)
+        return packed
 
     def _mfma_lds_bytes(self):
         """LDS bytes of the fragment-order kernel's tile (its ``v5_layout``): the staged rows plus
@@ -272,12 +278,14 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
                 + self._heavy_stride * 8 + self._hlist_stride * 2)
 
     def _mfma_path(self, x, dt):
-        """Whether this call runs the fragment-order kernel (see ``mfma_weights``)."""
-        return (self.mfma_weights and dt == torch.bfloat16 and self.in_channels % 32 == 0
+        """Whether this call runs the fragment-order kernel (see ``mfma_weights``): bf16 or e4m3
+        input, channel chunks of 32 (bf16) or 64 (e4m3), 16-byte channels-last input rows."""
+        chunk, align = {torch.bfloat16: (32, 8), torch.float8_e4m3fn: (64, 16)}.get(dt, (0, 0))
+        return (self.mfma_weights and chunk > 0 and self.in_channels % chunk == 0
                 and self._mfma_lds_bytes() <= 160 * 1024
                 and self.out_channels % 256 == 0 and self.tile_src is not None and 0 < self._zero_row <= 1023
-                and self._k <= 255 and x.stride(1) == 1 and x.stride(2) % 8 == 0 and x.stride(0) % 8 == 0
-                and x.data_ptr() % 16 == 0)
+                and self._k <= 255 and x.stride(1) == 1 and x.stride(2) % align == 0
+                and x.stride(0) % align == 0 and x.data_ptr() % 16 == 0)
 
     @property
     def padded_channels(self):
@@ -358,14 +366,18 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
             a.tile_coll = self.tile_coll.data_ptr(); a.tile_coll_n = self.tile_coll_n.data_ptr()
             a.zero_row = self._zero_row
         if mfma:
-            a.tile_src = self.tile_src.data_ptr(); a.tile_coll_off = self.tile_coll_off.data_ptr()
-            a.tile_cent = self.tile_cent.data_ptr()
-            a.coll_off_stride = self._coll_off_stride; a.cent_stride = self._cent_stride
-            a.tile_heavy = self.tile_heavy.data_ptr(); a.tile_hlist = self.tile_hlist.data_ptr()
-            a.heavy_stride = self._heavy_stride; a.hlist_stride = self._hlist_stride
+            self._set_wide_tables(a)
         lib = _lib.load()
         _lib.check(lib.fovi_knnconv_fwd(a, _lib.stream_handle(x.device)), "fovi_knnconv_fwd")
         return y.transpose(1, 2)
+
+    def _set_wide_tables(self, a):
+        """The fragment-order kernel's tables, into the ``fovi_knnconv_args`` ``a``."""
+        a.tile_src = self.tile_src.data_ptr(); a.tile_coll_off = self.tile_coll_off.data_ptr()
+        a.tile_cent = self.tile_cent.data_ptr()
+        a.coll_off_stride = self._coll_off_stride; a.cent_stride = self._cent_stride
+        a.tile_heavy = self.tile_heavy.data_ptr(); a.tile_hlist = self.tile_hlist.data_ptr()
+        a.heavy_stride = self._heavy_stride; a.hlist_stride = self._hlist_stride
 
     # -- fp8 ----------------------------------------------------------------
     @property
@@ -390,7 +402,10 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
                              f"got {tuple(x.shape)}")
         if self.tile_lo is None:
             raise NotImplementedError("fp8 kNN-conv needs the tile tables (k <= 255, tile spans <= 65535)")
-        w, w_scale = self._packed_weight(torch.float8_e4m3fn)
+        mfma = self._mfma_path(x, torch.float8_e4m3fn)
+        self.last_weight_layout = "mfma" if mfma else "rows"
+        w, w_scale = (self._packed_weight_mfma(torch.float8_e4m3fn) if mfma
+                      else self._packed_weight(torch.float8_e4m3fn))
         bsz, n_out = x.shape[0], self.out_coords.shape[0]
         y = torch.empty(bsz, n_out, self.out_channels, dtype=torch.bfloat16, device=x.device)
         bias = None if self.bias is None else self.bias.detach().to(torch.float32).contiguous()
@@ -402,7 +417,9 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         a.n_out, a.k, a.n_ref = n_out, self._k, self.ref_coords.shape[0]
         a.slot_ptr = self.slot_ptr.data_ptr(); a.nbr_sorted = self.nbr_sorted.data_ptr()
         a.w = w.data_ptr(); a.w_dtype = _lib.F8E4M3
-        a.c_out, a.k_pad = self.out_channels, w.shape[1]
+        a.w_layout = _lib.W_MFMA if mfma else _lib.W_ROWS
+        a.c_out = self.out_channels
+        a.k_pad = self.in_channels * self.ref_coords.shape[0] if mfma else w.shape[1]
         a.bias = None if bias is None else bias.data_ptr()
         a.w_scale = w_scale.data_ptr(); a.x_scale_dev = scale.data_ptr()
         a.y = y.data_ptr(); a.y_dtype = _lib.BF16
@@ -416,6 +433,8 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         a.tile_points = T.TILE_POINTS; a.max_span = self._max_span
         a.tile_coll = self.tile_coll.data_ptr(); a.tile_coll_n = self.tile_coll_n.data_ptr()
         a.zero_row = self._zero_row
+        if mfma:
+            self._set_wide_tables(a)
         lib = _lib.load()
         _lib.check(lib.fovi_knnconv_fwd(a, _lib.stream_handle(x.device)), "fovi_knnconv_fwd(fp8)")
         return y.transpose(1, 2)

@@ -1521,20 +1521,23 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
 
   if (a->w_layout != FOVI_W_ROWS) {
-    if (a->w_layout != FOVI_W_MFMA || a->x_dtype != FOVI_BF16 || a->w_dtype != FOVI_BF16 || p.w_c_slot != p.C) {
-      set_error("fovi_knnconv_fwd: w_layout=%d needs BF16 input and weight", a->w_layout);
+    const int f8 = a->x_dtype == FOVI_F8E4M3 && a->w_dtype == FOVI_F8E4M3;
+    if (a->w_layout != FOVI_W_MFMA || !(f8 || (a->x_dtype == FOVI_BF16 && a->w_dtype == FOVI_BF16)) ||
+        p.w_c_slot != p.C) {
+      set_error("fovi_knnconv_fwd: w_layout=%d needs BF16 or F8E4M3 input and weight", a->w_layout);
       return 1;
     }
-    if (!v5_applies(p)) {
-      set_error("fovi_knnconv_fwd: fragment-order weights need c_in %% 32 == 0, channels-last 16-byte input "
-                "rows, the tile tables with zero_row <= 1024 and k <= 255");
+    if (!v5_applies(p, f8)) {
+      set_error("fovi_knnconv_fwd: fragment-order weights need c_in %% %d == 0, channels-last 16-byte input "
+                "rows, the wide-layer tables within 160 KB of LDS (zero_row <= 1023)%s", f8 ? 64 : 32,
+                f8 ? " and w_scale" : "");
       return 1;
     }
-    if (launch_knnconv_bf16_v5(p, a->y_dtype, s) != 0) {
+    if ((f8 ? launch_knnconv_fp8_v5(p, a->y_dtype, s) : launch_knnconv_bf16_v5(p, a->y_dtype, s)) != 0) {
       set_error("fovi_knnconv_fwd: tile span too large for the fragment-order kernel");
       return 1;
     }
-    return check_launch("fovi_knnconv_fwd(bf16 v5)");
+    return check_launch(f8 ? "fovi_knnconv_fwd(fp8 v5)" : "fovi_knnconv_fwd(bf16 v5)");
   }
 
   if (a->x_dtype == FOVI_F32 && a->w_dtype == FOVI_F32) {

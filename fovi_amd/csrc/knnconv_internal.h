@@ -109,8 +109,10 @@ static int pick_tile_n(int64_t cout, Fits fits) {
 }
 
 int launch_knnconv_fp8(const KnnParams& p, int out_t, hipStream_t s);
-// 1 if the fragment-order kernel takes this call (see knnconv_v5.hip), 0 if not.
-int v5_applies(const KnnParams& p);
+// 1 if the fragment-order kernel takes this call (see knnconv_v5.hip; f8:
+// e4m3 input and weight), 0 if not.
+int v5_applies(const KnnParams& p, int f8);
 int launch_knnconv_bf16_v5(const KnnParams& p, int out_t, hipStream_t s);
+int launch_knnconv_fp8_v5(const KnnParams& p, int out_t, hipStream_t s);
 
 }  // namespace fovi

@@ -30,10 +30,13 @@ namespace fovi {
 
 constexpr int V5_MT = 256;   // output points per tile
 constexpr int V5_NT = 256;   // output channels per tile
-constexpr int V5_CC = 32;    // channels per reduction chunk (one 64-byte LDS row)
+constexpr int V5_ROW = 64;   // bytes of an LDS row: one reduction chunk (32 bf16 or 64 e4m3 channels)
 constexpr int V5_NB = 3;     // collision tiles: slot v uses tile v % 3, so sums run up to two slots ahead
 
 constexpr int V5_STREAM_MAX = 6;   // neighbours of a stream entry; more: a heavy entry
+
+typedef int i32x8 __attribute__((ext_vector_type(8)));        // e4m3 MFMA operand (32 bytes)
+typedef uint32_t u32x8v __attribute__((ext_vector_type(8)));
 
 // LDS byte layout of a tile. The staged rows S come first, at offset 0, then
 // the heavy-sum rows, so the host tables can hold absolute LDS byte offsets
@@ -45,10 +48,10 @@ struct V5Layout {
 __host__ __device__ inline V5Layout v5_layout(int V, int zero_row, int coff_stride, int cent_stride,
                                               int heavy_stride, int hlist_stride) {
   V5Layout l;
-  int o = (zero_row + 1) * V5_CC * 2;               // staged rows + zero row
-  l.heavy_rows = o; o += heavy_stride * V5_CC * 2;  // heavy sums, one 64-byte row per heavy entry
+  int o = (zero_row + 1) * V5_ROW;                  // staged rows + zero row
+  l.heavy_rows = o; o += heavy_stride * V5_ROW;     // heavy sums, one row per heavy entry
   o = (o + 127) & ~127;
-  l.acol_off = o;   o += (V5_NB * V5_MT + 1) * V5_CC * 2; // V5_NB 256 x 32 bf16 collision tiles + a trash row
+  l.acol_off = o;   o += (V5_NB * V5_MT + 1) * V5_ROW; // V5_NB collision tiles of 256 rows + a trash row
   l.src_off = o;    o += V * V5_MT * 2;             // per (slot, row) A source, slot-major
   l.coff_off = o;   o += coff_stride * 4;           // per-slot collision entry offsets
   l.cent_off = o;   o += cent_stride * 16;          // collision entries
@@ -58,7 +61,7 @@ __host__ __device__ inline V5Layout v5_layout(int V, int zero_row, int coff_stri
   return l;
 }
 
-constexpr uint32_t V5_TILE_BYTES = V5_MT * V5_CC * 2;   // one collision tile
+constexpr uint32_t V5_TILE_BYTES = V5_MT * V5_ROW;   // one collision tile
 
 // Byte offset of 16-byte part 0 of 64-byte row r under the swz32 XOR swizzle;
 // part q of the row is at row_off(r) ^ (q << 4).
@@ -71,12 +74,42 @@ __device__ __forceinline__ u32x4 lds16(const uint8_t* smem, uint32_t off) {
   return *reinterpret_cast<const u32x4*>(smem + off);
 }
 
-// a += the 8 bf16 values of x (widened to fp32; fp32 adds in order).
-__device__ __forceinline__ void acc_bf16x8(f32x8& a, u32x4 x) { a += unpack_bf16x8(x); }
-
-__device__ __forceinline__ u32x4 pack_bf16x8(const f32x8& a) {
-  return u32x4{cvt_pk_bf16(a[0], a[1]), cvt_pk_bf16(a[2], a[3]), cvt_pk_bf16(a[4], a[5]), cvt_pk_bf16(a[6], a[7])};
-}
+// Element types. A 64-byte LDS row is one reduction chunk; collision sums
+// of a 16-byte part are fp32 (adds in list order from +0) rounded once to the
+// element type (bf16: RNE; e4m3: RNE, saturating).
+template <bool F8> struct V5Elem;
+template <> struct V5Elem<false> {
+  static constexpr int CC = 32;        // channels per chunk
+  static constexpr int ESZ = 2;        // bytes per element
+  typedef f32x8 Sum;                   // the 8 channels of a 16-byte part
+  static __device__ __forceinline__ void acc(Sum& a, u32x4 x) { a += unpack_bf16x8(x); }
+  static __device__ __forceinline__ u32x4 pack(const Sum& a) {
+    return u32x4{cvt_pk_bf16(a[0], a[1]), cvt_pk_bf16(a[2], a[3]), cvt_pk_bf16(a[4], a[5]), cvt_pk_bf16(a[6], a[7])};
+  }
+};
+template <> struct V5Elem<true> {
+  static constexpr int CC = 64;
+  static constexpr int ESZ = 1;
+  typedef f32x16 Sum;                  // the 16 channels of a 16-byte part
+  static __device__ __forceinline__ void acc(Sum& a, u32x4 x) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(x[w]), false);
+      const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(x[w]), true);
+      a[4 * w] += lo[0];
+      a[4 * w + 1] += lo[1];
+      a[4 * w + 2] += hi[0];
+      a[4 * w + 3] += hi[1];
+    }
+  }
+  static __device__ __forceinline__ u32x4 pack(const Sum& a) {
+    u32x4 out;
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      out[w] = cvt_pk_e4m3<true>(a[4 * w + 2], a[4 * w + 3], cvt_pk_e4m3<false>(a[4 * w], a[4 * w + 1], 0u));
+    return out;
+  }
+};
 
 // Index of the 1 KB weight fragment (iteration it, 32-column block cb,
 // half ks) in the MFMA-fragment order; iteration it = chunk * n_ref + slot.
@@ -84,15 +117,15 @@ __host__ __device__ inline int64_t v5_frag(int64_t it, int64_t ncb, int64_t cb, 
   return (it * ncb + cb) * 2 + ks;
 }
 
-template <int SV, typename OutT>
-__global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, int ncb, int64_t tiles_per_b,
-                                                                 int64_t n_tiles_n, int64_t total_tiles,
-                                                                 int64_t padded_tiles, int vec_out) {
+template <int SV, typename OutT, bool F8>
+__device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t tiles_per_b, int64_t n_tiles_n,
+                                        int64_t total_tiles, int64_t padded_tiles, int vec_out) {
+  typedef V5Elem<F8> E;
+  typedef typename E::Sum Sum;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int V = static_cast<int>(p.V);
   const int zr = p.zero_row;
   const V5Layout L = v5_layout(V, zr, p.coll_off_stride, p.cent_stride, p.heavy_stride, p.hlist_stride);
-  uint16_t* S = reinterpret_cast<uint16_t*>(smem);
   const uint16_t* srcs = reinterpret_cast<const uint16_t*>(smem + L.src_off);
   const int32_t* coff = reinterpret_cast<const int32_t*>(smem + L.coff_off);
   const u32x4* cent = reinterpret_cast<const u32x4*>(smem + L.cent_off);
@@ -116,16 +149,16 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
   const int64_t lo = p.tile_lo[pt];
   const int span = static_cast<int>(min(static_cast<int64_t>(zr), p.Nin - lo));
 
-  const char* xrows = reinterpret_cast<const char*>(static_cast<const uint16_t*>(p.x) + b * p.xs0 + lo * p.xs2);
+  const char* xrows = static_cast<const char*>(p.x) + (b * p.xs0 + lo * p.xs2) * E::ESZ;
   uint32_t s_off[SV];
   uint32_t s_ok = 0;
 #pragma unroll
   for (int j = 0; j < SV; ++j) {
     const int q = tid + 256 * j;
     s_ok |= static_cast<uint32_t>((q >> 2) < span) << j;
-    s_off[j] = static_cast<uint32_t>(((q >> 2) * p.xs2 + (q & 3) * 8) * 2);
+    s_off[j] = static_cast<uint32_t>((q >> 2) * p.xs2 * E::ESZ + (q & 3) * 16);
   }
-  const int ncc = static_cast<int>(p.C / V5_CC);
+  const int ncc = static_cast<int>(p.C / E::CC);
   const int nit = ncc * V;
   // this wave's weight fragments: column blocks cb0 .. cb0 + 3; the base of
   // an iteration's fragments is wave-uniform, the lane adds 16 bytes
@@ -133,7 +166,7 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
 
   u32x4 rs[SV];
   auto load_s = [&](int cc) {
-    const char* base = xrows + cc * V5_CC * 2;
+    const char* base = xrows + cc * V5_ROW;
 #pragma unroll
     for (int j = 0; j < SV; ++j)
       rs[j] = ((s_ok >> j) & 1) ? *reinterpret_cast<const u32x4*>(base + s_off[j]) : u32x4{0u, 0u, 0u, 0u};
@@ -142,7 +175,7 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
 #pragma unroll
     for (int j = 0; j < SV; ++j) {
       const int q = tid + 256 * j;
-      if ((s_ok >> j) & 1) *reinterpret_cast<u32x4*>(&S[swz32(q >> 2, q & 3)]) = rs[j];
+      if ((s_ok >> j) & 1) *reinterpret_cast<u32x4*>(smem + (row_off(q >> 2) ^ ((q & 3) << 4))) = rs[j];
     }
   };
   auto load_w = [&](int it, u32x4 (&dst)[8]) {
@@ -192,23 +225,23 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
         if (dst[u]) *dst[u] = t[u];
     }
   }
-  if (tid < 4) *reinterpret_cast<u32x4*>(&S[zr * V5_CC + tid * 8]) = u32x4{0u, 0u, 0u, 0u};
+  if (tid < 4) *reinterpret_cast<u32x4*>(smem + zr * V5_ROW + tid * 16) = u32x4{0u, 0u, 0u, 0u};
 
   // Collision sums. A unit is (entry, 16-byte part): entry = unit / 4. Its
   // first four neighbours are summed from the entry's words 1-2, neighbours 5
   // and 6 from word 3 (missing ones are the zero row).
   auto unit_sum4 = [&](const u32x4 ce, uint32_t pq) {
-    f32x8 a = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    acc_bf16x8(a, lds16(smem, (ce[1] & 0xffffu) ^ pq));
-    acc_bf16x8(a, lds16(smem, (ce[1] >> 16) ^ pq));
-    acc_bf16x8(a, lds16(smem, (ce[2] & 0xffffu) ^ pq));
-    acc_bf16x8(a, lds16(smem, (ce[2] >> 16) ^ pq));
+    Sum a = {};
+    E::acc(a, lds16(smem, (ce[1] & 0xffffu) ^ pq));
+    E::acc(a, lds16(smem, (ce[1] >> 16) ^ pq));
+    E::acc(a, lds16(smem, (ce[2] & 0xffffu) ^ pq));
+    E::acc(a, lds16(smem, (ce[2] >> 16) ^ pq));
     return a;
   };
-  auto unit_rest = [&](f32x8& a, const u32x4 ce, uint32_t pq) {
+  auto unit_rest = [&](Sum& a, const u32x4 ce, uint32_t pq) {
     if (((ce[0] >> 16) & 0xffu) > 4) {
-      acc_bf16x8(a, lds16(smem, (ce[3] & 0xffffu) ^ pq));
-      acc_bf16x8(a, lds16(smem, (ce[3] >> 16) ^ pq));
+      E::acc(a, lds16(smem, (ce[3] & 0xffffu) ^ pq));
+      E::acc(a, lds16(smem, (ce[3] >> 16) ^ pq));
     }
   };
   // collision tile offset of a unit (the entry holds tile and row)
@@ -223,15 +256,15 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
       const int cnt = static_cast<int>((w0 >> 16) & 0xffu);
       if (cnt == 0) continue;
       const uint32_t pq = static_cast<uint32_t>(u & 3) << 4;
-      f32x8 a = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      Sum a = {};
       for (int j = 0; j < cnt; j += 4) {
         uint32_t r[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) r[q] = j + q < cnt ? hlist[w1 + j + q] : zoff;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) acc_bf16x8(a, lds16(smem, r[q] ^ pq));
+        for (int q = 0; q < 4; ++q) E::acc(a, lds16(smem, r[q] ^ pq));
       }
-      *reinterpret_cast<u32x4*>(smem + ((w0 & 0xffffu) ^ pq)) = pack_bf16x8(a);
+      *reinterpret_cast<u32x4*>(smem + ((w0 & 0xffffu) ^ pq)) = E::pack(a);
     }
   };
   // units [from, to) of the tile's unit stream (the entry list in slot order,
@@ -240,9 +273,9 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
     for (int u = from + tid; u < to; u += 256) {
       const u32x4 ce = cent[u >> 2];
       const uint32_t pq = static_cast<uint32_t>(u & 3) << 4;
-      f32x8 a = unit_sum4(ce, pq);
+      Sum a = unit_sum4(ce, pq);
       unit_rest(a, ce, pq);
-      *reinterpret_cast<u32x4*>(smem + unit_dst(ce, pq)) = pack_bf16x8(a);
+      *reinterpret_cast<u32x4*>(smem + unit_dst(ce, pq)) = E::pack(a);
     }
   };
 
@@ -262,7 +295,11 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
     rowm[i] = wm * 128 + i * 32 + (lane & 31);
     rowm_off[i] = acol + row_off(rowm[i]);
   }
-  const uint32_t qx = static_cast<uint32_t>(lane >> 5) << 4;   // 16-byte part of ks = 0
+  // the two 16-byte parts of a row this lane feeds to the MFMAs: bf16, parts
+  // (lane / 32) and 2 + lane / 32 (K halves ks = 0, 1); e4m3, parts
+  // 2 (lane / 32) and 2 (lane / 32) + 1 (channels 32 (lane / 32) .. + 32)
+  const uint32_t qx0 = F8 ? static_cast<uint32_t>(lane >> 5) << 5 : static_cast<uint32_t>(lane >> 5) << 4;
+  const uint32_t qx1 = F8 ? qx0 ^ 16u : qx0 ^ 32u;
 
   u32x4 wa[8], wb[8];
   load_w(0, wa);
@@ -300,12 +337,12 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
     const int vn = v + 1 == V ? 0 : v + 1;
     const int need_n = 4 * coff[vn + 1], lim_n = 4 * coff[min(vn + V5_NB, V)];
 
-    bf16x8 af[2][4];
+    u32x4 af[2][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t a = ecur[i] == 0xffffu ? rowm_off[i] + vb * V5_TILE_BYTES : ecur[i];
-      af[0][i] = __builtin_bit_cast(bf16x8, lds16(smem, a ^ qx));
-      af[1][i] = __builtin_bit_cast(bf16x8, lds16(smem, a ^ qx ^ 32u));
+      af[0][i] = lds16(smem, a ^ qx0);
+      af[1][i] = lds16(smem, a ^ qx1);
     }
     load_w(more ? it + 1 : it, bn);
 #pragma unroll
@@ -315,19 +352,35 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
     const uint32_t pq = static_cast<uint32_t>(tid & 3) << 4;
     u32x4 ce = cent[u < lim ? (u >> 2) : 0];
     if (u >= lim) ce[0] = 0;      // count 0: written to the trash row
-    f32x8 sum = unit_sum4(ce, pq);
+    Sum sum = unit_sum4(ce, pq);
 
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    if constexpr (F8) {
+      // one 32x32x64 e4m3 MFMA per block (unit scales); lane operands: 32
+      // channels = the two parts, weight fragments j * 2 + 0, 1
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks][i], __builtin_bit_cast(bf16x8, bc[j * 2 + ks]),
-                                                              acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 4; ++j) {
+          const i32x8 a8 = __builtin_bit_cast(i32x8, u32x8v{af[0][i][0], af[0][i][1], af[0][i][2], af[0][i][3],
+                                                            af[1][i][0], af[1][i][1], af[1][i][2], af[1][i][3]});
+          const u32x4 b0 = bc[j * 2], b1 = bc[j * 2 + 1];
+          const i32x8 b8 = __builtin_bit_cast(i32x8, u32x8v{b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]});
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, acc[i][j], 0, 0, 0, 127, 0, 127);
+        }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, af[ks][i]),
+                                                                __builtin_bit_cast(bf16x8, bc[j * 2 + ks]), acc[i][j],
+                                                                0, 0, 0);
+    }
 
     unit_rest(sum, ce, pq);
-    *reinterpret_cast<u32x4*>(smem + (((ce[0] >> 16) & 0xffu) ? unit_dst(ce, pq) : trash)) = pack_bf16x8(sum);
+    *reinterpret_cast<u32x4*>(smem + (((ce[0] >> 16) & 0xffu) ? unit_dst(ce, pq) : trash)) = E::pack(sum);
     bpos = min(bpos + 256, lim);
     __syncthreads();
     v = vn;
@@ -354,17 +407,21 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
   }
 
   OutT* y = static_cast<OutT*>(p.y) + b * p.ys0;
-  float bo[4];
+  float bo[4], sc[4];
+  const float xs = F8 ? (p.x_scale_dev ? *p.x_scale_dev : p.x_scale) : 1.0f;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int64_t o = o0 + wn * 128 + j * 32 + (lane & 31);
     bo[j] = (p.bias && o < p.Cout) ? p.bias[o] : 0.0f;
+    sc[j] = F8 && o < p.Cout ? xs * p.w_scale[o] : 1.0f;
   }
+  // y = acc + bias (bf16); x_scale * w_scale[o] * acc + bias (e4m3)
+  auto out_val = [&](float a, int j) { return epilogue(F8 ? a * sc[j] + bo[j] : a + bo[j], p.relu); };
   if (vec_out) {
     // bf16 channels-last output: each wave transposes its 32-row blocks
     // through LDS (the collision tiles, free now) and stores 16-byte pieces,
     // four 256-byte row runs per store instruction
-    uint16_t* E = reinterpret_cast<uint16_t*>(smem + acol) + wave * 32 * 128;
+    uint16_t* Eo = reinterpret_cast<uint16_t*>(smem + acol) + wave * 32 * 128;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -372,7 +429,7 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          E[row * 128 + j * 32 + (lane & 31)] = f32_to_bf16_bits(epilogue(acc[i][j][r] + bo[j], p.relu));
+          Eo[row * 128 + j * 32 + (lane & 31)] = f32_to_bf16_bits(out_val(acc[i][j][r], j));
         }
       __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS writes are done
       __builtin_amdgcn_wave_barrier();
@@ -380,7 +437,7 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
       for (int q = 0; q < 8; ++q) {
         const int piece = q * 64 + lane;
         const int row = piece >> 4, part = piece & 15;
-        const u32x4 val = *reinterpret_cast<const u32x4*>(&E[row * 128 + part * 8]);
+        const u32x4 val = *reinterpret_cast<const u32x4*>(&Eo[row * 128 + part * 8]);
         const int64_t n = n0 + wm * 128 + i * 32 + row;
         const int64_t o = o0 + wn * 128 + part * 8;
         if (n < p.Nout && o < p.Cout)
@@ -400,12 +457,40 @@ __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, in
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int64_t n = n0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (n < p.Nout) Elem<OutT>::store(y + o * p.ys1 + n * p.ys2, epilogue(acc[i][j][r] + bo[j], p.relu));
+        if (n < p.Nout) Elem<OutT>::store(y + o * p.ys1 + n * p.ys2, out_val(acc[i][j][r], j));
       }
   }
 }
 
-template <int SV>
+template <int SV, typename OutT>
+__global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, int ncb, int64_t tiles_per_b,
+                                                                 int64_t n_tiles_n, int64_t total_tiles,
+                                                                 int64_t padded_tiles, int vec_out) {
+  v5_body<SV, OutT, false>(p, ncb, tiles_per_b, n_tiles_n, total_tiles, padded_tiles, vec_out);
+}
+
+template <int SV, typename OutT>
+__global__ __launch_bounds__(256, 1) void knnconv_fp8_v5_kernel(KnnParams p, int ncb, int64_t tiles_per_b,
+                                                                int64_t n_tiles_n, int64_t total_tiles,
+                                                                int64_t padded_tiles, int vec_out) {
+  v5_body<SV, OutT, true>(p, ncb, tiles_per_b, n_tiles_n, total_tiles, padded_tiles, vec_out);
+}
+
+template <int SV, bool F8, typename OutT>
+static void launch_v5_kernel(const KnnParams& p, hipStream_t s, size_t lds, dim3 grid, int ncb, int64_t tiles_per_b,
+                             int64_t n_tiles_n, int64_t total, int64_t padded, int vec_out) {
+  const void* fn = F8 ? reinterpret_cast<const void*>(&knnconv_fp8_v5_kernel<SV, OutT>)
+                      : reinterpret_cast<const void*>(&knnconv_bf16_v5_kernel<SV, OutT>);
+  (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+  if constexpr (F8)
+    hipLaunchKernelGGL((knnconv_fp8_v5_kernel<SV, OutT>), grid, dim3(256), lds, s, p, ncb, tiles_per_b, n_tiles_n,
+                       total, padded, vec_out);
+  else
+    hipLaunchKernelGGL((knnconv_bf16_v5_kernel<SV, OutT>), grid, dim3(256), lds, s, p, ncb, tiles_per_b, n_tiles_n,
+                       total, padded, vec_out);
+}
+
+template <int SV, bool F8>
 static void launch_v5_sv(const KnnParams& p, int out_t, hipStream_t s) {
   const int64_t tiles_per_b = (p.Nout + V5_MT - 1) / V5_MT;
   const int64_t n_tiles_n = (p.Cout + V5_NT - 1) / V5_NT;
@@ -417,86 +502,97 @@ static void launch_v5_sv(const KnnParams& p, int out_t, hipStream_t s) {
   // 16-byte channels-last bf16 stores: unit channel stride, rows and base 16-byte aligned
   const int vec_out = out_t == FOVI_BF16 && p.ys1 == 1 && p.ys2 % 8 == 0 && p.ys0 % 8 == 0 && p.Cout % 8 == 0 &&
                       reinterpret_cast<uintptr_t>(p.y) % 16 == 0;
-  dim3 grid(static_cast<unsigned>(padded));
-  if (out_t == FOVI_BF16) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&knnconv_bf16_v5_kernel<SV, uint16_t>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    hipLaunchKernelGGL((knnconv_bf16_v5_kernel<SV, uint16_t>), grid, dim3(256), lds, s, p, ncb, tiles_per_b,
-                       n_tiles_n, total, padded, vec_out);
-  } else {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&knnconv_bf16_v5_kernel<SV, float>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    hipLaunchKernelGGL((knnconv_bf16_v5_kernel<SV, float>), grid, dim3(256), lds, s, p, ncb, tiles_per_b,
-                       n_tiles_n, total, padded, 0);
-  }
+  const dim3 grid(static_cast<unsigned>(padded));
+  if (out_t == FOVI_BF16)
+    launch_v5_kernel<SV, F8, uint16_t>(p, s, lds, grid, ncb, tiles_per_b, n_tiles_n, total, padded, vec_out);
+  else
+    launch_v5_kernel<SV, F8, float>(p, s, lds, grid, ncb, tiles_per_b, n_tiles_n, total, padded, 0);
 }
 
-int v5_applies(const KnnParams& p) {
+int v5_applies(const KnnParams& p, int f8) {
   if (p.w_layout != FOVI_W_MFMA) return 0;
-  if (p.C % V5_CC != 0 || p.zero_row <= 0 || p.zero_row > 1023 || !p.tile_lo || !p.tile_src ||
-      !p.tile_coll_off || !p.tile_cent || !p.tile_heavy || !p.tile_hlist || p.V > 255)
+  if (p.C % (f8 ? V5Elem<true>::CC : V5Elem<false>::CC) != 0 || p.zero_row <= 0 || p.zero_row > 1023 ||
+      !p.tile_lo || !p.tile_src || !p.tile_coll_off || !p.tile_cent || !p.tile_heavy || !p.tile_hlist || p.V > 255)
     return 0;
+  if (f8 && !p.w_scale) return 0;
   if (p.coll_off_stride <= p.V || p.coll_off_stride % 4 != 0 || p.cent_stride < 1) return 0;
   if (p.heavy_stride < 2 || p.heavy_stride % 2 != 0 || p.hlist_stride < 8 || p.hlist_stride % 8 != 0) return 0;
-  if ((p.zero_row + 1 + p.heavy_stride) * V5_CC * 2 > 0xffff) return 0;   // 16-bit row offsets
+  if ((p.zero_row + 1 + p.heavy_stride) * V5_ROW > 0xffff) return 0;   // 16-bit row offsets
   if ((reinterpret_cast<uintptr_t>(p.tile_src) | reinterpret_cast<uintptr_t>(p.tile_coll_off) |
        reinterpret_cast<uintptr_t>(p.tile_cent) | reinterpret_cast<uintptr_t>(p.tile_heavy) |
        reinterpret_cast<uintptr_t>(p.tile_hlist)) % 16 != 0)
     return 0;
-  if (p.xs1 != 1 || p.xs2 % 8 != 0 || p.xs0 % 8 != 0 || reinterpret_cast<uintptr_t>(p.x) % 16 != 0) return 0;
+  // channels-last rows, 16-byte aligned
+  const int64_t al = f8 ? 16 : 8;
+  if (p.xs1 != 1 || p.xs2 % al != 0 || p.xs0 % al != 0 || reinterpret_cast<uintptr_t>(p.x) % 16 != 0) return 0;
   if (reinterpret_cast<uintptr_t>(p.w) % 16 != 0) return 0;
   return v5_layout(static_cast<int>(p.V), p.zero_row, p.coll_off_stride, p.cent_stride, p.heavy_stride,
                    p.hlist_stride).total <= 160 * 1024;
 }
 
-int launch_knnconv_bf16_v5(const KnnParams& p, int out_t, hipStream_t s) {
+template <bool F8>
+static int launch_v5(const KnnParams& p, int out_t, hipStream_t s) {
   const int sv = (p.zero_row * 4 + 255) / 256;
-  if (sv <= 4) launch_v5_sv<4>(p, out_t, s);
-  else if (sv <= 8) launch_v5_sv<8>(p, out_t, s);
-  else if (sv <= 12) launch_v5_sv<12>(p, out_t, s);
-  else if (sv <= 16) launch_v5_sv<16>(p, out_t, s);
+  if (sv <= 4) launch_v5_sv<4, F8>(p, out_t, s);
+  else if (sv <= 8) launch_v5_sv<8, F8>(p, out_t, s);
+  else if (sv <= 12) launch_v5_sv<12, F8>(p, out_t, s);
+  else if (sv <= 16) launch_v5_sv<16, F8>(p, out_t, s);
   else return 1;
   return 0;
 }
 
-// Fragment-order weight: fragment (it, cb, ks) holds, for lane l and e < 8,
-// w[o = cb * 32 + l % 32][c * n_ref + v] with it = (c / 32) * n_ref + p, slot
-// v = order[p] (v = p without an order) and c % 32 = ks * 16 + (l / 32) * 8 + e
-// (zero for o >= c_out).
-__global__ void pack_weight_mfma_kernel(const float* w_ref, int64_t c_out, int64_t c_in, int64_t n_ref,
-                                        uint16_t* out, int64_t ncb, int64_t total, const int32_t* order) {
+int launch_knnconv_bf16_v5(const KnnParams& p, int out_t, hipStream_t s) { return launch_v5<false>(p, out_t, s); }
+int launch_knnconv_fp8_v5(const KnnParams& p, int out_t, hipStream_t s) { return launch_v5<true>(p, out_t, s); }
+
+// Fragment-order weight, 1 KB fragments f = (it * ncb + cb) * 2 + h with
+// it = chunk * n_ref + p and slot v = order[p] (v = p without an order);
+// lane l of fragment f holds w[o = cb * 32 + l % 32][c * n_ref + v] (zero for
+// o >= c_out) for
+//  * bf16 (32-channel chunks), e < 8: c % 32 = h * 16 + (l / 32) * 8 + e;
+//  * e4m3 (64-channel chunks, divided by w_scale[o]), e < 16:
+//    c % 64 = (l / 32) * 32 + h * 16 + e.
+__global__ void pack_weight_mfma_kernel(const float* w_ref, int64_t c_out, int64_t c_in, int64_t n_ref, void* out,
+                                        int64_t ncb, int64_t total, const int32_t* order, const float* w_scale) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (idx >= total) return;
-  const int e = static_cast<int>(idx & 7);
-  const int l = static_cast<int>((idx >> 3) & 63);
-  const int64_t frag = idx >> 9;
-  const int ks = static_cast<int>(frag & 1);
+  const bool f8 = w_scale != nullptr;
+  const int eb = f8 ? 4 : 3;   // log2 of elements per lane and fragment
+  const int e = static_cast<int>(idx & ((1 << eb) - 1));
+  const int l = static_cast<int>((idx >> eb) & 63);
+  const int64_t frag = idx >> (eb + 6);
+  const int h = static_cast<int>(frag & 1);
   const int64_t cb = (frag >> 1) % ncb;
   const int64_t it = (frag >> 1) / ncb;
   const int64_t pos = it % n_ref, cc = it / n_ref;
   const int64_t v = order ? order[pos] : pos;
   const int64_t o = cb * 32 + (l & 31);
-  const int64_t c = cc * V5_CC + ks * 16 + (l >> 5) * 8 + e;
+  const int64_t c = f8 ? cc * 64 + (l >> 5) * 32 + h * 16 + e : cc * 32 + h * 16 + (l >> 5) * 8 + e;
   const float val = o < c_out ? w_ref[o * c_in * n_ref + c * n_ref + v] : 0.0f;
-  out[idx] = f32_to_bf16_bits(val);
+  if (f8) static_cast<uint8_t*>(out)[idx] = o < c_out ? f32_to_e4m3(val / w_scale[o]) : 0;
+  else static_cast<uint16_t*>(out)[idx] = f32_to_bf16_bits(val);
 }
 
 }  // namespace fovi
 
 extern "C" int64_t fovi_knnconv_weight_mfma_elems(int64_t c_out, int64_t c_in, int64_t n_ref) {
   using namespace fovi;
-  if (c_out <= 0 || c_in <= 0 || n_ref <= 0 || c_in % V5_CC != 0) return -1;
+  if (c_out <= 0 || c_in <= 0 || n_ref <= 0 || c_in % 32 != 0) return -1;
   const int64_t ncb = (c_out + V5_NT - 1) / V5_NT * (V5_NT / 32);
   return c_in * n_ref * ncb * 32;
 }
 
 extern "C" int fovi_knnconv_pack_weight_mfma(const float* w_ref, int64_t c_out, int64_t c_in, int64_t n_ref,
                                              void* w_frag, int32_t out_dtype, const int32_t* slot_order,
-                                             void* stream) {
+                                             const float* w_scale, void* stream) {
   using namespace fovi;
   clear_error();
   if (!w_ref || !w_frag) { set_error("fovi_knnconv_pack_weight_mfma: null pointer"); return 1; }
-  if (out_dtype != FOVI_BF16) { set_error("fovi_knnconv_pack_weight_mfma: only BF16 is supported"); return 1; }
+  if (out_dtype != FOVI_BF16 && out_dtype != FOVI_F8E4M3) {
+    set_error("fovi_knnconv_pack_weight_mfma: out_dtype must be BF16 or F8E4M3"); return 1;
+  }
+  if (out_dtype == FOVI_F8E4M3 && (!w_scale || c_in % 64 != 0)) {
+    set_error("fovi_knnconv_pack_weight_mfma: F8E4M3 needs w_scale and c_in %% 64 == 0"); return 1;
+  }
   const int64_t total = fovi_knnconv_weight_mfma_elems(c_out, c_in, n_ref);
   if (total < 0) {
     set_error("fovi_knnconv_pack_weight_mfma: bad sizes c_out=%lld c_in=%lld (multiple of 32) n_ref=%lld",
@@ -505,7 +601,7 @@ extern "C" int fovi_knnconv_pack_weight_mfma(const float* w_ref, int64_t c_out, 
   }
   const int64_t ncb = (c_out + V5_NT - 1) / V5_NT * (V5_NT / 32);
   hipLaunchKernelGGL(pack_weight_mfma_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), w_ref, c_out, c_in, n_ref, static_cast<uint16_t*>(w_frag),
-                     ncb, total, slot_order);
+                     static_cast<hipStream_t>(stream), w_ref, c_out, c_in, n_ref, w_frag, ncb, total, slot_order,
+                     out_dtype == FOVI_F8E4M3 ? w_scale : nullptr);
   return check_launch("fovi_knnconv_pack_weight_mfma");
 }

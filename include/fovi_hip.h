@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 14
+#define FOVI_ABI_VERSION 15
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -209,23 +209,26 @@ int fovi_knnconv_pack_weight(const float* w_ref, int64_t c_out, int64_t c_in, in
                              const float* w_scale, void* stream);
 
 /*
- * Weight in MFMA-fragment order for the wide-layer bf16 kernel (w_layout =
+ * Weight in MFMA-fragment order for the wide-layer kernels (w_layout =
  * FOVI_W_MFMA). Same source as fovi_knnconv_pack_weight (w_ref = KNNConvLayer.weight,
  * fp32 [c_out, c_in * n_ref], index c * n_ref + v, fovi/arch/knn.py:462,524);
- * the output is fovi_knnconv_weight_mfma_elems(c_out, c_in, n_ref) bf16
- * values: 1 KB fragments f = ((it * ncb + cb) * 2 + ks), it = (c / 32) * n_ref + v,
- * ncb = 8 * ceil(c_out / 256); lane l of fragment f holds, at 8 * l + e,
- * w_ref[o = 32 * cb + l % 32][c * n_ref + v] with c % 32 = 16 * ks + 8 * (l / 32) + e
- * (zero for o >= c_out). c_in must be a multiple of 32; only BF16 output.
+ * the output is fovi_knnconv_weight_mfma_elems(c_out, c_in, n_ref) elements of
+ * out_dtype in 1 KB fragments f = (it * ncb + cb) * 2 + h, ncb = 8 * ceil(c_out / 256),
+ * it = chunk * n_ref + p. Lane l of fragment f holds w_ref[o = 32 * cb + l % 32][c * n_ref + v]
+ * (zero for o >= c_out) at
+ *   BF16 (32-channel chunks, c_in % 32 == 0): 8 * l + e, c % 32 = 16 * h + 8 * (l / 32) + e;
+ *   F8E4M3 (64-channel chunks, c_in % 64 == 0): 16 * l + e, c % 64 = 32 * (l / 32) + 16 * h + e,
+ *     the value divided by w_scale[o] and rounded to OCP e4m3 (RNE, saturating).
  * slot_order (device int32 [n_ref], or NULL for 0, 1, ...) is the order in
- * which the kernel visits the slots of a channel chunk: position p of
- * iteration it = (c / 32) * n_ref + p holds slot v = slot_order[p]. The
- * wide-layer tables (tile_src, tile_cent, tile_coll_off) must be laid out in
- * the same order.
+ * which the kernel visits the slots of a channel chunk: position p holds slot
+ * v = slot_order[p]. The wide-layer tables (tile_src, tile_cent, tile_coll_off)
+ * must be laid out in the same order. w_scale (device fp32 [c_out]) is read
+ * for F8E4M3 only.
  */
 int64_t fovi_knnconv_weight_mfma_elems(int64_t c_out, int64_t c_in, int64_t n_ref);
 int fovi_knnconv_pack_weight_mfma(const float* w_ref, int64_t c_out, int64_t c_in, int64_t n_ref,
-                                  void* w_frag, int32_t out_dtype, const int32_t* slot_order, void* stream);
+                                  void* w_frag, int32_t out_dtype, const int32_t* slot_order,
+                                  const float* w_scale, void* stream);
 
 /*
  * Per-tensor OCP e4m3 quantization of activations for the fp8 kNN-conv path

@@ -144,3 +144,58 @@ def test_fp8_rejects_unsupported_shapes():
     xq = quantize_e4m3(torch.randn(1, 32, 256, device="cuda"))
     with pytest.raises(RuntimeError, match="multiple of 64"):
         layer(xq)
+
+
+def test_pack_weight_mfma_fp8_bytes():
+    """e4m3 fragment-order weight: fragment (it, cb, h), lane l, byte e holds
+    q(W[32 cb + l % 32, c * V + v]) with c = 64 (it // V) + 32 (l // 32) + 16 h + e, v = it % V."""
+    layer = _layer(16, 16, 9, 128, 256, seed=3)
+    layer.set_slot_order(None)
+    w_frag, w_scale = layer._packed_weight_mfma(torch.float8_e4m3fn)
+    w = layer.weight.detach().cpu()
+    s = w.abs().amax(1) / 448.0
+    assert torch.equal(w_scale.cpu(), s)
+    q = (w / s[:, None]).to(torch.float8_e4m3fn).view(torch.uint8).reshape(256, 128, 9)   # [o, c, v]
+    got = w_frag.cpu().view(torch.uint8).reshape(-1, 8, 2, 64, 16)                         # [it, cb, h, l, e]
+    assert got.shape[0] == 2 * 9
+    l, e = torch.arange(64)[:, None], torch.arange(16)[None, :]
+    for it in (0, 4, 9, 17):
+        for cb in (0, 3, 7):
+            for h in (0, 1):
+                c = 64 * (it // 9) + 32 * (l // 32) + 16 * h + e
+                want = q[32 * cb + l % 32, c, it % 9]
+                assert torch.equal(got[it, cb, h], want), (it, cb, h)
+
+
+@pytest.mark.parametrize("res_in,res_out,k,c_in,c_out,bias,act,batch", [
+    (64, 64, 25, 128, 256, True, None, 2),       # two channel chunks
+    (16, 16, 9, 192, 512, False, "relu", 3),     # three chunks, two channel tiles, fused ReLU
+    (24, 12, 25, 64, 256, True, None, 2),        # strided: one partial point tile
+    (128, 128, 25, 256, 256, False, None, 2),    # C5 geometry
+])
+def test_fp8_fragment_order_kernel(res_in, res_out, k, c_in, c_out, bias, act, batch):
+    """The wide-layer e4m3 kernel: oracle bound, and with the plain slot order bit-identical to
+    the row-packed e4m3 kernel (same e4m3 slot sums, same K=64 accumulation order)."""
+    layer = _layer(res_in, res_out, k, c_in, c_out, bias, seed=7)
+    x = torch.randn(batch, c_in, res_in * res_in, generator=torch.Generator().manual_seed(8)).bfloat16()
+    xq = layer.quantize_input(x.cuda().transpose(1, 2).contiguous().transpose(1, 2))
+    run = (lambda: layer.forward_fused(xq, act)) if act else (lambda: layer(xq))
+    with torch.no_grad():
+        y = run()
+        assert layer.last_weight_layout == "mfma"
+        layer.mfma_weights = False
+        y_rows = run()
+        assert layer.last_weight_layout == "rows"
+        layer.mfma_weights = True
+        layer.set_slot_order(None)
+        y_plain = run()
+        assert layer.last_weight_layout == "mfma"
+    rows = slice(0, 1) if res_in >= 128 else None
+    ref = _fp8_oracle(layer, xq, rows=rows)
+    if act:
+        ref = torch.relu(ref)
+    got = y[:1] if rows is not None else y
+    assert_close_rel(got.float().cpu(), ref, 1e-2, "fp8 fragment-order kernel vs fp8 oracle")
+    assert _cos(got.float().cpu(), ref) >= 0.9999
+    assert_close_rel(y.float().cpu(), y_rows.float().cpu(), 1e-2, "fragment-order vs row-packed (fp8)")
+    assert torch.equal(y_plain, y_rows), "fp8 fragment-order (plain slot order) and row-packed kernels differ"
