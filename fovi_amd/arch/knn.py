@@ -150,8 +150,9 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         # few-channel bf16 layers: slot sums through a workspace, then a dense GEMM
         # (False: the single fused kernel, which needs no workspace)
         self.two_pass_few_channels = True
-        # wide bf16 layers (c_in % 32 == 0, c_out % 256 == 0): weights in MFMA-fragment order
-        # for the 256 x 256-tile kernel (False: the row-packed kernels)
+        # wide layers (bf16 c_in % 32 == 0 or e4m3 c_in % 64 == 0, c_out filling >= 3/4 of its
+        # 256-channel tiles, tables within LDS): weights in MFMA-fragment order for the
+        # 256 x 256-tile kernel (False: the row-packed kernels)
         self.mfma_weights = True
 
     # -- setup ---------------------------------------------------------------
@@ -277,13 +278,20 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         return (o + (3 * 256 + 1) * 32 * 2 + v * 256 * 2 + self._coll_off_stride * 4 + self._cent_stride * 16
                 + self._heavy_stride * 8 + self._hlist_stride * 2)
 
+    def _mfma_column_use(self):
+        """Fraction of the fragment-order kernel's 256-channel output tiles that holds real
+        channels (the weight is zero-padded up to the tile)."""
+        c = self.out_channels
+        return c / (256 * -(-c // 256))
+
     def _mfma_path(self, x, dt):
         """Whether this call runs the fragment-order kernel (see ``mfma_weights``): bf16 or e4m3
         input, channel chunks of 32 (bf16) or 64 (e4m3), 16-byte channels-last input rows."""
         chunk, align = {torch.bfloat16: (32, 8), torch.float8_e4m3fn: (64, 16)}.get(dt, (0, 0))
         return (self.mfma_weights and chunk > 0 and self.in_channels % chunk == 0
                 and self._mfma_lds_bytes() <= 160 * 1024
-                and self.out_channels % 256 == 0 and self.tile_src is not None and 0 < self._zero_row <= 1023
+                and self.out_channels % 8 == 0 and self._mfma_column_use() >= 0.75
+                and self.tile_src is not None and 0 < self._zero_row <= 1023
                 and self._k <= 255 and x.stride(1) == 1 and x.stride(2) % align == 0
                 and x.stride(0) % align == 0 and x.data_ptr() % 16 == 0)
 

@@ -230,6 +230,8 @@ def test_bf16_few_channels_padded_rows(c_in, k, side):
     (24, 12, 25, 64, 256, True, None, 3),     # strided: 144 outputs (one partial point tile)
     (16, 16, 25, 64, 256, False, None, 2),    # k = 25 on a small lattice (seam-heavy tiles)
     (128, 128, 25, 256, 256, False, None, 2), # C3 geometry
+    (24, 12, 25, 64, 192, True, "relu", 4),   # one 256-channel tile, 192 real channels
+    (16, 16, 9, 192, 384, False, None, 3),    # C2 layer 3: two tiles, 384 real
 ])
 def test_fragment_order_kernel(res_in, res_out, k, c_in, c_out, bias, act, batch):
     """Wide bf16 layers take the fragment-order (256 x 256 tile) kernel; it matches the oracle
