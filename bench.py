@@ -161,6 +161,28 @@ def _init_weights(layers, dev, seed):
                 c.bias.zero_()
 
 
+def bench_pool(steps, warmup, dev):
+    """kNN max pooling of the reference AlexNet (pool after a conv block, knnalexnet.py:90-101):
+    256 images, 64 channels on 1024 log-polar points -> 256 points, k=9, bf16 channels-last.
+    Algorithmic bytes: every input row once (all are neighbours) plus the output."""
+    import torch
+    from fovi_amd.arch.knn import KNNPoolingLayer
+    from fovi_amd.sensing.coords import SamplingCoords
+    B, C = 256, 64
+    ci = SamplingCoords(16, 2.78, 32, style="logpolar")
+    co = SamplingCoords(16, 2.78, 16, style="logpolar")
+    layer = KNNPoolingLayer(9, ci, co, mode="max", device=dev)
+    g = torch.Generator(device=dev).manual_seed(3)
+    x = torch.randn(B, ci.shape[0], C, generator=g, device=dev, dtype=torch.bfloat16).transpose(1, 2)
+    with torch.no_grad():
+        ms = time_steps(lambda: layer(x), steps, warmup)
+    nbytes = B * C * (ci.shape[0] + co.shape[0]) * 2
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"[pool] {ms:.4f} ms/step  {gbs:.0f} GB/s algorithmic ({100 * gbs / PEAK_HBM_GBS:.1f}% of HBM peak); "
+        f"bytes {nbytes / 1e6:.1f} MB")
+    return dict(ms=ms, gbs=gbs, bytes=nbytes)
+
+
 def bench_c2(steps, warmup, dev):
     """C2: 256 images 3x224x224 fp32 -> bilinear sampler (4096 log-polar points, bf16 out) ->
     5 kNN-conv layers 64/192/384/256/256, k=49/25/9/9/9, strides 2,2,1,1,1, ReLU between."""
@@ -310,12 +332,12 @@ def main():
     ap.add_argument("--no-sampler", action="store_true")
     ap.add_argument("--no-e2e", action="store_true", help="skip the C2/C4 end-to-end legs")
     ap.add_argument("--no-fp8", action="store_true", help="skip the C5 fp8 leg")
-    ap.add_argument("--only", default="", help="comma list of legs to run (c3,c5,sampler,c2,c4,cpu,copy); "
+    ap.add_argument("--only", default="", help="comma list of legs to run (c3,c5,sampler,pool,c2,c4,cpu,copy); "
                                                 "for profiling runs, the JSON line then holds only those legs")
     args = ap.parse_args()
     if args.only:
         legs = set(args.only.split(","))
-        unknown = legs - {"c3", "c5", "sampler", "c2", "c4", "cpu", "copy"}
+        unknown = legs - {"c3", "c5", "sampler", "pool", "c2", "c4", "cpu", "copy"}
         if unknown:
             ap.error(f"unknown legs {sorted(unknown)}")
         if legs & {"c5", "cpu"}:
@@ -325,7 +347,7 @@ def main():
         args.no_e2e = not (legs & {"c2", "c4"})
         args.no_cpu_baseline = "cpu" not in legs
     else:
-        legs = {"c3", "c5", "sampler", "c2", "c4", "cpu"}
+        legs = {"c3", "c5", "sampler", "pool", "c2", "c4", "cpu"}
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               f"(the forward would shard over the batch with no communication)", file=sys.stderr)
@@ -336,6 +358,7 @@ def main():
     c5 = None if args.no_fp8 else bench_c5(c3, args.steps, args.warmup)
     c4 = None if args.no_sampler else bench_c4_sampler(args.steps, args.warmup, dev, "nearest")
     c4b = None if args.no_sampler else bench_c4_sampler(args.steps, args.warmup, dev, "bilinear")
+    pool = bench_pool(args.steps, args.warmup, dev) if "pool" in legs else None
     c2 = None if args.no_e2e or "c2" not in legs else bench_c2(args.steps, args.warmup, dev)
     c4e = None if args.no_e2e or "c4" not in legs else bench_c4_frontend(args.steps, args.warmup, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline_c3(c3)
@@ -383,6 +406,12 @@ def main():
                          "traffic": {"nearest": measured_traffic("sampler_rings_kernel<bf16,nearest>"),
                                      "bilinear": measured_traffic("sampler_rings_kernel<bf16,bilinear>")}},
         }
+    if pool is not None:
+        line["knn_pool"] = {"workload": "kNN max pooling (AlexNet block): 256 images, 64 channels, 1024 -> 256 "
+                                        "log-polar points, k=9, bf16 channels-last",
+                            "GB/s": round(pool["gbs"], 1), "ms": round(pool["ms"], 4),
+                            "roofline": {"bound": "hbm", "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                         "frac": round(pool["gbs"] / PEAK_HBM_GBS, 4)}}
     if c2 is not None:
         line["c2_alexnet"] = {"workload": "C2: 256 images 3x224x224 -> bilinear sampler (4096 pts) -> 5 kNN-conv "
                                           "layers 64/192/384/256/256, k=49/25/9/9/9, ReLU between, bf16",

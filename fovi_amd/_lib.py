@@ -14,19 +14,20 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
 
-ABI_VERSION = 15
+ABI_VERSION = 16
 F32, BF16, F8E4M3 = 0, 1, 2
 NEAREST, BILINEAR = 0, 1
 PAD_ZEROS, PAD_BORDER = 0, 1
 ACT_NONE, ACT_RELU = 0, 1
 W_ROWS, W_MFMA = 0, 1
+POOL_MAX, POOL_AVG, POOL_SUM, POOL_GAUSSIAN = 0, 1, 2, 3
 
 _DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float8_e4m3fn: F8E4M3}
 
 # Every symbol include/fovi_hip.h declares.
 EXPORTED = ("fovi_abi_version", "fovi_last_error", "fovi_sampler_fwd", "fovi_knnconv_fwd",
             "fovi_knnconv_pack_weight", "fovi_knnconv_weight_mfma_elems", "fovi_knnconv_pack_weight_mfma",
-            "fovi_quantize_e4m3")
+            "fovi_quantize_e4m3", "fovi_knnpool_fwd")
 
 
 class SamplerArgs(C.Structure):
@@ -84,6 +85,18 @@ class QuantizeArgs(C.Structure):
     ]
 
 
+class KnnPoolArgs(C.Structure):
+    _fields_ = [
+        ("x", C.c_void_p), ("x_dtype", C.c_int32), ("mode", C.c_int32),
+        ("batch", C.c_int64), ("channels", C.c_int64), ("n_in", C.c_int64),
+        ("x_stride", C.c_int64 * 3),
+        ("nbr", C.c_void_p), ("weights", C.c_void_p),
+        ("n_out", C.c_int64), ("k", C.c_int64),
+        ("y", C.c_void_p), ("y_dtype", C.c_int32), ("reserved0", C.c_int32),
+        ("y_stride", C.c_int64 * 3),
+    ]
+
+
 _lib = None
 
 
@@ -111,6 +124,8 @@ def load(path: str = LIB_PATH):
     lib.fovi_knnconv_pack_weight_mfma.restype = C.c_int
     lib.fovi_quantize_e4m3.argtypes = [C.POINTER(QuantizeArgs), C.c_void_p]
     lib.fovi_quantize_e4m3.restype = C.c_int
+    lib.fovi_knnpool_fwd.argtypes = [C.POINTER(KnnPoolArgs), C.c_void_p]
+    lib.fovi_knnpool_fwd.restype = C.c_int
     got = lib.fovi_abi_version()
     if got != ABI_VERSION:
         raise RuntimeError(f"{path}: ABI version {got}, expected {ABI_VERSION}")

@@ -38,6 +38,7 @@ from .fp8 import Fp8Activations, headroom_for, quantize_e4m3
 __all__ = [
     "KNNBaseLayer",
     "KNNConvLayer",
+    "KNNPoolingLayer",
     "KNN_CONV_REGISTRY",
     "get_knn_conv_layer",
     "get_in_out_coords",
@@ -495,6 +496,114 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         return (f"{self.__class__.__name__}(\n\tin_channels={self.in_channels}\n\tout_channels="
                 f"{self.out_channels}\n\tk={self.k}\n\tn_ref={self.ref_coords.shape[0]}\n\tin_coords="
                 f"{self.in_coords}\n\tout_coords={self.out_coords}\n\tsample_cortex={self.sample_cortex}\n)")
+
+
+def _normalize(x, dim=None):
+    """Min-max normalisation (reference fovi/utils/__init__.py:126-167): (x - min) / (max - min)
+    with min and max over ``dim`` (kept) or over the whole tensor."""
+    if dim is not None:
+        lo, hi = x.min(dim).values.unsqueeze(dim), x.max(dim).values.unsqueeze(dim)
+    else:
+        lo, hi = x.min(), x.max()
+    return (x - lo) / (hi - lo)
+
+
+class _KnnPoolFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, layer):
+        return layer._launch(x)
+
+    @staticmethod
+    def backward(ctx, *grads):
+        raise NotImplementedError("fovi_amd KNNPoolingLayer: backward is not implemented (forward-only "
+                                  "HIP kernel)")
+
+
+_POOL_MODES = {"max": _lib.POOL_MAX, "avg": _lib.POOL_AVG, "sum": _lib.POOL_SUM, "gaussian": _lib.POOL_GAUSSIAN}
+
+
+class KNNPoolingLayer(nn.Module, KNNBaseLayer):
+    """kNN pooling on a sensor point cloud (HIP forward; reference ``knn.py:272-394``).
+
+    Same constructor, attributes and results as the reference: each output point reduces
+    its k nearest input points (cortical distance) per channel by max, NaN-ignoring mean
+    or sum, or a Gaussian-weighted mean; pad-token neighbours (index >= N_in) read NaN.
+    The forward is ``fovi_knnpool_fwd`` (one fused gather-reduce launch, fp32 arithmetic);
+    channels-last inputs give channels-last outputs (the ``[B, C, N]`` view of
+    ``[B, N, C]`` storage), as the kNN-conv layers do.
+    """
+
+    def __init__(self, k, in_coords, out_coords, mode="max", device="cuda", sample_cortex=True, gauss_sigma=10,
+                 batch_size=None):
+        super().__init__()
+        self.k = k
+        self.in_coords = in_coords
+        self.out_coords = out_coords
+        self.device = device
+        assert mode in ["max", "avg", "sum", "gaussian"]
+        self.mode = mode
+        self.sample_cortex = sample_cortex
+        self.batch_size = batch_size
+        assert isinstance(in_coords, SamplingCoords) and isinstance(out_coords, SamplingCoords)
+        self.k = torch.minimum(torch.tensor(self.k), torch.tensor(self.in_coords.shape[0]))   # knn.py:311
+        self._k = int(self.k.item())
+        knn_indices, knn_distances = self._compute_knns(batch_size)
+        self.knn_indices = knn_indices.to(device)
+        self.knn_distances = knn_distances.to(device)
+        # padding mask / token (knn.py:317-321)
+        self.knn_pad_token_val = self.in_coords.shape[0]
+        self.knn_indices_pad_mask = self.knn_indices >= self.in_coords.shape[0]
+        self.knn_indices_pad_token = self.knn_indices.clone()
+        self.knn_indices_pad_token[self.knn_indices_pad_mask] = self.knn_pad_token_val
+        if self.mode == "gaussian":
+            self.gauss_sigma = gauss_sigma
+            self.gaussian_weights = self._compute_gaussian_weights()
+        # kernel tables: each output point's k neighbours (and weights) contiguous
+        self.register_buffer("nbr_rows", self.knn_indices_pad_token.t().contiguous().to(torch.int32),
+                             persistent=False)
+        self.register_buffer("weight_rows", self.gaussian_weights.t().contiguous().to(torch.float32)
+                             if self.mode == "gaussian" else None, persistent=False)
+
+    def _compute_gaussian_weights(self):
+        """exp(-d^2 / (2 sigma^2)) over the per-point min-max normalised neighbour distances,
+        divided by (sum + 1e-8) per output point (reference knn.py:325-343). ``[k, N_out]``."""
+        k_distances = _normalize(self.knn_distances, dim=0)
+        gaussian_weights = torch.exp(-k_distances ** 2 / (2 * self.gauss_sigma ** 2))
+        return gaussian_weights / (gaussian_weights.sum(dim=0, keepdim=True) + 1e-8)
+
+    def _launch(self, x):
+        _lib.require_device(x, self.nbr_rows)
+        if x.dim() != 3 or x.shape[2] != self.in_coords.shape[0]:
+            raise ValueError(f"KNNPoolingLayer: expected [B, C, {self.in_coords.shape[0]}], got {tuple(x.shape)}")
+        if x.dtype not in (torch.float32, torch.bfloat16):
+            raise TypeError(f"KNNPoolingLayer: input must be float32 or bfloat16, got {x.dtype}")
+        bsz, c, n_out = x.shape[0], x.shape[1], self.out_coords.shape[0]
+        # the Gaussian mode multiplies by fp32 weights: the reference's result is promoted
+        dt = torch.promote_types(x.dtype, torch.float32) if self.mode == "gaussian" else x.dtype
+        if x.stride(1) == 1 and c > 1:
+            y = torch.empty(bsz, n_out, c, dtype=dt, device=x.device).transpose(1, 2)
+        else:
+            y = torch.empty(bsz, c, n_out, dtype=dt, device=x.device)
+        a = _lib.KnnPoolArgs()
+        a.x = x.data_ptr(); a.x_dtype = _lib.dtype_code(x.dtype); a.mode = _POOL_MODES[self.mode]
+        a.batch, a.channels, a.n_in = bsz, c, x.shape[2]
+        a.x_stride[:] = list(x.stride())
+        a.nbr = self.nbr_rows.data_ptr()
+        a.weights = self.weight_rows.data_ptr() if self.weight_rows is not None else None
+        a.n_out, a.k = n_out, self._k
+        a.y = y.data_ptr(); a.y_dtype = _lib.dtype_code(dt)
+        a.y_stride[:] = list(y.stride())
+        lib = _lib.load()
+        _lib.check(lib.fovi_knnpool_fwd(a, _lib.stream_handle(x.device)), "fovi_knnpool_fwd")
+        return y
+
+    def forward(self, X_l):
+        """``[B, C, N_in] -> [B, C, N_out]`` (reference knn.py:345-394)."""
+        return _KnnPoolFn.apply(X_l, self)
+
+    def __repr__(self):
+        return (f"KNNPoolingLayer(\n\tmode={self.mode}\n\tk={self.k}\n\tin_coords={self.in_coords}\n"
+                f"\tout_coords={self.out_coords}\n\tsample_cortex={self.sample_cortex}\n)")
 
 
 def get_in_out_coords(in_res, fov, cmf_a, stride, style="isotropic", auto_match_cart_resources=1,

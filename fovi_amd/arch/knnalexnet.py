@@ -1,10 +1,11 @@
-"""AlexNet-style kNN-CNN blocks, drop-in for ``fovi.arch.knnalexnet`` (conv path only).
+"""AlexNet-style kNN-CNN blocks, drop-in for ``fovi.arch.knnalexnet``.
 
-``KNNAlexNetBlock`` = kNN-conv → norm → activation (→ kNN pooling in the
-reference, ``fovi/arch/knnalexnet.py:13-127``). When no norm sits between
+``KNNAlexNetBlock`` = kNN-conv → norm → activation → optional kNN pooling
+(reference ``fovi/arch/knnalexnet.py:13-127``). When no norm sits between
 the conv and a ReLU, the ReLU is applied in the kNN-conv kernel's store.
-Norms other than 'none'/'batch' and the kNN pooling layers are not built
-(pooling raises). ``KNNAlexNet`` chains the blocks (``knnalexnet.py:131-241``).
+Norms other than 'none'/'batch' are not built. ``KNNAlexNet`` chains the
+blocks and the optional output average-pooling layer
+(``knnalexnet.py:131-241``).
 """
 from __future__ import annotations
 
@@ -12,7 +13,7 @@ import numpy as np
 import torch.nn as nn
 
 from ..sensing.coords import auto_match_num_coords
-from .knn import get_in_out_coords, get_knn_conv_layer
+from .knn import KNNPoolingLayer, get_in_out_coords, get_knn_conv_layer
 
 __all__ = ["KNNAlexNetBlock", "KNNAlexNet"]
 
@@ -49,21 +50,33 @@ class KNNAlexNetBlock(nn.Module):
                                device=device, ref_frame_side_length=ref_side) if conv_layer is not None else None
         self.norm = _get_norm(norm_type, self.out_coords.shape[0], out_channels, device)
         self.activation = activation() if activation is not None else None
-        if pool:
-            raise NotImplementedError("kNN pooling layers are not built; use pool=False")
         self.pool = None
+        if pool:
+            # pooled grid from the block's input resolution, as the reference builds it
+            # (knnalexnet.py:90-101)
+            _, pooled_coords, out_cart_res = get_in_out_coords(
+                self.in_coords.resolution, fov, cmf_a, pool_stride, style=style,
+                auto_match_cart_resources=auto_match_cart_resources, in_cart_res=out_cart_res, device=device)
+            self.pool = KNNPoolingLayer(k=pool_k, in_coords=self.out_coords, out_coords=pooled_coords,
+                                        mode=pool_mode, device=device, sample_cortex=sample_cortex)
+            self.out_coords = pooled_coords
         self.out_res = self.out_coords.resolution
         self.out_cart_res = out_cart_res
 
     def forward(self, x):
-        if self.conv is not None:
-            if self.norm is None and isinstance(self.activation, nn.ReLU) and hasattr(self.conv, "forward_fused"):
-                return self.conv.forward_fused(x, "relu")
-            x = self.conv(x)
-        if self.norm is not None:
-            x = self.norm(x)
-        if self.activation is not None:
-            x = self.activation(x)
+        fused = (self.conv is not None and self.norm is None and isinstance(self.activation, nn.ReLU)
+                 and hasattr(self.conv, "forward_fused"))
+        if fused:
+            x = self.conv.forward_fused(x, "relu")
+        else:
+            if self.conv is not None:
+                x = self.conv(x)
+            if self.norm is not None:
+                x = self.norm(x)
+            if self.activation is not None:
+                x = self.activation(x)
+        if self.pool is not None:
+            x = self.pool(x)
         return x
 
 
@@ -87,7 +100,14 @@ class KNNAlexNet(nn.Module):
             in_channels, in_res, cart_res = feats, block.out_res, block.out_cart_res
             blocks.append(block)
         if out_res is not None and out_res != -1:
-            raise NotImplementedError("the output kNN pooling layer is not built; use out_res=None")
+            # output average pooling (knnalexnet.py:193-209): a stride-1 grid of the last block's
+            # points, k = (2 ceil(in_res / out_radii))^2
+            in_coords = blocks[-1].out_coords
+            out_coords, out_radii, cart_res = in_coords.get_strided_coords(
+                1, auto_match_cart_resources=auto_match_cart_resources, in_cart_res=out_res)
+            k = int(2 * np.ceil(in_res / out_radii)) ** 2
+            blocks.append(KNNPoolingLayer(k=k, mode="avg", in_coords=in_coords, out_coords=out_coords,
+                                          sample_cortex=sample_cortex, device=device))
         self.layers = nn.ModuleList(blocks)
         self.n_classes = n_classes
         self.out_channels = features_per_layer[-1]

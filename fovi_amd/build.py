@@ -14,7 +14,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libfovi_hip.so")
-SOURCES = ["abi.hip", "sampler.hip", "knnconv.hip", "knnconv_v5.hip", "knnconv_fp8.hip", "quantize.hip"]
+SOURCES = ["abi.hip", "sampler.hip", "knnconv.hip", "knnconv_v5.hip", "knnconv_fp8.hip", "quantize.hip",
+           "knnpool.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

@@ -1,0 +1,245 @@
+// kNN pooling forward (KNNPoolingLayer.forward, fovi/arch/knn.py:345-394).
+//
+// An HBM-bound gather: every output point reads its k neighbours' feature
+// rows and reduces them per channel in fp32 (max, NaN-ignoring mean or sum,
+// or a Gaussian-weighted mean renormalised over the non-NaN neighbours),
+// rounding once to the output type. Pad-token indices (>= n_in) read NaN,
+// as the reference's appended NaN column does.
+//  * Channels-last rows (the layout the kNN-conv kernels produce): one
+//    thread per (batch row, output point, 16-byte channel group), so the
+//    threads of a point read each neighbour row with contiguous 16-byte
+//    loads and store 16-byte output pieces; consecutive points share
+//    neighbours, and each XCD takes a contiguous range of batch rows, so
+//    the rows are fetched into one L2.
+//  * Any other strides: one thread per (batch row, output point, channel).
+#include "common.h"
+
+namespace fovi {
+
+struct PoolParams {
+  const void* x;
+  int64_t B, C, Nin, Nout, K;
+  int64_t xs0, xs1, xs2;
+  const int32_t* nbr;
+  const float* w;
+  void* y;
+  int64_t ys0, ys1, ys2;
+  int mode;
+};
+
+// Per-channel reduction state of one output value.
+struct PoolAcc {
+  float a, b;   // max: running max | mean/sum: sum, count | gaussian: sum of weights, sum of x * w
+};
+
+__device__ __forceinline__ void pool_init(PoolAcc& s, int mode) {
+  s.a = mode == FOVI_POOL_MAX ? -__builtin_inff() : 0.0f;
+  s.b = 0.0f;
+}
+
+// pass 0 of the Gaussian mode sums the weights of the non-NaN features
+__device__ __forceinline__ void pool_add(PoolAcc& s, int mode, float v, float w) {
+  const bool nan = v != v;
+  switch (mode) {
+    case FOVI_POOL_MAX: s.a = fmaxf(s.a, nan ? -__builtin_inff() : v); break;
+    case FOVI_POOL_AVG: if (!nan) { s.a += v; s.b += 1.0f; } break;
+    case FOVI_POOL_SUM: if (!nan) s.a += v; break;
+    default: if (!nan) s.a += w; break;
+  }
+}
+
+// pass 1 of the Gaussian mode: x * (w / (S + 1e-8)) over the non-NaN features
+__device__ __forceinline__ void pool_add_weighted(PoolAcc& s, float v, float w) {
+  if (v == v) s.b += v * (w / (s.a + 1e-8f));
+}
+
+__device__ __forceinline__ float pool_result(const PoolAcc& s, int mode) {
+  switch (mode) {
+    case FOVI_POOL_AVG: return s.a / s.b;   // 0 / 0 = NaN when every feature is NaN
+    case FOVI_POOL_GAUSSIAN: return s.b;
+    default: return s.a;
+  }
+}
+
+template <typename T> struct Vec16;
+template <> struct Vec16<float> {
+  static constexpr int N = 4;
+  static __device__ __forceinline__ void load(const float* p, float (&v)[4]) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = a[i];
+  }
+};
+template <> struct Vec16<uint16_t> {
+  static constexpr int N = 8;
+  static __device__ __forceinline__ void load(const uint16_t* p, float (&v)[8]) {
+    const uint4 a = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+};
+
+// NV consecutive output channels (unit channel stride, aligned row): 16-byte stores
+template <typename OutT, int NV> struct Vec16Out;
+template <int NV> struct Vec16Out<uint16_t, NV> {
+  static __device__ __forceinline__ void store(uint16_t* y, const float (&o)[NV]) {
+#pragma unroll
+    for (int q = 0; q < NV / 8; ++q) {
+      uint4 w;
+      w.x = cvt_pk(o[8 * q], o[8 * q + 1]); w.y = cvt_pk(o[8 * q + 2], o[8 * q + 3]);
+      w.z = cvt_pk(o[8 * q + 4], o[8 * q + 5]); w.w = cvt_pk(o[8 * q + 6], o[8 * q + 7]);
+      *reinterpret_cast<uint4*>(y + 8 * q) = w;
+    }
+  }
+  static __device__ __forceinline__ uint32_t cvt_pk(float a, float b) {
+    return static_cast<uint32_t>(f32_to_bf16_bits(a)) | (static_cast<uint32_t>(f32_to_bf16_bits(b)) << 16);
+  }
+};
+template <int NV> struct Vec16Out<float, NV> {
+  static __device__ __forceinline__ void store(float* y, const float (&o)[NV]) {
+#pragma unroll
+    for (int q = 0; q < NV / 4; ++q) *reinterpret_cast<f32x4*>(y + 4 * q) = f32x4{o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]};
+  }
+};
+
+// channels-last rows: thread = (batch row, output point, channel group of 16
+// bytes); blocks in XCD-aware order; 32-bit index arithmetic (checked on the host)
+template <typename InT, typename OutT>
+__global__ __launch_bounds__(256) void knnpool_rows_kernel(PoolParams p, uint32_t groups, int vec_out,
+                                                           uint32_t blocks_per_b, int64_t total_blocks,
+                                                           int64_t padded_blocks) {
+  constexpr int NV = Vec16<InT>::N;
+  // each XCD (and its L2) takes a contiguous range of batch rows
+  const int64_t tile = xcd_tile(blockIdx.x, padded_blocks);
+  if (tile >= total_blocks) return;
+  const uint32_t t = static_cast<uint32_t>(tile % blocks_per_b) * 256u + threadIdx.x;
+  if (t >= static_cast<uint32_t>(p.Nout) * groups) return;
+  const uint32_t g = t % groups, n = t / groups;
+  const int64_t b = tile / blocks_per_b;
+  const InT* xb = static_cast<const InT*>(p.x) + b * p.xs0 + g * NV;
+  const int32_t* nb = p.nbr + static_cast<int64_t>(n) * p.K;
+  const float* wn = p.w ? p.w + static_cast<int64_t>(n) * p.K : nullptr;
+  PoolAcc s[NV];
+#pragma unroll
+  for (int c = 0; c < NV; ++c) pool_init(s[c], p.mode);
+  const int passes = p.mode == FOVI_POOL_GAUSSIAN ? 2 : 1;
+  for (int pass = 0; pass < passes; ++pass) {
+    for (int64_t j = 0; j < p.K; ++j) {
+      const int64_t idx = nb[j];
+      const float w = wn ? wn[j] : 0.0f;
+      float v[NV];
+      if (idx >= 0 && idx < p.Nin) {
+        Vec16<InT>::load(xb + idx * p.xs2, v);
+      } else {
+#pragma unroll
+        for (int c = 0; c < NV; ++c) v[c] = __builtin_nanf("");
+      }
+#pragma unroll
+      for (int c = 0; c < NV; ++c) {
+        if (pass == 0) pool_add(s[c], p.mode, v[c], w);
+        else pool_add_weighted(s[c], v[c], w);
+      }
+    }
+  }
+  OutT* yo = static_cast<OutT*>(p.y) + b * p.ys0 + static_cast<int64_t>(n) * p.ys2 + g * NV * p.ys1;
+  float o[NV];
+#pragma unroll
+  for (int c = 0; c < NV; ++c) o[c] = pool_result(s[c], p.mode);
+  if (vec_out) {
+    Vec16Out<OutT, NV>::store(yo, o);
+  } else {
+#pragma unroll
+    for (int c = 0; c < NV; ++c) Elem<OutT>::store(yo + c * p.ys1, o[c]);
+  }
+}
+
+// any strides: thread = (b, n, c)
+template <typename InT, typename OutT>
+__global__ __launch_bounds__(256) void knnpool_any_kernel(PoolParams p, int64_t total) {
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
+       t += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t c = t % p.C;
+    const int64_t n = (t / p.C) % p.Nout;
+    const int64_t b = t / (p.C * p.Nout);
+    const InT* xb = static_cast<const InT*>(p.x) + b * p.xs0 + c * p.xs1;
+    const int32_t* nb = p.nbr + n * p.K;
+    const float* wn = p.w ? p.w + n * p.K : nullptr;
+    PoolAcc s;
+    pool_init(s, p.mode);
+    const int passes = p.mode == FOVI_POOL_GAUSSIAN ? 2 : 1;
+    for (int pass = 0; pass < passes; ++pass)
+      for (int64_t j = 0; j < p.K; ++j) {
+        const int64_t idx = nb[j];
+        const float v = idx >= 0 && idx < p.Nin ? Elem<InT>::load(xb + idx * p.xs2) : __builtin_nanf("");
+        const float w = wn ? wn[j] : 0.0f;
+        if (pass == 0) pool_add(s, p.mode, v, w);
+        else pool_add_weighted(s, v, w);
+      }
+    Elem<OutT>::store(static_cast<OutT*>(p.y) + b * p.ys0 + c * p.ys1 + n * p.ys2, pool_result(s, p.mode));
+  }
+}
+
+template <typename InT, typename OutT>
+static void launch_pool(const PoolParams& p, hipStream_t s) {
+  constexpr int NV = Vec16<InT>::N;
+  const bool rows = p.xs1 == 1 && p.C % NV == 0 && p.xs2 % NV == 0 && p.xs0 % NV == 0 &&
+                    reinterpret_cast<uintptr_t>(p.x) % 16 == 0;
+  const int64_t groups = p.C / NV;
+  const int64_t pts = p.Nout * groups;
+  const int64_t blocks_per_b = (pts + 255) / 256;
+  const int64_t total_blocks = blocks_per_b * p.B;
+  const int64_t padded = (total_blocks + 7) / 8 * 8;
+  if (rows && pts <= 0x7fffffffLL && padded <= 0x7fffffffLL) {
+    const dim3 grid(static_cast<unsigned>(padded));
+    // whole channel groups to unit-stride, 16-byte aligned output rows
+    const int vec_out = p.ys1 == 1 && (p.ys2 * sizeof(OutT)) % 16 == 0 && (p.ys0 * sizeof(OutT)) % 16 == 0 &&
+                        (NV * sizeof(OutT)) % 16 == 0 && reinterpret_cast<uintptr_t>(p.y) % 16 == 0;
+    hipLaunchKernelGGL((knnpool_rows_kernel<InT, OutT>), grid, dim3(256), 0, s, p, static_cast<uint32_t>(groups),
+                       vec_out, static_cast<uint32_t>(blocks_per_b), total_blocks, padded);
+    return;
+  }
+  const int64_t total = p.B * p.Nout * p.C;
+  const int64_t blocks = std::min<int64_t>((total + 255) / 256, 256 * 64);
+  hipLaunchKernelGGL((knnpool_any_kernel<InT, OutT>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, p,
+                     total);
+}
+
+}  // namespace fovi
+
+extern "C" int fovi_knnpool_fwd(const fovi_knnpool_args* a, void* stream) {
+  using namespace fovi;
+  clear_error();
+  if (!a || !a->x || !a->nbr || !a->y) { set_error("fovi_knnpool_fwd: null pointer"); return 1; }
+  if (a->mode < FOVI_POOL_MAX || a->mode > FOVI_POOL_GAUSSIAN) {
+    set_error("fovi_knnpool_fwd: bad mode %d", a->mode); return 1;
+  }
+  if (a->mode == FOVI_POOL_GAUSSIAN && !a->weights) {
+    set_error("fovi_knnpool_fwd: the Gaussian mode needs weights"); return 1;
+  }
+  if ((a->x_dtype != FOVI_F32 && a->x_dtype != FOVI_BF16) || (a->y_dtype != FOVI_F32 && a->y_dtype != FOVI_BF16)) {
+    set_error("fovi_knnpool_fwd: x and y must be F32 or BF16"); return 1;
+  }
+  if (a->batch < 0 || a->channels < 0 || a->n_in < 0 || a->n_out < 0 || a->k < 1) {
+    set_error("fovi_knnpool_fwd: bad sizes (k must be >= 1)"); return 1;
+  }
+  if (a->batch * a->channels * a->n_out == 0) return 0;
+  PoolParams p;
+  p.x = a->x; p.B = a->batch; p.C = a->channels; p.Nin = a->n_in; p.Nout = a->n_out; p.K = a->k;
+  p.xs0 = a->x_stride[0]; p.xs1 = a->x_stride[1]; p.xs2 = a->x_stride[2];
+  p.nbr = a->nbr; p.w = a->mode == FOVI_POOL_GAUSSIAN ? a->weights : nullptr;
+  p.y = a->y; p.ys0 = a->y_stride[0]; p.ys1 = a->y_stride[1]; p.ys2 = a->y_stride[2];
+  p.mode = a->mode;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (a->x_dtype == FOVI_F32) {
+    if (a->y_dtype == FOVI_F32) launch_pool<float, float>(p, s);
+    else launch_pool<float, uint16_t>(p, s);
+  } else {
+    if (a->y_dtype == FOVI_F32) launch_pool<uint16_t, float>(p, s);
+    else launch_pool<uint16_t, uint16_t>(p, s);
+  }
+  return check_launch("fovi_knnpool_fwd");
+}

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 15
+#define FOVI_ABI_VERSION 16
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -263,6 +263,43 @@ typedef struct fovi_quantize_args {
 } fovi_quantize_args;
 
 int fovi_quantize_e4m3(const fovi_quantize_args* args, void* stream);
+
+/*
+ * kNN pooling forward: replaces KNNPoolingLayer.forward (fovi/arch/knn.py:345-394).
+ *
+ *   y[b, c, n] = reduce over j < k of x[b, c, nbr[n * k + j]]
+ *
+ * nbr is the reference's knn_indices_pad_token transposed to [n_out, k]; an
+ * index >= n_in is the pad token, whose feature is NaN (knn.py:357). NaN
+ * features (pad or input) are handled as the reference does:
+ *   FOVI_POOL_MAX:      NaN -> -inf, then max (knn.py:371-373);
+ *   FOVI_POOL_AVG:      mean over the non-NaN features (torch.nanmean; NaN when none);
+ *   FOVI_POOL_SUM:      sum over the non-NaN features (torch.nansum);
+ *   FOVI_POOL_GAUSSIAN: weights[n * k + j] zeroed where the feature is NaN,
+ *                       divided by (their sum + 1e-8), then sum of feature x
+ *                       weight over the non-NaN features (knn.py:376-389).
+ * Arithmetic in fp32, one rounding to y_dtype. x and y: F32 or BF16, any
+ * element strides [batch, channel, point]; the fast path is channels-last
+ * rows (x_stride[1] == 1, 16-byte aligned rows).
+ */
+enum fovi_pool_mode { FOVI_POOL_MAX = 0, FOVI_POOL_AVG = 1, FOVI_POOL_SUM = 2, FOVI_POOL_GAUSSIAN = 3 };
+
+typedef struct fovi_knnpool_args {
+  const void* x;
+  int32_t x_dtype;
+  int32_t mode;               /* fovi_pool_mode */
+  int64_t batch, channels, n_in;
+  int64_t x_stride[3];
+  const int32_t* nbr;         /* [n_out, k] */
+  const float* weights;       /* [n_out, k], FOVI_POOL_GAUSSIAN only */
+  int64_t n_out, k;
+  void* y;
+  int32_t y_dtype;
+  int32_t reserved0;
+  int64_t y_stride[3];
+} fovi_knnpool_args;
+
+int fovi_knnpool_fwd(const fovi_knnpool_args* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -21,6 +21,13 @@ Pinning (what checks each function beyond retyping its formula):
     (e4m3_round_bruteforce), a closed form for constant inputs (slot sums =
     neighbour counts, rounded to e4m3 above 16), equality with
     knnconv_forward where every slot holds at most one neighbour.
+  * knnpool_ref.knnpool_forward: the float64 loop form of the four modes
+    (knnpool_ref.knnpool_bruteforce, NaN handled per definition), closed
+    forms (max/avg/sum of a constant, of an arithmetic ramp), torch.nanmean /
+    nansum on the same gathered tensor; knnpool_ref.gaussian_weights: a
+    scalar loop of exp(-d^2 / 2 sigma^2) over min-max normalised distances,
+    columns summing to 1 - 1e-8 relative, the largest weight at the nearest
+    neighbour.
   * The host tables the oracle consumes (sensor coordinates, kNN indices,
     ref slots; built by fovi_amd, not by this package) are pinned bit for bit
     by vectors the reference itself wrote (tests/golden/tables.npz, from

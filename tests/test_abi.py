@@ -56,6 +56,15 @@ def test_argument_validation_without_gpu():
     q.scale_in, q.headroom = 16, 0.5
     assert lib.fovi_quantize_e4m3(q, None) != 0
     assert b"headroom" in lib.fovi_last_error()
+    pa = _lib.KnnPoolArgs()
+    assert lib.fovi_knnpool_fwd(pa, None) != 0
+    assert b"null pointer" in lib.fovi_last_error()
+    pa.x, pa.nbr, pa.y, pa.mode, pa.k = 16, 16, 16, _lib.POOL_GAUSSIAN, 9
+    assert lib.fovi_knnpool_fwd(pa, None) != 0             # Gaussian mode without weights
+    assert b"weights" in lib.fovi_last_error()
+    pa.mode, pa.k = _lib.POOL_MAX, 0
+    assert lib.fovi_knnpool_fwd(pa, None) != 0
+    assert b"k must be" in lib.fovi_last_error()
 
 
 def _c_layout(struct, fields, tmp_path):
@@ -74,7 +83,8 @@ def _c_layout(struct, fields, tmp_path):
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
 @pytest.mark.parametrize("py,c", [(_lib.SamplerArgs, "fovi_sampler_args"), (_lib.KnnConvArgs, "fovi_knnconv_args"),
-                                  (_lib.QuantizeArgs, "fovi_quantize_args")])
+                                  (_lib.QuantizeArgs, "fovi_quantize_args"),
+                                  (_lib.KnnPoolArgs, "fovi_knnpool_args")])
 def test_struct_layout_matches_header(py, c, tmp_path):
     fields = [f for f, _ in py._fields_]
     size, offs = _c_layout(c, fields, tmp_path)

@@ -1,0 +1,174 @@
+"""kNN pooling (reference fovi/arch/knn.py:272-394): the oracle pinned on the CPU, the HIP kernel
+against it on the GPU."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from fovi_amd import _lib
+from fovi_amd.arch.knn import KNNPoolingLayer
+from fovi_amd.sensing.coords import SamplingCoords
+from oracle import knnpool_ref as P
+from tests.helpers import assert_close_rel
+
+MODES = ["max", "avg", "sum", "gaussian"]
+
+
+def _tables(n_in=40, n_out=12, k=5, seed=0, pads=True):
+    g = torch.Generator().manual_seed(seed)
+    idx = torch.randint(0, n_in, (k, n_out), generator=g)
+    if pads:
+        idx[k - 1, ::3] = n_in + 2                      # pad tokens
+    dist = torch.rand(k, n_out, generator=g)
+    dist[0] = 0.0                                      # the nearest neighbour first, as a kNN table has it
+    return idx, dist
+
+
+# ------------------------------------------------------------------- CPU: oracle pinning ---
+@pytest.mark.parametrize("mode", MODES)
+def test_pool_oracle_matches_bruteforce_with_nans_and_pads(mode):
+    idx, dist = _tables()
+    x = torch.randn(2, 3, 40, generator=torch.Generator().manual_seed(1), dtype=torch.float64)
+    x[0, 1, 5] = float("nan")
+    x[1, :, 7] = float("nan")
+    w = P.gaussian_weights(dist.double(), 10.0) if mode == "gaussian" else None
+    got = P.knnpool_forward(x, idx, 40, mode, w).numpy()
+    want = P.knnpool_bruteforce(x, idx, 40, mode, w)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(want)
+    assert np.allclose(got[ok], want[ok], rtol=1e-12, atol=1e-12)
+
+
+def test_pool_oracle_closed_forms():
+    idx, _ = _tables(pads=False)
+    k = idx.shape[0]
+    const = torch.full((1, 2, 40), 2.5, dtype=torch.float64)
+    for mode, want in (("max", 2.5), ("avg", 2.5), ("sum", 2.5 * k)):
+        assert torch.allclose(P.knnpool_forward(const, idx, 40, mode), torch.full((1, 2, 12), want,
+                                                                                  dtype=torch.float64))
+    ramp = torch.arange(40, dtype=torch.float64).reshape(1, 1, 40)      # x[i] = i
+    assert torch.equal(P.knnpool_forward(ramp, idx, 40, "max")[0, 0], idx.max(0).values.double())
+    assert torch.allclose(P.knnpool_forward(ramp, idx, 40, "sum")[0, 0], idx.sum(0).double())
+    # an all-pad neighbourhood: max -inf, mean NaN, sum 0
+    allpad = torch.full((k, 1), 40)
+    x = torch.randn(1, 1, 40, dtype=torch.float64)
+    assert P.knnpool_forward(x, allpad, 40, "max").item() == -math.inf
+    assert math.isnan(P.knnpool_forward(x, allpad, 40, "avg").item())
+    assert P.knnpool_forward(x, allpad, 40, "sum").item() == 0.0
+
+
+def test_gaussian_weights_closed_form():
+    _, dist = _tables(n_out=7, k=6)
+    sigma = 0.7
+    w = P.gaussian_weights(dist.double(), sigma)
+    for n in range(7):
+        d = [dist[j, n].item() for j in range(6)]
+        lo, hi = min(d), max(d)
+        e = [math.exp(-((v - lo) / (hi - lo)) ** 2 / (2 * sigma ** 2)) for v in d]
+        s = sum(e)
+        for j in range(6):
+            assert abs(w[j, n].item() - e[j] / (s + 1e-8)) < 1e-12
+        assert abs(w[:, n].sum().item() - s / (s + 1e-8)) < 1e-12
+        assert w[:, n].argmax().item() == int(np.argmin(d))
+
+
+def test_pool_layer_attributes_and_tables():
+    ci = SamplingCoords(16, 2.78, 32, style="logpolar")
+    co = SamplingCoords(16, 2.78, 16, style="logpolar")
+    layer = KNNPoolingLayer(9, ci, co, mode="gaussian", device="cpu", gauss_sigma=2.0)
+    assert layer._k == 9 and layer.knn_indices.shape == (9, 256) and layer.knn_distances.shape == (9, 256)
+    assert torch.equal(layer.nbr_rows, layer.knn_indices_pad_token.t().to(torch.int32))
+    assert torch.allclose(layer.gaussian_weights, P.gaussian_weights(layer.knn_distances, 2.0))
+    assert torch.equal(layer.weight_rows, layer.gaussian_weights.t().float())
+    assert not layer.knn_indices_pad_mask.any()          # log-polar neighbourhoods have no pad ring
+    big = KNNPoolingLayer(5000, ci, co, mode="max", device="cpu")
+    assert big._k == 1024                                # k clamped to the input size (knn.py:311)
+
+
+# ------------------------------------------------------------------------- GPU: kernel ---
+def _pool_args(x, nbr_rows, weights, n_out, k, mode, y):
+    a = _lib.KnnPoolArgs()
+    a.x = x.data_ptr(); a.x_dtype = _lib.dtype_code(x.dtype); a.mode = mode
+    a.batch, a.channels, a.n_in = x.shape
+    a.x_stride[:] = list(x.stride())
+    a.nbr = nbr_rows.data_ptr()
+    a.weights = weights.data_ptr() if weights is not None else None
+    a.n_out, a.k = n_out, k
+    a.y = y.data_ptr(); a.y_dtype = _lib.dtype_code(y.dtype)
+    a.y_stride[:] = list(y.stride())
+    return a
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("channels_last", [True, False])
+def test_knnpool_layer_vs_oracle(mode, dt, channels_last):
+    ci = SamplingCoords(16, 2.78, 32, style="logpolar")
+    co = SamplingCoords(16, 2.78, 16, style="logpolar")
+    layer = KNNPoolingLayer(9, ci, co, mode=mode, device="cuda", gauss_sigma=3.0)
+    x = torch.randn(3, 64, 1024, generator=torch.Generator().manual_seed(4)).to(dt)
+    x[1, 5, 100:140] = float("nan")                                   # NaN features are skipped
+    xd = x.cuda()
+    if channels_last:
+        xd = xd.transpose(1, 2).contiguous().transpose(1, 2)
+    with torch.no_grad():
+        y = layer(xd)
+    want_dt = torch.float32 if mode == "gaussian" else dt             # the reference promotes
+    assert y.dtype == want_dt and y.shape == (3, 64, 256)
+    assert (y.stride(1) == 1) == channels_last
+    w = layer.gaussian_weights.cpu() if mode == "gaussian" else None
+    ref = P.knnpool_forward(x.float(), layer.knn_indices.cpu(), 1024, mode, w)
+    got = y.float().cpu()
+    assert torch.equal(torch.isnan(got), torch.isnan(ref))
+    ok = ~torch.isnan(ref)
+    if mode == "max":
+        assert torch.equal(got[ok], ref[ok].to(dt).float())            # a max is exact
+    else:
+        tol = 1e-5 if want_dt == torch.float32 else 1e-2
+        assert_close_rel(got[ok], ref[ok], tol, f"kNN pooling {mode}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", MODES)
+def test_knnpool_pad_tokens_through_the_c_abi(mode):
+    """Indices >= n_in read the reference's appended NaN column."""
+    idx, dist = _tables(n_in=40, n_out=12, k=5)
+    x = torch.randn(2, 8, 40, generator=torch.Generator().manual_seed(2))
+    w = P.gaussian_weights(dist, 10.0) if mode == "gaussian" else None
+    y = torch.empty(2, 8, 12, device="cuda")
+    nbr = idx.t().contiguous().to(torch.int32).cuda()
+    wr = w.t().contiguous().cuda() if w is not None else None
+    xd = x.cuda()
+    a = _pool_args(xd, nbr, wr, 12, 5, {"max": _lib.POOL_MAX, "avg": _lib.POOL_AVG, "sum": _lib.POOL_SUM,
+                                        "gaussian": _lib.POOL_GAUSSIAN}[mode], y)
+    lib = _lib.load()
+    _lib.check(lib.fovi_knnpool_fwd(a, _lib.stream_handle(xd.device)), "fovi_knnpool_fwd")
+    torch.cuda.synchronize()
+    ref = P.knnpool_forward(x, idx, 40, mode, w)
+    assert_close_rel(y.cpu(), ref, 1e-5, f"pad tokens, {mode}")
+
+
+@pytest.mark.gpu
+def test_alexnet_blocks_with_pooling():
+    """Blocks with pooling (reference knnalexnet.py:90-127) and the output average pooling
+    layer (knnalexnet.py:193-209): the pooled outputs equal the pooling layers applied to the
+    block outputs, on the pooled grids."""
+    from fovi_amd.arch.knnalexnet import KNNAlexNet
+    net = KNNAlexNet(32, 3, [32, 64], [1, 2], [0], [9, 9], out_res=8, style="logpolar", norm_type="none",
+                     cmf_a=2.78, device="cuda", auto_match_cart_resources=0)
+    assert net.layers[0].pool is not None and net.layers[1].pool is None
+    assert isinstance(net.layers[2], KNNPoolingLayer) and net.layers[2].mode == "avg"
+    x = torch.rand(2, 3, 1024, generator=torch.Generator().manual_seed(9)).bfloat16().cuda()
+    with torch.no_grad():
+        h0 = net.layers[0].conv.forward_fused(x, "relu")
+        p0 = net.layers[0].pool(h0)
+        assert p0.shape[2] == net.layers[0].out_coords.shape[0]
+        ref0 = P.knnpool_forward(h0.float().cpu(), net.layers[0].pool.knn_indices.cpu(), h0.shape[2], "max")
+        assert torch.equal(p0.float().cpu(), ref0)
+        y = net(x)
+        h1 = net.layers[1](p0)
+        ref = P.knnpool_forward(h1.float().cpu(), net.layers[2].knn_indices.cpu(), h1.shape[2], "avg")
+    assert y.shape == (2, 64, net.layers[2].out_coords.shape[0])
+    assert_close_rel(y.float().cpu(), ref, 1e-2, "output pooling")
