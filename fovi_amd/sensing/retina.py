@@ -13,7 +13,7 @@ import torch
 import torch.nn as nn
 
 from .coords import find_desired_res
-from .samplers import GridSampler
+from .samplers import GaussianKNNGridSampler, GridSampler, KNNGridSampler
 
 __all__ = ["RetinalTransform", "GaussianColorDecay"]
 
@@ -59,8 +59,12 @@ class RetinalTransform(nn.Module):
         elif sampler == "grid_bilinear":
             self.sampler = GridSampler(fov, cmf_a, resolution, device=device, mode="bilinear", style=style,
                                        padding_mode=padding_mode)
-        elif sampler in ("pooling", "gaussian_pooling"):
-            raise NotImplementedError(f"sampler {sampler!r}: kNN pooling samplers are not built")
+        elif sampler == "gaussian_pooling":
+            self.sampler = GaussianKNNGridSampler(fov, cmf_a, resolution, fixation_size=self.fixation_size,
+                                                  device=device, style=style, **kwargs)
+        elif sampler == "pooling":
+            self.sampler = KNNGridSampler(fov, cmf_a, resolution, fixation_size=self.fixation_size, device=device,
+                                          style=style, **kwargs)
         else:
             raise ValueError(f"Invalid sampler: {sampler}")
         self.pre_transforms = pre_transforms

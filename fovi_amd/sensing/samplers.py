@@ -19,7 +19,7 @@ import torch.nn as nn
 from .. import _lib
 from .coords import SamplingCoords, xy_to_colrow
 
-__all__ = ["BaseGridSampler", "GridSampler", "fixation_half_sizes"]
+__all__ = ["BaseGridSampler", "GridSampler", "KNNGridSampler", "GaussianKNNGridSampler", "fixation_half_sizes"]
 
 _MODES = {"nearest": _lib.NEAREST, "bilinear": _lib.BILINEAR}
 _PADS = {"zeros": _lib.PAD_ZEROS, "border": _lib.PAD_BORDER}
@@ -184,3 +184,65 @@ class GridSampler(BaseGridSampler):
     def __repr__(self):
         return (f"GridSampler(fov={self.fov}, cmf_a={self.cmf_a}, style={self.style}, "
                 f"resolution={self.resolution}, mode={self.mode}, n={len(self.coords)})")
+
+
+class KNNGridSampler(BaseGridSampler):
+    """Two-layer foveated sampler (reference ``samplers.py:134-230``): nearest samples on a
+    denser "photoreceptor" grid (``res_mult`` x the resolution, ``cmf_a_mult`` x a), then kNN
+    average pooling onto the sensor grid. Both stages are HIP launches: the sampler kernel on
+    the dense grid and ``fovi_knnpool_fwd``."""
+
+    pool_mode = "avg"
+
+    def __init__(self, fov, cmf_a, resolution, res_mult=3, cmf_a_mult=1, fixation_size=3000, k=None,
+                 style="isotropic", sample_cortex=True, dtype=torch.float, device="cuda"):
+        super().__init__()
+        from ..arch.knn import KNNPoolingLayer
+        self.highres_coords = SamplingCoords(fov, cmf_a_mult * cmf_a, res_mult * resolution, device=device,
+                                             style=style, dtype=dtype)
+        self.coords = SamplingCoords(fov, cmf_a, resolution, device=device, style=style, dtype=dtype)
+        if k is None:
+            # the ratio of the numbers of points of the two grids (samplers.py:164-166)
+            k = int(np.round(len(self.highres_coords) / len(self.coords)))
+            print(f"auto-set knngridsampler k={k}")
+        self.pooler = KNNPoolingLayer(k, self.highres_coords, self.coords, mode=self.pool_mode, device=device,
+                                      sample_cortex=sample_cortex)
+        self.sampling_grid = self._prep_grid_for_grid_sample(self.highres_coords.cartesian)
+        self.out_sampling_grid = self._prep_grid_for_grid_sample(self.coords.cartesian)
+        self.polar_radius = self.coords.polar[:, 0]
+        self.fov = fov
+        self.cmf_a = cmf_a
+        self.resolution = resolution
+        self.fixation_size = fixation_size
+        self.k = k
+        self.dtype = dtype
+        self.device = device
+        self.style = style
+        self.num_coords = len(self.coords)
+        self.sample_cortex = sample_cortex
+        self.rf_sizes = self.coords.get_scatter_sizes()
+        # the dense first layer: nearest samples, zeros padding (the reference's grid_sample call)
+        self._dense = GridSampler(fov, cmf_a_mult * cmf_a, res_mult * resolution, device=device, dtype=dtype,
+                                  mode="nearest", style=style, coords=self.highres_coords)
+
+    def forward(self, img, fix_loc=None, fixation_size=None):
+        """``[B, C, H, W]`` images -> ``[B, C, N]`` pooled samples (reference samplers.py:187-209)."""
+        img = img.to(self.device).to(self.dtype)
+        dense = self._dense(img, fix_loc=fix_loc, fixation_size=fixation_size)
+        return self.pooler(dense)
+
+    def all_coords(self, device=None):
+        if device is None:
+            return self.coords.cartesian, self.coords.polar, self.coords.plotting
+        return self.coords.cartesian.to(device), self.coords.polar.to(device), self.coords.plotting.to(device)
+
+    def __repr__(self):
+        return (f"KNNGridSampler(fov={self.fov}, cmf_a={self.cmf_a}, resolution={self.resolution}, "
+                f"num_coords={self.num_coords}, fixation_size={self.fixation_size}, k={self.k}, "
+                f"dtype={self.dtype}, device={self.device}, style={self.style})")
+
+
+class GaussianKNNGridSampler(KNNGridSampler):
+    """``KNNGridSampler`` with Gaussian-weighted pooling (reference ``samplers.py:233-259``)."""
+
+    pool_mode = "gaussian"

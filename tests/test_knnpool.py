@@ -172,3 +172,26 @@ def test_alexnet_blocks_with_pooling():
         ref = P.knnpool_forward(h1.float().cpu(), net.layers[2].knn_indices.cpu(), h1.shape[2], "avg")
     assert y.shape == (2, 64, net.layers[2].out_coords.shape[0])
     assert_close_rel(y.float().cpu(), ref, 1e-2, "output pooling")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("sampler,mode", [("pooling", "avg"), ("gaussian_pooling", "gaussian")])
+def test_knn_grid_samplers_vs_oracle(sampler, mode):
+    """RetinalTransform's kNN pooling samplers (reference samplers.py:134-259, retina.py:99-102):
+    nearest samples on the dense grid, then kNN pooling onto the sensor grid."""
+    from fovi_amd.sensing.retina import RetinalTransform
+    from oracle import sampler_ref
+    rt = RetinalTransform(16, start_res=64, fov=16, cmf_a=2.78, style="logpolar", sampler=sampler, device="cuda",
+                          auto_match_cart_resources=0, res_mult=2)
+    s = rt.sampler
+    assert s.highres_coords.shape[0] == 4 * s.coords.shape[0] and s.k == 4 and s.pooler.mode == mode
+    img = torch.rand(2, 3, 64, 64, generator=torch.Generator().manual_seed(5))
+    fix_loc = torch.tensor([[0.5, 0.5], [0.4, 0.6]])
+    with torch.no_grad():
+        y = rt(img.cuda(), fix_loc, 64)
+    dense, _ = sampler_ref.sampler_forward(img, s.sampling_grid.cpu(), fix_loc, np.array([[64, 64]] * 2),
+                                           mode="nearest")
+    w = s.pooler.gaussian_weights.cpu() if mode == "gaussian" else None
+    ref = P.knnpool_forward(dense, s.pooler.knn_indices.cpu(), dense.shape[2], mode, w)
+    assert y.shape == (2, 3, s.coords.shape[0])
+    assert_close_rel(y.float().cpu(), ref, 1e-5, f"kNN grid sampler ({mode})")
