@@ -73,6 +73,26 @@ def bench_c3(steps, warmup, dev):
     return dict(ms=ms, flops=flops, tflops=tflops, layer=layer, x=x)
 
 
+def bench_c3_backward(c3, steps, warmup):
+    """Backward of the C3 layer (input and weight gradients, bf16): the slot sums a
+    [B*N, V*C], dW = dy^T a, G = dy W and the transposed gather of G into dx. Reported
+    against the two GEMMs' flops (2x the forward's); the slot-sum and gather kernels move
+    B*N*V*C*2 bytes each way."""
+    import torch
+    layer, x = c3["layer"], c3["x"]
+    g = torch.Generator(device=x.device).manual_seed(5)
+    n = layer.out_coords.shape[0]
+    dy = torch.randn(x.shape[0], n, layer.out_channels, generator=g, device=x.device,
+                     dtype=torch.bfloat16).transpose(1, 2)
+    layer._inverse_tables(x.device)
+    ms = time_steps(lambda: layer._backward(x, layer.weight, dy, True, True), steps, warmup)
+    flops = 2.0 * c3["flops"]
+    tflops = flops / (ms * 1e-3) / 1e12
+    log(f"[c3 backward] {ms:.3f} ms/step  {tflops:.1f} TFLOP/s over the two GEMMs "
+        f"({100 * tflops / PEAK_BF16_TFLOPS:.1f}% of bf16 peak)")
+    return dict(ms=ms, tflops=tflops)
+
+
 def bench_c5(c3, steps, warmup):
     """C5: the C3 layer with e4m3 activations (per-tensor scale) and weights
     (per-output-channel scales), fp32 accumulation, bf16 output. The input is
@@ -332,22 +352,22 @@ def main():
     ap.add_argument("--no-sampler", action="store_true")
     ap.add_argument("--no-e2e", action="store_true", help="skip the C2/C4 end-to-end legs")
     ap.add_argument("--no-fp8", action="store_true", help="skip the C5 fp8 leg")
-    ap.add_argument("--only", default="", help="comma list of legs to run (c3,c5,sampler,pool,c2,c4,cpu,copy); "
+    ap.add_argument("--only", default="", help="comma list of legs to run (c3,c5,bwd,sampler,pool,c2,c4,cpu,copy); "
                                                 "for profiling runs, the JSON line then holds only those legs")
     args = ap.parse_args()
     if args.only:
         legs = set(args.only.split(","))
-        unknown = legs - {"c3", "c5", "sampler", "pool", "c2", "c4", "cpu", "copy"}
+        unknown = legs - {"c3", "c5", "bwd", "sampler", "pool", "c2", "c4", "cpu", "copy"}
         if unknown:
             ap.error(f"unknown legs {sorted(unknown)}")
-        if legs & {"c5", "cpu"}:
+        if legs & {"c5", "cpu", "bwd"}:
             legs.add("c3")
         args.no_fp8 = "c5" not in legs
         args.no_sampler = "sampler" not in legs
         args.no_e2e = not (legs & {"c2", "c4"})
         args.no_cpu_baseline = "cpu" not in legs
     else:
-        legs = {"c3", "c5", "sampler", "pool", "c2", "c4", "cpu"}
+        legs = {"c3", "c5", "bwd", "sampler", "pool", "c2", "c4", "cpu"}
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               f"(the forward would shard over the batch with no communication)", file=sys.stderr)
@@ -356,6 +376,7 @@ def main():
     dev = torch.device("cuda:0")
     c3 = bench_c3(args.steps, args.warmup, dev) if "c3" in legs else None
     c5 = None if args.no_fp8 else bench_c5(c3, args.steps, args.warmup)
+    bwd = bench_c3_backward(c3, args.steps, args.warmup) if "bwd" in legs else None
     c4 = None if args.no_sampler else bench_c4_sampler(args.steps, args.warmup, dev, "nearest")
     c4b = None if args.no_sampler else bench_c4_sampler(args.steps, args.warmup, dev, "bilinear")
     pool = bench_pool(args.steps, args.warmup, dev) if "pool" in legs else None
@@ -394,6 +415,10 @@ def main():
                           "roofline": {"bound": "mfma", "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
                                        "frac": round(c5["tflops"] / PEAK_FP8_TFLOPS, 4)},
                           "quantize_ms": round(c5["ms_q"], 4), "quantize_GB/s": round(c5["q_gbs"], 1)}
+    if bwd is not None:
+        line["c3_backward"] = {"workload": "C3 layer backward, bf16: input and weight gradients (slot sums, "
+                                           "two library GEMMs, inverse-table gather)",
+                               "ms": round(bwd["ms"], 4), "TFLOP/s": round(bwd["tflops"], 2)}
     if c4 is not None:
         line["sampler_c4"] = {
             "workload": "C4 sampler: 128 images 3x512x512 bf16, 4 fixations each (512 views), "

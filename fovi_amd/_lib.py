@@ -14,7 +14,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
 
-ABI_VERSION = 16
+ABI_VERSION = 17
 F32, BF16, F8E4M3 = 0, 1, 2
 NEAREST, BILINEAR = 0, 1
 PAD_ZEROS, PAD_BORDER = 0, 1
@@ -27,7 +27,7 @@ _DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float8_e4m3fn: F8
 # Every symbol include/fovi_hip.h declares.
 EXPORTED = ("fovi_abi_version", "fovi_last_error", "fovi_sampler_fwd", "fovi_knnconv_fwd",
             "fovi_knnconv_pack_weight", "fovi_knnconv_weight_mfma_elems", "fovi_knnconv_pack_weight_mfma",
-            "fovi_quantize_e4m3", "fovi_knnpool_fwd")
+            "fovi_quantize_e4m3", "fovi_knnpool_fwd", "fovi_knnconv_slotsum", "fovi_knnconv_bwd_x")
 
 
 class SamplerArgs(C.Structure):
@@ -97,6 +97,26 @@ class KnnPoolArgs(C.Structure):
     ]
 
 
+class SlotsumArgs(C.Structure):
+    _fields_ = [
+        ("x", C.c_void_p), ("x_dtype", C.c_int32), ("a_dtype", C.c_int32),
+        ("batch", C.c_int64), ("c_in", C.c_int64), ("n_in", C.c_int64),
+        ("x_stride", C.c_int64 * 3),
+        ("n_out", C.c_int64), ("k", C.c_int64), ("n_ref", C.c_int64),
+        ("slot_ptr", C.c_void_p), ("nbr_sorted", C.c_void_p), ("a", C.c_void_p),
+    ]
+
+
+class BwdXArgs(C.Structure):
+    _fields_ = [
+        ("g", C.c_void_p), ("g_dtype", C.c_int32), ("dx_dtype", C.c_int32),
+        ("batch", C.c_int64), ("c_in", C.c_int64), ("n_in", C.c_int64), ("n_out", C.c_int64),
+        ("n_ref", C.c_int64),
+        ("inv_ptr", C.c_void_p), ("inv", C.c_void_p), ("dx", C.c_void_p),
+        ("dx_stride", C.c_int64 * 3),
+    ]
+
+
 _lib = None
 
 
@@ -126,6 +146,10 @@ def load(path: str = LIB_PATH):
     lib.fovi_quantize_e4m3.restype = C.c_int
     lib.fovi_knnpool_fwd.argtypes = [C.POINTER(KnnPoolArgs), C.c_void_p]
     lib.fovi_knnpool_fwd.restype = C.c_int
+    lib.fovi_knnconv_slotsum.argtypes = [C.POINTER(SlotsumArgs), C.c_void_p]
+    lib.fovi_knnconv_slotsum.restype = C.c_int
+    lib.fovi_knnconv_bwd_x.argtypes = [C.POINTER(BwdXArgs), C.c_void_p]
+    lib.fovi_knnconv_bwd_x.restype = C.c_int
     got = lib.fovi_abi_version()
     if got != ABI_VERSION:
         raise RuntimeError(f"{path}: ABI version {got}, expected {ABI_VERSION}")

@@ -19,8 +19,13 @@ return bf16 (the reference's autocast behaviour); fp32 inputs run the fp32
 kernel. ``Fp8Activations`` inputs (``layer.quantize_input``), or any input
 when ``layer.fp8`` is set, run the e4m3 MFMA kernel (per-tensor activation
 scale, per-output-channel weight scale ``amax|W[o]|/448``, fp32 accumulation,
-bf16 output); the reference has no fp8 path. Backward is not built: calling
-it raises.
+bf16 output); the reference has no fp8 path.
+
+Backward (autograd through ``_KnnConvFn``): the slot sums again
+(``fovi_knnconv_slotsum``) for ``dW = dy^T a``, ``dy W`` as a library GEMM and
+its transposed gather (``fovi_knnconv_bwd_x``, over the inverse neighbour
+table, no atomics) for ``dx``; fp32 and bf16 inputs. The fp8 path has no
+backward.
 """
 from __future__ import annotations
 
@@ -67,14 +72,25 @@ class KNNBaseLayer:
 
 
 class _KnnConvFn(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, x, layer, weight, bias, activation=None):
-        return layer._launch(x, activation)
+    """Forward ``fovi_knnconv_fwd``; backward = the slot sums again (``fovi_knnconv_slotsum``)
+    and the transposed gather (``fovi_knnconv_bwd_x``) around two library GEMMs."""
 
     @staticmethod
-    def backward(ctx, *grads):
-        raise NotImplementedError("fovi_amd KNNConvLayer: backward is not implemented (forward-only "
-                                  "HIP kernels)")
+    def forward(ctx, x, layer, weight, bias, activation=None):
+        y = layer._launch(x, activation)
+        ctx.layer, ctx.activation, ctx.has_bias = layer, activation, bias is not None
+        ctx.save_for_backward(x, weight, y if activation == "relu" else None)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, weight, y = ctx.saved_tensors
+        layer = ctx.layer
+        if ctx.activation == "relu":
+            dy = dy * (y > 0)
+        dx, dw = layer._backward(x, weight, dy, ctx.needs_input_grad[0], ctx.needs_input_grad[2])
+        db = dy.sum(dim=(0, 2)).to(torch.float32) if ctx.has_bias and ctx.needs_input_grad[3] else None
+        return dx, None, dw, db, None
 
 
 class KNNConvLayer(nn.Module, KNNBaseLayer):
@@ -387,6 +403,59 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         a.coll_off_stride = self._coll_off_stride; a.cent_stride = self._cent_stride
         a.tile_heavy = self.tile_heavy.data_ptr(); a.tile_hlist = self.tile_hlist.data_ptr()
         a.heavy_stride = self._heavy_stride; a.hlist_stride = self._hlist_stride
+
+    # -- backward --------------------------------------------------------------
+    def _backward(self, x, weight, dy, need_x, need_w):
+        """Gradients of ``y = W a(x) + b`` (a = the slot sums of the gathered inputs, columns
+        c * V + v in the reference weight): ``dW = dy^T a`` and ``dx = gather^T (dy W)``. The
+        GEMMs run in the input's dtype (fp32 accumulation), the gathers in fp32."""
+        _lib.require_device(x, dy)
+        if x.dtype not in (torch.float32, torch.bfloat16):
+            raise TypeError(f"KNNConvLayer backward: input must be float32 or bfloat16, got {x.dtype}")
+        bsz, c, n_in = x.shape
+        n_out, v, c_out = self.out_coords.shape[0], self.ref_coords.shape[0], self.out_channels
+        dt = x.dtype
+        dy2 = dy.to(dt).permute(0, 2, 1).reshape(bsz * n_out, c_out)
+        w_sm = weight.detach().to(dt).reshape(c_out, c, v).permute(0, 2, 1).reshape(c_out, v * c)
+        lib = _lib.load()
+        stream = _lib.stream_handle(x.device)
+        dx = dw = None
+        if need_w:
+            a_mat = torch.empty(bsz * n_out, v * c, dtype=dt, device=x.device)
+            sa = _lib.SlotsumArgs()
+            sa.x = x.data_ptr(); sa.x_dtype = _lib.dtype_code(dt); sa.a_dtype = _lib.dtype_code(dt)
+            sa.batch, sa.c_in, sa.n_in = bsz, c, n_in
+            sa.x_stride[:] = list(x.stride())
+            sa.n_out, sa.k, sa.n_ref = n_out, self._k, v
+            sa.slot_ptr = self.slot_ptr.data_ptr(); sa.nbr_sorted = self.nbr_sorted.data_ptr()
+            sa.a = a_mat.data_ptr()
+            _lib.check(lib.fovi_knnconv_slotsum(sa, stream), "fovi_knnconv_slotsum")
+            dw_sm = dy2.t() @ a_mat                                     # [C_out, V * C]
+            dw = dw_sm.reshape(c_out, v, c).permute(0, 2, 1).reshape(c_out, c * v).to(weight.dtype)
+        if need_x:
+            g = (dy2 @ w_sm).contiguous()                               # [B * N_out, V * C]
+            inv_ptr, inv = self._inverse_tables(x.device)
+            dx = (torch.empty(bsz, n_in, c, dtype=dt, device=x.device).transpose(1, 2) if x.stride(1) == 1
+                  else torch.empty(bsz, c, n_in, dtype=dt, device=x.device))
+            ba = _lib.BwdXArgs()
+            ba.g = g.data_ptr(); ba.g_dtype = _lib.dtype_code(dt); ba.dx_dtype = _lib.dtype_code(dt)
+            ba.batch, ba.c_in, ba.n_in, ba.n_out, ba.n_ref = bsz, c, n_in, n_out, v
+            ba.inv_ptr = inv_ptr.data_ptr(); ba.inv = inv.data_ptr()
+            ba.dx = dx.data_ptr()
+            ba.dx_stride[:] = list(dx.stride())
+            _lib.check(lib.fovi_knnconv_bwd_x(ba, stream), "fovi_knnconv_bwd_x")
+        return dx, dw
+
+    def _inverse_tables(self, device):
+        """Per input point, the (output, slot) pairs that read it (``knn_tables.inverse_tables``),
+        built on the first backward and kept on the device."""
+        inv = getattr(self, "_inv_tables", None)
+        if inv is None or inv[0].device != device:
+            ptr, ent = T.inverse_tables(self.slot_ptr.cpu(), self.nbr_sorted.cpu(), self.in_coords.shape[0],
+                                        self.ref_coords.shape[0])
+            inv = (ptr.to(device), ent.to(device))
+            self._inv_tables = inv
+        return inv
 
     # -- fp8 ----------------------------------------------------------------
     @property

@@ -172,6 +172,36 @@ def csr_tables(knn_idx, slots, n_in, n_ref):
     return torch.from_numpy(ptr), torch.from_numpy(nbr)
 
 
+def inverse_tables(slot_ptr, nbr_sorted, n_in, n_ref):
+    """Inverse of the CSR neighbour lists, the input-gradient gather of the backward.
+
+    For every input point i, the entries ``n * n_ref + v`` of the (output point, slot) pairs
+    whose list holds i, in increasing order: ``inv[inv_ptr[i]:inv_ptr[i + 1]]``. Returns
+    ``(inv_ptr [n_in + 1] int32, inv [E] int32)``.
+    """
+    ptr = slot_ptr.numpy().astype(np.int64)
+    nbr = nbr_sorted.numpy().astype(np.int64)
+    n_out = ptr.shape[0]
+    cnt = ptr & 0xFFFF
+    beg = ptr >> 16
+    # the slot of every list position: position j of output n is in slot v when beg <= j < beg + cnt
+    k = nbr.shape[1]
+    slot_of = np.full((n_out, k), -1, np.int64)
+    for v in range(n_ref):
+        j = np.arange(k)[None, :]
+        inside = (j >= beg[:, v:v + 1]) & (j < beg[:, v:v + 1] + cnt[:, v:v + 1])
+        slot_of = np.where(inside, v, slot_of)
+    valid = (nbr >= 0) & (nbr < n_in) & (slot_of >= 0)
+    ins = nbr[valid]
+    ent = (np.arange(n_out)[:, None] * n_ref + slot_of)[valid]
+    order = np.lexsort((ent, ins))
+    ins, ent = ins[order], ent[order]
+    inv_ptr = np.zeros(n_in + 1, np.int64)
+    np.add.at(inv_ptr, ins + 1, 1)
+    inv_ptr = np.cumsum(inv_ptr)
+    return torch.from_numpy(inv_ptr.astype(np.int32)), torch.from_numpy(ent.astype(np.int32))
+
+
 TILE_POINTS = 256  # output points per workgroup tile of the staged-row kernel
 
 

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 16
+#define FOVI_ABI_VERSION 17
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -300,6 +300,51 @@ typedef struct fovi_knnpool_args {
 } fovi_knnpool_args;
 
 int fovi_knnpool_fwd(const fovi_knnpool_args* args, void* stream);
+
+/*
+ * kNN-conv backward, the two gather kernels around its two GEMMs (the
+ * gradients autograd forms through KNNConvLayer.forward, fovi/arch/knn.py:484-557;
+ * the reference has no hand-written backward):
+ *
+ *   fovi_knnconv_slotsum: the reduction matrix of the forward,
+ *     a[(b * n_out + n) * n_ref * c_in + v * c_in + c] = sum over the inputs i
+ *     in slot v of output n (slot_ptr / nbr_sorted, as fovi_knnconv_args) of
+ *     x[b, c, i], fp32 sums in list order rounded once to a_dtype. With it,
+ *     dW (slot-major columns) = dy^T a.
+ *   fovi_knnconv_bwd_x: the input gradient from g = dy W (slot-major columns),
+ *     dx[b, c, i] = sum over the entries e = n * n_ref + v of input i's inverse
+ *     list (inv[inv_ptr[i] .. inv_ptr[i + 1]]: every (output, slot) that reads
+ *     input i) of g[(b * n_out + n) * n_ref * c_in + v * c_in + c], fp32 sums
+ *     rounded once to dx_dtype.
+ * x, a, g, dx: F32 or BF16; a and g dense row-major; x and dx any element
+ * strides [batch, channel, point].
+ */
+typedef struct fovi_knnconv_slotsum_args {
+  const void* x;
+  int32_t x_dtype;
+  int32_t a_dtype;
+  int64_t batch, c_in, n_in;
+  int64_t x_stride[3];
+  int64_t n_out, k, n_ref;
+  const int32_t* slot_ptr;    /* [n_out, n_ref] */
+  const int32_t* nbr_sorted;  /* [n_out, k] */
+  void* a;                    /* [batch * n_out, n_ref * c_in] */
+} fovi_knnconv_slotsum_args;
+
+int fovi_knnconv_slotsum(const fovi_knnconv_slotsum_args* args, void* stream);
+
+typedef struct fovi_knnconv_bwd_x_args {
+  const void* g;              /* [batch * n_out, n_ref * c_in] */
+  int32_t g_dtype;
+  int32_t dx_dtype;
+  int64_t batch, c_in, n_in, n_out, n_ref;
+  const int32_t* inv_ptr;     /* [n_in + 1] */
+  const int32_t* inv;         /* entries n * n_ref + v */
+  void* dx;
+  int64_t dx_stride[3];
+} fovi_knnconv_bwd_x_args;
+
+int fovi_knnconv_bwd_x(const fovi_knnconv_bwd_x_args* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -65,6 +65,10 @@ def test_argument_validation_without_gpu():
     pa.mode, pa.k = _lib.POOL_MAX, 0
     assert lib.fovi_knnpool_fwd(pa, None) != 0
     assert b"k must be" in lib.fovi_last_error()
+    assert lib.fovi_knnconv_slotsum(_lib.SlotsumArgs(), None) != 0
+    assert b"null pointer" in lib.fovi_last_error()
+    assert lib.fovi_knnconv_bwd_x(_lib.BwdXArgs(), None) != 0
+    assert b"null pointer" in lib.fovi_last_error()
 
 
 def _c_layout(struct, fields, tmp_path):
@@ -84,7 +88,9 @@ def _c_layout(struct, fields, tmp_path):
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
 @pytest.mark.parametrize("py,c", [(_lib.SamplerArgs, "fovi_sampler_args"), (_lib.KnnConvArgs, "fovi_knnconv_args"),
                                   (_lib.QuantizeArgs, "fovi_quantize_args"),
-                                  (_lib.KnnPoolArgs, "fovi_knnpool_args")])
+                                  (_lib.KnnPoolArgs, "fovi_knnpool_args"),
+                                  (_lib.SlotsumArgs, "fovi_knnconv_slotsum_args"),
+                                  (_lib.BwdXArgs, "fovi_knnconv_bwd_x_args")])
 def test_struct_layout_matches_header(py, c, tmp_path):
     fields = [f for f, _ in py._fields_]
     size, offs = _c_layout(c, fields, tmp_path)
