@@ -136,14 +136,19 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         self._init_conv_like()
 
         self.slots = self.compute_local_rf_slots(knn_indices)
-        slot_ptr, nbr_sorted = T.csr_tables(knn_indices, self.slots, n_in, n_ref)
         self.knn_indices = knn_indices.to(device)
         self.knn_distances = knn_distances.to(device)
         self.knn_indices_pad_token = pad_token.to(device)
         self.knn_indices_pad_mask = self.knn_indices_pad_mask.to(device)
+        self._init_tables(knn_indices, self.slots, n_in, n_ref, device)
+
+    def _init_tables(self, knn_indices, slots, n_in, n_ref, device):
+        """Device tables of the forward kernels from the kNN table ``[k, N_out]`` (indices >=
+        n_in are pad tokens) and the slots ``[N_out, k]``, and the per-layer switches."""
+        slot_ptr, nbr_sorted = T.csr_tables(knn_indices, slots, n_in, n_ref)
         self.register_buffer("slot_ptr", slot_ptr.to(device), persistent=False)
         self.register_buffer("nbr_sorted", nbr_sorted.to(device), persistent=False)
-        tiles = T.direct_tables(knn_indices, self.slots, n_in, n_ref)
+        tiles = T.direct_tables(knn_indices, slots, n_in, n_ref)
         self._max_span = 0
         self._zero_row = 0
         for name, t in zip(("tile_lo", "tile_span", "tile_ent", "tile_nbr", "tile_coll", "tile_coll_n"),
@@ -167,6 +172,9 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         # few-channel bf16 layers: slot sums through a workspace, then a dense GEMM
         # (False: the single fused kernel, which needs no workspace)
         self.two_pass_few_channels = True
+        # input gradient as a kNN-conv forward over the inverse tables (False: a GEMM into
+        # [B * N_out, V * C] and the inverse-table gather, fovi_knnconv_bwd_x)
+        self.dx_by_transposed_conv = True
         # wide layers (bf16 c_in % 32 == 0 or e4m3 c_in % 64 == 0, c_out filling >= 3/4 of its
         # 256-channel tiles, tables within LDS): weights in MFMA-fragment order for the
         # 256 x 256-tile kernel (False: the row-packed kernels)
@@ -432,7 +440,9 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
             _lib.check(lib.fovi_knnconv_slotsum(sa, stream), "fovi_knnconv_slotsum")
             dw_sm = dy2.t() @ a_mat                                     # [C_out, V * C]
             dw = dw_sm.reshape(c_out, v, c).permute(0, 2, 1).reshape(c_out, c * v).to(weight.dtype)
-        if need_x:
+        if need_x and self.dx_by_transposed_conv:
+            dx = self._transposed(x.device)(dy.to(dt), weight)
+        elif need_x:
             g = (dy2 @ w_sm).contiguous()                               # [B * N_out, V * C]
             inv_ptr, inv = self._inverse_tables(x.device)
             dx = (torch.empty(bsz, n_in, c, dtype=dt, device=x.device).transpose(1, 2) if x.stride(1) == 1
@@ -445,6 +455,15 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
             ba.dx_stride[:] = list(dx.stride())
             _lib.check(lib.fovi_knnconv_bwd_x(ba, stream), "fovi_knnconv_bwd_x")
         return dx, dw
+
+    def _transposed(self, device):
+        """The input gradient as a kNN-conv forward (``_TransposedKnnConv``), built on the first
+        backward and kept."""
+        t = getattr(self, "_transposed_conv", None)
+        if t is None or t.weight.device != device:
+            t = _TransposedKnnConv(self, device)
+            self._transposed_conv = t
+        return t
 
     def _inverse_tables(self, device):
         """Per input point, the (output, slot) pairs that read it (``knn_tables.inverse_tables``),
@@ -565,6 +584,44 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         return (f"{self.__class__.__name__}(\n\tin_channels={self.in_channels}\n\tout_channels="
                 f"{self.out_channels}\n\tk={self.k}\n\tn_ref={self.ref_coords.shape[0]}\n\tin_coords="
                 f"{self.in_coords}\n\tout_coords={self.out_coords}\n\tsample_cortex={self.sample_cortex}\n)")
+
+
+class _TransposedKnnConv(KNNConvLayer):
+    """The input gradient of a ``KNNConvLayer`` as a kNN-conv forward of its own.
+
+    ``dx[b, c, i] = sum over the (n, v) whose slot v holds i of sum_o dy[b, o, n] W[o, c V + v]``:
+    a kNN-conv from the output points to the input points with the inverse neighbour table
+    (``knn_tables.inverse_knn``: the lists of input i hold the outputs n that read i, in the
+    slot i sits in) and the weight ``W_T[c, o V + v] = W[o, c V + v]``, so it runs the forward
+    kernels (fused gather, slot sum and MFMA GEMM) with no ``[B N_out, V C]`` intermediate.
+    """
+
+    def __init__(self, layer, device):
+        nn.Module.__init__(self)
+        n_in, n_out = layer.in_coords.shape[0], layer.out_coords.shape[0]
+        n_ref = layer.ref_coords.shape[0]
+        idx, slots = T.inverse_knn(layer.slot_ptr.cpu(), layer.nbr_sorted.cpu(), n_in, n_ref)
+        self.in_channels, self.out_channels = layer.out_channels, layer.in_channels
+        self.in_coords, self.out_coords = layer.out_coords, layer.in_coords
+        self.ref_coords = layer.ref_coords
+        self._k = idx.shape[0]
+        self.bias = None
+        self.weight = torch.zeros(layer.in_channels, layer.out_channels * n_ref, device=device)
+        self._weight_key = None
+        self._init_tables(idx, slots, n_out, n_ref, device)
+
+    def forward(self, dy, weight):
+        """``dx`` of the layer for the output gradient ``dy [B, C_out, N_out]`` and the weight
+        the forward ran with: ``[B, C_in, N_in]`` (a transposed view of channels-last storage),
+        in ``dy``'s dtype."""
+        key = (weight._version, weight.data_ptr())
+        if key != self._weight_key:
+            c_out, c_in_v = weight.shape
+            n_ref = self.ref_coords.shape[0]
+            w_t = weight.detach().reshape(c_out, c_in_v // n_ref, n_ref).permute(1, 0, 2)
+            self.weight.copy_(w_t.reshape(self.weight.shape))
+            self._weight_key = key
+        return self._launch(dy)
 
 
 def _normalize(x, dim=None):

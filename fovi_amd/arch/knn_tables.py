@@ -202,6 +202,29 @@ def inverse_tables(slot_ptr, nbr_sorted, n_in, n_ref):
     return torch.from_numpy(inv_ptr.astype(np.int32)), torch.from_numpy(ent.astype(np.int32))
 
 
+def inverse_knn(slot_ptr, nbr_sorted, n_in, n_ref):
+    """The kNN table of the transposed convolution (the input gradient): for every input
+    point i, the output points whose lists hold i, with the slot i sits in there.
+
+    Returns ``(idx [k', N_in] int64, slots [N_in, k'] int64)`` in the forward's table format,
+    k' the largest number of lists an input point is in (at least 1); shorter columns end in
+    the pad token ``N_out``, whose slot is 0.
+    """
+    inv_ptr, inv = inverse_tables(slot_ptr, nbr_sorted, n_in, n_ref)
+    n_out = slot_ptr.shape[0]
+    ptr = inv_ptr.numpy().astype(np.int64)
+    ent = inv.numpy().astype(np.int64)
+    deg = ptr[1:] - ptr[:-1]
+    kk = max(int(deg.max()) if n_in else 0, 1)
+    pos = np.arange(ent.shape[0]) - np.repeat(ptr[:-1], deg)
+    row = np.repeat(np.arange(n_in), deg)
+    idx = np.full((n_in, kk), n_out, np.int64)
+    sl = np.zeros((n_in, kk), np.int64)
+    idx[row, pos] = ent // n_ref
+    sl[row, pos] = ent % n_ref
+    return torch.from_numpy(np.ascontiguousarray(idx.T)), torch.from_numpy(sl)
+
+
 TILE_POINTS = 256  # output points per workgroup tile of the staged-row kernel
 
 

@@ -125,6 +125,25 @@ def test_decomposed_backward_matches_oracle_autograd(relu):
     assert torch.allclose(dx, dx_ref, rtol=1e-12, atol=1e-12)
 
 
+@pytest.mark.parametrize("pads", [True, False])
+def test_input_gradient_is_the_transposed_conv(pads):
+    """dx of the oracle's autograd = the oracle forward over the inverse kNN table
+    (knn_tables.inverse_knn) with the weight W_T[c, o V + v] = W[o, c V + v]."""
+    idx, slots, rf, ptr, nbr = _synthetic(pads=pads)
+    n_in, n_out, V, C, C_out, B = 30, 11, 4, 5, 7, 2
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(B, C, n_in, generator=g, dtype=torch.float64)
+    w = torch.randn(C_out, C * V, generator=g, dtype=torch.float64)
+    dy = torch.randn(B, C_out, n_out, generator=g, dtype=torch.float64)
+    dx_ref, _, _ = _oracle_grads(x, idx, n_in, rf.double(), w, None, dy)
+    idx_t, slots_t = T.inverse_knn(ptr, nbr, n_in, V)
+    assert idx_t.shape[1] == n_in and slots_t.shape == (n_in, idx_t.shape[0])
+    assert idx_t.shape[0] == max(int(torch.bincount(idx[idx < n_in].flatten(), minlength=n_in).max()), 1)
+    w_t = w.reshape(C_out, C, V).permute(1, 0, 2).reshape(C, C_out * V)
+    dx = knnconv_ref.knnconv_forward(dy, idx_t, n_out, T.slots_to_one_hot(slots_t, V).double(), w_t)
+    assert torch.allclose(dx, dx_ref, rtol=1e-12, atol=1e-12)
+
+
 def test_inverse_tables_of_a_layer_geometry():
     """On a real log-polar layer: counts per input point equal its occurrences in the kNN table."""
     t = layer_tables(32, 16, 25)
@@ -163,8 +182,10 @@ def _layer(res_in, res_out, k, c_in, c_out, bias, seed=1):
     (24, 12, 30, 5, 40, True, False, False),      # ragged: non-square k, odd channels
     (64, 32, 49, 3, 64, False, False, True),      # C2 layer 1 (few channels)
 ])
-def test_layer_backward_vs_oracle(dt, res_in, res_out, k, c_in, c_out, bias, channels_last, relu):
+@pytest.mark.parametrize("tconv", [True, False], ids=["dx_tconv", "dx_gather"])
+def test_layer_backward_vs_oracle(dt, res_in, res_out, k, c_in, c_out, bias, channels_last, relu, tconv):
     layer = _layer(res_in, res_out, k, c_in, c_out, bias)
+    layer.dx_by_transposed_conv = tconv
     n_in = res_in * res_in
     g = torch.Generator().manual_seed(7)
     x = torch.randn(2, c_in, n_in, generator=g).to(dt)
