@@ -80,6 +80,31 @@ class RetinalTransform(nn.Module):
         x = self.sampler(x, fix_loc=fix_loc, fixation_size=fixation_size, **kwargs)
         if self.post_transforms is not None and self.training:
             x = self.post_transforms(x.unsqueeze(3)).clone().squeeze(3)
+        return self._finish(x)
+
+    @torch.autocast(device_type="cuda", enabled=False)
+    def forward_views(self, x, fix_loc, fixation_size):
+        """``forward`` for ``F`` fixations of every image in one sampler launch: ``fix_loc
+        [B, F, 2]`` (h, w) in [0, 1], ``fixation_size [B, F, 2]`` (h, w) pixels -> ``[B, F, C, N]``,
+        view ``(b, f)`` equal to ``forward(x, fix_loc[:, f], fixation_size[:, f])[b]``. Random
+        pre/post transforms are drawn per call, so in training mode they need the per-fixation
+        calls: this raises when they are set."""
+        if self.training and (self.pre_transforms is not None or self.post_transforms is not None):
+            raise ValueError("forward_views: pre/post transforms are drawn per call; call forward per fixation")
+        bsz, n_fix = x.shape[0], fix_loc.shape[1]
+        if tuple(fix_loc.shape) != (bsz, n_fix, 2):
+            raise ValueError(f"fix_loc must be [{bsz}, F, 2]; got {tuple(fix_loc.shape)}")
+        loc = torch.as_tensor(fix_loc).to(dtype=self.dtype, device=self.device).reshape(bsz * n_fix, 2)
+        size = torch.as_tensor(fixation_size).detach().cpu()
+        if tuple(size.shape) != (bsz, n_fix, 2):
+            raise ValueError(f"fixation_size must be [{bsz}, {n_fix}, 2]; got {tuple(size.shape)}")
+        view_image = torch.arange(bsz).repeat_interleave(n_fix)
+        y = self.sampler.sample_views(x, loc, size.reshape(bsz * n_fix, 2).numpy(), view_image=view_image)
+        y = self._finish(y)
+        return y.reshape(bsz, n_fix, *y.shape[1:])
+
+    def _finish(self, x):
+        """Colour decay, eval-mode grayscale, grid reshape and dtype of the sampled ``[V, C, N]``."""
         if self.foveal_color is not None:
             x = self.foveal_color(x, self.sampler.polar_radius)
         if not self.training and self.no_color_val:

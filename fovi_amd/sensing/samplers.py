@@ -231,6 +231,12 @@ class KNNGridSampler(BaseGridSampler):
         dense = self._dense(img, fix_loc=fix_loc, fixation_size=fixation_size)
         return self.pooler(dense)
 
+    def sample_views(self, img, fix_loc=None, fixation_size=None, view_image=None):
+        """``[V, C, N]`` pooled samples of ``V`` views (view ``v`` reads image ``view_image[v]``):
+        one dense sampler launch for all views, then the pooling."""
+        img = img.to(self.device).to(self.dtype)
+        return self.pooler(self._dense.sample_views(img, fix_loc, fixation_size, view_image=view_image))
+
     def all_coords(self, device=None):
         if device is None:
             return self.coords.cartesian, self.coords.polar, self.coords.plotting

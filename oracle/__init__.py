@@ -28,6 +28,11 @@ Pinning (what checks each function beyond retyping its formula):
     scalar loop of exp(-d^2 / 2 sigma^2) over min-max normalised distances,
     columns summing to 1 - 1e-8 relative, the largest weight at the nearest
     neighbour.
+  * policy_ref (the fixation draws): closed forms over one stream of
+    uniforms (eval mode: only the centres, lo + (hi - lo) u; training: four
+    draws per image, area, log-aspect, y, x), bit for bit; random_crop by
+    invariants (the crop inside the image at integer corners, its area and
+    aspect within the ranges up to rounding) and its clamped fallback.
   * The host tables the oracle consumes (sensor coordinates, kNN indices,
     ref slots; built by fovi_amd, not by this package) are pinned bit for bit
     by vectors the reference itself wrote (tests/golden/tables.npz, from
