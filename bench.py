@@ -58,7 +58,8 @@ def bench_c3(steps, warmup, dev):
     t0 = time.time()
     coords = SamplingCoords(16, 2.78, RES, style="logpolar")
     layer = KNNConvLayer(C, C, K, coords, coords, device=dev)
-    log(f"[c3] tables built in {time.time() - t0:.1f}s")
+    t_tables = time.time() - t0
+    log(f"[c3] layer and tables built in {t_tables:.2f}s (kNN search on the GPU: {layer._gpu_tables(RES * RES)})")
     g = torch.Generator(device=dev).manual_seed(1)
     with torch.no_grad():
         layer.weight.copy_(torch.randn(layer.weight.shape, generator=g, device=dev) * (1.0 / (C * K)) ** 0.5)
@@ -70,7 +71,7 @@ def bench_c3(steps, warmup, dev):
     flops = 2.0 * B * RES * RES * C * C * layer.ref_coords.shape[0]
     tflops = flops / (ms * 1e-3) / 1e12
     log(f"[c3] {ms:.3f} ms/step  {tflops:.1f} TFLOP/s  ({100 * tflops / PEAK_BF16_TFLOPS:.1f}% of bf16 peak)")
-    return dict(ms=ms, flops=flops, tflops=tflops, layer=layer, x=x)
+    return dict(ms=ms, flops=flops, tflops=tflops, layer=layer, x=x, table_s=t_tables)
 
 
 def bench_c3_backward(c3, steps, warmup):
@@ -423,6 +424,8 @@ def main():
                      "traffic": measured_traffic("knnconv_bf16_v5_kernel")},
         "cpu_baseline": cpu,
     }
+    if "table_s" in c3:
+        line["c3_layer_build_s"] = round(c3["table_s"], 3)
     if c5 is not None:
         line["c5_fp8"] = {"workload": "C5: C3 layer with OCP e4m3 activations (per-tensor scale) and weights "
                                       "(per-output-channel scales), fp32 accumulate, bf16 out",

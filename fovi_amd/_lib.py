@@ -14,7 +14,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
 
-ABI_VERSION = 17
+ABI_VERSION = 18
 F32, BF16, F8E4M3 = 0, 1, 2
 NEAREST, BILINEAR = 0, 1
 PAD_ZEROS, PAD_BORDER = 0, 1
@@ -27,7 +27,8 @@ _DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float8_e4m3fn: F8
 # Every symbol include/fovi_hip.h declares.
 EXPORTED = ("fovi_abi_version", "fovi_last_error", "fovi_sampler_fwd", "fovi_knnconv_fwd",
             "fovi_knnconv_pack_weight", "fovi_knnconv_weight_mfma_elems", "fovi_knnconv_pack_weight_mfma",
-            "fovi_quantize_e4m3", "fovi_knnpool_fwd", "fovi_knnconv_slotsum", "fovi_knnconv_bwd_x")
+            "fovi_quantize_e4m3", "fovi_knnpool_fwd", "fovi_knnconv_slotsum", "fovi_knnconv_bwd_x",
+            "fovi_knn_logpolar_candidates", "fovi_knn_select")
 
 
 class SamplerArgs(C.Structure):
@@ -117,6 +118,24 @@ class BwdXArgs(C.Structure):
     ]
 
 
+class KnnLogpolarArgs(C.Structure):
+    _fields_ = [
+        ("src", C.c_void_p), ("dst", C.c_void_p),
+        ("n_in", C.c_int64), ("n_out", C.c_int64), ("k", C.c_int64),
+        ("theta_hi", C.c_float), ("theta_half", C.c_float),
+        ("cap", C.c_int64),
+        ("cand_idx", C.c_void_p), ("cand_sq", C.c_void_p), ("cand_n", C.c_void_p),
+    ]
+
+
+class KnnSelectArgs(C.Structure):
+    _fields_ = [
+        ("n_out", C.c_int64), ("k", C.c_int64), ("cap", C.c_int64),
+        ("cand_idx", C.c_void_p), ("cand_d", C.c_void_p), ("cand_n", C.c_void_p),
+        ("idx", C.c_void_p), ("dist", C.c_void_p),
+    ]
+
+
 _lib = None
 
 
@@ -150,6 +169,10 @@ def load(path: str = LIB_PATH):
     lib.fovi_knnconv_slotsum.restype = C.c_int
     lib.fovi_knnconv_bwd_x.argtypes = [C.POINTER(BwdXArgs), C.c_void_p]
     lib.fovi_knnconv_bwd_x.restype = C.c_int
+    lib.fovi_knn_logpolar_candidates.argtypes = [C.POINTER(KnnLogpolarArgs), C.c_void_p]
+    lib.fovi_knn_logpolar_candidates.restype = C.c_int
+    lib.fovi_knn_select.argtypes = [C.POINTER(KnnSelectArgs), C.c_void_p]
+    lib.fovi_knn_select.restype = C.c_int
     got = lib.fovi_abi_version()
     if got != ABI_VERSION:
         raise RuntimeError(f"{path}: ABI version {got}, expected {ABI_VERSION}")

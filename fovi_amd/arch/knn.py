@@ -65,10 +65,20 @@ class KNNBaseLayer:
         self.sample_coords_cart = torch.cat([in_c.cartesian.cpu(), in_c.cartesian_pad_coords.cpu()], 0)
         if in_c.style in ("image", "logpolar"):
             assert out_c.style == in_c.style
-            idx, dist, src = T.knn_logpolar(in_c.cortical.cpu(), out_c.cortical.cpu(), self._k, batch_size)
+            if self._gpu_tables(in_c.shape[0]):
+                idx, dist, src = T.knn_logpolar_device(in_c.cortical.cpu(), out_c.cortical.cpu(), self._k,
+                                                       self.device)
+            else:
+                idx, dist, src = T.knn_logpolar(in_c.cortical.cpu(), out_c.cortical.cpu(), self._k, batch_size)
             self.sample_coords = src
             return idx, dist
         raise NotImplementedError(f"style {in_c.style!r}: only log-polar neighbourhoods are built")
+
+    def _gpu_tables(self, n_in):
+        """Whether the neighbour search runs on the GPU (``knn_tables.knn_logpolar_device``, the
+        host's results bit for bit): a CUDA layer where the GPU search applies."""
+        dev = torch.device(self.device) if not isinstance(self.device, torch.device) else self.device
+        return dev.type == "cuda" and torch.cuda.is_available() and T.knn_logpolar_device_ok(n_in, self._k)
 
 
 class _KnnConvFn(torch.autograd.Function):

@@ -59,19 +59,86 @@ def _minmax01(x):
     return (x - lo) / (hi - lo)
 
 
+def _logpolar_prep(in_cortical, out_cortical):
+    """Per-column min-max normalised coordinates (reference knn.py:113-114) and the angle
+    wrap constants: the largest normalised angle and the half range (knn.py:135-141)."""
+    src = _minmax01(in_cortical.clone())
+    dst = _minmax01(out_cortical.clone())
+    theta_hi = src[:, 1].max()
+    theta_half = src[:, 1].min() + (theta_hi - src[:, 1].min()) / 2
+    return src, dst, theta_hi, theta_half
+
+
+def knn_logpolar_device_ok(n_in, k):
+    """Whether ``knn_logpolar_device`` applies: the GPU search reproduces the host's tie order
+    where torch's CPU topk runs its heap selection (k * 64 <= n_in), for k <= 256."""
+    return 1 <= k <= 256 and k * 64 <= n_in
+
+
+def knn_logpolar_device(in_cortical, out_cortical, k, device, max_bytes=2 << 30):
+    """``knn_logpolar`` with the O(N_in N_out) scan on the GPU: the same ``(indices [k, N_out]
+    int64, distances [k, N_out] fp32, normalised input coords)``, bit for bit, on the CPU.
+
+    ``fovi_knn_logpolar_candidates`` emits per output point the inputs the host's heap
+    selection could admit, with their exact squared distances; their square roots are taken
+    here with the host builder's own call (``** (1 / 2)`` on a CPU tensor, whose rounding is
+    not always IEEE); ``fovi_knn_select`` replays the selection over them. Output points go
+    in chunks of at most ``max_bytes`` of candidate storage (``n_in`` slots per point, so no
+    row can overflow).
+    """
+    from .. import _lib
+    src, dst, theta_hi, theta_half = _logpolar_prep(in_cortical, out_cortical)
+    n_in, n_out = src.shape[0], dst.shape[0]
+    if not knn_logpolar_device_ok(n_in, k):
+        raise ValueError(f"knn_logpolar_device: needs 1 <= k <= 256 and k * 64 <= n_in (k={k}, n_in={n_in})")
+    s_d = src.to(device=device, dtype=torch.float32).contiguous()
+    d_d = dst.to(device=device, dtype=torch.float32).contiguous()
+    dev = s_d.device
+    cap = n_in
+    chunk = max(1, min(n_out, max_bytes // (cap * 12)))
+    idx = torch.empty(k, n_out, dtype=torch.int32)
+    dist = torch.empty(k, n_out, dtype=torch.float32)
+    lib = _lib.load()
+    stream = _lib.stream_handle(dev)
+    slots = torch.arange(cap, device=dev)
+    for s0 in range(0, n_out, chunk):
+        m = min(chunk, n_out - s0)
+        cand_idx = torch.empty(m, cap, dtype=torch.int32, device=dev)
+        cand_sq = torch.empty(m, cap, dtype=torch.float32, device=dev)
+        cand_n = torch.empty(m, dtype=torch.int32, device=dev)
+        a = _lib.KnnLogpolarArgs()
+        a.src, a.dst = s_d.data_ptr(), d_d[s0:s0 + m].data_ptr()
+        a.n_in, a.n_out, a.k = n_in, m, k
+        a.theta_hi, a.theta_half = float(theta_hi), float(theta_half)
+        a.cap = cap
+        a.cand_idx, a.cand_sq, a.cand_n = cand_idx.data_ptr(), cand_sq.data_ptr(), cand_n.data_ptr()
+        _lib.check(lib.fovi_knn_logpolar_candidates(a, stream), "fovi_knn_logpolar_candidates")
+        mask = slots.unsqueeze(0) < cand_n.unsqueeze(1)
+        cand_d = torch.empty_like(cand_sq)
+        cand_d[mask] = (cand_sq[mask].cpu() ** (1 / 2)).to(dev)          # the host builder's square root
+        del cand_sq
+        out_i = torch.empty(k, m, dtype=torch.int32, device=dev)
+        out_d = torch.empty(k, m, dtype=torch.float32, device=dev)
+        sa = _lib.KnnSelectArgs()
+        sa.n_out, sa.k, sa.cap = m, k, cap
+        sa.cand_idx, sa.cand_d, sa.cand_n = cand_idx.data_ptr(), cand_d.data_ptr(), cand_n.data_ptr()
+        sa.idx, sa.dist = out_i.data_ptr(), out_d.data_ptr()
+        _lib.check(lib.fovi_knn_select(sa, stream), "fovi_knn_select")
+        idx[:, s0:s0 + m] = out_i.cpu()
+        dist[:, s0:s0 + m] = out_d.cpu()
+    return idx.long(), dist, src
+
+
 def knn_logpolar(in_cortical, out_cortical, k, batch_size=None):
     """k nearest inputs per output on the wrapped log-polar cortical lattice.
 
     Returns ``(indices [k, N_out] int64, distances [k, N_out] fp32,
     normalised input cortical coords [N_in, 2])``.
     """
-    src = _minmax01(in_cortical.clone())
-    dst = _minmax01(out_cortical.clone())
+    src, dst, theta_hi, theta_half = _logpolar_prep(in_cortical, out_cortical)
     n_out = dst.shape[0]
     idx = torch.zeros((k, n_out), dtype=torch.long)
     dist = torch.zeros((k, n_out), dtype=torch.float32)
-    theta_hi = src[:, 1].max()
-    theta_half = src[:, 1].min() + (theta_hi - src[:, 1].min()) / 2
     step = _chunk(src.shape[0], n_out, batch_size)
     for s in range(0, n_out, step):
         e = min(s + step, n_out)

@@ -1,0 +1,257 @@
+// kNN search on the wrapped log-polar cortical lattice for gfx950: the
+// O(N_in * N_out) part of a kNN layer's table construction
+// (fovi/arch/knn.py:101-152, log-polar branch), with the host builder's
+// results bit for bit.
+//
+// The host builder takes torch's CPU square root, which is not always the
+// correctly rounded one, and torch's CPU topk, whose order among equal
+// distances comes from its heap selection. So the search runs in two passes
+// around one host step:
+//   1. knn_lp_candidates_kernel (one thread per output point): the scan in
+//      input order with IEEE distances and a size-k max-heap that tracks the
+//      running k-th smallest; it emits (index, squared distance) for the first
+//      k inputs and every input within a small margin below that running
+//      value: every input the host's heap can admit (the host's distances
+//      are within an ulp of the IEEE ones, so its running k-th value is too).
+//   2. the host takes the square roots of the emitted squared distances (exact
+//      fp32 on both sides) with the same torch call the host builder makes.
+//   3. knn_select_kernel replays the host's selection over the candidates in
+//      input order: the heap steps of the C++ standard library's partial_sort
+//      as libstdc++ builds it (heap select: make the heap of the first k,
+//      replace the top by every later element that compares strictly smaller,
+//      sifting the hole down to a leaf and the value back up; then sort the
+//      heap by repeated pops), which torch's CPU topk(largest=False) runs when
+//      k * 64 <= n. Inputs never emitted are never admitted by that heap, so
+//      skipping them changes nothing.
+// Heaps live in LDS, interleaved by thread. Uniform input loads (every lane
+// reads the same point) go through the scalar cache; all stores are vector
+// stores.
+#include "common.h"
+
+namespace fovi {
+namespace {
+
+constexpr int KNN_THREADS = 64;
+constexpr int KNN_MAX_K = 256;
+// admission margin of the candidate scan, relative: 8 ulp of fp32 at the running k-th distance
+constexpr float KNN_MARGIN = 1.0f + 0x1p-20f;
+
+struct KnnLpParams {
+  const float* src;
+  const float* dst;
+  int64_t n_in, n_out;
+  int k;
+  float theta_hi, theta_half;
+};
+
+// The topk comparator for the smallest values: NaN counts as larger than any number.
+__device__ __forceinline__ bool knn_less(float x, float y) {
+  return (!__builtin_isnan(x) && __builtin_isnan(y)) || x < y;
+}
+
+// Sift a value into the heap [0, len) (element j at hv[j * T]) from the hole at `hole`:
+// the hole moves down along the larger child to a leaf, then the value moves up.
+__device__ __forceinline__ void heap_adjust(float* hv, int32_t* hi, int hole, int len, float val, int32_t idx) {
+  constexpr int T = KNN_THREADS;
+  const int top = hole;
+  int child = hole;
+  while (child < (len - 1) / 2) {
+    child = 2 * (child + 1);
+    if (knn_less(hv[child * T], hv[(child - 1) * T])) --child;
+    hv[hole * T] = hv[child * T];
+    hi[hole * T] = hi[child * T];
+    hole = child;
+  }
+  if ((len & 1) == 0 && child == (len - 2) / 2) {
+    child = 2 * (child + 1);
+    hv[hole * T] = hv[(child - 1) * T];
+    hi[hole * T] = hi[(child - 1) * T];
+    hole = child - 1;
+  }
+  int parent = (hole - 1) / 2;
+  while (hole > top && knn_less(hv[parent * T], val)) {
+    hv[hole * T] = hv[parent * T];
+    hi[hole * T] = hi[parent * T];
+    hole = parent;
+    parent = (hole - 1) / 2;
+  }
+  hv[hole * T] = val;
+  hi[hole * T] = idx;
+}
+
+// Squared distance of input i to the output at (r0, t0): |drho|^2 + |dtheta|^2 with the angle
+// wrap, fp32 products and sum with no contraction (the build passes -ffp-contract=off): the
+// same value on the host and on the GPU.
+__device__ __forceinline__ float lp_sq(const float* src, int64_t i, float r0, float t0, float theta_hi,
+                                       float theta_half) {
+  const float dr = fabsf(src[2 * i] - r0);
+  float dt = fabsf(src[2 * i + 1] - t0);
+  if (dt > theta_half) dt = theta_hi - dt;
+  return dr * dr + dt * dt;
+}
+
+// Heap in LDS of the first k (value, index) pairs, made a max-heap.
+__device__ __forceinline__ void heap_make(float* hv, int32_t* hi, int k) {
+  constexpr int T = KNN_THREADS;
+  if (k < 2) return;
+  for (int parent = (k - 2) / 2;; --parent) {
+    heap_adjust(hv, hi, parent, k, hv[parent * T], hi[parent * T]);
+    if (parent == 0) break;
+  }
+}
+
+// Pass 1: the scan in index order with IEEE distances. Emits every input the exact heap
+// (whatever rounding its square roots have, within a few ulp) could admit: the first k,
+// then each input whose distance is below the running k-th smallest times (1 + 2^-20).
+// Emitted as (index, squared distance dr*dr + dt*dt, exact in fp32 on any device).
+__global__ __launch_bounds__(KNN_THREADS) void knn_lp_candidates_kernel(KnnLpParams p, int64_t cap,
+                                                                        int32_t* cand_idx, float* cand_sq,
+                                                                        int32_t* cand_n) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  constexpr int T = KNN_THREADS;
+  const int t = threadIdx.x;
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * T + t;
+  if (n >= p.n_out) return;                      // no block-wide synchronisation below
+  float* hv = reinterpret_cast<float*>(smem) + t;
+  int32_t* hi = reinterpret_cast<int32_t*>(smem + static_cast<size_t>(p.k) * T * sizeof(float)) + t;
+  const float r0 = p.dst[2 * n], t0 = p.dst[2 * n + 1];
+  const int k = p.k;
+  int32_t* ci = cand_idx + n * cap;
+  float* cs = cand_sq + n * cap;
+  int64_t m = 0;
+  for (int j = 0; j < k; ++j) {
+    const float sq = lp_sq(p.src, j, r0, t0, p.theta_hi, p.theta_half);
+    hv[j * T] = sqrtf(sq);
+    hi[j * T] = j;
+    ci[m] = j;
+    cs[m] = sq;
+    ++m;
+  }
+  heap_make(hv, hi, k);
+  float top = hv[0];
+  for (int64_t i = k; i < p.n_in; ++i) {
+    const float sq = lp_sq(p.src, i, r0, t0, p.theta_hi, p.theta_half);
+    const float d = sqrtf(sq);
+    if (d < top * KNN_MARGIN) {
+      if (m < cap) {
+        ci[m] = static_cast<int32_t>(i);
+        cs[m] = sq;
+      }
+      ++m;
+    }
+    if (knn_less(d, top)) {
+      heap_adjust(hv, hi, 0, k, d, static_cast<int32_t>(i));
+      top = hv[0];
+    }
+  }
+  cand_n[n] = static_cast<int32_t>(m < INT32_MAX ? m : INT32_MAX);
+}
+
+// Pass 2: the exact heap selection over the candidates (in index order) with the distances
+// the host rounded, then the heap sort; outputs in the k-major layout of knn_indices.
+__global__ __launch_bounds__(KNN_THREADS) void knn_select_kernel(int64_t n_out, int k, int64_t cap,
+                                                                 const int32_t* cand_idx, const float* cand_d,
+                                                                 const int32_t* cand_n, int32_t* idx, float* dist) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  constexpr int T = KNN_THREADS;
+  const int t = threadIdx.x;
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * T + t;
+  if (n >= n_out) return;                        // no block-wide synchronisation below
+  float* hv = reinterpret_cast<float*>(smem) + t;
+  int32_t* hi = reinterpret_cast<int32_t*>(smem + static_cast<size_t>(k) * T * sizeof(float)) + t;
+  const int32_t* ci = cand_idx + n * cap;
+  const float* cd = cand_d + n * cap;
+  const int64_t m = cand_n[n] < cap ? cand_n[n] : cap;
+  for (int j = 0; j < k; ++j) {
+    hv[j * T] = cd[j];
+    hi[j * T] = ci[j];
+  }
+  heap_make(hv, hi, k);
+  float top = hv[0];
+  for (int64_t j = k; j < m; ++j) {
+    const float d = cd[j];
+    if (knn_less(d, top)) {
+      heap_adjust(hv, hi, 0, k, d, ci[j]);
+      top = hv[0];
+    }
+  }
+  for (int last = k - 1; last >= 1; --last) {    // sort the heap: ascending
+    const float v = hv[last * T];
+    const int32_t ix = hi[last * T];
+    hv[last * T] = hv[0];
+    hi[last * T] = hi[0];
+    heap_adjust(hv, hi, 0, last, v, ix);
+  }
+  for (int j = 0; j < k; ++j) {
+    idx[j * n_out + n] = hi[j * T];
+    dist[j * n_out + n] = hv[j * T];
+  }
+}
+
+static int reserve_lds(const void* kernel, size_t lds, const char* what) {
+  if (lds > 64 * 1024 &&
+      hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess) {
+    set_error("%s: cannot reserve %zu bytes of LDS", what, lds);
+    return 1;
+  }
+  return 0;
+}
+
+}  // namespace
+}  // namespace fovi
+
+using namespace fovi;
+
+static bool knn_sizes_ok(int64_t k, int64_t n_in, int64_t n_out, const char* what) {
+  if (k < 1 || k > KNN_MAX_K || n_out < 0 || n_in < k * 64 || n_in > INT32_MAX) {
+    set_error("%s: need 1 <= k <= %d, k * 64 <= n_in < 2^31 (k=%lld, n_in=%lld, n_out=%lld)", what, KNN_MAX_K,
+              (long long)k, (long long)n_in, (long long)n_out);
+    return false;
+  }
+  return true;
+}
+
+extern "C" int fovi_knn_logpolar_candidates(const fovi_knn_logpolar_args* a, void* stream) {
+  clear_error();
+  if (!a || !a->src || !a->dst || !a->cand_idx || !a->cand_sq || !a->cand_n) {
+    set_error("fovi_knn_logpolar_candidates: null pointer");
+    return 1;
+  }
+  if (!knn_sizes_ok(a->k, a->n_in, a->n_out, "fovi_knn_logpolar_candidates")) return 1;
+  if (a->cap < a->k) {
+    set_error("fovi_knn_logpolar_candidates: cap %lld < k %lld", (long long)a->cap, (long long)a->k);
+    return 1;
+  }
+  if (a->n_out == 0) return 0;
+  KnnLpParams p;
+  p.src = a->src; p.dst = a->dst; p.n_in = a->n_in; p.n_out = a->n_out; p.k = static_cast<int>(a->k);
+  p.theta_hi = a->theta_hi; p.theta_half = a->theta_half;
+  const size_t lds = static_cast<size_t>(p.k) * KNN_THREADS * (sizeof(float) + sizeof(int32_t));
+  if (reserve_lds(reinterpret_cast<const void*>(&knn_lp_candidates_kernel), lds, "fovi_knn_logpolar_candidates"))
+    return 1;
+  const unsigned blocks = static_cast<unsigned>((a->n_out + KNN_THREADS - 1) / KNN_THREADS);
+  hipLaunchKernelGGL(knn_lp_candidates_kernel, dim3(blocks), dim3(KNN_THREADS), lds,
+                     static_cast<hipStream_t>(stream), p, a->cap, a->cand_idx, a->cand_sq, a->cand_n);
+  return check_launch("fovi_knn_logpolar_candidates");
+}
+
+extern "C" int fovi_knn_select(const fovi_knn_select_args* a, void* stream) {
+  clear_error();
+  if (!a || !a->cand_idx || !a->cand_d || !a->cand_n || !a->idx || !a->dist) {
+    set_error("fovi_knn_select: null pointer");
+    return 1;
+  }
+  if (a->k < 1 || a->k > KNN_MAX_K || a->n_out < 0 || a->cap < a->k) {
+    set_error("fovi_knn_select: need 1 <= k <= %d and cap >= k (k=%lld, cap=%lld)", KNN_MAX_K, (long long)a->k,
+              (long long)a->cap);
+    return 1;
+  }
+  if (a->n_out == 0) return 0;
+  const int k = static_cast<int>(a->k);
+  const size_t lds = static_cast<size_t>(k) * KNN_THREADS * (sizeof(float) + sizeof(int32_t));
+  if (reserve_lds(reinterpret_cast<const void*>(&knn_select_kernel), lds, "fovi_knn_select")) return 1;
+  const unsigned blocks = static_cast<unsigned>((a->n_out + KNN_THREADS - 1) / KNN_THREADS);
+  hipLaunchKernelGGL(knn_select_kernel, dim3(blocks), dim3(KNN_THREADS), lds, static_cast<hipStream_t>(stream),
+                     a->n_out, k, a->cap, a->cand_idx, a->cand_d, a->cand_n, a->idx, a->dist);
+  return check_launch("fovi_knn_select");
+}

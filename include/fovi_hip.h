@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 17
+#define FOVI_ABI_VERSION 18
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -345,6 +345,55 @@ typedef struct fovi_knnconv_bwd_x_args {
 } fovi_knnconv_bwd_x_args;
 
 int fovi_knnconv_bwd_x(const fovi_knnconv_bwd_x_args* args, void* stream);
+
+/*
+ * kNN search on the wrapped log-polar cortical lattice, the table of
+ * KNNBaseLayer._compute_knns / _compute_euclidean_distances_batched
+ * (fovi/arch/knn.py:23-57,101-152) for sample_cortex=True on log-polar
+ * coordinates, in two GPU passes around one host step:
+ *
+ *   fovi_knn_logpolar_candidates: per output point n, the scan over the
+ *     inputs in index order of the squared distance
+ *       sq(i, n) = |rho_i - rho_n|^2 + dth^2, dth = |theta_i - theta_n|,
+ *       replaced by theta_hi - dth when dth > theta_half,
+ *     in fp32 with no contraction, on the min-max normalised coordinates
+ *     (src, dst: [n, 2] rows (rho, theta)). Writes cand_idx[n * cap + j] and
+ *     cand_sq[n * cap + j] for the first k inputs and every later input whose
+ *     IEEE distance sqrt(sq) is below (1 + 2^-20) times the running k-th
+ *     smallest, in index order, and their number to cand_n[n] (entries past
+ *     cap are counted, not written: cand_n[n] > cap means the row overflowed).
+ *   (host) cand_d = sqrt(cand_sq) with the host builder's own square root.
+ *   fovi_knn_select: per output point, the k smallest of its candidates in
+ *     the order torch's CPU topk(largest=False) returns them for k * 64 <= n_in
+ *     (a size-k max-heap over the candidates in index order that admits
+ *     strictly smaller values, then heap-sorted): idx [k, n_out] (k-major, as
+ *     knn_indices) and dist [k, n_out]. Reads min(cand_n[n], cap) candidates.
+ *
+ * Needs 1 <= k <= 256, k * 64 <= n_in < 2^31 and cap >= k.
+ */
+typedef struct fovi_knn_logpolar_args {
+  const float* src;           /* [n_in, 2] */
+  const float* dst;           /* [n_out, 2] */
+  int64_t n_in, n_out, k;
+  float theta_hi, theta_half;
+  int64_t cap;                /* candidates per output row */
+  int32_t* cand_idx;          /* [n_out, cap] */
+  float* cand_sq;             /* [n_out, cap] */
+  int32_t* cand_n;            /* [n_out] */
+} fovi_knn_logpolar_args;
+
+int fovi_knn_logpolar_candidates(const fovi_knn_logpolar_args* args, void* stream);
+
+typedef struct fovi_knn_select_args {
+  int64_t n_out, k, cap;
+  const int32_t* cand_idx;    /* [n_out, cap] */
+  const float* cand_d;        /* [n_out, cap] */
+  const int32_t* cand_n;      /* [n_out] */
+  int32_t* idx;               /* [k, n_out] */
+  float* dist;                /* [k, n_out] */
+} fovi_knn_select_args;
+
+int fovi_knn_select(const fovi_knn_select_args* args, void* stream);
 
 #ifdef __cplusplus
 }

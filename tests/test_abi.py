@@ -68,6 +68,8 @@ def test_argument_validation_without_gpu():
     assert lib.fovi_knnconv_slotsum(_lib.SlotsumArgs(), None) != 0
     assert b"null pointer" in lib.fovi_last_error()
     assert lib.fovi_knnconv_bwd_x(_lib.BwdXArgs(), None) != 0
+    assert lib.fovi_knn_logpolar_candidates(_lib.KnnLogpolarArgs(), None) != 0
+    assert lib.fovi_knn_select(_lib.KnnSelectArgs(), None) != 0
     assert b"null pointer" in lib.fovi_last_error()
 
 
@@ -90,7 +92,9 @@ def _c_layout(struct, fields, tmp_path):
                                   (_lib.QuantizeArgs, "fovi_quantize_args"),
                                   (_lib.KnnPoolArgs, "fovi_knnpool_args"),
                                   (_lib.SlotsumArgs, "fovi_knnconv_slotsum_args"),
-                                  (_lib.BwdXArgs, "fovi_knnconv_bwd_x_args")])
+                                  (_lib.BwdXArgs, "fovi_knnconv_bwd_x_args"),
+                                  (_lib.KnnLogpolarArgs, "fovi_knn_logpolar_args"),
+                                  (_lib.KnnSelectArgs, "fovi_knn_select_args")])
 def test_struct_layout_matches_header(py, c, tmp_path):
     fields = [f for f, _ in py._fields_]
     size, offs = _c_layout(c, fields, tmp_path)

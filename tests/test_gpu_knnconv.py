@@ -116,12 +116,17 @@ def test_weight_update_repacks():
     assert_close_rel(y1.cpu(), 2 * y0.cpu(), 1e-6)
 
 
-def test_backward_raises():
-    layer = _layer(16, 16, 9, 8, 8)
-    x = torch.randn(1, 8, 256, device="cuda", requires_grad=True)
-    y = layer(x)
-    with pytest.raises(NotImplementedError):
-        y.sum().backward()
+def test_gradients_flow_and_fp8_has_no_graph():
+    """The layer is differentiable (values checked in test_knnconv_bwd.py); the fp8 path is
+    forward only: its output carries no autograd graph."""
+    layer = _layer(16, 16, 9, 64, 64, bias=True)
+    x = torch.randn(1, 64, 256, device="cuda").bfloat16().requires_grad_(True)
+    layer(x).float().sum().backward()
+    assert x.grad.shape == x.shape and layer.weight.grad.shape == layer.weight.shape
+    assert layer.bias.grad.shape == (64,)
+    layer.fp8 = True
+    y8 = layer(x)
+    assert y8.grad_fn is None
 
 
 def test_c3_large_layer_slice_and_batch_independence():
