@@ -75,10 +75,10 @@ def bench_c3(steps, warmup, dev):
 
 
 def bench_c3_backward(c3, steps, warmup):
-    """Backward of the C3 layer (input and weight gradients, bf16): the slot sums a
-    [B*N, V*C], dW = dy^T a, G = dy W and the transposed gather of G into dx. Reported
-    against the two GEMMs' flops (2x the forward's); the slot-sum and gather kernels move
-    B*N*V*C*2 bytes each way."""
+    """Backward of the C3 layer (input and weight gradients, bf16): dx as a kNN-conv forward
+    over the inverse neighbour table (the wide-layer kernel), dW by the pair-list kernel
+    (fovi_knnconv_dw, no slot-sum matrix). Reported against the two products' flops (2x the
+    forward's)."""
     import torch
     layer, x = c3["layer"], c3["x"]
     g = torch.Generator(device=x.device).manual_seed(5)
@@ -434,8 +434,8 @@ def main():
                                        "frac": round(c5["tflops"] / PEAK_FP8_TFLOPS, 4)},
                           "quantize_ms": round(c5["ms_q"], 4), "quantize_GB/s": round(c5["q_gbs"], 1)}
     if bwd is not None:
-        line["c3_backward"] = {"workload": "C3 layer backward, bf16: input and weight gradients (slot sums, "
-                                           "two library GEMMs, inverse-table gather)",
+        line["c3_backward"] = {"workload": "C3 layer backward, bf16: input gradient (kNN-conv forward over the "
+                                           "inverse table) and weight gradient (per-slot pair-list MFMA kernel)",
                                "ms": round(bwd["ms"], 4), "TFLOP/s": round(bwd["tflops"], 2)}
     if c4 is not None:
         line["sampler_c4"] = {

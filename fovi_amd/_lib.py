@@ -14,7 +14,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
 
-ABI_VERSION = 18
+ABI_VERSION = 19
 F32, BF16, F8E4M3 = 0, 1, 2
 NEAREST, BILINEAR = 0, 1
 PAD_ZEROS, PAD_BORDER = 0, 1
@@ -28,7 +28,8 @@ _DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float8_e4m3fn: F8
 EXPORTED = ("fovi_abi_version", "fovi_last_error", "fovi_sampler_fwd", "fovi_knnconv_fwd",
             "fovi_knnconv_pack_weight", "fovi_knnconv_weight_mfma_elems", "fovi_knnconv_pack_weight_mfma",
             "fovi_quantize_e4m3", "fovi_knnpool_fwd", "fovi_knnconv_slotsum", "fovi_knnconv_bwd_x",
-            "fovi_knn_logpolar_candidates", "fovi_knn_select")
+            "fovi_knn_logpolar_candidates", "fovi_knn_select", "fovi_knnconv_dw_workspace_bytes",
+            "fovi_knnconv_dw")
 
 
 class SamplerArgs(C.Structure):
@@ -136,6 +137,19 @@ class KnnSelectArgs(C.Structure):
     ]
 
 
+class KnnConvDwArgs(C.Structure):
+    _fields_ = [
+        ("x", C.c_void_p), ("x_stride", C.c_int64 * 3),
+        ("dy", C.c_void_p), ("dy_stride", C.c_int64 * 3),
+        ("batch", C.c_int64), ("c_in", C.c_int64), ("c_out", C.c_int64), ("n_in", C.c_int64),
+        ("n_out", C.c_int64), ("n_ref", C.c_int64),
+        ("pair_off", C.c_void_p), ("pairs", C.c_void_p),
+        ("n_chunks", C.c_int64), ("images_per_group", C.c_int64),
+        ("workspace", C.c_void_p), ("workspace_bytes", C.c_int64),
+        ("dw", C.c_void_p),
+    ]
+
+
 _lib = None
 
 
@@ -173,6 +187,10 @@ def load(path: str = LIB_PATH):
     lib.fovi_knn_logpolar_candidates.restype = C.c_int
     lib.fovi_knn_select.argtypes = [C.POINTER(KnnSelectArgs), C.c_void_p]
     lib.fovi_knn_select.restype = C.c_int
+    lib.fovi_knnconv_dw_workspace_bytes.argtypes = [C.c_int64] * 6
+    lib.fovi_knnconv_dw_workspace_bytes.restype = C.c_int64
+    lib.fovi_knnconv_dw.argtypes = [C.POINTER(KnnConvDwArgs), C.c_void_p]
+    lib.fovi_knnconv_dw.restype = C.c_int
     got = lib.fovi_abi_version()
     if got != ABI_VERSION:
         raise RuntimeError(f"{path}: ABI version {got}, expected {ABI_VERSION}")

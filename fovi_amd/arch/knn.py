@@ -185,6 +185,11 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         # input gradient as a kNN-conv forward over the inverse tables (False: a GEMM into
         # [B * N_out, V * C] and the inverse-table gather, fovi_knnconv_bwd_x)
         self.dx_by_transposed_conv = True
+        # bf16 weight gradient by fovi_knnconv_dw (False: the slot sums and a library GEMM)
+        self.dw_fused = True
+        # its work split: output points per pair segment, images per workgroup
+        self.dw_chunk = 4096
+        self.dw_images_per_group = 4
         # wide layers (bf16 c_in % 32 == 0 or e4m3 c_in % 64 == 0, c_out filling >= 3/4 of its
         # 256-channel tiles, tables within LDS): weights in MFMA-fragment order for the
         # 256 x 256-tile kernel (False: the row-packed kernels)
@@ -438,7 +443,9 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         lib = _lib.load()
         stream = _lib.stream_handle(x.device)
         dx = dw = None
-        if need_w:
+        if need_w and self.dw_fused and self._dw_fused_ok(x, dt):
+            dw = self._dw_fused(x, dy).to(weight.dtype)
+        elif need_w:
             a_mat = torch.empty(bsz * n_out, v * c, dtype=dt, device=x.device)
             sa = _lib.SlotsumArgs()
             sa.x = x.data_ptr(); sa.x_dtype = _lib.dtype_code(dt); sa.a_dtype = _lib.dtype_code(dt)
@@ -465,6 +472,52 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
             ba.dx_stride[:] = list(dx.stride())
             _lib.check(lib.fovi_knnconv_bwd_x(ba, stream), "fovi_knnconv_bwd_x")
         return dx, dw
+
+    def _dw_fused_ok(self, x, dt):
+        """Whether ``fovi_knnconv_dw`` takes the weight gradient: bf16, channel counts multiples
+        of 8, channels-last input rows 16-byte aligned."""
+        return (dt == torch.bfloat16 and self.in_channels % 8 == 0 and self.out_channels % 8 == 0
+                and x.stride(1) == 1 and x.stride(2) % 8 == 0 and x.stride(0) % 8 == 0
+                and x.data_ptr() % 16 == 0)
+
+    def _dw_fused(self, x, dy):
+        """``dW`` (fp32, reference layout) by ``fovi_knnconv_dw``: per slot a GEMM over its
+        (output, input) pairs, no slot-sum matrix; one workgroup per slot, chunk of
+        ``dw_chunk`` output points and ``dw_images_per_group`` images."""
+        bsz, c, n_in = x.shape
+        n_out, v, c_out = self.out_coords.shape[0], self.ref_coords.shape[0], self.out_channels
+        dyc = dy.to(torch.bfloat16)
+        if not (dyc.stride(1) == 1 and dyc.stride(2) % 8 == 0 and dyc.stride(0) % 8 == 0
+                and dyc.data_ptr() % 16 == 0):
+            dyc = dyc.transpose(1, 2).contiguous().transpose(1, 2)
+        pair_off, pairs = self._slot_pairs(x.device)
+        lib = _lib.load()
+        n_chunks = (pair_off.numel() - 1) // v
+        ipg = self.dw_images_per_group
+        nbytes = lib.fovi_knnconv_dw_workspace_bytes(bsz, ipg, n_chunks, c, c_out, v)
+        ws = torch.empty(nbytes // 4, dtype=torch.float32, device=x.device)
+        dw = torch.empty(c_out, c * v, dtype=torch.float32, device=x.device)
+        a = _lib.KnnConvDwArgs()
+        a.x = x.data_ptr(); a.x_stride[:] = list(x.stride())
+        a.dy = dyc.data_ptr(); a.dy_stride[:] = list(dyc.stride())
+        a.batch, a.c_in, a.c_out, a.n_in, a.n_out, a.n_ref = bsz, c, c_out, n_in, n_out, v
+        a.pair_off = pair_off.data_ptr(); a.pairs = pairs.data_ptr()
+        a.n_chunks = n_chunks
+        a.images_per_group = ipg
+        a.workspace = ws.data_ptr(); a.workspace_bytes = nbytes
+        a.dw = dw.data_ptr()
+        _lib.check(lib.fovi_knnconv_dw(a, _lib.stream_handle(x.device)), "fovi_knnconv_dw")
+        return dw
+
+    def _slot_pairs(self, device):
+        """``knn_tables.slot_pairs`` of this layer, built on the first backward and kept."""
+        sp = getattr(self, "_slot_pair_tables", None)
+        if sp is None or sp[0].device != device:
+            off, pairs = T.slot_pairs(self.slot_ptr.cpu(), self.nbr_sorted.cpu(), self.ref_coords.shape[0],
+                                      chunk=self.dw_chunk)
+            sp = (off.to(device), pairs.to(device))
+            self._slot_pair_tables = sp
+        return sp
 
     def _transposed(self, device):
         """The input gradient as a kNN-conv forward (``_TransposedKnnConv``), built on the first

@@ -269,6 +269,38 @@ def inverse_tables(slot_ptr, nbr_sorted, n_in, n_ref):
     return torch.from_numpy(inv_ptr.astype(np.int32)), torch.from_numpy(ent.astype(np.int32))
 
 
+def slot_pairs(slot_ptr, nbr_sorted, n_ref, chunk=256, step=32):
+    """The (output, input) pairs of every slot, the reduction lists of the weight gradient,
+    cut into segments of ``chunk`` consecutive output points.
+
+    Returns ``(pair_off [n_chunks * n_ref + 1] int32, pairs [2 * pair_off[-1]] int32)``:
+    segment ``q * n_ref + v`` holds slot v's pairs ``(n, i)`` with ``n // chunk == q``, in
+    output order and list order within an output, padded with ``(-1, -1)`` to a multiple of
+    ``step``.
+    """
+    ptr = slot_ptr.numpy().astype(np.int64)
+    nbr = nbr_sorted.numpy().astype(np.int64)
+    n_out, k = nbr.shape
+    n_chunks = max(1, -(-n_out // chunk))
+    cnt = ptr & 0xFFFF
+    beg = ptr >> 16
+    j = np.arange(k)[None, None, :]
+    inside = (j >= beg[:, :, None]) & (j < (beg + cnt)[:, :, None])           # [n_out, V, k]
+    n_idx, v_idx, j_idx = np.nonzero(inside)
+    seg_idx = (n_idx // chunk) * n_ref + v_idx
+    order = np.lexsort((j_idx, n_idx, seg_idx))
+    n_idx, seg_idx, j_idx = n_idx[order], seg_idx[order], j_idx[order]
+    i_idx = nbr[n_idx, j_idx]
+    counts = np.bincount(seg_idx, minlength=n_chunks * n_ref)
+    padded = -(-counts // step) * step
+    off = np.concatenate([[0], np.cumsum(padded)])
+    pairs = np.full((int(off[-1]), 2), -1, np.int64)
+    pos = off[seg_idx] + (np.arange(len(seg_idx)) - np.concatenate([[0], np.cumsum(counts)])[seg_idx])
+    pairs[pos, 0] = n_idx
+    pairs[pos, 1] = i_idx
+    return torch.from_numpy(off.astype(np.int32)), torch.from_numpy(pairs.reshape(-1).astype(np.int32))
+
+
 def inverse_knn(slot_ptr, nbr_sorted, n_in, n_ref):
     """The kNN table of the transposed convolution (the input gradient): for every input
     point i, the output points whose lists hold i, with the slot i sits in there.

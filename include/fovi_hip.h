@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 18
+#define FOVI_ABI_VERSION 19
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -394,6 +394,41 @@ typedef struct fovi_knn_select_args {
 } fovi_knn_select_args;
 
 int fovi_knn_select(const fovi_knn_select_args* args, void* stream);
+
+/*
+ * Weight gradient of the kNN convolution without the slot-sum matrix (the
+ * gradient autograd forms for F.linear's weight through knn.py:521-555):
+ *   dw[o * c_in * n_ref + c * n_ref + v] = sum over images b and over the
+ *   pairs (n, i) of slot v of dy[b, n, o] * x[b, i, c],
+ * fp32 accumulation of bf16 products, fp32 output in the reference weight
+ * layout. pairs holds (n, i) int32 pairs in n_chunks * n_ref segments,
+ * segment q * n_ref + v at [pair_off[q * n_ref + v], pair_off[q * n_ref + v + 1])
+ * holding slot v's pairs of one chunk of output points (the layer: 256
+ * consecutive points per chunk, output order), each segment padded to a
+ * multiple of 32 with (-1, -1). One workgroup takes one segment for
+ * images_per_group consecutive images; the workspace holds its partial tile
+ * (fovi_knnconv_dw_workspace_bytes). x and
+ * dy bf16 channels-last (element strides [batch, channel, point] with channel
+ * stride 1, rows 16-byte aligned); c_in and c_out multiples of 8.
+ */
+typedef struct fovi_knnconv_dw_args {
+  const void* x;              /* bf16 [batch, c_in, n_in] (strides below) */
+  int64_t x_stride[3];
+  const void* dy;             /* bf16 [batch, c_out, n_out] */
+  int64_t dy_stride[3];
+  int64_t batch, c_in, c_out, n_in, n_out, n_ref;
+  const int32_t* pair_off;    /* [n_chunks * n_ref + 1] */
+  const int32_t* pairs;       /* [2 * pair_off[n_chunks * n_ref]] */
+  int64_t n_chunks;
+  int64_t images_per_group;
+  void* workspace;
+  int64_t workspace_bytes;
+  float* dw;                  /* [c_out, c_in * n_ref] */
+} fovi_knnconv_dw_args;
+
+int64_t fovi_knnconv_dw_workspace_bytes(int64_t batch, int64_t images_per_group, int64_t n_chunks, int64_t c_in,
+                                        int64_t c_out, int64_t n_ref);
+int fovi_knnconv_dw(const fovi_knnconv_dw_args* args, void* stream);
 
 #ifdef __cplusplus
 }

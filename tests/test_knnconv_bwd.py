@@ -144,6 +144,39 @@ def test_input_gradient_is_the_transposed_conv(pads):
     assert torch.allclose(dx, dx_ref, rtol=1e-12, atol=1e-12)
 
 
+@pytest.mark.parametrize("pads", [True, False])
+@pytest.mark.parametrize("chunk", [256, 4])
+def test_slot_pairs_bruteforce_and_weight_gradient(pads, chunk):
+    """knn_tables.slot_pairs: segment q * V + v holds the (n, i) list entries in slot v with
+    n // chunk == q, output order, padded to 32 with (-1, -1); dW from the pairs equals the
+    oracle's autograd."""
+    idx, slots, rf, ptr, nbr = _synthetic(pads=pads)
+    off, pairs = T.slot_pairs(ptr, nbr, 4, chunk=chunk)
+    n_chunks = -(-11 // chunk)
+    assert off.numel() == n_chunks * 4 + 1
+    assert off[0] == 0 and (off % 32 == 0).all() and pairs.numel() == 2 * off[-1]
+    pr = pairs.reshape(-1, 2)
+    for q in range(n_chunks):
+        for v in range(4):
+            want = [(n, idx[j, n].item()) for n in range(q * chunk, min(11, (q + 1) * chunk)) for j in range(6)
+                    if slots[n, j].item() == v and idx[j, n].item() < 30]
+            got = [tuple(t) for t in pr[off[q * 4 + v]:off[q * 4 + v + 1]].tolist()]
+            real = [t for t in got if t[0] >= 0]
+            assert sorted(real) == sorted(want) and [t[0] for t in real] == sorted(t[0] for t in real)
+            assert all(t == (-1, -1) for t in got[len(real):]) and len(got) - len(real) < 32
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(2, 5, 30, generator=g, dtype=torch.float64)
+    w = torch.randn(7, 20, generator=g, dtype=torch.float64)
+    dy = torch.randn(2, 7, 11, generator=g, dtype=torch.float64)
+    _, dw_ref, _ = _oracle_grads(x, idx, 30, rf.double(), w, None, dy)
+    dw = torch.zeros(7, 5, 4, dtype=torch.float64)
+    for sg in range(n_chunks * 4):
+        for n, i in pr[off[sg]:off[sg + 1]].tolist():
+            if n >= 0:
+                dw[:, :, sg % 4] += dy[:, :, n].t() @ x[:, :, i]
+    assert torch.allclose(dw.reshape(7, 20), dw_ref, rtol=1e-12, atol=1e-12)
+
+
 def test_inverse_tables_of_a_layer_geometry():
     """On a real log-polar layer: counts per input point equal its occurrences in the kNN table."""
     t = layer_tables(32, 16, 25)
@@ -182,10 +215,11 @@ def _layer(res_in, res_out, k, c_in, c_out, bias, seed=1):
     (24, 12, 30, 5, 40, True, False, False),      # ragged: non-square k, odd channels
     (64, 32, 49, 3, 64, False, False, True),      # C2 layer 1 (few channels)
 ])
-@pytest.mark.parametrize("tconv", [True, False], ids=["dx_tconv", "dx_gather"])
+@pytest.mark.parametrize("tconv", [True, False], ids=["dx_tconv+dw_fused", "dx_gather+dw_gemm"])
 def test_layer_backward_vs_oracle(dt, res_in, res_out, k, c_in, c_out, bias, channels_last, relu, tconv):
     layer = _layer(res_in, res_out, k, c_in, c_out, bias)
     layer.dx_by_transposed_conv = tconv
+    layer.dw_fused = tconv
     n_in = res_in * res_in
     g = torch.Generator().manual_seed(7)
     x = torch.randn(2, c_in, n_in, generator=g).to(dt)
@@ -258,3 +292,46 @@ def test_entry_points_with_pad_tokens_through_the_c_abi(dt):
             if i < n_in:
                 want[:, :, i] += gmr[:, n * V + slots[n, j].item()]
     assert_close_rel(dx.double().cpu(), want, 1e-6 if dt == torch.float32 else 1e-2, "dx gather")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("res_in,res_out,k,c_in,c_out,batch,chunk,ipg", [
+    (32, 32, 25, 256, 256, 3, 256, 3),    # C3 neighbourhood, one full tile, 4 point chunks, all images
+    (32, 32, 25, 256, 256, 3, 4096, 1),   # one chunk, one image per workgroup
+    (32, 16, 25, 40, 72, 2, 256, 1),      # partial tiles in both channel axes
+    (16, 16, 9, 320, 264, 3, 48, 2),      # two tiles in each axis, 6 chunks (last partial), odd split
+])
+def test_fused_weight_gradient_vs_oracle(res_in, res_out, k, c_in, c_out, batch, chunk, ipg):
+    """fovi_knnconv_dw through the C-ABI against the oracle's autograd dW (bf16 operands,
+    fp32 accumulation: 1e-2 relative against the oracle on the bf16-rounded operands)."""
+    layer = _layer(res_in, res_out, k, c_in, c_out, False)
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(batch, c_in, res_in * res_in, generator=g).bfloat16()
+    dy = torch.randn(batch, c_out, layer.out_coords.shape[0], generator=g).bfloat16()
+    xd = x.cuda().transpose(1, 2).contiguous().transpose(1, 2)
+    dyd = dy.cuda().transpose(1, 2).contiguous().transpose(1, 2)
+    v = layer.ref_coords.shape[0]
+    pair_off, pairs = T.slot_pairs(layer.slot_ptr.cpu(), layer.nbr_sorted.cpu(), v, chunk=chunk)
+    pair_off, pairs = pair_off.cuda(), pairs.cuda()
+    n_chunks = (pair_off.numel() - 1) // v
+    lib = _lib.load()
+    nbytes = lib.fovi_knnconv_dw_workspace_bytes(batch, ipg, n_chunks, c_in, c_out, v)
+    ws = torch.empty(nbytes // 4, device="cuda")
+    dw = torch.full((c_out, c_in * v), float("nan"), device="cuda")
+    a = _lib.KnnConvDwArgs()
+    a.x = xd.data_ptr(); a.x_stride[:] = list(xd.stride())
+    a.dy = dyd.data_ptr(); a.dy_stride[:] = list(dyd.stride())
+    a.batch, a.c_in, a.c_out, a.n_in, a.n_out, a.n_ref = batch, c_in, c_out, res_in * res_in, dy.shape[2], v
+    a.pair_off = pair_off.data_ptr(); a.pairs = pairs.data_ptr()
+    a.n_chunks = n_chunks
+    a.images_per_group = ipg
+    a.workspace = ws.data_ptr(); a.workspace_bytes = nbytes
+    a.dw = dw.data_ptr()
+    _lib.check(lib.fovi_knnconv_dw(a, _lib.stream_handle(xd.device)), "fovi_knnconv_dw")
+    torch.cuda.synchronize()
+    _, dw_ref, _ = _oracle_grads(x.float(), layer.knn_indices.cpu(), res_in * res_in, layer.local_rf.cpu(),
+                                 layer.weight.detach().cpu(), None, dy.float())
+    assert_close_rel(dw.cpu(), dw_ref, 1e-2, "fused dW")
+    # the layer's own path gives the same
+    layer.dw_chunk, layer.dw_images_per_group = chunk, ipg
+    assert torch.equal(layer._dw_fused(xd, dyd), dw)
