@@ -14,7 +14,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
 
-ABI_VERSION = 19
+ABI_VERSION = 20
 F32, BF16, F8E4M3 = 0, 1, 2
 NEAREST, BILINEAR = 0, 1
 PAD_ZEROS, PAD_BORDER = 0, 1
@@ -29,7 +29,7 @@ EXPORTED = ("fovi_abi_version", "fovi_last_error", "fovi_sampler_fwd", "fovi_knn
             "fovi_knnconv_pack_weight", "fovi_knnconv_weight_mfma_elems", "fovi_knnconv_pack_weight_mfma",
             "fovi_quantize_e4m3", "fovi_knnpool_fwd", "fovi_knnconv_slotsum", "fovi_knnconv_bwd_x",
             "fovi_knn_logpolar_candidates", "fovi_knn_select", "fovi_knnconv_dw_workspace_bytes",
-            "fovi_knnconv_dw")
+            "fovi_knnconv_dw", "fovi_knnpool_bwd")
 
 
 class SamplerArgs(C.Structure):
@@ -96,6 +96,20 @@ class KnnPoolArgs(C.Structure):
         ("n_out", C.c_int64), ("k", C.c_int64),
         ("y", C.c_void_p), ("y_dtype", C.c_int32), ("reserved0", C.c_int32),
         ("y_stride", C.c_int64 * 3),
+    ]
+
+
+class KnnPoolBwdArgs(C.Structure):
+    _fields_ = [
+        ("x", C.c_void_p), ("x_dtype", C.c_int32), ("mode", C.c_int32),
+        ("batch", C.c_int64), ("channels", C.c_int64), ("n_in", C.c_int64),
+        ("x_stride", C.c_int64 * 3),
+        ("nbr", C.c_void_p), ("weights", C.c_void_p),
+        ("n_out", C.c_int64), ("k", C.c_int64),
+        ("dy", C.c_void_p), ("dy_dtype", C.c_int32), ("dx_dtype", C.c_int32),
+        ("dy_stride", C.c_int64 * 3),
+        ("inv_ptr", C.c_void_p), ("inv", C.c_void_p), ("state", C.c_void_p),
+        ("dx", C.c_void_p), ("dx_stride", C.c_int64 * 3),
     ]
 
 
@@ -191,6 +205,8 @@ def load(path: str = LIB_PATH):
     lib.fovi_knnconv_dw_workspace_bytes.restype = C.c_int64
     lib.fovi_knnconv_dw.argtypes = [C.POINTER(KnnConvDwArgs), C.c_void_p]
     lib.fovi_knnconv_dw.restype = C.c_int
+    lib.fovi_knnpool_bwd.argtypes = [C.POINTER(KnnPoolBwdArgs), C.c_void_p]
+    lib.fovi_knnpool_bwd.restype = C.c_int
     got = lib.fovi_abi_version()
     if got != ABI_VERSION:
         raise RuntimeError(f"{path}: ABI version {got}, expected {ABI_VERSION}")

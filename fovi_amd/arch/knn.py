@@ -698,14 +698,19 @@ def _normalize(x, dim=None):
 
 
 class _KnnPoolFn(torch.autograd.Function):
+    """Forward ``fovi_knnpool_fwd``; backward ``fovi_knnpool_bwd`` (gather over the inverse
+    neighbour table, the reference's NaN masks carry no gradient)."""
+
     @staticmethod
     def forward(ctx, x, layer):
+        ctx.layer = layer
+        ctx.save_for_backward(x)
         return layer._launch(x)
 
     @staticmethod
-    def backward(ctx, *grads):
-        raise NotImplementedError("fovi_amd KNNPoolingLayer: backward is not implemented (forward-only "
-                                  "HIP kernel)")
+    def backward(ctx, dy):
+        (x,) = ctx.saved_tensors
+        return ctx.layer._backward(x, dy), None
 
 
 _POOL_MODES = {"max": _lib.POOL_MAX, "avg": _lib.POOL_AVG, "sum": _lib.POOL_SUM, "gaussian": _lib.POOL_GAUSSIAN}
@@ -789,6 +794,38 @@ class KNNPoolingLayer(nn.Module, KNNBaseLayer):
     def forward(self, X_l):
         """``[B, C, N_in] -> [B, C, N_out]`` (reference knn.py:345-394)."""
         return _KnnPoolFn.apply(X_l, self)
+
+    def _backward(self, x, dy):
+        """``dx`` in ``x``'s dtype and layout (``fovi_knnpool_bwd``)."""
+        _lib.require_device(x, dy)
+        bsz, c, n_in = x.shape
+        n_out = self.out_coords.shape[0]
+        inv = getattr(self, "_inv_rows", None)
+        if inv is None or inv[0].device != x.device:
+            ptr, ent = T.inverse_rows(self.nbr_rows.cpu(), n_in)
+            inv = (ptr.to(x.device), ent.to(x.device))
+            self._inv_rows = inv
+        dx = (torch.empty(bsz, n_in, c, dtype=x.dtype, device=x.device).transpose(1, 2) if x.stride(1) == 1
+              else torch.empty(bsz, c, n_in, dtype=x.dtype, device=x.device))
+        if dy.dtype not in (torch.float32, torch.bfloat16):
+            dy = dy.float()
+        state = None if self.mode == "sum" else torch.empty(bsz * n_out * c, dtype=torch.float32, device=x.device)
+        a = _lib.KnnPoolBwdArgs()
+        a.x = x.data_ptr(); a.x_dtype = _lib.dtype_code(x.dtype); a.mode = _POOL_MODES[self.mode]
+        a.batch, a.channels, a.n_in = bsz, c, n_in
+        a.x_stride[:] = list(x.stride())
+        a.nbr = self.nbr_rows.data_ptr()
+        a.weights = self.weight_rows.data_ptr() if self.weight_rows is not None else None
+        a.n_out, a.k = n_out, self._k
+        a.dy = dy.data_ptr(); a.dy_dtype = _lib.dtype_code(dy.dtype)
+        a.dy_stride[:] = list(dy.stride())
+        a.dx_dtype = _lib.dtype_code(dx.dtype)
+        a.inv_ptr, a.inv = inv[0].data_ptr(), inv[1].data_ptr()
+        a.state = None if state is None else state.data_ptr()
+        a.dx = dx.data_ptr(); a.dx_stride[:] = list(dx.stride())
+        lib = _lib.load()
+        _lib.check(lib.fovi_knnpool_bwd(a, _lib.stream_handle(x.device)), "fovi_knnpool_bwd")
+        return dx
 
     def __repr__(self):
         return (f"KNNPoolingLayer(\n\tmode={self.mode}\n\tk={self.k}\n\tin_coords={self.in_coords}\n"

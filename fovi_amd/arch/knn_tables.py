@@ -301,6 +301,21 @@ def slot_pairs(slot_ptr, nbr_sorted, n_ref, chunk=256, step=32):
     return torch.from_numpy(off.astype(np.int32)), torch.from_numpy(pairs.reshape(-1).astype(np.int32))
 
 
+def inverse_rows(nbr_rows, n_in):
+    """Per input point, the entries ``n * k + j`` of the row-major neighbour table
+    ``nbr_rows [N_out, k]`` that hold it (indices outside [0, n_in) dropped), in increasing
+    order: ``(inv_ptr [n_in + 1] int32, inv [E] int32)``."""
+    nbr = nbr_rows.numpy().astype(np.int64).reshape(-1)
+    ent = np.arange(nbr.shape[0], dtype=np.int64)
+    ok = (nbr >= 0) & (nbr < n_in)
+    nbr, ent = nbr[ok], ent[ok]
+    order = np.lexsort((ent, nbr))
+    nbr, ent = nbr[order], ent[order]
+    ptr = np.zeros(n_in + 1, np.int64)
+    np.add.at(ptr, nbr + 1, 1)
+    return torch.from_numpy(np.cumsum(ptr).astype(np.int32)), torch.from_numpy(ent.astype(np.int32))
+
+
 def inverse_knn(slot_ptr, nbr_sorted, n_in, n_ref):
     """The kNN table of the transposed convolution (the input gradient): for every input
     point i, the output points whose lists hold i, with the slot i sits in there.

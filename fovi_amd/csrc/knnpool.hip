@@ -243,3 +243,145 @@ extern "C" int fovi_knnpool_fwd(const fovi_knnpool_args* a, void* stream) {
   }
   return check_launch("fovi_knnpool_fwd");
 }
+
+// ----------------------------------------------------------------------------------- backward
+// The gradient autograd forms through the reference forward (gather, the NaN handling of each
+// mode, the reduction): dx[b, c, i] = sum over the (n, j) whose j-th neighbour is input i of
+// coef * dy[b, c, n], and 0 where x[b, c, i] is NaN (the reference masks those features):
+//   max:      coef = 1 for the first neighbour position holding the maximum (torch.max over a
+//             dim returns the first one), NaN features reading as -inf;
+//   avg:      coef = 1 / (number of non-NaN features of (b, c, n));
+//   sum:      coef = 1;
+//   gaussian: coef = w[n, j] / (sum of the non-NaN features' weights + 1e-8).
+// Two passes: the per-output state (argmax position, count, or weight sum + 1e-8) into an fp32
+// workspace [b, n, c], then one thread per input element summing over its inverse list.
+
+namespace fovi {
+namespace {
+
+struct PoolBwdParams {
+  const void* x;
+  int64_t B, C, Nin, Nout, K;
+  int64_t xs0, xs1, xs2;
+  const int32_t* nbr;
+  const float* w;
+  const void* dy;
+  int64_t ds0, ds1, ds2;
+  const int32_t* inv_ptr;
+  const int32_t* inv;
+  float* state;
+  void* dx;
+  int64_t gs0, gs1, gs2;
+  int mode;
+};
+
+template <typename InT>
+__global__ __launch_bounds__(256) void knnpool_bwd_state_kernel(PoolBwdParams p, int64_t total) {
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
+       t += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t c = t % p.C;
+    const int64_t n = (t / p.C) % p.Nout;
+    const int64_t b = t / (p.C * p.Nout);
+    const InT* xb = static_cast<const InT*>(p.x) + b * p.xs0 + c * p.xs1;
+    const int32_t* nb = p.nbr + n * p.K;
+    float best = -__builtin_inff(), sum = 0.0f;
+    int64_t arg = 0;
+    for (int64_t j = 0; j < p.K; ++j) {
+      const int64_t idx = nb[j];
+      const float v = idx >= 0 && idx < p.Nin ? Elem<InT>::load(xb + idx * p.xs2) : __builtin_nanf("");
+      const bool nan = v != v;
+      if (p.mode == FOVI_POOL_MAX) {
+        const float m = nan ? -__builtin_inff() : v;
+        if (j == 0 || m > best) { best = m; arg = j; }      // first position of the maximum
+      } else if (!nan) {
+        sum += p.mode == FOVI_POOL_GAUSSIAN ? p.w[n * p.K + j] : 1.0f;
+      }
+    }
+    p.state[(b * p.Nout + n) * p.C + c] =
+        p.mode == FOVI_POOL_MAX ? static_cast<float>(arg) : (p.mode == FOVI_POOL_GAUSSIAN ? sum + 1e-8f : sum);
+  }
+}
+
+template <typename InT, typename GT, typename DT>
+__global__ __launch_bounds__(256) void knnpool_bwd_dx_kernel(PoolBwdParams p, int64_t total) {
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < total;
+       t += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t c = t % p.C;
+    const int64_t i = (t / p.C) % p.Nin;
+    const int64_t b = t / (p.C * p.Nin);
+    const float xv = Elem<InT>::load(static_cast<const InT*>(p.x) + b * p.xs0 + c * p.xs1 + i * p.xs2);
+    float acc = 0.0f;
+    if (xv == xv) {
+      const GT* dyb = static_cast<const GT*>(p.dy) + b * p.ds0 + c * p.ds1;
+      for (int32_t q = p.inv_ptr[i]; q < p.inv_ptr[i + 1]; ++q) {
+        const int64_t e = p.inv[q];
+        const int64_t n = e / p.K, j = e - n * p.K;
+        const float g = Elem<GT>::load(dyb + n * p.ds2);
+        const float st = p.mode == FOVI_POOL_SUM ? 1.0f : p.state[(b * p.Nout + n) * p.C + c];
+        switch (p.mode) {
+          case FOVI_POOL_MAX: if (st == static_cast<float>(j)) acc += g; break;
+          case FOVI_POOL_AVG: acc += g / st; break;
+          case FOVI_POOL_SUM: acc += g; break;
+          default: acc += g * (p.w[e] / st); break;
+        }
+      }
+    }
+    Elem<DT>::store(static_cast<DT*>(p.dx) + b * p.gs0 + c * p.gs1 + i * p.gs2, acc);
+  }
+}
+
+template <typename InT, typename GT>
+static void launch_pool_bwd(const PoolBwdParams& p, bool dx_f32, hipStream_t s) {
+  const int64_t n1 = p.B * p.Nout * p.C, n2 = p.B * p.Nin * p.C;
+  auto grid = [](int64_t n) { return dim3(static_cast<unsigned>(std::min<int64_t>((n + 255) / 256, 256 * 64))); };
+  if (p.mode != FOVI_POOL_SUM && n1 > 0)
+    hipLaunchKernelGGL((knnpool_bwd_state_kernel<InT>), grid(n1), dim3(256), 0, s, p, n1);
+  if (n2 == 0) return;
+  if (dx_f32) hipLaunchKernelGGL((knnpool_bwd_dx_kernel<InT, GT, float>), grid(n2), dim3(256), 0, s, p, n2);
+  else hipLaunchKernelGGL((knnpool_bwd_dx_kernel<InT, GT, uint16_t>), grid(n2), dim3(256), 0, s, p, n2);
+}
+
+}  // namespace
+}  // namespace fovi
+
+extern "C" int fovi_knnpool_bwd(const fovi_knnpool_bwd_args* a, void* stream) {
+  using namespace fovi;
+  clear_error();
+  if (!a || !a->x || !a->nbr || !a->dy || !a->inv_ptr || !a->inv || !a->dx) {
+    set_error("fovi_knnpool_bwd: null pointer"); return 1;
+  }
+  if (a->mode < FOVI_POOL_MAX || a->mode > FOVI_POOL_GAUSSIAN) {
+    set_error("fovi_knnpool_bwd: bad mode %d", a->mode); return 1;
+  }
+  if (a->mode == FOVI_POOL_GAUSSIAN && !a->weights) {
+    set_error("fovi_knnpool_bwd: the Gaussian mode needs weights"); return 1;
+  }
+  if (a->mode != FOVI_POOL_SUM && !a->state) {
+    set_error("fovi_knnpool_bwd: this mode needs the state workspace"); return 1;
+  }
+  const auto okd = [](int d) { return d == FOVI_F32 || d == FOVI_BF16; };
+  if (!okd(a->x_dtype) || !okd(a->dy_dtype) || !okd(a->dx_dtype)) {
+    set_error("fovi_knnpool_bwd: x, dy and dx must be F32 or BF16"); return 1;
+  }
+  if (a->batch < 0 || a->channels < 0 || a->n_in < 0 || a->n_out < 0 || a->k < 1) {
+    set_error("fovi_knnpool_bwd: bad sizes (k must be >= 1)"); return 1;
+  }
+  PoolBwdParams p;
+  p.x = a->x; p.B = a->batch; p.C = a->channels; p.Nin = a->n_in; p.Nout = a->n_out; p.K = a->k;
+  p.xs0 = a->x_stride[0]; p.xs1 = a->x_stride[1]; p.xs2 = a->x_stride[2];
+  p.nbr = a->nbr; p.w = a->weights;
+  p.dy = a->dy; p.ds0 = a->dy_stride[0]; p.ds1 = a->dy_stride[1]; p.ds2 = a->dy_stride[2];
+  p.inv_ptr = a->inv_ptr; p.inv = a->inv; p.state = a->state;
+  p.dx = a->dx; p.gs0 = a->dx_stride[0]; p.gs1 = a->dx_stride[1]; p.gs2 = a->dx_stride[2];
+  p.mode = a->mode;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool dx32 = a->dx_dtype == FOVI_F32;
+  if (a->x_dtype == FOVI_F32) {
+    if (a->dy_dtype == FOVI_F32) launch_pool_bwd<float, float>(p, dx32, s);
+    else launch_pool_bwd<float, uint16_t>(p, dx32, s);
+  } else {
+    if (a->dy_dtype == FOVI_F32) launch_pool_bwd<uint16_t, float>(p, dx32, s);
+    else launch_pool_bwd<uint16_t, uint16_t>(p, dx32, s);
+  }
+  return check_launch("fovi_knnpool_bwd");
+}

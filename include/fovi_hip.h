@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 19
+#define FOVI_ABI_VERSION 20
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -300,6 +300,44 @@ typedef struct fovi_knnpool_args {
 } fovi_knnpool_args;
 
 int fovi_knnpool_fwd(const fovi_knnpool_args* args, void* stream);
+
+/*
+ * kNN pooling backward: the input gradient autograd forms through
+ * KNNPoolingLayer.forward (fovi/arch/knn.py:345-394):
+ *   dx[b, c, i] = sum over the (n, j) with nbr[n * k + j] == i of coef * dy[b, c, n],
+ * and 0 where x[b, c, i] is NaN (the reference's NaN masks carry no gradient):
+ *   FOVI_POOL_MAX:      coef = 1 at the first position j of the maximum of
+ *                       (b, c, n) (NaN read as -inf), as torch.max over a dim;
+ *   FOVI_POOL_AVG:      coef = 1 / (number of non-NaN features of (b, c, n));
+ *   FOVI_POOL_SUM:      coef = 1;
+ *   FOVI_POOL_GAUSSIAN: coef = weights[n * k + j] / (sum of the non-NaN
+ *                       features' weights + 1e-8).
+ * inv_ptr [n_in + 1] / inv: per input i, the entries n * k + j whose neighbour
+ * is i (pad tokens excluded), any order. state: fp32 workspace
+ * [batch * n_out * channels] (all modes but FOVI_POOL_SUM). fp32 sums, one
+ * rounding to dx_dtype. x, dy, dx: F32 or BF16, any element strides.
+ */
+typedef struct fovi_knnpool_bwd_args {
+  const void* x;
+  int32_t x_dtype;
+  int32_t mode;               /* fovi_pool_mode */
+  int64_t batch, channels, n_in;
+  int64_t x_stride[3];
+  const int32_t* nbr;         /* [n_out, k] */
+  const float* weights;       /* [n_out, k], FOVI_POOL_GAUSSIAN only */
+  int64_t n_out, k;
+  const void* dy;
+  int32_t dy_dtype;
+  int32_t dx_dtype;
+  int64_t dy_stride[3];
+  const int32_t* inv_ptr;     /* [n_in + 1] */
+  const int32_t* inv;
+  float* state;
+  void* dx;
+  int64_t dx_stride[3];
+} fovi_knnpool_bwd_args;
+
+int fovi_knnpool_bwd(const fovi_knnpool_bwd_args* args, void* stream);
 
 /*
  * kNN-conv backward, the two gather kernels around its two GEMMs (the

