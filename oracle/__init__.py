@@ -28,6 +28,12 @@ Pinning (what checks each function beyond retyping its formula):
     scalar loop of exp(-d^2 / 2 sigma^2) over min-max normalised distances,
     columns summing to 1 - 1e-8 relative, the largest weight at the nearest
     neighbour.
+  * Gradients (torch autograd through knnconv_forward and knnpool_forward,
+    in tests/test_knnconv_bwd.py and tests/test_knnpool.py): gradcheck
+    (float64 finite differences), the closed form dW = dy^T a with the
+    brute-force slot sums, the input gradient as the forward over the inverse
+    neighbour table, and a float64 loop form of the pooling gradient rules
+    (NaN features, pad tokens, the first maximum among ties).
   * policy_ref (the fixation draws): closed forms over one stream of
     uniforms (eval mode: only the centres, lo + (hi - lo) u; training: four
     draws per image, area, log-aspect, y, x), bit for bit; random_crop by
