@@ -188,8 +188,8 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         # bf16 weight gradient by fovi_knnconv_dw (False: the slot sums and a library GEMM)
         self.dw_fused = True
         # its work split: output points per pair segment, images per workgroup
-        self.dw_chunk = 4096
-        self.dw_images_per_group = 4
+        self.dw_chunk = 1 << 30
+        self.dw_images_per_group = 1
         # wide layers (bf16 c_in % 32 == 0 or e4m3 c_in % 64 == 0, c_out filling >= 3/4 of its
         # 256-channel tiles, tables within LDS): weights in MFMA-fragment order for the
         # 256 x 256-tile kernel (False: the row-packed kernels)
@@ -514,7 +514,7 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         sp = getattr(self, "_slot_pair_tables", None)
         if sp is None or sp[0].device != device:
             off, pairs = T.slot_pairs(self.slot_ptr.cpu(), self.nbr_sorted.cpu(), self.ref_coords.shape[0],
-                                      chunk=self.dw_chunk)
+                                      chunk=self.dw_chunk, step=64)
             sp = (off.to(device), pairs.to(device))
             self._slot_pair_tables = sp
         return sp

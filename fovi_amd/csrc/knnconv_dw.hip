@@ -3,18 +3,19 @@
 // dW[o, c * V + v] = sum over images b and over the (output n, input i) pairs whose
 // neighbour i sits in slot v of n of dy[b, n, o] * x[b, i, c]: for every slot a GEMM whose
 // reduction runs over that slot's pair list (the sum of a collision slot is linear, so its
-// pairs enter one by one). The pairs are cut into segments by output-point chunk; a
-// workgroup owns one segment (chunk q, slot v) for all images and one 256 x 256 (o, c) tile;
-// its eight waves, two per SIMD so one wave's memory waits overlap the other's MFMAs, hold
-// 128 x 64 fp32 blocks in AGPRs (8 blocks of v_mfma_f32_32x32x16_bf16). Workgroups are numbered slot-fastest and mapped XCD by XCD, so
-// the V workgroups of a chunk run together on one XCD, walk the images in step and read
-// each dy and x row of the chunk from that XCD's L2. Per step of 32 pairs the workgroup loads the 32 dy rows and the
-// 32 x rows (16-byte chunks, full rows per 32 lanes) into LDS in their natural [pair][channel]
-// layout, double-buffered one step ahead; both MFMA operands need the pair index contiguous
-// per lane, which the transposed LDS read ds_read_b64_tr_b16 delivers: within a 16-lane
-// group, lane j addresses four channels of pair row k0 + j/4 and lane i receives channel i of
-// pairs k0 .. k0 + 3. Rows are 576 bytes apart so those reads hit 64 distinct banks.
-// Per-split partial tiles go to a caller workspace; a second kernel sums the splits into the
+// pairs enter one by one). The pairs come in segments (one slot, one chunk of output
+// points); a workgroup owns one segment, a group of images and one 256 x 256 (o, c) tile.
+// Its eight waves, two per SIMD so one wave's memory waits overlap the other's MFMAs, hold
+// 128 x 64 fp32 blocks (8 blocks of v_mfma_f32_32x32x16_bf16). Workgroups are numbered
+// slot-fastest and mapped XCD by XCD, so the V workgroups of a chunk share one L2.
+//
+// Per step of 64 pairs the workgroup loads the 64 dy rows and the 64 x rows (16-byte
+// chunks, a full row per 32 lanes) into LDS in their natural [pair][channel] layout, double
+// buffered one step ahead. Both MFMA operands need the pair index contiguous per lane, which
+// the transposed LDS read ds_read_b64_tr_b16 delivers: within a 16-lane group, lane j
+// addresses four channels of pair row k0 + j/4 and lane i receives channel i of pairs
+// k0 .. k0 + 3. Rows are 576 bytes apart so those reads hit 64 distinct banks.
+// Per-workgroup partial tiles go to a caller workspace; a second kernel sums them into the
 // reference weight layout (column c * V + v), fp32.
 #include "common.h"
 
@@ -22,10 +23,11 @@ namespace fovi {
 namespace {
 
 constexpr int DW_T = 256;          // o and c tile
-constexpr int DW_K = 32;           // pairs per step
+constexpr int DW_K = 64;           // pairs per step
+constexpr int DW_R = DW_K / 16;    // rows per thread and operand in a step (512 threads, 32 per row)
 constexpr int DW_RS = 576;         // LDS bytes per pair row (256 bf16 + 64 bytes of bank skew)
 constexpr int DW_BUF = DW_K * DW_RS;            // one operand, one step
-constexpr int DW_LDS = 2 * 2 * DW_BUF;          // two operands, two steps: 73,728 bytes
+constexpr int DW_LDS = 2 * 2 * DW_BUF;          // two operands, two steps: 147,456 bytes
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
@@ -37,7 +39,7 @@ struct DwParams {
   const uint16_t* dy;
   int64_t ds0, ds2;                // dy[b * ds0 + n * ds2 + o]
   int64_t B, C, Cout, Nin, Nout, V;
-  const int32_t* pair_off;         // [NQ * V + 1], segment q * V + v; multiples of DW_K
+  const int32_t* pair_off;         // [NQ * V + 1], segment q * V + v
   const int32_t* pairs;            // (n, i) per pair; n < 0 pads
   int64_t NQ, ipg, S, tiles_o, tiles_c;
   float* part;                     // [S, NQ, V, tiles_o, tiles_c, 256, 256]
@@ -65,11 +67,12 @@ __global__ __launch_bounds__(512, 1) void knnconv_dw_kernel(DwParams p, int64_t 
   // eight waves, two per SIMD: wave (wm, wn) holds o rows wm*128 .. +127, c columns wn*64 .. +63
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, wm = wave >> 2, wn = wave & 3;
   const int64_t seg = q * p.V + v;
-  const int64_t P0 = p.pair_off[seg], steps_img = (p.pair_off[seg + 1] - P0) / DW_K;
+  const int64_t P0 = p.pair_off[seg], P1 = p.pair_off[seg + 1];
+  const int64_t steps_img = (P1 - P0 + DW_K - 1) / DW_K;     // the last step's tail reads as pads
   const int64_t b_beg = split * p.ipg;
   const int64_t steps = steps_img * (min(p.B, b_beg + p.ipg) - b_beg);
 
-  // load task: pair rows t/32 + 16r (r = 0, 1), 16-byte chunk g of the row; chunks past the
+  // load task: pair rows t/32 + 16r (r < DW_R), 16-byte chunk g of the row; chunks past the
   // channels load chunk 0 and pads load row 0, both masked to zero when stored
   const int g = t & 31, pr0 = t >> 5;
   const bool okc = c0 + 8 * g < p.C, oko = o0 + 8 * g < p.Cout;
@@ -83,13 +86,17 @@ __global__ __launch_bounds__(512, 1) void knnconv_dw_kernel(DwParams p, int64_t 
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  int2 pe[2];                                   // pair entries of the step being prefetched
-  u32x4v rd[2], rx[2];                          // rows of the step in flight
+  int2 pe[DW_R];                                // pair entries of the step being prefetched
+  u32x4v rd[DW_R], rx[DW_R];                    // rows of the step in flight
   uint32_t m = 0;                               // their live bits
   auto load_pairs = [&](int64_t st) __attribute__((always_inline)) {
     const int64_t base = P0 + DW_K * ((st < steps ? st : 0) % steps_img);
 #pragma unroll
-    for (int r = 0; r < 2; ++r) pe[r] = *reinterpret_cast<const int2*>(p.pairs + 2 * (base + pr0 + 16 * r));
+    for (int r = 0; r < DW_R; ++r) {
+      const int64_t pi = base + pr0 + 16 * r;
+      pe[r] = *reinterpret_cast<const int2*>(p.pairs + 2 * (pi < P1 ? pi : P1 - 1));
+      if (pi >= P1) pe[r].x = -1;                 // past the segment: a pad
+    }
   };
   auto load_rows = [&](int64_t st) __attribute__((always_inline)) {
     const bool on = st < steps;
@@ -98,13 +105,13 @@ __global__ __launch_bounds__(512, 1) void knnconv_dw_kernel(DwParams p, int64_t 
     const uint16_t* db = p.dy + b * p.ds0 + o0;
     m = 0;
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+    for (int r = 0; r < DW_R; ++r) {
       const bool live = on && pe[r].x >= 0;
       const uint32_t n = live ? pe[r].x : 0, i = live ? pe[r].y : 0;
       // 32-bit element offsets within the image (the host checks they fit)
       rd[r] = *reinterpret_cast<const u32x4v*>(db + (n * static_cast<uint32_t>(p.ds2) + 8u * gd));
       rx[r] = *reinterpret_cast<const u32x4v*>(xb + (i * static_cast<uint32_t>(p.xs2) + 8u * gc));
-      m |= static_cast<uint32_t>(live && oko) << r | static_cast<uint32_t>(live && okc) << (2 + r);
+      m |= static_cast<uint32_t>(live && oko) << r | static_cast<uint32_t>(live && okc) << (DW_R + r);
     }
   };
   auto store_rows = [&](int buf) __attribute__((always_inline)) {
@@ -112,9 +119,9 @@ __global__ __launch_bounds__(512, 1) void knnconv_dw_kernel(DwParams p, int64_t 
     uint8_t* bx = bd + DW_BUF;
     const u32x4v z = {0, 0, 0, 0};
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
+    for (int r = 0; r < DW_R; ++r) {
       *reinterpret_cast<u32x4v*>(bd + (pr0 + 16 * r) * DW_RS + 16 * g) = (m >> r & 1) ? rd[r] : z;
-      *reinterpret_cast<u32x4v*>(bx + (pr0 + 16 * r) * DW_RS + 16 * g) = (m >> (2 + r) & 1) ? rx[r] : z;
+      *reinterpret_cast<u32x4v*>(bx + (pr0 + 16 * r) * DW_RS + 16 * g) = (m >> (DW_R + r) & 1) ? rx[r] : z;
     }
   };
 
@@ -136,7 +143,7 @@ __global__ __launch_bounds__(512, 1) void knnconv_dw_kernel(DwParams p, int64_t 
       const uint8_t* bd = smem + (st & 1) * 2 * DW_BUF;
       const uint8_t* bx = bd + DW_BUF;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
+      for (int kb = 0; kb < DW_K / 16; ++kb) {
         bf16x8 af[4], bf[2];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {

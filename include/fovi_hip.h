@@ -442,8 +442,8 @@ int fovi_knn_select(const fovi_knn_select_args* args, void* stream);
  * layout. pairs holds (n, i) int32 pairs in n_chunks * n_ref segments,
  * segment q * n_ref + v at [pair_off[q * n_ref + v], pair_off[q * n_ref + v + 1])
  * holding slot v's pairs of one chunk of output points (the layer: 256
- * consecutive points per chunk, output order), each segment padded to a
- * multiple of 32 with (-1, -1). One workgroup takes one segment for
+ * consecutive points per chunk, output order), optionally padded with
+ * (-1, -1) entries (the layer pads to multiples of 64, the kernel's step). One workgroup takes one segment for
  * images_per_group consecutive images; the workspace holds its partial tile
  * (fovi_knnconv_dw_workspace_bytes). x and
  * dy bf16 channels-last (element strides [batch, channel, point] with channel
