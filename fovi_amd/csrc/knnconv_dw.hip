@@ -183,20 +183,22 @@ __global__ __launch_bounds__(512, 1) void knnconv_dw_kernel(DwParams p, int64_t 
       }
 }
 
-// dW[o, c * V + v] = sum over the chunks of the partial tiles (fp32)
+// dW[o, c * V + v] = sum over the (image group, chunk) partial tiles (fp32); one thread per
+// (v, o, c), consecutive threads along c (coalesced partial reads)
 __global__ __launch_bounds__(256) void knnconv_dw_reduce_kernel(DwParams p, float* dw) {
-  const int64_t total = p.Cout * p.C;
+  const int64_t total = p.V * p.Cout * p.C;
   for (int64_t q = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < total;
        q += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t o = q / p.C, c = q % p.C;
+    const int64_t c = q % p.C;
+    const int64_t o = (q / p.C) % p.Cout;
+    const int64_t v = q / (p.C * p.Cout);
     const int64_t tile = (o / DW_T) * p.tiles_c + c / DW_T;
     const int64_t in_tile = (o % DW_T) * DW_T + c % DW_T;
-    for (int64_t v = 0; v < p.V; ++v) {
-      float sum = 0.0f;
-      for (int64_t sq = 0; sq < p.S * p.NQ; ++sq)
-        sum += p.part[((sq * p.V + v) * p.tiles_o * p.tiles_c + tile) * (DW_T * DW_T) + in_tile];
-      dw[o * p.C * p.V + c * p.V + v] = sum;
-    }
+    const int64_t stride = p.V * p.tiles_o * p.tiles_c * (DW_T * DW_T);   // next (group, chunk)
+    const float* src = p.part + (v * p.tiles_o * p.tiles_c + tile) * (DW_T * DW_T) + in_tile;
+    float sum = 0.0f;
+    for (int64_t sq = 0; sq < p.S * p.NQ; ++sq) sum += src[sq * stride];
+    dw[o * p.C * p.V + c * p.V + v] = sum;
   }
 }
 
@@ -260,8 +262,8 @@ extern "C" int fovi_knnconv_dw(const fovi_knnconv_dw_args* a, void* stream) {
   hipLaunchKernelGGL(knnconv_dw_kernel, dim3(static_cast<unsigned>(padded)), dim3(512), DW_LDS, s, p, total,
                      padded);
   if (check_launch("fovi_knnconv_dw")) return 1;
-  const int64_t n = p.Cout * p.C;
-  hipLaunchKernelGGL(knnconv_dw_reduce_kernel, dim3(static_cast<unsigned>(std::min<int64_t>((n + 255) / 256, 4096))),
+  const int64_t n = p.V * p.Cout * p.C;
+  hipLaunchKernelGGL(knnconv_dw_reduce_kernel, dim3(static_cast<unsigned>(std::min<int64_t>((n + 255) / 256, 65536))),
                      dim3(256), 0, s, p, a->dw);
   return check_launch("fovi_knnconv_dw(reduce)");
 }
