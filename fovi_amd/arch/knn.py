@@ -525,7 +525,9 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         t = getattr(self, "_transposed_conv", None)
         if t is None or t.weight.device != device:
             t = _TransposedKnnConv(self, device)
-            self._transposed_conv = t
+            # kept outside the module tree: not a submodule, parameter or state-dict entry, and
+            # not found by code that walks modules() for kNN layers
+            object.__setattr__(self, "_transposed_conv", t)
         return t
 
     def _inverse_tables(self, device):

@@ -245,6 +245,9 @@ def test_layer_backward_vs_oracle(dt, res_in, res_out, k, c_in, c_out, bias, cha
     assert_close_rel(layer.weight.grad.cpu(), dw_ref, tol, "dW")
     if bias:
         assert_close_rel(layer.bias.grad.cpu(), db_ref, 1e-5 if dt == torch.float32 else 1e-2, "db")
+    # the backward's helper objects stay out of the module tree and the state dict
+    assert [n for n, _ in layer.named_modules()] == [""]
+    assert set(layer.state_dict()) <= {"weight", "bias"}
 
 
 @pytest.mark.gpu
