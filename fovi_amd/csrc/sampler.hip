@@ -187,6 +187,24 @@ __global__ __launch_bounds__(256) void sampler_kernel(SamplerParams p, int64_t b
   for (int64_t c = 0; c < p.C; ++c) Elem<OutT>::store(out + c * p.os1, t.value(src + c * p.is1));
 }
 
+// 16 bytes of consecutive samples from LDS to one unit-stride, 16-byte aligned store.
+template <typename T> struct Vec16Store;
+template <> struct Vec16Store<float> {
+  static __device__ __forceinline__ void store(float* p, const float* v) {
+    *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
+  }
+};
+template <> struct Vec16Store<uint16_t> {
+  static __device__ __forceinline__ void store(uint16_t* p, const float* v) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = static_cast<uint32_t>(f32_to_bf16_bits(v[2 * i])) |
+             (static_cast<uint32_t>(f32_to_bf16_bits(v[2 * i + 1])) << 16);
+    *reinterpret_cast<uint4*>(p) = uint4{w[0], w[1], w[2], w[3]};
+  }
+};
+
 // Blocked path for grids of whole rings (point = ring * ring_len + angle,
 // ring_len % 32 == 0, rings % 8 == 0) and at most 4 channels (NC, or 0 for a
 // run-time count <= 4). A block takes 8 rings x 32 angles of one view, each
@@ -194,13 +212,15 @@ __global__ __launch_bounds__(256) void sampler_kernel(SamplerParams p, int64_t b
 // neighbours in the image, so the lanes of one gather share cache lines
 // (about 1.75x fewer distinct lines per load than a wave along one ring). The
 // block's samples are staged in LDS and written back along the rings (64-byte
-// runs per channel plane). The grid is only a processing order: every point
+// runs per channel plane, 16 bytes per lane when the planes are unit-stride
+// and aligned). The grid is only a processing order: every point
 // of the view is sampled exactly once whatever the geometry, so results do
 // not depend on it. Block indices and in-image / in-view offsets are 32-bit
 // (the host checks the extents).
 template <typename InT, typename OutT, int MODE, int PAD, bool PAIRS, int NC>
 __global__ __launch_bounds__(256) void sampler_rings_kernel(SamplerParams p, uint32_t blocks_per_view,
-                                                            uint32_t total_blocks, uint32_t padded_blocks) {
+                                                            uint32_t total_blocks, uint32_t padded_blocks,
+                                                            int vec_out) {
   __shared__ float st[4][256];
   const uint32_t per = padded_blocks >> 3;
   const uint32_t lb = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
@@ -232,8 +252,22 @@ __global__ __launch_bounds__(256) void sampler_rings_kernel(SamplerParams p, uin
   for (int c = 0; c < 4; ++c)
     if (c < C) st[c][li] = val[c];
   __syncthreads();
-  const uint32_t pw = (ring0 + (tid >> 5)) * ring_len + ang0 + (tid & 31);
   OutT* out = static_cast<OutT*>(p.out) + static_cast<int64_t>(v) * p.os0;
+  if (vec_out) {
+    // 16-byte runs: a ring's 32 angles are contiguous in a channel plane, so the block's
+    // samples leave in 8 rings x C x (32 / VPL) pieces of VPL values, one store per lane
+    constexpr int VPL = 16 / sizeof(OutT);
+    constexpr int PPR = 32 / VPL;                   // pieces per ring
+    if (tid < 8 * PPR * C) {
+      const int c = tid / (8 * PPR), r = (tid / PPR) % 8, part = tid % PPR;
+      const float* sv = &st[c][r * 32 + part * VPL];
+      const int32_t o = static_cast<int32_t>((ring0 + r) * ring_len + ang0 + part * VPL) +
+                        c * static_cast<int32_t>(p.os1);
+      Vec16Store<OutT>::store(out + o, sv);
+    }
+    return;
+  }
+  const uint32_t pw = (ring0 + (tid >> 5)) * ring_len + ang0 + (tid & 31);
   const int32_t o = static_cast<int32_t>(pw) * static_cast<int32_t>(p.os2);
 #pragma unroll
   for (int c = 0; c < 4; ++c)
@@ -254,15 +288,19 @@ static bool rings_path(const SamplerParams& p, int64_t n_views) {
 template <typename InT, typename OutT, int MODE, int PAD, bool PAIRS>
 static void launch_rings(const SamplerParams& p, uint32_t bpv, uint32_t total, uint32_t padded, hipStream_t s) {
   dim3 grid(padded);
+  // unit-stride channel planes with 16-byte aligned plane and view starts: whole 16-byte runs
+  constexpr int64_t VPL = 16 / sizeof(OutT);
+  const int vec_out = p.os2 == 1 && p.os1 % VPL == 0 && p.os0 % VPL == 0 &&
+                      reinterpret_cast<uintptr_t>(p.out) % 16 == 0;
   if (p.C == 3)
     hipLaunchKernelGGL((sampler_rings_kernel<InT, OutT, MODE, PAD, PAIRS, 3>), grid, dim3(256), 0, s, p, bpv, total,
-                       padded);
+                       padded, vec_out);
   else if (p.C == 1)
     hipLaunchKernelGGL((sampler_rings_kernel<InT, OutT, MODE, PAD, PAIRS, 1>), grid, dim3(256), 0, s, p, bpv, total,
-                       padded);
+                       padded, vec_out);
   else
     hipLaunchKernelGGL((sampler_rings_kernel<InT, OutT, MODE, PAD, PAIRS, 0>), grid, dim3(256), 0, s, p, bpv, total,
-                       padded);
+                       padded, vec_out);
 }
 
 template <typename InT, typename OutT, int MODE, int PAD>
