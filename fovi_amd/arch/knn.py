@@ -56,13 +56,26 @@ class KNNBaseLayer:
     """Neighbour search shared by kNN layers (reference ``knn.py:14-224``)."""
 
     def _compute_knns(self, batch_size=None):
+        """(indices ``[k, N_out]``, distances ``[k, N_out]``) of the k nearest inputs per output
+        (reference ``knn.py:23-152``); indices >= N_in are points of the input's pad ring.
+
+        Log-polar sensors search the wrapped 2-D log-polar lattice without pads; isotropic
+        sensors search the 3-D cortical manifold over points and pad ring
+        (``sample_cortex=True``); ``sample_cortex=False`` searches the visual field over
+        points and pad ring. Output batches are sized as the reference sizes them (pads
+        counted, at most 5e8 pairs per batch)."""
         if self.sample_cortex == "geodesic":
             raise NotImplementedError("geodesic neighbourhoods need pygeodesic, which is not available")
-        if not self.sample_cortex:
-            raise NotImplementedError("visual-field (sample_cortex=False) neighbourhoods need the "
-                                      "isotropic pad ring, which is not built")
         in_c, out_c = self.in_coords, self.out_coords
-        self.sample_coords_cart = torch.cat([in_c.cartesian.cpu(), in_c.cartesian_pad_coords.cpu()], 0)
+        pads = in_c.cartesian_pad_coords.cpu()
+        n_out = out_c.shape[0]
+        if batch_size is None:
+            batch_size = T.default_batch(in_c.shape[0] + pads.shape[0], n_out)
+        batch_size = min(batch_size, n_out)
+        self.sample_coords_cart = torch.cat([in_c.cartesian.cpu(), pads], 0)
+        if not self.sample_cortex:
+            self.sample_coords = self.sample_coords_cart
+            return T.knn_euclidean(self.sample_coords, out_c.cartesian.cpu(), self._k, batch_size)
         if in_c.style in ("image", "logpolar"):
             assert out_c.style == in_c.style
             if self._gpu_tables(in_c.shape[0]):
@@ -72,7 +85,10 @@ class KNNBaseLayer:
                 idx, dist, src = T.knn_logpolar(in_c.cortical.cpu(), out_c.cortical.cpu(), self._k, batch_size)
             self.sample_coords = src
             return idx, dist
-        raise NotImplementedError(f"style {in_c.style!r}: only log-polar neighbourhoods are built")
+        if in_c.cortical is None:
+            raise ValueError(f"style {in_c.style!r} has no cortical coordinates: use sample_cortex=False")
+        self.sample_coords = torch.cat([in_c.cortical.cpu(), in_c.cortical_pad_coords.cpu()], 0)
+        return T.knn_euclidean(self.sample_coords, out_c.cortical.cpu(), self._k, batch_size)
 
     def _gpu_tables(self, n_in):
         """Whether the neighbour search runs on the GPU (``knn_tables.knn_logpolar_device``, the
@@ -214,6 +230,8 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         self.ref_coords = ref.to(self.device, dtype=self.in_coords.dtype)
 
     def compute_local_rf_slots(self, knn_indices):
+        if not self.sample_cortex:
+            return T.visual_rf_slots(knn_indices, self.sample_coords, self.ref_coords.cpu())
         return T.local_rf_slots(knn_indices, self.sample_coords, self.sample_coords_cart,
                                 self.out_coords.cortical.cpu(), self.out_coords.cartesian.cpu(),
                                 self.ref_coords.cpu())

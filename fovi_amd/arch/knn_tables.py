@@ -46,10 +46,15 @@ __all__ = [
 _PAIR_BUDGET = 500_000_000  # distance-matrix elements per chunk (reference knn.py:43-49)
 
 
+def default_batch(n_in, n_out):
+    """Outputs per distance batch: at most ``_PAIR_BUDGET`` input-output pairs (reference
+    ``knn.py:43-52``; ``n_in`` counts the pad ring)."""
+    return int(np.minimum(n_out / np.maximum(0.0001, n_in * n_out / _PAIR_BUDGET), n_out))
+
+
 def _chunk(n_in, n_out, batch_size):
     if batch_size is None:
-        pairs = n_in * n_out
-        batch_size = int(np.minimum(n_out / np.maximum(0.0001, pairs / _PAIR_BUDGET), n_out))
+        batch_size = default_batch(n_in, n_out)
     return max(1, min(batch_size, n_out))
 
 
@@ -154,7 +159,9 @@ def knn_logpolar(in_cortical, out_cortical, k, batch_size=None):
 
 
 def knn_euclidean(in_pts, out_pts, k, batch_size=None):
-    """k nearest inputs per output by plain ``cdist`` (non-log-polar styles)."""
+    """k nearest inputs per output by plain Euclidean ``cdist`` over batches of outputs, then
+    ``topk`` (reference ``knn.py:119-152``: isotropic cortical manifold or visual field, pad
+    ring included in ``in_pts``)."""
     n_out = out_pts.shape[0]
     idx = torch.zeros((k, n_out), dtype=torch.long)
     dist = torch.zeros((k, n_out), dtype=torch.float32)
@@ -201,6 +208,19 @@ def local_rf_slots(knn_idx, src_cortical, src_cart, out_cortical, out_cart, ref_
     hi = local.max(dim=0, keepdim=True)[0]
     local = 2 * (local - lo) / (hi - lo + 1e-6) - 1
     nearest = torch.argmin(torch.cdist(local, ref_coords), dim=2)   # [k, N_out]
+    return nearest.t().contiguous()
+
+
+def visual_rf_slots(knn_idx, src_cart, ref_coords):
+    """Ref slot id ``[N_out, k]`` (int64) of every neighbour for visual-field neighbourhoods
+    (``sample_cortex=False``): the neighbours' visual (x, y), min-max normalised to [-1, 1]
+    per output, nearest ref point (reference ``knn.py:620-647`` without the cortical
+    re-projection)."""
+    local = src_cart[knn_idx]                         # [k, N_out, 2]
+    lo = local.min(dim=0, keepdim=True)[0]
+    hi = local.max(dim=0, keepdim=True)[0]
+    local = 2 * (local - lo) / (hi - lo + 1e-6) - 1
+    nearest = torch.argmin(torch.cdist(local, ref_coords), dim=2)
     return nearest.t().contiguous()
 
 

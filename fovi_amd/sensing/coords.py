@@ -16,9 +16,16 @@ bit, so each step keeps the reference's dtype chain:
   terms evaluated on a 0-dim fp32 tensor (``coords.py:46-53``), then per-column
   min-max normalisation (``fovi/utils/__init__.py:126-167``).
 
-Only the 'logpolar' and 'uniform' styles are built (every benchmark
-configuration is log-polar). 'isotropic' needs the 3-D cortical manifold and
-raises ``NotImplementedError``.
+The 'isotropic' style (the reference's default) keeps the same radii with
+a per-ring angle count that makes neighbouring angles as far apart as
+neighbouring rings (``coords.py:345-361``), maps the points onto the 3-D
+cortical sensor manifold (``fovi/sensing/manifold.py:14-215,347-375``: the
+cortical height is the integral of ``sqrt(M(r)^2 - (d rho/dr)^2)``, a
+trapezoid rule on a 1e-4-degree mesh interpolated linearly) and adds the pad
+ring beyond the last ring (``coords.py:68-87``). Both keep the reference's
+numpy dtype chain: the points enter the manifold in fp64, the pad ring in
+fp32, one point at a time in numpy scalars. 'isotropic_fixn' (random
+per-ring angle removal) is not built.
 """
 from __future__ import annotations
 
@@ -37,6 +44,7 @@ __all__ = [
 ]
 
 _LOGPOLAR_STYLES = ("logpolar", "logpolar_as_grid")
+_ISOTROPIC_STYLES = ("isotropic",)
 _UNIFORM_STYLES = ("uniform", "uniform_as_grid")
 
 
@@ -47,7 +55,7 @@ def logpolar_ring_radii(fov, cmf_a, res):
     ``[log a, log(fov/2 + a) + dw]`` with ``res + 1`` samples (the extra sample
     is dropped), mapped back with ``r = exp(w) - a`` and divided by ``fov/2``
     (reference ``coords.py:322-370``; the isotropic angle counts computed there
-    are discarded by the log-polar style and are not evaluated here).
+    are ``isotropic_ring_counts``).
     """
     res = int(res)
     r_max = fov / 2
@@ -59,23 +67,137 @@ def logpolar_ring_radii(fov, cmf_a, res):
     return 1 * (r[:-1] / (fov / 2))
 
 
-def _logpolar_points(fov, cmf_a, res, max_val):
-    """fp64 cartesian and polar point sets, ring-major (index = ring*res + angle)."""
-    radii = logpolar_ring_radii(fov, cmf_a, res) * max_val
-    angles = np.linspace(0, 2 * np.pi, res, endpoint=False)
-    n = res * res
+def isotropic_ring_counts(fov, cmf_a, res):
+    """Angles per ring of the isotropic sampling (``res`` ints): 1 at the centre, then the
+    number of steps of the mean neighbouring-ring spacing that fit in the ring's
+    circumference, counted by the reference's own ``torch.arange`` call on the fp32 radii
+    (reference ``coords.py:345-361``)."""
+    res = int(res)
+    r_max = fov / 2
+    w_lo = np.log(cmf_a)
+    w_hi = np.log(r_max + cmf_a)
+    dw = (w_hi - w_lo) / (res - 1)
+    w = torch.linspace(w_lo, w_hi + dw, steps=res + 1)
+    r = torch.exp(w) - cmf_a
+    counts = [1]
+    for i in range(1, res):
+        spacing = ((r[i] - r[i - 1]) + (r[i + 1] - r[i])) / 2
+        counts.append(len(torch.arange(0, 2 * torch.pi * r[i], spacing)))
+    return counts
+
+
+def _ring_points(radii, counts):
+    """fp64 cartesian and polar point sets, ring-major, ``counts[i]`` angles on ring i."""
+    n = int(sum(counts))
     cart = np.empty((n, 2), dtype=np.float64)
     polar = np.empty((n, 2), dtype=np.float64)
-    cos_a = [math.cos(a) for a in angles]
-    sin_a = [math.sin(a) for a in angles]
-    for i, r32 in enumerate(radii.tolist()):
+    at = 0
+    for r32, cnt in zip(radii.tolist(), counts):
         # r32 is the exact fp32 radius widened to a Python float (IEEE double)
-        row = slice(i * res, (i + 1) * res)
-        cart[row, 0] = [r32 * c for c in cos_a]
-        cart[row, 1] = [r32 * s for s in sin_a]
+        angles = np.linspace(0, 2 * np.pi, cnt, endpoint=False)
+        row = slice(at, at + cnt)
+        cart[row, 0] = [r32 * math.cos(a) for a in angles]
+        cart[row, 1] = [r32 * math.sin(a) for a in angles]
         polar[row, 0] = r32
         polar[row, 1] = angles
+        at += cnt
     return torch.from_numpy(cart), torch.from_numpy(polar)
+
+
+def _logpolar_points(fov, cmf_a, res, max_val):
+    """fp64 cartesian and polar point sets, ring-major (index = ring*res + angle)."""
+    return _ring_points(logpolar_ring_radii(fov, cmf_a, res) * max_val, [res] * res)
+
+
+def _isotropic_points(fov, cmf_a, res, max_val):
+    return _ring_points(logpolar_ring_radii(fov, cmf_a, res) * max_val, isotropic_ring_counts(fov, cmf_a, res))
+
+
+def _isotropic_plotting(cart64, fov, cmf_a):
+    """Complex-log plotting coordinates with the hemifields pulled apart (reference
+    ``coords.py:281-294``)."""
+    fov_xy = cart64 * (fov / 2)
+    z = torch.log(torch.abs(fov_xy[:, 0]) + 1j * fov_xy[:, 1] + cmf_a)
+    plot = torch.stack([z.real, -z.imag], 1)
+    edge = np.log(fov / 2 + cmf_a)
+    half_sd = torch.std(plot[:, 0]) * .5
+    left = cart64[:, 0] < 0
+    plot[left, 0] = half_sd + edge - plot[left, 0]
+    plot[~left, 0] = plot[~left, 0] - (half_sd + edge)
+    return plot
+
+
+def _pad_ring(polar, dtype, padding_distance=0.5):
+    """Points on rings beyond the last ring, spaced by the outermost ring gap in radius and in
+    angle, out to ``padding_distance`` (reference ``coords.py:68-87``).
+
+    ``torch.arange`` with a 0-d tensor step returns the default dtype, so radii and angles are
+    fp32 whatever ``polar``'s dtype, and the reference's ``np.cos(angle)`` of a 0-d fp32
+    tensor is numpy's fp32 cosine; each coordinate is that fp32 cos/sin times the fp32 radius,
+    then the set is rounded to ``dtype``."""
+    radii = torch.sort(torch.unique(polar[:, 0])).values
+    gap = radii[-1] - radii[-2]
+    start = radii[-1] + gap
+    angles = torch.arange(0, 2 * np.pi, gap)
+    rings = torch.arange(start, start + padding_distance, gap)
+    assert angles.dtype == rings.dtype == torch.float32
+    cos_a = torch.from_numpy(np.array([np.cos(a) for a in angles.numpy()], dtype=np.float32))
+    sin_a = torch.from_numpy(np.array([np.sin(a) for a in angles.numpy()], dtype=np.float32))
+    ring_t = rings.unsqueeze(1)
+    xy = torch.stack([ring_t * cos_a, ring_t * sin_a], dim=2)
+    return xy.reshape(-1, 2).to(dtype=dtype)
+
+
+class _CorticalManifold:
+    """Cortical height of the 3-D sensor manifold as a function of eccentricity (degrees),
+    for M(r) = k / (r + a) (reference ``manifold.py:32-48,117-137``): the running trapezoid
+    integral of ``sqrt(M^2 - (d rho/dr)^2)`` over ``np.arange(0, 2 fov, 1e-4)``,
+    interpolated linearly."""
+
+    _cache = {}
+
+    def __init__(self, cmf_a, fov, k=10):
+        from scipy.integrate import cumulative_trapezoid
+        from scipy.interpolate import interp1d
+        self.cmf_a, self.fov, self.k = cmf_a, fov, k
+        mesh = np.arange(0, 2 * fov, 0.0001)
+        integrand = (self.mag(mesh) ** 2 - self.drho_dr(mesh) ** 2) ** 0.5
+        self.height = interp1d(mesh, cumulative_trapezoid(integrand, x=mesh, initial=0), kind="linear")
+
+    @classmethod
+    def get(cls, cmf_a, fov, k=10):
+        key = (cmf_a, fov, k)
+        if key not in cls._cache:
+            cls._cache[key] = cls(cmf_a, fov, k)
+        return cls._cache[key]
+
+    def mag(self, r):
+        return self.k / (self.cmf_a + r)
+
+    def rho(self, r):
+        return self.mag(r) * np.sin(np.deg2rad(r)) * (180 / np.pi)
+
+    def drho_dr(self, r):
+        dmag = -self.k * ((self.cmf_a + r) ** (-2))
+        return dmag * np.sin(np.deg2rad(r)) * (180 / np.pi) + self.mag(r) * np.cos(np.deg2rad(r))
+
+    def to_cortex(self, xy):
+        """Visual (x, y) in degrees -> cortical cartesian (x_c, y_c, z), one point at a time in
+        numpy scalars of ``xy``'s dtype, z in fp64 (reference ``manifold.py:139-171,202-211``)."""
+        out = []
+        for x, y in xy:
+            r = np.sqrt(x ** 2 + y ** 2)
+            theta = np.arctan2(y, x)
+            rho = self.rho(r)
+            out.append((rho * np.cos(theta), rho * np.sin(theta), self.height(r)))
+        return np.array(out)
+
+
+def sensor_manifold_coords(cartesian, cmf_a, fov, k=10):
+    """Cortical cartesian coordinates ``[n, 3]`` (fp64 tensor) of normalised visual points
+    ``cartesian`` (numpy, [-1, 1]) on the 3-D sensor manifold (reference
+    ``manifold.py:347-375``)."""
+    return torch.tensor(_CorticalManifold.get(cmf_a, fov, k).to_cortex(cartesian * (fov / 2)))
 
 
 def _minmax_columns(x):
@@ -101,12 +223,12 @@ def _uniform_points(res, max_val):
     return cart, polar
 
 
-def num_sampling_coords(fov, cmf_a, res, style="logpolar", device="cpu"):
+def num_sampling_coords(fov, cmf_a, res, style="isotropic", device="cpu"):
     """Number of sensor points for ``res`` (reference ``coords.py:567-586``)."""
     if style in _LOGPOLAR_STYLES + _UNIFORM_STYLES + ("isotropic_fixn",):
         return res ** 2
     if style == "isotropic":
-        raise NotImplementedError("isotropic point counts need the cortical manifold")
+        return int(sum(isotropic_ring_counts(fov, cmf_a, res)))
     raise ValueError(f"Style {style} not recognized")
 
 
@@ -161,14 +283,17 @@ def xy_to_colrow(xy):
 class SamplingCoords:
     """Sensor point set with cartesian, polar and cortical coordinates.
 
-    Constructor and attributes follow the reference ``SamplingCoords``
-    (``fovi/sensing/coords.py:10-201``): ``cartesian [N,2]`` in [-1,1],
-    ``polar [N,2]`` (radius, angle), ``cortical [N,2]`` normalised to [0,1]
-    per column, ``shape``, ``resolution``, ``style``. Points are ring-major:
-    index ``ring * res + angle``.
+    Constructor (default style 'isotropic') and attributes follow the reference
+    ``SamplingCoords`` (``fovi/sensing/coords.py:10-201``): ``cartesian [N,2]`` in
+    [-1,1], ``polar [N,2]`` (radius, angle), ``cortical`` (log-polar: ``[N,2]``
+    normalised to [0,1] per column; isotropic: ``[N,3]`` on the cortical manifold;
+    uniform: None), ``plotting``, ``cartesian_pad_coords [P,2]`` (the pad ring),
+    ``cortical_pad_coords [P,3]`` (isotropic), ``shape``, ``resolution``, ``style``.
+    Points are ring-major: log-polar index ``ring * res + angle``; isotropic rings
+    hold ``isotropic_ring_counts`` points each.
     """
 
-    def __init__(self, fov, cmf_a, res, device="cpu", style="logpolar", dtype=torch.float, max_val=1):
+    def __init__(self, fov, cmf_a, res, device="cpu", style="isotropic", dtype=torch.float, max_val=1):
         if isinstance(res, float) and res.is_integer():
             res = int(res)
         self.fov = fov
@@ -178,26 +303,38 @@ class SamplingCoords:
         self.style = style
         self.dtype = dtype
         self.max_val = max_val
+        plotting = None
         if res == 1:
             cart = torch.zeros(1, 2, dtype=torch.float64)
             polar = torch.zeros(1, 2, dtype=torch.float64)
             cortical = torch.zeros(1, 3, dtype=torch.float64)
         elif style in _LOGPOLAR_STYLES:
             cart, polar = _logpolar_points(fov, cmf_a, res, max_val)
+            pad = _pad_ring(polar, dtype)
             cortical = _logpolar_cortical(cart, polar, fov, cmf_a)
         elif style in _UNIFORM_STYLES:
             cart, polar = _uniform_points(res, max_val)
+            pad = _pad_ring(polar, dtype)
             cortical = None
+        elif style in _ISOTROPIC_STYLES:
+            cart, polar = _isotropic_points(fov, cmf_a, res, max_val)
+            plotting = _isotropic_plotting(cart, fov, cmf_a)
+            pad = _pad_ring(polar, dtype)
+            cortical = sensor_manifold_coords(cart.numpy(), cmf_a, fov)
+            self.cortical_pad_coords = sensor_manifold_coords(pad.numpy(), cmf_a, fov).to(
+                device=device, dtype=dtype)
         else:
-            raise NotImplementedError(
-                f"style {style!r}: only 'logpolar' and 'uniform' sensor geometries are built")
+            raise NotImplementedError(f"style {style!r}: 'logpolar', 'uniform' and 'isotropic' are built")
         self.cartesian = cart.to(device=device, dtype=dtype)
         self.polar = polar.to(device=device, dtype=dtype)
         self.cortical = None if cortical is None else cortical.to(device=device, dtype=dtype)
-        self.plotting = self.cortical if self.cortical is not None else self.cartesian
-        # log-polar styles add no pad points (the reference's pad ring is only
-        # reachable through the isotropic/cartesian distance paths)
-        self.cartesian_pad_coords = torch.zeros(0, 2, dtype=dtype, device=device)
+        if plotting is not None:
+            self.plotting = plotting.to(device=device, dtype=dtype)
+        else:
+            self.plotting = self.cortical if self.cortical is not None else self.cartesian
+        # the pad ring beyond the outermost ring (none for a one-point sensor); only the
+        # isotropic manifold and the visual-field neighbour searches reach it
+        self.cartesian_pad_coords = (pad if res != 1 else torch.zeros(0, 2, dtype=dtype)).to(device=device)
         self.shape = self.cartesian.shape
 
     def get_strided_coords(self, stride, auto_match_cart_resources=0, in_cart_res=None,

@@ -4,7 +4,8 @@ assignments computed by the reference itself (nblauch/fovi, read from
 
 Run only in the build container, where the reference checkout exists:
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py               # tables.npz (log-polar layers)
+    python tests/golden/make_golden.py --isotropic   # isotropic.npz (isotropic sensor)
 
 The reference is loaded by file path under a synthetic package name; the two
 modules it imports that are absent here and unused on this path (trimesh in
@@ -26,7 +27,7 @@ import torch
 REF = "/root/reference/fovi"
 OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tables.npz")
 
-# name -> (res_in, res_out, k, ref_frame_side_length); fov 16, cmf_a 2.78 (SURVEY configs)
+# name -> (res_in, res_out, k, ref_frame_side_length); fov 16, cmf_a 2.78 (the benchmark configs)
 CONFIGS = {
     "c1": (64, 64, 9, None),
     "c2_l1": (64, 32, 49, None),
@@ -105,5 +106,71 @@ def main():
     print(f"wrote {OUT} ({os.path.getsize(OUT) / 1024:.0f} KiB)")
 
 
+# isotropic sensor (the reference's default style): point sets, pad rings and layers
+ISO_RES = (8, 16, 24)
+ISO_LAYERS = {"iso_16_8": (16, 8, 9), "iso_24_12": (24, 12, 25), "iso_16_16": (16, 16, 9)}
+# visual-field neighbourhoods (sample_cortex=False): name -> (style, res_in, res_out, k)
+VIS_LAYERS = {"vis_iso_16_8": ("isotropic", 16, 8, 9), "vis_lp_16_8": ("logpolar", 16, 8, 9)}
+# pad rings of the other styles: name -> (style, res)
+PAD_RINGS = {"pad_logpolar16": ("logpolar", 16), "pad_uniform8": ("uniform", 8)}
+ISO_OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "isotropic.npz")
+
+
+def main_isotropic():
+    """Writes tests/golden/isotropic.npz: the 'isotropic' SamplingCoords attributes (its 3-D
+    cortical manifold, fovi/sensing/manifold.py:14-215,347-375, and pad ring, coords.py:68-87),
+    the neighbour / slot tables of isotropic layers (the 3-D cdist branch of knn.py:101-152
+    with pad tokens, and knn.py:599-647), of visual-field layers (sample_cortex=False,
+    knn.py:117-119,620-647) and the pad rings of the log-polar and uniform styles."""
+    coords_mod, knn_mod = load_reference()
+    out = {"torch_version": np.array(torch.__version__), "numpy_version": np.array(np.__version__)}
+    for res in ISO_RES:
+        c = coords_mod.SamplingCoords(16, 2.78, res, device="cpu", style="isotropic")
+        for key in ("cartesian", "polar", "plotting", "cortical", "cartesian_pad_coords", "cortical_pad_coords"):
+            out[f"res{res}__{key}"] = getattr(c, key).numpy()
+        print(f"isotropic res {res}: {c.cartesian.shape[0]} points, {c.cartesian_pad_coords.shape[0]} pad points",
+              flush=True)
+    for name, (r_in, r_out, k) in ISO_LAYERS.items():
+        cin = coords_mod.SamplingCoords(16, 2.78, r_in, device="cpu", style="isotropic")
+        cout = coords_mod.SamplingCoords(16, 2.78, r_out, device="cpu", style="isotropic")
+        layer = knn_mod.KNNConvLayer(1, 1, k, cin, cout, device="cpu")
+        rf = layer.local_rf.numpy()
+        assert np.all(rf.sum(2) == 1)
+        out[f"{name}__idx"] = layer.knn_indices.numpy().astype(np.int32)
+        out[f"{name}__dist"] = layer.knn_distances.numpy()
+        out[f"{name}__slots"] = rf.argmax(2).astype(np.uint8)
+        print(f"{name}: k={k} n_in={cin.cartesian.shape[0]} n_out={cout.cartesian.shape[0]} "
+              f"pads used {int((layer.knn_indices >= cin.cartesian.shape[0]).sum())}", flush=True)
+    for name, (style, r_in, r_out, k) in VIS_LAYERS.items():
+        cin = coords_mod.SamplingCoords(16, 2.78, r_in, device="cpu", style=style)
+        cout = coords_mod.SamplingCoords(16, 2.78, r_out, device="cpu", style=style)
+        layer = knn_mod.KNNConvLayer(1, 1, k, cin, cout, device="cpu", sample_cortex=False)
+        rf = layer.local_rf.numpy()
+        assert np.all(rf.sum(2) == 1)
+        out[f"{name}__idx"] = layer.knn_indices.numpy().astype(np.int32)
+        out[f"{name}__dist"] = layer.knn_distances.numpy()
+        out[f"{name}__slots"] = rf.argmax(2).astype(np.uint8)
+        print(f"{name}: pads used {int((layer.knn_indices >= cin.cartesian.shape[0]).sum())}", flush=True)
+    for name, (style, res) in PAD_RINGS.items():
+        out[name] = coords_mod.SamplingCoords(16, 2.78, res, device="cpu", style=style).cartesian_pad_coords.numpy()
+    # a scaled sensor (max_val below 1) and the auto-matched strided pair of the default style
+    c = coords_mod.SamplingCoords(16, 2.78, 16, device="cpu", style="isotropic", max_val=0.9)
+    for key in ("cartesian", "plotting", "cortical", "cartesian_pad_coords", "cortical_pad_coords"):
+        out[f"scaled16__{key}"] = getattr(c, key).numpy()
+    cin, cout, out_cart_res = knn_mod.get_in_out_coords(None, 16, 2.78, 2, style="isotropic", in_cart_res=32,
+                                                        device="cpu", max_out_coord_val="auto")
+    out["auto__resolutions"] = np.array([cin.resolution, cout.resolution, out_cart_res])
+    for key in ("cartesian", "cortical"):
+        out[f"auto__in_{key}"] = getattr(cin, key).numpy()
+        out[f"auto__out_{key}"] = getattr(cout, key).numpy()
+    print(f"auto-matched isotropic pair: res {cin.resolution} -> {cout.resolution}, "
+          f"{cin.cartesian.shape[0]} -> {cout.cartesian.shape[0]} points", flush=True)
+    np.savez_compressed(ISO_OUT, **out)
+    print(f"wrote {ISO_OUT} ({os.path.getsize(ISO_OUT) / 1024:.0f} KiB)")
+
+
 if __name__ == "__main__":
-    main()
+    if "--isotropic" in sys.argv:
+        main_isotropic()
+    else:
+        main()
