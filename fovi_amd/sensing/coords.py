@@ -24,8 +24,10 @@ cortical height is the integral of ``sqrt(M(r)^2 - (d rho/dr)^2)``, a
 trapezoid rule on a 1e-4-degree mesh interpolated linearly) and adds the pad
 ring beyond the last ring (``coords.py:68-87``). Both keep the reference's
 numpy dtype chain: the points enter the manifold in fp64, the pad ring in
-fp32, one point at a time in numpy scalars. 'isotropic_fixn' (random
-per-ring angle removal) is not built.
+fp32, one point at a time in numpy scalars. 'isotropic_fixn' fixes the point
+count to ``res**2`` by adding or removing single angles on rings drawn with
+numpy's global RNG, by the same calls in the same order (``coords.py:224-258``),
+so a seeded run builds the reference's sensor.
 """
 from __future__ import annotations
 
@@ -44,7 +46,7 @@ __all__ = [
 ]
 
 _LOGPOLAR_STYLES = ("logpolar", "logpolar_as_grid")
-_ISOTROPIC_STYLES = ("isotropic",)
+_ISOTROPIC_STYLES = ("isotropic", "isotropic_fixn")
 _UNIFORM_STYLES = ("uniform", "uniform_as_grid")
 
 
@@ -109,8 +111,41 @@ def _logpolar_points(fov, cmf_a, res, max_val):
     return _ring_points(logpolar_ring_radii(fov, cmf_a, res) * max_val, [res] * res)
 
 
-def _isotropic_points(fov, cmf_a, res, max_val):
-    return _ring_points(logpolar_ring_radii(fov, cmf_a, res) * max_val, isotropic_ring_counts(fov, cmf_a, res))
+def fixn_ring_counts(fov, cmf_a, n_points):
+    """(rings, angles per ring) of an isotropic sensor with exactly ``n_points`` points: the
+    resolution whose count is nearest, then one angle added to or removed from rings drawn
+    by ``np.random.choice`` over the outer 80% of rings (global numpy RNG, the reference's
+    calls and order, ``coords.py:224-258``); a ring down to one angle passes its removal
+    outwards."""
+    res, _ = find_desired_res(fov, cmf_a, n_points, style="isotropic", quiet=True)
+    counts = isotropic_ring_counts(fov, cmf_a, res)
+    diff = sum(counts) - n_points
+    n_rad = len(counts)
+    add = -1 if diff > 0 else 1
+    if diff != 0:
+        rad_idx = []
+        rad_min = int(0.2 * n_rad)
+        while len(rad_idx) < abs(diff):
+            this_diff = min(abs(diff) - len(rad_idx), n_rad - 1)
+            draw = np.random.choice(np.arange(rad_min, n_rad), size=min(this_diff, n_rad - rad_min), replace=False)
+            rad_idx = np.concatenate([rad_idx, draw])
+        rad_idx = rad_idx.astype(int)
+        for ii in range(abs(diff)):
+            j = rad_idx[ii]
+            while counts[j] <= 1 and add < 0:
+                j += 1
+            counts[j] += add
+        if min(counts) <= 0:
+            raise AssertionError("some radii have no angles")
+    return res, counts
+
+
+def _isotropic_points(fov, cmf_a, res, max_val, fixn=False):
+    if fixn:
+        rings, counts = fixn_ring_counts(fov, cmf_a, res ** 2)
+    else:
+        rings, counts = res, isotropic_ring_counts(fov, cmf_a, res)
+    return _ring_points(logpolar_ring_radii(fov, cmf_a, rings) * max_val, counts)
 
 
 def _isotropic_plotting(cart64, fov, cmf_a):
@@ -317,14 +352,14 @@ class SamplingCoords:
             pad = _pad_ring(polar, dtype)
             cortical = None
         elif style in _ISOTROPIC_STYLES:
-            cart, polar = _isotropic_points(fov, cmf_a, res, max_val)
+            cart, polar = _isotropic_points(fov, cmf_a, res, max_val, fixn=style == "isotropic_fixn")
             plotting = _isotropic_plotting(cart, fov, cmf_a)
             pad = _pad_ring(polar, dtype)
             cortical = sensor_manifold_coords(cart.numpy(), cmf_a, fov)
             self.cortical_pad_coords = sensor_manifold_coords(pad.numpy(), cmf_a, fov).to(
                 device=device, dtype=dtype)
         else:
-            raise NotImplementedError(f"style {style!r}: 'logpolar', 'uniform' and 'isotropic' are built")
+            raise ValueError(f"Style {style} not recognized")
         self.cartesian = cart.to(device=device, dtype=dtype)
         self.polar = polar.to(device=device, dtype=dtype)
         self.cortical = None if cortical is None else cortical.to(device=device, dtype=dtype)

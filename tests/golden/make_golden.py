@@ -121,7 +121,8 @@ def main_isotropic():
     cortical manifold, fovi/sensing/manifold.py:14-215,347-375, and pad ring, coords.py:68-87),
     the neighbour / slot tables of isotropic layers (the 3-D cdist branch of knn.py:101-152
     with pad tokens, and knn.py:599-647), of visual-field layers (sample_cortex=False,
-    knn.py:117-119,620-647) and the pad rings of the log-polar and uniform styles."""
+    knn.py:117-119,620-647), the pad rings of the log-polar and uniform styles and seeded
+    'isotropic_fixn' sensors (coords.py:224-258)."""
     coords_mod, knn_mod = load_reference()
     out = {"torch_version": np.array(torch.__version__), "numpy_version": np.array(np.__version__)}
     for res in ISO_RES:
@@ -153,6 +154,13 @@ def main_isotropic():
         print(f"{name}: pads used {int((layer.knn_indices >= cin.cartesian.shape[0]).sum())}", flush=True)
     for name, (style, res) in PAD_RINGS.items():
         out[name] = coords_mod.SamplingCoords(16, 2.78, res, device="cpu", style=style).cartesian_pad_coords.numpy()
+    # 'isotropic_fixn': the point count fixed to res**2 by seeded random angle moves
+    for seed, res in ((0, 16), (1, 24)):
+        np.random.seed(seed)
+        c = coords_mod.SamplingCoords(16, 2.78, res, device="cpu", style="isotropic_fixn")
+        for key in ("cartesian", "polar", "cortical"):
+            out[f"fixn{res}__{key}"] = getattr(c, key).numpy()
+        print(f"isotropic_fixn res {res} (seed {seed}): {c.cartesian.shape[0]} points", flush=True)
     # a scaled sensor (max_val below 1) and the auto-matched strided pair of the default style
     c = coords_mod.SamplingCoords(16, 2.78, 16, device="cpu", style="isotropic", max_val=0.9)
     for key in ("cartesian", "plotting", "cortical", "cartesian_pad_coords", "cortical_pad_coords"):

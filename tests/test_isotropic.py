@@ -57,6 +57,17 @@ def test_scaled_and_auto_matched_sensors_match_reference():
         _equal(getattr(cout, key), f"auto__out_{key}")
 
 
+@pytest.mark.parametrize("seed,res", [(0, 16), (1, 24)])
+def test_fixn_sensor_matches_reference(seed, res):
+    """'isotropic_fixn' moves single angles between rings drawn by numpy's global RNG: a
+    seeded run builds the reference's sensor, with exactly res**2 points."""
+    np.random.seed(seed)
+    c = _coords(res, "isotropic_fixn")
+    assert c.shape[0] == res * res == num_sampling_coords(FOV, CMF_A, res, style="isotropic_fixn")
+    for key in ("cartesian", "polar", "cortical"):
+        _equal(getattr(c, key), f"fixn{res}__{key}")
+
+
 def test_pad_rings_of_other_styles_match_reference():
     _equal(_coords(16, "logpolar").cartesian_pad_coords, "pad_logpolar16")
     _equal(_coords(8, "uniform").cartesian_pad_coords, "pad_uniform8")
