@@ -222,3 +222,95 @@ def test_isotropic_knnpool_vs_oracle(mode):
     xr = x.clone().requires_grad_(True)
     knnpool_ref.knnpool_forward(xr, layer.knn_indices.cpu(), n_in, mode, w).backward(dy)
     assert_close_rel(xd.grad.cpu(), xr.grad, 1e-5, f"isotropic pool backward {mode}")
+
+
+# ------------------------------------------------------- the notebook's isotropic AlexNet ---
+def _notebook_alexnet(device, norm_type):
+    """fovi_alexnet2023 with arch_spec base_lowres as config/fovi_alexnet.yaml builds it
+    (architectures.py:73-120): 64-pixel auto-matched isotropic input, a=0.5, fov 16,
+    channels 96/256/384/384/256, k = 11^2/5^2/3^2/3^2/3^2, strides 2/1/1/1/1, pooling after
+    blocks 0, 1 and 4, ref_frame_mult 2, one output point."""
+    from fovi_amd.arch.knnalexnet import KNNAlexNet
+    return KNNAlexNet(64, 3, [96, 256, 384, 384, 256], [2, 1, 1, 1, 1], [0, 1, 4], [121, 25, 9, 9, 9], out_res=1,
+                      auto_match_cart_resources=1, style="isotropic", norm_type=norm_type, fov=16.0, cmf_a=0.5,
+                      device=device, ref_frame_mult=2)
+
+
+def _knn_layers(net):
+    return [m for m in net.modules() if isinstance(m, (KNNConvLayer, KNNPoolingLayer))]
+
+
+def test_notebook_alexnet_coords_per_layer():
+    """step2_knnconv cell 12 prints 'Number of coords per layer: [4085, 964, 230, 230, 60,
+    60, 60, 60, 16, 1]' for this network (fovinet.py:516-528: the first layer's inputs,
+    then every kNN layer's outputs)."""
+    layers = _knn_layers(_notebook_alexnet("cpu", "force_batch"))
+    assert [len(layers[0].in_coords)] + [len(l.out_coords) for l in layers] == [4085, 964, 230, 230, 60, 60, 60,
+                                                                               60, 16, 1]
+    assert layers[0]._k == 121 and layers[0].ref_coords.shape[0] == 484
+
+
+@pytest.mark.gpu
+def test_notebook_alexnet_forward_backward_vs_oracle():
+    """The notebook network (no normalisation, so the chain is kNN-conv + ReLU and kNN
+    pooling only) in fp32 on the GPU. Output: against the oracles composed layer by layer
+    (1e-4 relative: nine fp32 layers, each within 1e-5). Input gradient: the chain rule over
+    the oracles' vector-Jacobian products, each taken at the GPU's own layer input and ReLU
+    mask (a maximum or a ReLU sign decided by the last ulp would otherwise route gradient
+    differently). Every parameter gets a finite gradient."""
+    from fovi_amd.arch.knnalexnet import KNNAlexNetBlock
+    net = _notebook_alexnet("cuda", "none")
+    g = torch.Generator().manual_seed(21)
+    with torch.no_grad():
+        for layer in _knn_layers(net):
+            if isinstance(layer, KNNConvLayer):
+                c_in = layer.in_channels
+                layer.weight.copy_(torch.randn(layer.weight.shape, generator=g) * (2.0 / (c_in * layer._k)) ** 0.5)
+    x = torch.rand(2, 3, 4085, generator=g)
+    xd = x.cuda().requires_grad_(True)
+    y = net(xd)
+    assert y.shape == (2, 256, 1)
+    dy = torch.randn(y.shape, generator=g)
+    y.backward(dy.cuda())
+    for name, prm in net.named_parameters():
+        assert prm.grad is not None and torch.isfinite(prm.grad).all(), name
+
+    def conv_ref(layer, h):
+        b = None if layer.bias is None else layer.bias.detach().cpu()
+        return knnconv_ref.knnconv_forward(h, layer.knn_indices.cpu(), layer.in_coords.shape[0],
+                                           layer.local_rf.cpu(), layer.weight.detach().cpu(), b)
+
+    def pool_ref(layer, h):
+        w = layer.gaussian_weights.cpu() if layer.mode == "gaussian" else None
+        return knnpool_ref.knnpool_forward(h, layer.knn_indices.cpu(), layer.in_coords.shape[0], layer.mode, w)
+
+    # the GPU chain step by step: (kind, layer, input, output) of every kNN layer
+    steps, h = [], xd.detach()
+    with torch.no_grad():
+        for mod in net.layers:
+            if isinstance(mod, KNNAlexNetBlock):
+                out = mod.conv.forward_fused(h, "relu")
+                steps.append(("conv", mod.conv, h.cpu(), out.cpu()))
+                h = out
+                if mod.pool is not None:
+                    out = mod.pool(h)
+                    steps.append(("pool", mod.pool, h.cpu(), out.cpu()))
+                    h = out
+            else:
+                out = mod(h)
+                steps.append(("pool", mod, h.cpu(), out.cpu()))
+                h = out
+    assert torch.equal(h.cpu(), y.detach().cpu())
+    ref = x
+    for kind, layer, _, _ in steps:
+        ref = torch.relu(conv_ref(layer, ref)) if kind == "conv" else pool_ref(layer, ref)
+    assert_close_rel(y.detach().cpu(), ref, 1e-4, "notebook AlexNet output")
+    grad = dy
+    for kind, layer, inp, out in reversed(steps):
+        hr = inp.clone().requires_grad_(True)
+        if kind == "conv":
+            conv_ref(layer, hr).backward(grad * (out > 0))
+        else:
+            pool_ref(layer, hr).backward(grad)
+        grad = hr.grad
+    assert_close_rel(xd.grad.cpu(), grad, 1e-4, "notebook AlexNet input gradient")
