@@ -90,6 +90,24 @@ class KNNBaseLayer:
         self.sample_coords = torch.cat([in_c.cortical.cpu(), in_c.cortical_pad_coords.cpu()], 0)
         return T.knn_euclidean(self.sample_coords, out_c.cortical.cpu(), self._k, batch_size)
 
+    def _compute_all_distances(self):
+        """Distances ``[N_in + P, N_out]`` between every input point (pad ring included) and
+        every output point in one ``cdist`` call: cortical for ``sample_cortex=True``
+        (isotropic sensors), visual field for ``sample_cortex=False`` (reference
+        ``knn.py:155-224``, non-geodesic branches)."""
+        if self.sample_cortex == "geodesic":
+            raise NotImplementedError("geodesic distances need pygeodesic, which is not available")
+        in_c, out_c = self.in_coords, self.out_coords
+        pads = in_c.cartesian_pad_coords.cpu()
+        self.sample_coords_cart = torch.cat([in_c.cartesian.cpu(), pads], 0)
+        if not self.sample_cortex:
+            self.sample_coords = self.sample_coords_cart
+            return torch.cdist(self.sample_coords, out_c.cartesian.cpu())
+        if in_c.style not in ("isotropic", "isotropic_fixn"):
+            raise ValueError(f"all-pairs cortical distances need the isotropic manifold, not {in_c.style!r}")
+        self.sample_coords = torch.cat([in_c.cortical.cpu(), in_c.cortical_pad_coords.cpu()], 0)
+        return torch.cdist(self.sample_coords, out_c.cortical.cpu())
+
     def _gpu_tables(self, n_in):
         """Whether the neighbour search runs on the GPU (``knn_tables.knn_logpolar_device``, the
         host's results bit for bit): a CUDA layer where the GPU search applies."""
@@ -147,23 +165,36 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         self._k = int(self.k.item())
 
         knn_indices, knn_distances = self._compute_knns(batch_size)
-        self.knn_indices_pad_mask = knn_indices >= n_in
+        self._setup(knn_indices, knn_distances, bias)
+
+    def _setup(self, knn_indices, knn_distances, bias, param_device=None):
+        """Pad tokens, ref grid, parameters (created on ``param_device``, default the layer's
+        device, then moved there), ref slots and device tables of a neighbour table
+        ``[k, N_out]`` whose entries >= N_in (pad ring) or < 0 (padding of a partition) carry
+        no input (reference ``knn.py:445-471``)."""
+        n_in, device = self.in_coords.shape[0], self.device
+        self.knn_indices_pad_mask = (knn_indices >= n_in) | (knn_indices < 0)
         pad_token = knn_indices.clone()
         pad_token[self.knn_indices_pad_mask] = n_in
         self.knn_indices_batch_cache = pad_token
 
-        self.compute_reference_coords(arch_flag)
+        self.compute_reference_coords(self.arch_flag)
         n_ref = self.ref_coords.shape[0]
-        self.weight = nn.Parameter(torch.empty(out_channels, in_channels * n_ref, device=device))
+        pdev = device if param_device is None else param_device
+        self.weight = nn.Parameter(torch.empty(self.out_channels, self.in_channels * n_ref, device=pdev))
         if bias:
-            self.bias = nn.Parameter(torch.empty(out_channels, device=device))
+            self.bias = nn.Parameter(torch.empty(self.out_channels, device=pdev))
         else:
             self.register_parameter("bias", None)
         self._init_conv_like()
+        if param_device is not None:
+            self.weight.data = self.weight.data.to(device)
+            if self.bias is not None:
+                self.bias.data = self.bias.data.to(device)
 
         self.slots = self.compute_local_rf_slots(knn_indices)
         self.knn_indices = knn_indices.to(device)
-        self.knn_distances = knn_distances.to(device)
+        self.knn_distances = None if knn_distances is None else knn_distances.to(device)
         self.knn_indices_pad_token = pad_token.to(device)
         self.knn_indices_pad_mask = self.knn_indices_pad_mask.to(device)
         self._init_tables(knn_indices, self.slots, n_in, n_ref, device)

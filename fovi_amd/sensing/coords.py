@@ -166,18 +166,18 @@ def _pad_ring(polar, dtype, padding_distance=0.5):
     """Points on rings beyond the last ring, spaced by the outermost ring gap in radius and in
     angle, out to ``padding_distance`` (reference ``coords.py:68-87``).
 
-    ``torch.arange`` with a 0-d tensor step returns the default dtype, so radii and angles are
-    fp32 whatever ``polar``'s dtype, and the reference's ``np.cos(angle)`` of a 0-d fp32
-    tensor is numpy's fp32 cosine; each coordinate is that fp32 cos/sin times the fp32 radius,
-    then the set is rounded to ``dtype``."""
+    ``torch.arange`` with a 0-d tensor step returns the default dtype (fp32 unless changed),
+    whatever ``polar``'s dtype, and the reference's ``np.cos(angle)`` of such a 0-d tensor is
+    numpy's cosine in that dtype; each coordinate is that cos/sin times the radius, then the
+    set is rounded to ``dtype``."""
     radii = torch.sort(torch.unique(polar[:, 0])).values
     gap = radii[-1] - radii[-2]
     start = radii[-1] + gap
     angles = torch.arange(0, 2 * np.pi, gap)
-    rings = torch.arange(start, start + padding_distance, gap)
-    assert angles.dtype == rings.dtype == torch.float32
-    cos_a = torch.from_numpy(np.array([np.cos(a) for a in angles.numpy()], dtype=np.float32))
-    sin_a = torch.from_numpy(np.array([np.sin(a) for a in angles.numpy()], dtype=np.float32))
+    rings = torch.arange(start, start + padding_distance, gap).to(angles.dtype)
+    ang = angles.numpy()
+    cos_a = torch.from_numpy(np.array([np.cos(a) for a in ang], dtype=ang.dtype))
+    sin_a = torch.from_numpy(np.array([np.sin(a) for a in ang], dtype=ang.dtype))
     ring_t = rings.unsqueeze(1)
     xy = torch.stack([ring_t * cos_a, ring_t * sin_a], dim=2)
     return xy.reshape(-1, 2).to(dtype=dtype)
@@ -338,6 +338,10 @@ class SamplingCoords:
         self.style = style
         self.dtype = dtype
         self.max_val = max_val
+        # the points are built on the host; a tensor scale (max_out_coord_val='auto') may live
+        # on the device, and its fp32 product with the radii is the same IEEE multiply there
+        if isinstance(max_val, torch.Tensor):
+            max_val = max_val.detach().cpu()
         plotting = None
         if res == 1:
             cart = torch.zeros(1, 2, dtype=torch.float64)

@@ -9,15 +9,16 @@ import torch.nn.functional as F
 def knnconv_forward(x, knn_indices, n_in, local_rf, weight, bias=None):
     """KNNConvLayer.forward restated with torch CPU fp32 (reference fovi/arch/knn.py:484-557).
 
-    x [B, C, N_in]; knn_indices [k, N_out] (indices >= n_in are the pad
-    token, knn.py:451-453); local_rf [N_out, k, V] one-hot; weight
+    x [B, C, N_in]; knn_indices [k, N_out] (indices >= n_in, and the -1 that pads a
+    partitioning patch embedding's groups, are the pad token, knn.py:451-453 and
+    knnvit.py:196-198); local_rf [N_out, k, V] one-hot; weight
     [C_out, C*V] with reduction index c*V + v. Returns [B, C_out, N_out].
     """
     B, C, _ = x.shape
     k, n_out = knn_indices.shape
     V = local_rf.shape[2]
     idx = knn_indices.clone()
-    idx[idx >= n_in] = n_in
+    idx[(idx >= n_in) | (idx < 0)] = n_in
     xp = torch.cat([x, torch.zeros(B, C, 1, dtype=x.dtype)], dim=2)                      # knn.py:495
     g = torch.gather(xp, 2, idx.reshape(1, 1, -1).expand(B, C, -1)).reshape(B, C, k, n_out)  # knn.py:500
     g = g.permute(0, 1, 3, 2).reshape(B * C, n_out, k)                                  # knn.py:521
@@ -100,7 +101,7 @@ def knnconv_fp8_forward(xq, x_scale, knn_indices, n_in, local_rf, wq, w_scale, b
     k, n_out = knn_indices.shape
     V = local_rf.shape[2]
     idx = knn_indices.clone()
-    idx[idx >= n_in] = n_in
+    idx[(idx >= n_in) | (idx < 0)] = n_in
     xp = torch.cat([xq.double(), torch.zeros(B, C, 1, dtype=torch.float64)], dim=2)
     g = torch.gather(xp, 2, idx.reshape(1, 1, -1).expand(B, C, -1)).reshape(B, C, k, n_out)
     g = g.permute(0, 1, 3, 2)                                                   # [B, C, N, k]

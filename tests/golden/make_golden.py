@@ -113,6 +113,10 @@ ISO_LAYERS = {"iso_16_8": (16, 8, 9), "iso_24_12": (24, 12, 25), "iso_16_16": (1
 VIS_LAYERS = {"vis_iso_16_8": ("isotropic", 16, 8, 9), "vis_lp_16_8": ("logpolar", 16, 8, 9)}
 # pad rings of the other styles: name -> (style, res)
 PAD_RINGS = {"pad_logpolar16": ("logpolar", 16), "pad_uniform8": ("uniform", 8)}
+# partitioning patch embeddings: name -> (class, cmf_a, cart_patch_size); 64-pixel input grid
+PATCH_LAYERS = {"part_a05": ("PartitioningPatchEmbedding", 0.5, 16),
+                "kpart_a05": ("KNNPartitioningPatchEmbedding", 0.5, 16),
+                "kpart_a2786": ("KNNPartitioningPatchEmbedding", 2.785765, 8)}
 ISO_OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "isotropic.npz")
 
 
@@ -122,7 +126,8 @@ def main_isotropic():
     the neighbour / slot tables of isotropic layers (the 3-D cdist branch of knn.py:101-152
     with pad tokens, and knn.py:599-647), of visual-field layers (sample_cortex=False,
     knn.py:117-119,620-647), the pad rings of the log-polar and uniform styles and seeded
-    'isotropic_fixn' sensors (coords.py:224-258)."""
+    'isotropic_fixn' sensors (coords.py:224-258) and the tables of the partitioning patch
+    embeddings (knnvit.py:102-290, Euclidean distances)."""
     coords_mod, knn_mod = load_reference()
     out = {"torch_version": np.array(torch.__version__), "numpy_version": np.array(np.__version__)}
     for res in ISO_RES:
@@ -173,6 +178,18 @@ def main_isotropic():
         out[f"auto__out_{key}"] = getattr(cout, key).numpy()
     print(f"auto-matched isotropic pair: res {cin.resolution} -> {cout.resolution}, "
           f"{cin.cartesian.shape[0]} -> {cout.cartesian.shape[0]} points", flush=True)
+    # partitioning patch embeddings (Euclidean cortical distances; knnvit.py:102-290)
+    _load("fovi_ref.arch.vit", os.path.join(REF, "arch", "vit.py"), None)
+    vit_mod = _load("fovi_ref.arch.knnvit", os.path.join(REF, "arch", "knnvit.py"), None)
+    for name, (cls, cmf_a, patch) in PATCH_LAYERS.items():
+        layer = getattr(vit_mod, cls)(3, 8, 64, 16, cmf_a, in_cart_res=64, cart_patch_size=patch, device="cpu",
+                                      sample_cortex=True)
+        rf = layer.local_rf.numpy()
+        assert np.all(rf.sum(2) == 1)
+        out[f"{name}__k"] = np.array(int(layer._k))
+        out[f"{name}__idx"] = layer.knn_indices.numpy().astype(np.int16)
+        out[f"{name}__slots"] = rf.argmax(2).astype(np.uint16)
+        print(f"{name}: k={layer._k} n_in={len(layer.in_coords)} n_out={len(layer.out_coords)}", flush=True)
     np.savez_compressed(ISO_OUT, **out)
     print(f"wrote {ISO_OUT} ({os.path.getsize(ISO_OUT) / 1024:.0f} KiB)")
 

@@ -314,3 +314,77 @@ def test_notebook_alexnet_forward_backward_vs_oracle():
             pool_ref(layer, hr).backward(grad)
         grad = hr.grad
     assert_close_rel(xd.grad.cpu(), grad, 1e-4, "notebook AlexNet input gradient")
+
+
+# -------------------------------------------------------- partitioning patch embeddings ---
+PATCH_LAYERS = {"part_a05": ("PartitioningPatchEmbedding", 0.5, 16),
+                "kpart_a05": ("KNNPartitioningPatchEmbedding", 0.5, 16),
+                "kpart_a2786": ("KNNPartitioningPatchEmbedding", 2.785765, 8)}
+
+
+def _patch_layer(name, device):
+    from fovi_amd.arch import knnvit
+    cls, cmf_a, patch = PATCH_LAYERS[name]
+    return getattr(knnvit, cls)(3, 8, 64, 16, cmf_a, in_cart_res=64, cart_patch_size=patch, device=device,
+                                sample_cortex=True)
+
+
+@pytest.mark.parametrize("name", list(PATCH_LAYERS))
+def test_partitioning_patch_embeddings_match_reference(name):
+    """k, neighbour tables (index -1 pads a partition's groups) and ref slots of the
+    partitioning patch embeddings, as the reference builds them with Euclidean distances."""
+    layer = _patch_layer(name, "cpu")
+    assert layer._k == int(GOLDEN[f"{name}__k"])
+    _equal(layer.knn_indices.to(torch.int16), f"{name}__idx")
+    _equal(layer.slots.numpy().astype(np.uint16), f"{name}__slots")
+
+
+def test_partition_is_a_partition():
+    """Every sensor point sits in exactly one group, the group of its nearest centre; -1 only
+    pads the tail of a group's column."""
+    layer = _patch_layer("part_a05", "cpu")
+    idx = layer.knn_indices
+    n_in = len(layer.in_coords)
+    real = idx[idx >= 0]
+    assert torch.equal(torch.sort(real).values, torch.arange(n_in))
+    nearest = torch.argmin(layer.distances[:n_in], 1)
+    cols = torch.arange(idx.shape[1]).expand_as(idx)[idx >= 0]
+    assert torch.equal(nearest[real], cols)
+    pad = idx < 0
+    assert torch.all(pad[1:] >= pad[:-1])
+
+
+def test_geodesic_partitioning_raises():
+    from fovi_amd.arch.knnvit import KNNPartitioningPatchEmbedding
+    with pytest.raises(NotImplementedError):
+        KNNPartitioningPatchEmbedding(3, 8, 64, 16, 0.5, in_cart_res=64, cart_patch_size=16, device="cpu")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["part_a05", "kpart_a2786"])
+def test_partitioning_patch_embedding_forward_vs_oracle(name):
+    layer = _patch_layer(name, "cuda")
+    n_in = len(layer.in_coords)
+    x = torch.rand(2, 3, n_in, generator=torch.Generator().manual_seed(31))
+    with torch.no_grad():
+        tokens = layer(x.cuda())
+    assert tokens.shape == (2, len(layer.out_coords), 8)
+    ref = knnconv_ref.knnconv_forward(x, layer.knn_indices.cpu(), n_in, layer.local_rf.cpu(),
+                                      layer.weight.detach().cpu())
+    assert_close_rel(tokens.transpose(1, 2).cpu(), ref, 1e-5, f"{name} tokens")
+
+
+def test_oracle_pads_negative_indices_like_the_pad_token():
+    """-1 entries (partition padding) and pad-ring entries contribute nothing: the oracle's
+    library-call form equals its float64 loop form, which skips both."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(2, 3, 10, generator=g)
+    idx = torch.randint(0, 10, (4, 6), generator=g)
+    idx[3, ::2] = -1
+    idx[2, 1] = 12
+    slots = torch.randint(0, 4, (6, 4), generator=g)
+    rf = torch.zeros(6, 4, 4).scatter_(2, slots.unsqueeze(2), 1)
+    w = torch.randn(5, 12, generator=g)
+    got = knnconv_ref.knnconv_forward(x, idx, 10, rf, w)
+    want = knnconv_ref.knnconv_bruteforce(x, idx, slots, 10, w)
+    assert np.allclose(got.numpy(), want, rtol=1e-5, atol=1e-5)
