@@ -1227,10 +1227,13 @@ static void launch_bf16_smallc_nt(const KnnParams& p, int out_t, hipStream_t s) 
 // ---------------------------------------------------------------------------
 // Few-channel layers with many slots, two passes through a workspace
 // ---------------------------------------------------------------------------
-// Pass 1 (slotsum_kernel): one wave per output point, lanes over slots; each
-// lane walks its slots' neighbour lists (index loads, then row loads, four
-// at a time) and writes the point's slot-major reduction row
-// A[b, n, v * CP + c] in bf16 (fp32 sums, one RNE rounding), zero padded to
+// Pass 1 (slotsum_kernel): one wave per output point, each lane owning every 64th
+// slot. A lane issues its slots' table entries together, then the first
+// neighbour index of each, then those neighbours' rows (three rounds of
+// independent loads instead of a dependent chain per slot); neighbours after
+// the first, rare at one neighbour per slot on average, follow in list order.
+// The lane writes the point's slot-major reduction row A[b, n, v * CP + c] in
+// bf16 (fp32 sums in list order from +0, one RNE rounding), zero padded to
 // k_pad. Few registers, many waves in flight: the neighbour-list latency is
 // hidden by occupancy, which the MFMA kernels (one 8-wave workgroup per CU)
 // cannot do. Pass 2 (dense_gemm_kernel): the MFMA tile core of the kernels
@@ -1239,11 +1242,15 @@ template <int CP>
 __global__ __launch_bounds__(256) void slotsum_kernel(KnnParams p, uint16_t* A, int64_t rows) {
   typedef typename RowVec<CP>::T RowT;
   constexpr int NW = CP / 2;
+  constexpr int SL = 4;                       // slots per lane per round
   const int lane = threadIdx.x & 63;
-  const int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);   // output row (b, n)
+  // XCD-aware order: each XCD sums a contiguous range of rows (whole images), so an image's
+  // rows are fetched into one L2 only (the grid is padded to a multiple of 8 blocks)
+  const int64_t m = xcd_tile(blockIdx.x, gridDim.x) * 4 + (threadIdx.x >> 6);   // output row (b, n)
   if (m >= rows) return;
   const int64_t b = m / p.Nout, n = m - b * p.Nout;
   const uint16_t* xb = static_cast<const uint16_t*>(p.x) + b * p.xs0;
+  const int32_t* nbn = p.nbr + n * p.K;
   uint16_t* arow = A + m * p.Kpad;
   uint32_t cmask[NW];
 #pragma unroll
@@ -1251,41 +1258,65 @@ __global__ __launch_bounds__(256) void slotsum_kernel(KnnParams p, uint16_t* A, 
     const int c0 = 2 * w;
     cmask[w] = (c0 < p.C ? 0x0000ffffu : 0u) | (c0 + 1 < p.C ? 0xffff0000u : 0u);
   }
+  auto add_row = [&](float* acc, const RowT& r) {
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const uint32_t bits = r[w] & cmask[w];
+      acc[2 * w] += __uint_as_float(bits << 16);
+      acc[2 * w + 1] += __uint_as_float(bits & 0xffff0000u);
+    }
+  };
+  RowT zero;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) zero[w] = 0u;
   const int64_t nslots = p.Kpad / CP;
-  for (int64_t v = lane; v < nslots; v += 64) {
-    float acc[CP];
+  for (int64_t v0 = 0; v0 < nslots; v0 += 64 * SL) {
+    int32_t e[SL];
 #pragma unroll
-    for (int c = 0; c < CP; ++c) acc[c] = 0.0f;
-    if (v < p.V) {
-      const int32_t e = p.slot_ptr[n * p.V + v];
-      const int cnt = e & 0xffff;
-      const int32_t* nb = p.nbr + n * p.K + (e >> 16);
-      for (int j0 = 0; j0 < cnt; j0 += 4) {
-        int idx[4];
+    for (int s = 0; s < SL; ++s) {
+      const int64_t v = v0 + lane + 64 * s;
+      e[s] = v < p.V ? p.slot_ptr[n * p.V + v] : 0;          // padding slots: no neighbour
+    }
+    int idx[SL];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) idx[u] = j0 + u < cnt ? nb[j0 + u] : -1;
-        RowT r[4];
+    for (int s = 0; s < SL; ++s) idx[s] = (e[s] & 0xffff) ? nbn[e[s] >> 16] : -1;
+    RowT r[SL];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          RowT z;
+    for (int s = 0; s < SL; ++s)
+      r[s] = idx[s] >= 0 ? *reinterpret_cast<const RowT*>(xb + static_cast<int64_t>(idx[s]) * p.xs2) : zero;
+    float acc[SL][CP];
 #pragma unroll
-          for (int w = 0; w < NW; ++w) z[w] = 0u;
-          r[u] = idx[u] >= 0 ? *reinterpret_cast<const RowT*>(xb + static_cast<int64_t>(idx[u]) * p.xs2) : z;
-        }
+    for (int s = 0; s < SL; ++s) {
+#pragma unroll
+      for (int c = 0; c < CP; ++c) acc[s][c] = 0.0f;
+      add_row(acc[s], r[s]);
+    }
+#pragma unroll
+    for (int s = 0; s < SL; ++s) {
+      const int cnt = e[s] & 0xffff;
+      const int32_t* nb = nbn + (e[s] >> 16);
+      for (int j0 = 1; j0 < cnt; j0 += 4) {
+        int id4[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) id4[u] = j0 + u < cnt ? nb[j0 + u] : -1;
+        RowT r4[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u)
+          r4[u] = id4[u] >= 0 ? *reinterpret_cast<const RowT*>(xb + static_cast<int64_t>(id4[u]) * p.xs2) : zero;
 #pragma unroll
-          for (int w = 0; w < NW; ++w) {
-            const uint32_t bits = r[u][w] & cmask[w];
-            acc[2 * w] += __uint_as_float(bits << 16);
-            acc[2 * w + 1] += __uint_as_float(bits & 0xffff0000u);
-          }
+        for (int u = 0; u < 4; ++u) add_row(acc[s], r4[u]);
       }
     }
-    RowT out;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) out[w] = cvt_pk_bf16(acc[2 * w], acc[2 * w + 1]);
-    *reinterpret_cast<RowT*>(arow + v * CP) = out;
+    for (int s = 0; s < SL; ++s) {
+      const int64_t v = v0 + lane + 64 * s;
+      if (v < nslots) {
+        RowT out;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) out[w] = cvt_pk_bf16(acc[s][2 * w], acc[s][2 * w + 1]);
+        *reinterpret_cast<RowT*>(arow + v * CP) = out;
+      }
+    }
   }
 }
 
@@ -1408,7 +1439,7 @@ static void launch_dense(const KnnParams& p, const uint16_t* A, int out_t, hipSt
 
 static int launch_two_pass(const KnnParams& p, int cp, uint16_t* A, int out_t, hipStream_t s) {
   const int64_t rows = p.B * p.Nout;
-  dim3 g1(static_cast<unsigned>((rows + 3) / 4));
+  dim3 g1(static_cast<unsigned>(((rows + 3) / 4 + 7) / 8 * 8));
   if (cp == 4) hipLaunchKernelGGL((slotsum_kernel<4>), g1, dim3(256), 0, s, p, A, rows);
   else hipLaunchKernelGGL((slotsum_kernel<8>), g1, dim3(256), 0, s, p, A, rows);
   if (check_launch("fovi_knnconv_fwd(slot sums)")) return 1;
