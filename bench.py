@@ -36,18 +36,40 @@ def log(msg):
 
 
 def time_steps(fn, steps, warmup):
+    """Median ms per step: ``warmup`` untimed steps, then ``steps`` steps, each between two HIP
+    events recorded on torch's current stream (the stream every C-ABI call here is enqueued on),
+    the whole timed region bracketed by device synchronisation (as fovi/utils/flops.py:279-417
+    times GPU work: events around each iteration, median)."""
     import torch
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(steps):
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for a, b in ev:
+        a.record()
         fn()
-    end.record()
+        b.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps  # ms per step
+    times = sorted(a.elapsed_time(b) for a, b in ev)
+    return times[len(times) // 2]
+
+
+def cpu_randn(shape, seed, dtype=None, dev=None):
+    """Seeded CPU normal draws moved to the device (portable across boxes)."""
+    import torch
+    t = torch.randn(*shape, generator=torch.Generator().manual_seed(seed))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t if dev is None else t.to(dev)
+
+
+def cpu_rand(shape, seed, dtype=None, dev=None):
+    """Seeded CPU uniform [0, 1) draws moved to the device."""
+    import torch
+    t = torch.rand(*shape, generator=torch.Generator().manual_seed(seed))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t if dev is None else t.to(dev)
 
 
 def bench_c3(steps, warmup, dev):
@@ -60,12 +82,10 @@ def bench_c3(steps, warmup, dev):
     layer = KNNConvLayer(C, C, K, coords, coords, device=dev)
     t_tables = time.time() - t0
     log(f"[c3] layer and tables built in {t_tables:.2f}s (kNN search on the GPU: {layer._gpu_tables(RES * RES)})")
-    g = torch.Generator(device=dev).manual_seed(1)
     with torch.no_grad():
-        layer.weight.copy_(torch.randn(layer.weight.shape, generator=g, device=dev) * (1.0 / (C * K)) ** 0.5)
-    gx = torch.Generator(device=dev).manual_seed(0)
+        layer.weight.copy_(cpu_randn(layer.weight.shape, 1, dev=dev) * (1.0 / (C * K)) ** 0.5)
     # channels-last storage [B, N, C], handed to the layer as the [B, C, N] view
-    x = torch.randn(B, RES * RES, C, generator=gx, device=dev, dtype=torch.bfloat16).transpose(1, 2)
+    x = cpu_randn((B, RES * RES, C), 0, torch.bfloat16, dev).transpose(1, 2)
     with torch.no_grad():
         ms = time_steps(lambda: layer(x), steps, warmup)
     flops = 2.0 * B * RES * RES * C * C * layer.ref_coords.shape[0]
@@ -81,10 +101,8 @@ def bench_c3_backward(c3, steps, warmup):
     forward's)."""
     import torch
     layer, x = c3["layer"], c3["x"]
-    g = torch.Generator(device=x.device).manual_seed(5)
     n = layer.out_coords.shape[0]
-    dy = torch.randn(x.shape[0], n, layer.out_channels, generator=g, device=x.device,
-                     dtype=torch.bfloat16).transpose(1, 2)
+    dy = cpu_randn((x.shape[0], n, layer.out_channels), 5, torch.bfloat16, x.device).transpose(1, 2)
     layer._inverse_tables(x.device)
     ms = time_steps(lambda: layer._backward(x, layer.weight, dy, True, True), steps, warmup)
     flops = 2.0 * c3["flops"]
@@ -106,12 +124,26 @@ def bench_c5(c3, steps, warmup):
         ms = time_steps(lambda: layer(xq), steps, warmup)
         ms_q = time_steps(lambda: layer.quantize_input(x), steps, warmup)
     tflops = c3["flops"] / (ms * 1e-3) / 1e12
+    # per-layer cosine of the bf16 output against the unquantized fp32 layer (the fp32 kernel at
+    # B=64), for the layer's scale amax * headroom / 448 and the plain amax / 448
+    from fovi_amd.arch.fp8 import quantize_e4m3
+
+    def cos(a, b):
+        a, b = a.double().flatten(), b.double().flatten()
+        return (a @ b / (a.norm() * b.norm())).item()
+    with torch.no_grad():
+        y32 = layer(x.float())
+        cos_layer = cos(layer(xq).float(), y32)
+        cos_plain = cos(layer(quantize_e4m3(x, 1.0)).float(), y32)
+        del y32
     # quantizer: amax pass reads x, quantize pass reads x and writes e4m3
     q_bytes = 2 * x.numel() * x.element_size() + x.numel()
     q_gbs = q_bytes / (ms_q * 1e-3) / 1e9
     log(f"[c5] {ms:.3f} ms/step  {tflops:.1f} TFLOP/s  ({100 * tflops / PEAK_FP8_TFLOPS:.1f}% of fp8 peak); "
-        f"quantize {ms_q:.3f} ms ({q_gbs:.0f} GB/s)")
-    return dict(ms=ms, tflops=tflops, ms_q=ms_q, q_gbs=q_gbs)
+        f"quantize {ms_q:.3f} ms ({q_gbs:.0f} GB/s); cosine vs fp32 {cos_layer:.6f} (headroom "
+        f"{layer.fp8_headroom:g}), {cos_plain:.6f} (amax/448)")
+    return dict(ms=ms, tflops=tflops, ms_q=ms_q, q_gbs=q_gbs, cos=cos_layer, cos_plain=cos_plain,
+                headroom=layer.fp8_headroom)
 
 
 def sampler_algorithmic_bytes(sampler, img, fix, sizes, vmap, mode):
@@ -145,9 +177,8 @@ def bench_c4_sampler(steps, warmup, dev, mode="nearest"):
     import torch
     from fovi_amd.sensing.samplers import GridSampler
     B, Fx, RES, S = 128, 4, 128, 512
-    gi = torch.Generator(device=dev).manual_seed(0)
     # two image sets (2 x 201 MB) rotated so the 256 MB MALL cannot hold the input
-    imgs = [torch.rand(B, 3, S, S, generator=gi, device=dev).bfloat16() for _ in range(2)]
+    imgs = [cpu_rand((B, 3, S, S), i, torch.bfloat16, dev) for i in range(2)]
     gf = torch.Generator().manual_seed(2)
     fix = 0.25 + 0.5 * torch.rand(B * Fx, 2, generator=gf)
     sizes = np.array([[S, S]] * (B * Fx))
@@ -173,11 +204,11 @@ def bench_c4_sampler(steps, warmup, dev, mode="nearest"):
 
 
 def _init_weights(layers, dev, seed):
+    """N(0, 1 / (C_in k)) weights (layer i drawn with seed + i), zero bias."""
     import torch
-    g = torch.Generator(device=dev).manual_seed(seed)
     with torch.no_grad():
-        for c in layers:
-            c.weight.copy_(torch.randn(c.weight.shape, generator=g, device=dev) * (1.0 / (c.in_channels * c._k)) ** 0.5)
+        for i, c in enumerate(layers):
+            c.weight.copy_(cpu_randn(c.weight.shape, seed + i, dev=dev) * (1.0 / (c.in_channels * c._k)) ** 0.5)
             if c.bias is not None:
                 c.bias.zero_()
 
@@ -193,8 +224,7 @@ def bench_pool(steps, warmup, dev):
     ci = SamplingCoords(16, 2.78, 32, style="logpolar")
     co = SamplingCoords(16, 2.78, 16, style="logpolar")
     layer = KNNPoolingLayer(9, ci, co, mode="max", device=dev)
-    g = torch.Generator(device=dev).manual_seed(3)
-    x = torch.randn(B, ci.shape[0], C, generator=g, device=dev, dtype=torch.bfloat16).transpose(1, 2)
+    x = cpu_randn((B, ci.shape[0], C), 3, torch.bfloat16, dev).transpose(1, 2)
     with torch.no_grad():
         ms = time_steps(lambda: layer(x), steps, warmup)
     nbytes = B * C * (ci.shape[0] + co.shape[0]) * 2
@@ -218,8 +248,7 @@ def bench_c2(steps, warmup, dev):
     _init_weights([blk.conv for blk in net.layers], dev, 3)
     sampler = GridSampler(16, 2.78, 64, device=dev, mode="bilinear", style="logpolar")
     log(f"[c2] model built in {time.time() - t0:.1f}s")
-    gi = torch.Generator(device=dev).manual_seed(0)
-    imgs = [torch.rand(B, 3, S, S, generator=gi, device=dev) for _ in range(2)]
+    imgs = [cpu_rand((B, 3, S, S), i, dev=dev) for i in range(2)]
     views = sampler.prepare_views(torch.full((B, 2), 0.5), np.array([[S, S]] * B), B, dev)
     # the sampler writes channels-last rows padded to 4 channels: the layout the first layer reads
     _, feats = net.layers[0].conv.padded_input(B)
@@ -257,8 +286,7 @@ def bench_c4_frontend(steps, warmup, dev):
     _init_weights([pe], dev, 4)
     sampler = GridSampler(16, 2.78, 128, device=dev, mode="nearest", style="logpolar")
     log(f"[c4] model built in {time.time() - t0:.1f}s")
-    gi = torch.Generator(device=dev).manual_seed(0)
-    imgs = [torch.rand(B, 3, S, S, generator=gi, device=dev).bfloat16() for _ in range(2)]
+    imgs = [cpu_rand((B, 3, S, S), i, torch.bfloat16, dev) for i in range(2)]
     gf = torch.Generator().manual_seed(2)
     fix = 0.25 + 0.5 * torch.rand(B * Fx, 2, generator=gf)
     views = sampler.prepare_views(fix, np.array([[S, S]] * (B * Fx)), B, dev,
@@ -321,29 +349,12 @@ def measured_traffic(kernel_prefix):
     return None if k is None else int(k["fetch_bytes"] + k["write_bytes"])
 
 
-def cpu_baseline_c3(c3, seconds_budget=25.0):
-    """Oracle (torch CPU fp32 restatement of knn.py:484-557) on a B=2 slice of C3."""
-    import torch
-    from oracle import knnconv_ref
-    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "16") or 16), 16)
-    torch.set_num_threads(threads)
-    layer = c3["layer"]
-    bs = 2
-    x = c3["x"][:bs].float().cpu().contiguous()
-    idx = layer.knn_indices.cpu()
-    rf = layer.local_rf.cpu()
-    w = layer.weight.detach().float().cpu()
-    n_in = layer.in_coords.shape[0]
-    knnconv_ref.knnconv_forward(x, idx, n_in, rf, w)  # warmup
-    times = []
-    t_start = time.time()
-    while len(times) < 5 and (time.time() - t_start) < seconds_budget:
-        t = time.time()
-        knnconv_ref.knnconv_forward(x, idx, n_in, rf, w)
-        times.append(time.time() - t)
-    times.sort()
-    med = times[len(times) // 2]
-    flops = c3["flops"] * bs / 64
+def _host_cores():
+    """(cores this process may run on, os.cpu_count(), the CPU model)."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count() or 1
     model = platform.processor() or platform.machine()
     try:
         with open("/proc/cpuinfo") as f:
@@ -353,17 +364,47 @@ def cpu_baseline_c3(c3, seconds_budget=25.0):
                     break
     except OSError:
         pass
-    return {"value": flops / med / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"C3 slice B={bs} of 64 (fp32 torch-CPU restatement of the reference op "
-                      f"sequence), median of {len(times)} runs = {med:.2f} s, linear in B; host "
-                      f"{model}, os.cpu_count()={os.cpu_count()}"}
+    return avail, os.cpu_count(), model
+
+
+def cpu_baseline_c3(c3, runs=5, warmup=1):
+    """The oracle (torch-CPU fp32 restatement of knn.py:484-557) on a B=1 slice of C3: ``warmup``
+    untimed runs, then ``runs`` timed ones, median, scaled linearly to the batch. Threads: every
+    core the process may run on."""
+    import torch
+    from oracle import knnconv_ref
+    avail, total, model = _host_cores()
+    torch.set_num_threads(avail)
+    layer = c3["layer"]
+    bs = 1
+    x = c3["x"][:bs].float().cpu().contiguous()
+    idx = layer.knn_indices.cpu()
+    rf = layer.local_rf.cpu()
+    w = layer.weight.detach().float().cpu()
+    n_in = layer.in_coords.shape[0]
+    for _ in range(warmup):
+        knnconv_ref.knnconv_forward(x, idx, n_in, rf, w)
+    times = []
+    for _ in range(runs):
+        t = time.time()
+        knnconv_ref.knnconv_forward(x, idx, n_in, rf, w)
+        times.append(time.time() - t)
+    times.sort()
+    med = times[len(times) // 2]
+    flops = c3["flops"] * bs / 64
+    log(f"[cpu] C3 slice B={bs}: runs {', '.join(f'{t:.2f}' for t in times)} s on {torch.get_num_threads()} "
+        f"threads")
+    return {"value": flops / med / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"C3 slice B={bs} of 64 (fp32 torch-CPU restatement of the reference op sequence, "
+                      f"knn.py:484-557), {warmup} warmup + {runs} timed runs, median {med:.2f} s, scaled "
+                      f"linearly in B; host {model}, {avail} cores available of os.cpu_count()={total}"}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sampler", action="store_true")
     ap.add_argument("--no-e2e", action="store_true", help="skip the C2/C4 end-to-end legs")
@@ -432,7 +473,10 @@ def main():
                           "TFLOP/s": round(c5["tflops"], 2), "ms": round(c5["ms"], 4),
                           "roofline": {"bound": "mfma", "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
                                        "frac": round(c5["tflops"] / PEAK_FP8_TFLOPS, 4)},
-                          "quantize_ms": round(c5["ms_q"], 4), "quantize_GB/s": round(c5["q_gbs"], 1)}
+                          "quantize_ms": round(c5["ms_q"], 4), "quantize_GB/s": round(c5["q_gbs"], 1),
+                          "cosine_vs_fp32": {f"amax*{c5['headroom']:g}/448 (layer scale)": round(c5["cos"], 6),
+                                             "amax/448": round(c5["cos_plain"], 6),
+                                             "reference": "unquantized fp32 layer (fp32 kernel), B=64"}}
     if bwd is not None:
         line["c3_backward"] = {"workload": "C3 layer backward, bf16: input gradient (kNN-conv forward over the "
                                            "inverse table) and weight gradient (per-slot pair-list MFMA kernel)",

@@ -47,9 +47,33 @@ __all__ = [
     "KNN_CONV_REGISTRY",
     "get_knn_conv_layer",
     "get_in_out_coords",
+    "register_with_reference",
 ]
 
 _KCHUNK = 64  # reduction chunk of the MFMA kernel; packed weights are padded to it
+
+# Attributes of a sensor point set the kNN layers read (those of the reference's
+# SamplingCoords, fovi/sensing/coords.py:21-66); cartesian_pad_coords (absent on the
+# reference's one-point sets) and cortical_pad_coords (isotropic styles only) are optional.
+_COORD_ATTRS = ("shape", "style", "cartesian", "cortical")
+
+
+def _check_coords(coords, what):
+    """Accepts any object with the reference ``SamplingCoords`` attributes the layers read
+    (this package's ``SamplingCoords``, the reference's own, or a plain namespace)."""
+    missing = [a for a in _COORD_ATTRS if not hasattr(coords, a)]
+    if missing:
+        raise TypeError(f"{what} lacks the SamplingCoords attributes {missing}")
+
+
+def _pad_coords(coords, name="cartesian_pad_coords"):
+    """The point set's pad ring in the space of ``cartesian`` or ``cortical`` (empty when it
+    has none)."""
+    pads = getattr(coords, name, None)
+    if pads is None:
+        like = coords.cartesian if name == "cartesian_pad_coords" else coords.cortical
+        return torch.zeros(0, like.shape[1], dtype=like.dtype)
+    return pads.cpu()
 
 
 class KNNBaseLayer:
@@ -67,7 +91,7 @@ class KNNBaseLayer:
         if self.sample_cortex == "geodesic":
             raise NotImplementedError("geodesic neighbourhoods need pygeodesic, which is not available")
         in_c, out_c = self.in_coords, self.out_coords
-        pads = in_c.cartesian_pad_coords.cpu()
+        pads = _pad_coords(in_c)
         n_out = out_c.shape[0]
         if batch_size is None:
             batch_size = T.default_batch(in_c.shape[0] + pads.shape[0], n_out)
@@ -87,7 +111,7 @@ class KNNBaseLayer:
             return idx, dist
         if in_c.cortical is None:
             raise ValueError(f"style {in_c.style!r} has no cortical coordinates: use sample_cortex=False")
-        self.sample_coords = torch.cat([in_c.cortical.cpu(), in_c.cortical_pad_coords.cpu()], 0)
+        self.sample_coords = torch.cat([in_c.cortical.cpu(), _pad_coords(in_c, "cortical_pad_coords")], 0)
         return T.knn_euclidean(self.sample_coords, out_c.cortical.cpu(), self._k, batch_size)
 
     def _compute_all_distances(self):
@@ -98,14 +122,14 @@ class KNNBaseLayer:
         if self.sample_cortex == "geodesic":
             raise NotImplementedError("geodesic distances need pygeodesic, which is not available")
         in_c, out_c = self.in_coords, self.out_coords
-        pads = in_c.cartesian_pad_coords.cpu()
+        pads = _pad_coords(in_c)
         self.sample_coords_cart = torch.cat([in_c.cartesian.cpu(), pads], 0)
         if not self.sample_cortex:
             self.sample_coords = self.sample_coords_cart
             return torch.cdist(self.sample_coords, out_c.cartesian.cpu())
         if in_c.style not in ("isotropic", "isotropic_fixn"):
             raise ValueError(f"all-pairs cortical distances need the isotropic manifold, not {in_c.style!r}")
-        self.sample_coords = torch.cat([in_c.cortical.cpu(), in_c.cortical_pad_coords.cpu()], 0)
+        self.sample_coords = torch.cat([in_c.cortical.cpu(), _pad_coords(in_c, "cortical_pad_coords")], 0)
         return torch.cdist(self.sample_coords, out_c.cortical.cpu())
 
     def _gpu_tables(self, n_in):
@@ -149,7 +173,8 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
                  batch_size=None,
                  ):
         super().__init__()
-        assert isinstance(in_coords, SamplingCoords) and isinstance(out_coords, SamplingCoords)
+        _check_coords(in_coords, "in_coords")
+        _check_coords(out_coords, "out_coords")
         self.in_channels = in_channels
         self.out_channels = out_channels
         self.in_coords = in_coords
@@ -258,7 +283,7 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
                 raise NotImplementedError(f"arch_flag {arch_flag!r}: only square ref grids are built")
             ref, side = T.reference_grid(self._k, doubleres="doubleres" in arch_flag)
         self.ref_grid_size = side
-        self.ref_coords = ref.to(self.device, dtype=self.in_coords.dtype)
+        self.ref_coords = ref.to(self.device, dtype=getattr(self.in_coords, "dtype", torch.float32))
 
     def compute_local_rf_slots(self, knn_indices):
         if not self.sample_cortex:
@@ -308,6 +333,15 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         divided on the host: torch's device kernel divides by a scalar via its reciprocal."""
         amax = src.abs().amax(1).cpu()
         return torch.where(amax > 0, amax / 448.0, torch.ones_like(amax)).to(src.device)
+
+    def invalidate_packed_weights(self):
+        """Drops the packed copies of ``weight``. They are keyed on the parameter's version, which
+        ``copy_``, optimiser steps and ``load_state_dict`` bump; an in-place change through
+        ``weight.data`` does not, so call this after one."""
+        self._packed = {}
+        t = getattr(self, "_transposed_conv", None)
+        if t is not None:
+            t._weight_key = None
 
     def set_slot_order(self, order=None):
         """Order in which the wide-layer kernel visits the slots of a channel chunk (a
@@ -675,11 +709,15 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
                 raise ValueError(f"Conv2d kernel size {conv_weight.shape[2]}x{conv_weight.shape[3]} != "
                                  f"ref_grid_size {s}x{s}. Set strict=False to resample the kernel.")
             conv_weight = F.interpolate(conv_weight, size=(s, s), mode="bilinear", align_corners=True)
-        self.weight.data.copy_(conv_weight.reshape(conv_weight.shape[0], -1))
-        if conv_bias is not None and self.bias is not None:
-            self.bias.data.copy_(conv_bias.data)
-        elif conv_bias is not None and self.bias is None:
+        if conv_bias is not None and self.bias is None:
             raise ValueError("Conv2d has bias but layer does not. Recreate layer with bias=True.")
+        # copy_ on the parameter itself (not .data) bumps its version, which keys the packed
+        # weight caches; they are cleared as well
+        with torch.no_grad():
+            self.weight.copy_(conv_weight.reshape(conv_weight.shape[0], -1))
+            if conv_bias is not None:
+                self.bias.copy_(conv_bias.detach())
+        self.invalidate_packed_weights()
 
     def load_conv2d_weights(self, conv2d, strict=False):
         self._load_conv_2d_weight(conv2d.weight.data.clone(), conv2d.bias, strict=strict)
@@ -789,7 +827,8 @@ class KNNPoolingLayer(nn.Module, KNNBaseLayer):
         self.mode = mode
         self.sample_cortex = sample_cortex
         self.batch_size = batch_size
-        assert isinstance(in_coords, SamplingCoords) and isinstance(out_coords, SamplingCoords)
+        _check_coords(in_coords, "in_coords")
+        _check_coords(out_coords, "out_coords")
         self.k = torch.minimum(torch.tensor(self.k), torch.tensor(self.in_coords.shape[0]))   # knn.py:311
         self._k = int(self.k.item())
         knn_indices, knn_distances = self._compute_knns(batch_size)
@@ -909,6 +948,29 @@ def get_in_out_coords(in_res, fov, cmf_a, stride, style="isotropic", auto_match_
 KNN_CONV_REGISTRY = {
     "default": KNNConvLayer,
 }
+
+
+def register_with_reference(ref_knn, name="mi355x", ref_knnalexnet=None):
+    """Plugs the kernel-backed layers into an unmodified fovi checkout.
+
+    ``ref_knn`` is the reference's ``fovi.arch.knn`` module. Registers, under ``name`` in its
+    ``KNN_CONV_REGISTRY`` (``knn.py:1007-1030``, where ``KNNAlexNetBlock``,
+    ``knnalexnet.py:56-57``, and ``cfg.model.conv_layer_cls``, ``architectures.py:114``, look
+    layers up), a ``KNNConvLayer`` subclass that is also a subclass of the reference's
+    ``KNNBaseLayer``, so ``FoviNet.list_knn_layers`` (``fovinet.py:504-514``) and the
+    visualizer's ``isinstance`` filters (``visualizer.py:360,482``) find it. The layers take
+    the reference's ``SamplingCoords`` as they come. With ``ref_knnalexnet`` (the
+    reference's ``fovi.arch.knnalexnet``) its blocks also build the kernel-backed
+    ``KNNPoolingLayer`` (``knnalexnet.py:90-101``). Returns ``(conv_cls, pool_cls)``."""
+    base = ref_knn.KNNBaseLayer
+    conv = type("MI355XKNNConvLayer", (KNNConvLayer, base),
+                {"__module__": __name__, "__doc__": KNNConvLayer.__doc__})
+    pool = type("MI355XKNNPoolingLayer", (KNNPoolingLayer, base),
+                {"__module__": __name__, "__doc__": KNNPoolingLayer.__doc__})
+    ref_knn.KNN_CONV_REGISTRY[name] = conv
+    if ref_knnalexnet is not None:
+        ref_knnalexnet.KNNPoolingLayer = pool
+    return conv, pool
 
 
 def get_knn_conv_layer(name: str):

@@ -242,8 +242,9 @@ def csr_tables(knn_idx, slots, n_in, n_ref):
     zeros in the reference and are dropped; unused tail entries are ``-1``.
     """
     k, n_out = knn_idx.shape
-    if k > 0xFFFF:
-        raise ValueError(f"k={k} does not fit the 16-bit CSR fields")
+    if k > 0x7FFF:
+        # begin << 16 must stay a non-negative int32: the kernels decode it with a signed shift
+        raise ValueError(f"k={k} does not fit the CSR fields (k <= 32767)")
     idx = knn_idx.t().numpy().astype(np.int64)             # [N_out, k]
     sl = slots.numpy().astype(np.int64)
     valid = (idx >= 0) & (idx < n_in)

@@ -4,6 +4,9 @@
 namespace fovi {
 
 static thread_local std::string g_last_error;
+static thread_local const char* g_last_path = "";
+
+void note_path(const char* name) { g_last_path = name; }
 
 void set_error(const char* fmt, ...) {
   char buf[512];
@@ -30,3 +33,5 @@ int check_launch(const char* what) {
 extern "C" int fovi_abi_version(void) { return FOVI_ABI_VERSION; }
 
 extern "C" const char* fovi_last_error(void) { return fovi::g_last_error.c_str(); }
+
+extern "C" const char* fovi_knnconv_last_path(void) { return fovi::g_last_path; }

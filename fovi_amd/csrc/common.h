@@ -19,6 +19,10 @@ void clear_error();
 // Returns 0, or records the HIP error of the last launch and returns 1.
 int check_launch(const char* what);
 
+// Records (thread-local) the kernel path fovi_knnconv_fwd took; `name` must be
+// a string literal. Read back by fovi_knnconv_last_path().
+void note_path(const char* name);
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));

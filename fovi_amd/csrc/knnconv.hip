@@ -7,12 +7,17 @@
 // so the [B, C, k, N] gather tensor, the one-hot einsum and its permute copies
 // of the reference (fovi/arch/knn.py:484-526) are never materialised.
 //
-// Kernels
+// Kernels (fovi_knnconv_fwd picks one per call; fovi_knnconv_last_path names it)
 //  * knnconv_f32_kernel: fp32 operands, any strides, fp32 FMA SGEMM tiling.
 //    The fp32 parity path.
-//  * knnconv_bf16_v2_kernel: the main bf16 path (channels-last rows,
-//    c_in % 32 == 0): 256-point tiles, CSR lists staged in LDS; see below.
-//  * knnconv_bf16_kernel: bf16 operands, fp32 accumulate on
+//  * the wide-layer kernels (knnconv_v5.hip): fragment-order weights.
+//  * knnconv_bf16_v4_kernel: channels-last rows, c_in % 32 == 0, with the
+//    tile tables: input rows staged in LDS, single-neighbour slots read in
+//    place; see below.
+//  * knnconv_bf16_v2_kernel: channels-last rows, c_in % 32 == 0, without the
+//    tile tables (k > 255, or spans past LDS): CSR lists staged in LDS.
+//  * few-channel kernels (c_in <= 8, rows padded to 4 or 8 channels).
+//  * knnconv_bf16_kernel: any strides and channel counts: bf16 operands, fp32 accumulate on
 //    v_mfma_f32_32x32x16_bf16. 128-point x NT-channel tiles, 4 waves (2x2),
 //    64-wide reduction chunks double buffered in LDS (XOR-swizzled 16-byte
 //    chunks so the MFMA fragment reads are bank-conflict free), next chunk's
@@ -481,242 +486,10 @@ static int v2_tile_n(const KnnParams& p) {
 }
 
 // ---------------------------------------------------------------------------
-// bf16 MFMA path with the tile's input rows staged in LDS
+// Shared by the staged-row kernels below: 256-point tiles, 32-channel chunks.
 // ---------------------------------------------------------------------------
-// Same tile shape and MFMA core as v2. The inputs of a 256-point tile form a
-// contiguous index range (six rings for a two-ring tile on the log-polar
-// lattice), copied into LDS one 32-channel chunk at a time (S, row stride 64
-// bytes) with coalesced loads; the next chunk's rows are loaded into
-// registers a whole channel chunk ahead and written when S is free. Each
-// (slot, chunk) A tile is then assembled LDS -> LDS from S through the
-// tile's CSR words (first neighbour, count and list start in one 32-bit word
-// per (slot, point), stored slot-major so a slot's words are contiguous;
-// further neighbours from a uint16 list; sums in fp32 with one RNE rounding
-// via v_cvt_pk_bf16_f32), one iteration ahead of the MFMAs that consume it.
-// The only global loads inside the reduction loop are the weight tiles,
-// addressed as 32-bit per-lane offsets from uniform bases. Iterations run
-// channel chunk outer, slot inner.
 constexpr int V3_MT = 256;
 constexpr int V3_CC = 32;
-
-size_t v3_lds_bytes(int nt, int64_t V, int64_t K, int max_span) {
-  return static_cast<size_t>(max_span) * V3_CC * 2 + 2 * V3_MT * V3_CC * 2 + 2 * nt * V3_CC * 2 +
-         static_cast<size_t>(V3_MT) * static_cast<size_t>(V) * 4 +
-         ((static_cast<size_t>(V3_MT) * static_cast<size_t>(K) + 7) & ~static_cast<size_t>(7)) * 2;
-}
-
-
-template <int NT, int SV, typename OutT>
-__global__ __launch_bounds__(512, 1) void knnconv_bf16_v3_kernel(KnnParams p, int64_t tiles_per_b,
-                                                                 int64_t n_tiles_n, int64_t total_tiles,
-                                                                 int64_t padded_tiles) {
-  constexpr int WN = NT / 2;
-  constexpr int CB = WN / 32;
-  constexpr int B_VECS = (NT * V3_CC / 8 + 511) / 512;
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  uint16_t* As = reinterpret_cast<uint16_t*>(smem);                     // [2][256*32]
-  uint16_t* Bs = As + 2 * V3_MT * V3_CC;                                // [2][NT*32]
-  uint32_t* ent = reinterpret_cast<uint32_t*>(Bs + 2 * NT * V3_CC);     // [V][256] slot-major
-  uint16_t* nbl = reinterpret_cast<uint16_t*>(ent + V3_MT * p.V);       // [256][K]
-  uint16_t* S = nbl + ((V3_MT * p.K + 7) & ~static_cast<int64_t>(7));   // [max_span][32]
-
-  const int64_t tile = xcd_tile(blockIdx.x, padded_tiles);
-  if (tile >= total_tiles) return;
-  const int64_t mt = tile / n_tiles_n;
-  const int64_t o0 = (tile % n_tiles_n) * NT;
-  const int64_t b = mt / tiles_per_b;
-  const int64_t pt = mt % tiles_per_b;          // point tile within the batch row
-  const int64_t n0 = pt * V3_MT;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 3, wn = wave >> 2;
-  const int V = static_cast<int>(p.V), K = static_cast<int>(p.K);
-  const int64_t lo = p.tile_lo[pt];
-  const int span = static_cast<int>(min(static_cast<int64_t>(p.max_span), p.Nin - lo));
-
-  // CSR words, transposed to slot-major so one slot's 256 rows are contiguous
-  for (int i = tid; i < V3_MT * V; i += 512) {
-    const int r = i / V, v = i - r * V;
-    ent[v * V3_MT + r] = p.tile_ent[n0 * p.V + i];
-  }
-  for (int i = tid; i < V3_MT * K; i += 512) nbl[i] = p.tile_nbr[n0 * p.K + i];
-
-  // per-lane 32-bit byte offsets against uniform bases
-  const char* xrows = reinterpret_cast<const char*>(static_cast<const uint16_t*>(p.x) + b * p.xs0 + lo * p.xs2);
-  const char* wbase = reinterpret_cast<const char*>(static_cast<const uint16_t*>(p.w) + o0 * p.Kpad);
-  uint32_t s_off[SV], w_off[B_VECS];
-  uint32_t s_ok = 0, w_ok = 0;   // bit j: vector j of this lane is in range
-#pragma unroll
-  for (int j = 0; j < SV; ++j) {
-    const int q = tid + 512 * j;
-    s_ok |= static_cast<uint32_t>((q >> 2) < span) << j;
-    s_off[j] = static_cast<uint32_t>(((q >> 2) * p.xs2 + (q & 3) * 8) * 2);
-  }
-#pragma unroll
-  for (int i = 0; i < B_VECS; ++i) {
-    const int q = tid + 512 * i;
-    w_ok |= static_cast<uint32_t>(q < NT * 4 && o0 + (q >> 2) < p.Cout) << i;
-    w_off[i] = static_cast<uint32_t>(((q >> 2) * p.Kpad + (q & 3) * 8) * 2);
-  }
-  const int ncc = static_cast<int>(p.C / V3_CC);
-  const int nit = ncc * V;
-  const int part = tid & 3;
-  const int row0 = tid >> 2;
-
-  u32x4 rs[SV], rb[B_VECS];
-  auto load_s = [&](int cc) {
-    const char* base = xrows + cc * V3_CC * 2;
-#pragma unroll
-    for (int j = 0; j < SV; ++j)
-      rs[j] = ((s_ok >> j) & 1) ? *reinterpret_cast<const u32x4*>(base + s_off[j]) : u32x4{0u, 0u, 0u, 0u};
-  };
-  auto store_s = [&]() {
-#pragma unroll
-    for (int j = 0; j < SV; ++j)
-      if ((s_ok >> j) & 1) *reinterpret_cast<u32x4*>(&S[(tid + 512 * j) * 8]) = rs[j];
-  };
-  auto load_w = [&](int cc, int v) {
-    const char* base = wbase + (static_cast<int64_t>(v) * p.C + cc * V3_CC) * 2;
-#pragma unroll
-    for (int i = 0; i < B_VECS; ++i)
-      rb[i] = ((w_ok >> i) & 1) ? *reinterpret_cast<const u32x4*>(base + w_off[i]) : u32x4{0u, 0u, 0u, 0u};
-  };
-  auto store_w = [&](int buf) {
-    uint16_t* bsm = Bs + buf * NT * V3_CC;
-#pragma unroll
-    for (int i = 0; i < B_VECS; ++i) {
-      const int q = tid + 512 * i;
-      if (q < NT * 4) *reinterpret_cast<u32x4*>(&bsm[swz32(q >> 2, q & 3)]) = rb[i];
-    }
-  };
-  auto build_a = [&](int v, int buf) {
-    uint16_t* a = As + buf * V3_MT * V3_CC;
-    const uint32_t* ev = ent + v * V3_MT;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int row = row0 + 128 * i;
-      const uint32_t e = ev[row];
-      const int cnt = (e >> 8) & 0xff;
-      u32x4 r = u32x4{0u, 0u, 0u, 0u};
-      if (cnt != 0) r = *reinterpret_cast<const u32x4*>(&S[(e >> 16) * V3_CC + part * 8]);
-      if (cnt > 1) {
-        const uint16_t* nb = nbl + row * K + (e & 0xff);
-        f32x8 acc8 = unpack_bf16x8(r);
-        for (int j = 1; j < cnt; ++j) acc8 += unpack_bf16x8(*reinterpret_cast<const u32x4*>(&S[nb[j] * V3_CC + part * 8]));
-        r = u32x4{cvt_pk_bf16(acc8[0], acc8[1]), cvt_pk_bf16(acc8[2], acc8[3]), cvt_pk_bf16(acc8[4], acc8[5]),
-                  cvt_pk_bf16(acc8[6], acc8[7])};
-      }
-      *reinterpret_cast<u32x4*>(&a[swz32(row, part)]) = r;
-    }
-  };
-
-  f32x16 acc[2][CB];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < CB; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-  // prologue: S(0), W(0), A(0); S(1) in flight
-  load_s(0);
-  load_w(0, 0);
-  store_s();
-  store_w(0);
-  if (ncc > 1) load_s(1);
-  __syncthreads();
-  build_a(0, 0);
-  __syncthreads();
-
-  int cc1 = 0, v1 = 0;   // chunk and slot of iteration it + 1
-  for (int it = 0; it < nit; ++it) {
-    const int cur = it & 1;
-    if (++v1 == V) { v1 = 0; ++cc1; }
-    const bool more = it + 1 < nit;
-    if (more) {
-      load_w(cc1, v1);
-      if (v1 == 0) {            // next iteration starts channel chunk cc1: refresh S
-        store_s();
-        __syncthreads();
-        if (cc1 + 1 < ncc) load_s(cc1 + 1);
-      }
-      build_a(v1, cur ^ 1);
-    }
-    const uint16_t* a = As + cur * V3_MT * V3_CC;
-    const uint16_t* bsm = Bs + cur * NT * V3_CC;
-#pragma unroll
-    for (int ks = 0; ks < V3_CC / 16; ++ks) {
-      const int q = ks * 2 + (lane >> 5);
-      bf16x8 af[2], bfr[CB];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        af[i] = *reinterpret_cast<const bf16x8*>(&a[swz32(wm * 64 + i * 32 + (lane & 31), q)]);
-#pragma unroll
-      for (int j = 0; j < CB; ++j)
-        bfr[j] = *reinterpret_cast<const bf16x8*>(&bsm[swz32(wn * WN + j * 32 + (lane & 31), q)]);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < CB; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
-    }
-    if (more) store_w(cur ^ 1);
-    __syncthreads();
-  }
-
-  OutT* y = static_cast<OutT*>(p.y) + b * p.ys0;
-#pragma unroll
-  for (int j = 0; j < CB; ++j) {
-    const int64_t o = o0 + wn * WN + j * 32 + (lane & 31);
-    if (o >= p.Cout) continue;
-    const float bo = p.bias ? p.bias[o] : 0.0f;
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t n = n0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (n < p.Nout) Elem<OutT>::store(y + o * p.ys1 + n * p.ys2, epilogue(acc[i][j][r] + bo, p.relu));
-      }
-  }
-}
-
-template <int NT, int SV>
-static void launch_bf16_v3_sv(const KnnParams& p, int out_t, hipStream_t s) {
-  const int64_t tiles_per_b = (p.Nout + V3_MT - 1) / V3_MT;
-  const int64_t n_tiles_n = (p.Cout + NT - 1) / NT;
-  const int64_t total = p.B * tiles_per_b * n_tiles_n;
-  const int64_t padded = (total + 7) / 8 * 8;
-  const size_t lds = v3_lds_bytes(NT, p.V, p.K, p.max_span);
-  dim3 grid(static_cast<unsigned>(padded));
-  if (out_t == FOVI_BF16) {
-    hipFuncSetAttribute(reinterpret_cast<const void*>(&knnconv_bf16_v3_kernel<NT, SV, uint16_t>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    hipLaunchKernelGGL((knnconv_bf16_v3_kernel<NT, SV, uint16_t>), grid, dim3(512), lds, s, p, tiles_per_b,
-                       n_tiles_n, total, padded);
-  } else {
-    hipFuncSetAttribute(reinterpret_cast<const void*>(&knnconv_bf16_v3_kernel<NT, SV, float>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    hipLaunchKernelGGL((knnconv_bf16_v3_kernel<NT, SV, float>), grid, dim3(512), lds, s, p, tiles_per_b,
-                       n_tiles_n, total, padded);
-  }
-}
-
-template <int NT>
-static bool launch_bf16_v3(const KnnParams& p, int out_t, hipStream_t s) {
-  const int sv = (p.max_span * 4 + 511) / 512;
-  if (sv <= 2) launch_bf16_v3_sv<NT, 2>(p, out_t, s);
-  else if (sv <= 4) launch_bf16_v3_sv<NT, 4>(p, out_t, s);
-  else if (sv <= 6) launch_bf16_v3_sv<NT, 6>(p, out_t, s);
-  else if (sv <= 8) launch_bf16_v3_sv<NT, 8>(p, out_t, s);
-  else return false;
-  return true;
-}
-
-// Widest channel tile whose LDS footprint fits with the staged rows; 0 if none.
-static int v3_tile_n(const KnnParams& p) {
-  if (p.max_span <= 0 || p.max_span > 1024) return 0;
-  return pick_tile_n(p.Cout, [&](int nt) { return v3_lds_bytes(nt, p.V, p.K, p.max_span) <= 160 * 1024; });
-}
 
 // ---------------------------------------------------------------------------
 // bf16 MFMA path reading single-neighbour slots straight from the staged rows
@@ -1508,6 +1281,7 @@ extern "C" int fovi_knnconv_pack_weight(const float* w_ref, int64_t c_out, int64
 extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
   using namespace fovi;
   clear_error();
+  note_path("");
   if (!a) { set_error("fovi_knnconv_fwd: null args"); return 1; }
   if (!a->x || !a->slot_ptr || !a->nbr_sorted || !a->w || !a->y) {
     set_error("fovi_knnconv_fwd: null pointer argument"); return 1;
@@ -1516,7 +1290,8 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
       a->c_out <= 0) {
     set_error("fovi_knnconv_fwd: bad sizes"); return 1;
   }
-  if (a->k > 65535) { set_error("fovi_knnconv_fwd: k=%lld exceeds 65535", (long long)a->k); return 1; }
+  // slot_ptr entries are begin << 16 | count in an int32 decoded with a signed shift: begin < 2^15
+  if (a->k > 32767) { set_error("fovi_knnconv_fwd: k=%lld exceeds 32767", (long long)a->k); return 1; }
   if (a->w_layout == FOVI_W_ROWS && a->k_pad % MM_KC != 0) {
     set_error("fovi_knnconv_fwd: k_pad=%lld must be a multiple of 64 >= c_in*n_ref=%lld",
               (long long)a->k_pad, (long long)(a->c_in * a->n_ref));
@@ -1568,6 +1343,7 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
       set_error("fovi_knnconv_fwd: tile span too large for the fragment-order kernel");
       return 1;
     }
+    note_path(f8 ? "fp8 v5" : "bf16 v5");
     return check_launch(f8 ? "fovi_knnconv_fwd(fp8 v5)" : "fovi_knnconv_fwd(bf16 v5)");
   }
 
@@ -1581,10 +1357,12 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
       hipLaunchKernelGGL((knnconv_f32_kernel<float>), grid, dim3(256), 0, s, p, tiles_per_b);
     else
       hipLaunchKernelGGL((knnconv_f32_kernel<uint16_t>), grid, dim3(256), 0, s, p, tiles_per_b);
+    note_path("f32");
     return check_launch("fovi_knnconv_fwd(f32)");
   }
   if (a->x_dtype == FOVI_F8E4M3 && a->w_dtype == FOVI_F8E4M3) {
     if (p.w_c_slot != p.C) { set_error("fovi_knnconv_fwd(fp8): w_c_slot must equal c_in"); return 1; }
+    note_path("fp8 rows");
     return launch_knnconv_fp8(p, a->y_dtype, s);
   }
   if (a->x_dtype == FOVI_BF16 && a->w_dtype == FOVI_BF16 && p.w_c_slot != p.C) {
@@ -1596,9 +1374,13 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
                             static_cast<uint64_t>(p.Kpad) * 2u;
       if (a->workspace && static_cast<uint64_t>(a->workspace_bytes) >= need &&
           reinterpret_cast<uintptr_t>(a->workspace) % 16 == 0)
+      {
+        note_path("bf16 few-channel two-pass");
         return launch_two_pass(p, cp, static_cast<uint16_t*>(a->workspace), a->y_dtype, s);
+      }
       if (cp == 4) launch_bf16_smallc_nt<4>(p, a->y_dtype, s);
       else launch_bf16_smallc_nt<8>(p, a->y_dtype, s);
+      note_path("bf16 few-channel");
       return check_launch("fovi_knnconv_fwd(bf16 small-c)");
     }
     set_error("fovi_knnconv_fwd: w_c_slot=%d needs channels-last input rows padded to it", cp);
@@ -1618,14 +1400,10 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
       else if (nt4 == 192) ok4 = launch_bf16_v4<192>(p, a->y_dtype, s);
       else if (nt4 == 128) ok4 = launch_bf16_v4<128>(p, a->y_dtype, s);
       else if (nt4 == 64) ok4 = launch_bf16_v4<64>(p, a->y_dtype, s);
-      if (ok4) return check_launch("fovi_knnconv_fwd(bf16 v4)");
-      const int nt = v3_tile_n(p);
-      bool ok = false;
-      if (nt == 256) ok = launch_bf16_v3<256>(p, a->y_dtype, s);
-      else if (nt == 192) ok = launch_bf16_v3<192>(p, a->y_dtype, s);
-      else if (nt == 128) ok = launch_bf16_v3<128>(p, a->y_dtype, s);
-      else if (nt == 64) ok = launch_bf16_v3<64>(p, a->y_dtype, s);
-      if (ok) return check_launch("fovi_knnconv_fwd(bf16 v3)");
+      if (ok4) {
+        note_path("bf16 v4");
+        return check_launch("fovi_knnconv_fwd(bf16 v4)");
+      }
     }
     if (rows16 && p.C % V2_CC == 0) {
       const int nt = v2_tile_n(p);
@@ -1634,7 +1412,10 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
       else if (nt == 192) rc = launch_bf16_v2<192>(p, a->y_dtype, s);
       else if (nt == 128) rc = launch_bf16_v2<128>(p, a->y_dtype, s);
       else if (nt == 64) rc = launch_bf16_v2<64>(p, a->y_dtype, s);
-      if (rc == 0) return check_launch("fovi_knnconv_fwd(bf16 v2)");
+      if (rc == 0) {
+        note_path("bf16 v2");
+        return check_launch("fovi_knnconv_fwd(bf16 v2)");
+      }
     }
     const bool vec = rows16 && p.C % MM_KC == 0;
     const bool wide = p.Cout % 128 == 0;
@@ -1642,6 +1423,7 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
     else if (vec) launch_bf16<64, true>(p, a->y_dtype, s);
     else if (wide) launch_bf16<128, false>(p, a->y_dtype, s);
     else launch_bf16<64, false>(p, a->y_dtype, s);
+    note_path(vec ? "bf16 generic (rows)" : "bf16 generic");
     return check_launch("fovi_knnconv_fwd(bf16)");
   }
   set_error("fovi_knnconv_fwd: unsupported dtypes x=%d w=%d", a->x_dtype, a->w_dtype);

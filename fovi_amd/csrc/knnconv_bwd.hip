@@ -210,6 +210,8 @@ extern "C" int fovi_knnconv_slotsum(const fovi_knnconv_slotsum_args* a, void* st
   if (a->batch < 0 || a->c_in < 1 || a->n_in < 0 || a->n_out < 0 || a->k < 1 || a->n_ref < 1) {
     set_error("fovi_knnconv_slotsum: bad sizes"); return 1;
   }
+  // slot_ptr entries are begin << 16 | count in an int32 decoded with a signed shift: begin < 2^15
+  if (a->k > 32767) { set_error("fovi_knnconv_slotsum: k=%lld exceeds 32767", (long long)a->k); return 1; }
   if (a->batch * a->n_out == 0) return 0;
   SlotsumParams p;
   p.x = a->x; p.B = a->batch; p.C = a->c_in; p.Nin = a->n_in; p.Nout = a->n_out; p.K = a->k; p.V = a->n_ref;

@@ -110,11 +110,17 @@ struct Taps {
       ix = fminf(fmaxf(ix, 0.0f), W - 1.0f);
       iy = fminf(fmaxf(iy, 0.0f), H - 1.0f);
     }
+    // Every bounds decision below is a float comparison (false for NaN), and
+    // coordinates are clamped to [-1, size] before any integer conversion, so
+    // infinite, NaN or huge coordinates select no tap and convert defined
+    // values (they sample zeros, as the reference's grid_sample does).
     if (MODE == FOVI_NEAREST) {
       const float rx = __builtin_rintf(ix);
       const float ry = __builtin_rintf(iy);
       inb = rx >= 0.0f && rx < W && ry >= 0.0f && ry < H;
-      off = inb ? static_cast<Off>(ry) * static_cast<Off>(p.is2) + static_cast<Off>(rx) * static_cast<Off>(p.is3) : 0;
+      const Off ox = static_cast<Off>(fminf(fmaxf(rx, 0.0f), W - 1.0f));
+      const Off oy = static_cast<Off>(fminf(fmaxf(ry, 0.0f), H - 1.0f));
+      off = inb ? oy * static_cast<Off>(p.is2) + ox * static_cast<Off>(p.is3) : 0;
       return;
     }
     const float fx = floorf(ix);
@@ -127,10 +133,12 @@ struct Taps {
     const bool x0 = fx >= 0.0f && fx < W, x1 = fx + 1.0f >= 0.0f && fx + 1.0f < W;
     y0 = fy >= 0.0f && fy < H;
     y1 = fy + 1.0f >= 0.0f && fy + 1.0f < H;
-    cx = static_cast<Off>(fx);
-    const Off cy = static_cast<Off>(fy);
+    cx = static_cast<Off>(fminf(fmaxf(fx, -1.0f), W));
+    const Off cy = static_cast<Off>(fminf(fmaxf(fy, -1.0f), H));
     const Off is2 = static_cast<Off>(p.is2), is3 = static_cast<Off>(p.is3);
-    pair = PAIRS && PixelPair<InT>::fits(cx, static_cast<Off>(p.W));
+    // the pair path needs both columns inside the image (float test) and, for bf16, the
+    // 8-byte word pair inside the row (integer test on the clamped column)
+    pair = PAIRS && x0 && x1 && PixelPair<InT>::fits(cx, static_cast<Off>(p.W));
     if (pair) {  // both columns inside the image; rows checked per row
       o_nw = y0 ? cy * is2 : 0;
       o_sw = y1 ? (cy + 1) * is2 : 0;

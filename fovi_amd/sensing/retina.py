@@ -19,7 +19,13 @@ __all__ = ["RetinalTransform", "GaussianColorDecay"]
 
 
 class GaussianColorDecay(nn.Module):
-    """``x * exp(-radius / sigma)``; identity for ``sigma=None`` (reference ``retina.py:365-404``)."""
+    """``x[b, c, n] * exp(-radius[n] / sigma)``; identity for ``sigma=None`` (reference
+    ``retina.py:365-404``).
+
+    Deviation: the reference multiplies the sampled ``[B, C, N]`` by ``decay.unsqueeze(1)``,
+    an ``[N, 1]`` tensor, which broadcasts as ``[1, N, 1]`` against the channel axis: it
+    raises for 1 < C != N and returns ``[B, N, N]`` for C = 1. Here the decay is applied per
+    sensor point, the eccentricity weighting that module describes."""
 
     def __init__(self, sigma):
         super().__init__()
@@ -108,8 +114,10 @@ class RetinalTransform(nn.Module):
         if self.foveal_color is not None:
             x = self.foveal_color(x, self.sampler.polar_radius)
         if not self.training and self.no_color_val:
-            w = torch.tensor([0.2989, 0.587, 0.114], dtype=x.dtype, device=x.device).view(1, 3, 1)
-            x = (x * w).sum(1, keepdim=True).expand(-1, 3, -1).clone()
+            # torchvision's rgb_to_grayscale(num_output_channels=3) of the reference (retina.py:150):
+            # 0.2989 R + 0.587 G + 0.114 B in x's dtype, repeated over three channels
+            r, g, b = x.unbind(1)
+            x = (0.2989 * r + 0.587 * g + 0.114 * b).to(x.dtype).unsqueeze(1).expand(-1, 3, -1).clone()
         if self.reshape_as_grid:
             x = x.reshape(x.shape[0], x.shape[1], self.resolution, self.resolution)
         return x.to(self.dtype)

@@ -43,6 +43,8 @@ def fixation_half_sizes(fixation_size, n):
         fs = fs.expand(n, 2)
     if fs.shape != (n, 2):
         raise ValueError(f"fixation_size must be [{n}, 2] (h, w); got {tuple(fs.shape)}")
+    if not bool(torch.isfinite(fs.to(torch.float64)).all()):
+        raise ValueError("fixation_size must be finite")
     half = fs / 2
     wide = half.dtype == torch.float64
     return half.to(torch.float64).contiguous(), int(wide)
@@ -104,7 +106,11 @@ class GridSampler(BaseGridSampler):
         pixels; ``view_image [V]`` image index per view (default: view v
         reads image v).
         """
-        fix_loc = torch.as_tensor(fix_loc, dtype=torch.float32).reshape(-1, 2).to(device).contiguous()
+        fix_loc = torch.as_tensor(fix_loc, dtype=torch.float32).reshape(-1, 2)
+        # non-finite centres or sizes would put taps at undefined pixel coordinates
+        if not bool(torch.isfinite(fix_loc).all()):
+            raise ValueError("fix_loc must be finite")
+        fix_loc = fix_loc.to(device).contiguous()
         n_views = fix_loc.shape[0]
         half, wide = fixation_half_sizes(fixation_size, n_views)
         vmap = None

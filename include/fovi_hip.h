@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 20
+#define FOVI_ABI_VERSION 21
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -93,7 +93,8 @@ int fovi_sampler_fwd(const fovi_sampler_args* args, void* stream);
  *
  * Neighbour lists are slot-major CSR per output point:
  *   slot_ptr[n * n_ref + v] = (begin << 16) | count, and the input indices
- *   are nbr_sorted[n * k + begin + i], i < count.
+ *   are nbr_sorted[n * k + begin + i], i < count (k <= 32767, so every entry
+ *   is a non-negative int32).
  * The weight is the packed form made by fovi_knnconv_pack_weight: row o holds
  * the reduction axis in slot-major order (v * c_in + c), zero padded to
  * k_pad (a multiple of 64).
@@ -113,7 +114,8 @@ int fovi_sampler_fwd(const fovi_sampler_args* args, void* stream);
  * tile_lo[t] .. tile_lo[t] + tile_span[t] - 1 (max_span = max tile_span);
  * tile_ent[n * n_ref + v] = (first << 16) | (count << 8) | begin and
  * tile_nbr[n * k + begin + i] = input index - tile_lo[t] (first = the i = 0
- * entry; zero_row when count is 0), same lists as the CSR tables. Used for
+ * entry; zero_row when count is 0), same lists as the CSR tables. With
+ * tile_coll / tile_coll_n also given they select the staged-row kernel for
  * channels-last bf16 input when the rows fit in LDS (k <= 255).
  * tile_coll[t * n_ref * tile_points + v * tile_points + i], i < tile_coll_n[t * n_ref + v],
  * lists the tile rows whose slot v has two or more neighbours (decreasing
@@ -193,6 +195,17 @@ typedef struct fovi_knnconv_args {
 } fovi_knnconv_args;
 
 int fovi_knnconv_fwd(const fovi_knnconv_args* args, void* stream);
+
+/*
+ * The kernel path the last successful fovi_knnconv_fwd call on this thread
+ * took ("" before any, or after a failed call): "f32", "bf16 v5", "fp8 v5",
+ * "fp8 rows", "bf16 v4", "bf16 v2", "bf16 few-channel", "bf16 few-channel
+ * two-pass", "bf16 generic (rows)" or "bf16 generic". Diagnostics only (no
+ * counterpart in the reference, whose forward is a fixed op sequence,
+ * fovi/arch/knn.py:538-557); tests use it to check which kernel a layer
+ * geometry selects.
+ */
+const char* fovi_knnconv_last_path(void);
 
 /*
  * Packs the reference weight layout for fovi_knnconv_fwd.

@@ -6,6 +6,15 @@ import torch
 import torch.nn.functional as F
 
 
+def grid_from_cartesian(cartesian):
+    """``[1, 1, N, 2]`` grid_sample grid of ``[N, 2]`` sensor points (x, y): column = x,
+    row = -y (reference ``BaseGridSampler._prep_grid_for_grid_sample``,
+    fovi/sensing/samplers.py:35-47, via ``xy_to_colrow(..., do_norm=False, format='-11')``,
+    fovi/sensing/coords.py:530-564)."""
+    cartesian = torch.as_tensor(cartesian)
+    return torch.stack((cartesian[:, 0], -cartesian[:, 1]), dim=1)[None, None]
+
+
 def transform_sampling_grid(sampling_grid, fix_loc, fixation_size, image_size):
     """Fixation transform of a (1,1,N,2) (x,-y) grid (reference fovi/sensing/coords.py:590-642).
 

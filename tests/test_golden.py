@@ -65,3 +65,16 @@ def test_tables_match_reference_vectors(golden, name):
 
 def test_fixture_records_torch_version(golden):
     assert str(golden["torch_version"]).startswith("2.")
+
+
+@pytest.mark.parametrize("name,res", [("c1", 64), ("c2_l2", 32), ("c2_l3", 16)])
+def test_sampling_grid_from_reference_cartesian(golden, name, res):
+    """GridSampler.sampling_grid is the grid the reference's _prep_grid_for_grid_sample makes
+    from its own sensor points (samplers.py:35-47): bit-identical (x, -y) rows."""
+    import torch
+
+    from fovi_amd.sensing.samplers import GridSampler
+    from oracle import sampler_ref
+    cart = torch.from_numpy(golden[f"{name}__in_cartesian"])
+    s = GridSampler(16, 2.78, res, device="cpu", style="logpolar")
+    assert torch.equal(s.sampling_grid, sampler_ref.grid_from_cartesian(cart))

@@ -199,3 +199,37 @@ def test_fp8_fragment_order_kernel(res_in, res_out, k, c_in, c_out, bias, act, b
     assert _cos(got.float().cpu(), ref) >= 0.9999
     assert_close_rel(y.float().cpu(), y_rows.float().cpu(), 1e-2, "fragment-order vs row-packed (fp8)")
     assert torch.equal(y_plain, y_rows), "fp8 fragment-order (plain slot order) and row-packed kernels differ"
+
+
+def test_c5_full_batch_cosines_per_scale():
+    """C5 at its full B=64. References, both at B=64 on the fp32 kernel (pinned to the oracle at
+    1e-5 by test_gpu_knnconv.py): the unquantized fp32 layer, and the fp32 formula on the
+    dequantized operands (e4m3 activations and weights, slot sums kept in fp32). Bars: cosine
+    >= 0.995 against the unquantized layer for the layer's scale amax * headroom / 448
+    (headroom 32 = the largest slot count 23 rounded up to a power of two); >= 0.9999 against
+    the dequantized formula (the kernel's extra e4m3 rounding of multi-neighbour slot sums).
+    The plain amax / 448 scale is measured for the record: its slot sums of up to 23 values can
+    pass 448 and saturate."""
+    layer = _layer(128, 128, 25, 256, 256, seed=11)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(64, 16384, 256, generator=g).bfloat16().cuda().transpose(1, 2)
+    assert layer.fp8_headroom == 32.0
+    results = {}
+    with torch.no_grad():
+        y32 = layer(x.float())                                   # unquantized fp32
+        for name, headroom in (("amax*32/448", layer.fp8_headroom), ("amax/448", 1.0)):
+            xq = quantize_e4m3(x, headroom)
+            y8 = layer(xq).float()
+            results[name] = _cos(y8, y32)
+            if name == "amax*32/448":
+                w_packed, w_scale = layer._packed_weight(torch.float8_e4m3fn)
+                w_deq = (knnconv_ref.quantize_e4m3(layer.weight.detach().cpu(), w_scale.cpu()[:, None]).float()
+                         * w_scale.cpu()[:, None])
+                w_keep = layer.weight.detach().clone()
+                layer.weight.copy_(w_deq.cuda())
+                y_deq = layer(xq.dequantize())
+                layer.weight.copy_(w_keep)
+                results["vs dequantized formula"] = _cos(y8, y_deq)
+    print("C5 cosines:", {k: round(v, 6) for k, v in results.items()}, flush=True)
+    assert results["amax*32/448"] >= 0.995
+    assert results["vs dequantized formula"] >= 0.9999

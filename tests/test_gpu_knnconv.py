@@ -278,3 +278,54 @@ def test_fragment_order_kernel_falls_back_when_tables_exceed_lds():
     assert layer.last_weight_layout == "rows"
     ref = _oracle(layer, x, layer.weight.detach().cpu().bfloat16().float())
     assert_close_rel(y.float().cpu(), ref, 1e-2)
+
+
+# Kernel path each benchmark geometry selects (fovi_knnconv_last_path), with the oracle check
+# for the paths no other test reaches on purpose.
+_SELECTION = [
+    # name, (res_in, res_out, k, c_in, c_out, side), input, expected path
+    ("C1 fp32", (64, 64, 9, 3, 64, None), "f32", "f32"),
+    ("C1 bf16", (64, 64, 9, 3, 64, None), "bf16", "bf16 few-channel two-pass"),
+    ("C2 layer 1", (64, 32, 49, 3, 64, None), "bf16", "bf16 few-channel two-pass"),
+    ("C2 layer 2", (32, 16, 25, 64, 192, None), "bf16", "bf16 v4"),
+    ("C2 layer 3", (16, 16, 9, 192, 384, None), "bf16", "bf16 v5"),
+    ("C2 layer 4", (16, 16, 9, 384, 256, None), "bf16", "bf16 v5"),
+    ("C2 layer 5", (16, 16, 9, 256, 256, None), "bf16", "bf16 v5"),
+    ("C3", (128, 128, 25, 256, 256, None), "bf16", "bf16 v5"),
+    ("C4 patch embedding", (128, 16, 256, 3, 384, 16), "bf16", "bf16 few-channel two-pass"),
+    ("C5", (128, 128, 25, 256, 256, None), "fp8", "fp8 v5"),
+    ("fp8, narrow output", (32, 16, 25, 64, 64, None), "fp8", "fp8 rows"),
+    ("bf16 channel-major", (32, 16, 25, 64, 192, None), "bf16 channel-major", "bf16 generic"),
+    ("bf16 rows, c_in % 32 != 0", (16, 16, 9, 48, 64, None), "bf16", "bf16 generic"),
+    ("bf16 rows, k = 256", (32, 4, 256, 64, 96, 16), "bf16", "bf16 generic (rows)"),
+    ("bf16 without tile tables", (32, 16, 25, 64, 192, None), "bf16 no tiles", "bf16 v2"),
+]
+
+
+@pytest.mark.parametrize("name,geom,mode,path", _SELECTION, ids=[s[0] for s in _SELECTION])
+def test_kernel_selection(name, geom, mode, path):
+    from fovi_amd import _lib
+    res_in, res_out, k, c_in, c_out, side = geom
+    layer = _layer(res_in, res_out, k, c_in, c_out, side, bias=True)
+    if mode == "bf16 no tiles":
+        layer.tile_lo = None            # a caller without the tile tables
+    x = torch.randn(1, c_in, res_in * res_in, generator=torch.Generator().manual_seed(21))
+    xd = x.cuda()
+    if mode == "f32":
+        run = lambda: layer(xd)
+    elif mode == "fp8":
+        xq = layer.quantize_input(xd.bfloat16().transpose(1, 2).contiguous().transpose(1, 2))
+        run = lambda: layer(xq)
+    else:
+        xd = xd.bfloat16()
+        if mode != "bf16 channel-major":
+            xd = xd.transpose(1, 2).contiguous().transpose(1, 2)
+        run = lambda: layer(xd)
+    with torch.no_grad():
+        y = run()
+    assert _lib.knnconv_last_path() == path, f"{name}: took {_lib.knnconv_last_path()!r}"
+    if path in ("bf16 v2", "bf16 generic (rows)", "bf16 generic", "fp8 rows"):
+        if path == "fp8 rows":
+            return          # the row-packed e4m3 kernel: tests/test_gpu_fp8.py
+        ref = _oracle(layer, x.bfloat16(), layer.weight.detach().cpu().bfloat16().float())
+        assert_close_rel(y.float().cpu(), ref, 1e-2, name)

@@ -5,6 +5,8 @@ bilinear fp32 values within 1e-5 relative (L2 and max-abs/max|ref|) and at
 least 99.9% of them bit-identical to torch's CPU grid_sample (the kernel uses
 its fused-multiply-add rounding); bf16 outputs within 1e-2 relative.
 """
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -171,3 +173,81 @@ def test_ring_blocked_order_equals_point_order(mode, pad, dt, channels):
     ref, _ = sampler_ref.sampler_forward(img[1:2].float().cpu(), s.sampling_grid.cpu(), fix[2:3], sizes[:1],
                                          mode, pad)
     assert_close_rel(blocked[2:3].float().cpu(), ref, 1e-5 if dt == torch.float32 else 1e-2)
+
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "tables.npz")
+
+
+@pytest.mark.parametrize("mode", ["nearest", "bilinear"])
+def test_oracle_grid_from_reference_cartesian(mode):
+    """The oracle's grid comes from the reference-written sensor points (64x64 log-polar,
+    tests/golden/tables.npz) through the reference's (x, -y) mapping, not from the build's
+    own sampling_grid."""
+    cart = torch.from_numpy(np.load(GOLDEN)["c1__in_cartesian"])
+    g = torch.Generator().manual_seed(12)
+    img = torch.rand(3, 3, 200, 240, generator=g)
+    fix_loc = torch.tensor([[0.5, 0.5], [0.35, 0.6], [0.7, 0.3]])
+    fix_size = np.array([[200, 240], [150, 150], [256, 200]])
+    s = GridSampler(16, 2.78, 64, device="cuda", mode=mode, style="logpolar")
+    out, grid = s.sample_views(img.cuda(), fix_loc, fix_size, return_grid=True)
+    ref, ref_grid = sampler_ref.sampler_forward(img, sampler_ref.grid_from_cartesian(cart), fix_loc, fix_size,
+                                                mode)
+    assert torch.equal(grid.cpu(), ref_grid.squeeze(1))
+    if mode == "nearest":
+        assert torch.equal(out.cpu(), ref)
+    else:
+        assert_close_rel(out.cpu(), ref, 1e-5, "bilinear vs the reference-cartesian oracle")
+
+
+@pytest.mark.parametrize("mode", ["nearest", "bilinear"])
+@pytest.mark.parametrize("axis", ["rows", "columns"])
+def test_half_lit_image_known_answer(mode, axis):
+    """Known answer of the axis convention: with the top half of the image lit (rows < H/2),
+    every sensor point above the fixation (y > 0, clear of the middle row) samples 1 and every
+    point below samples 0; with the right half lit (columns >= W/2), points with x > 0 sample
+    1. Centre fixation, window = image."""
+    H = W = 256
+    img = torch.zeros(2, 3, H, W)
+    if axis == "rows":
+        img[:, :, : H // 2, :] = 1.0
+    else:
+        img[:, :, :, W // 2:] = 1.0
+    s = GridSampler(16, 2.78, 64, device="cuda", mode=mode, style="logpolar")
+    out = s.sample_views(img.cuda(), torch.full((2, 2), 0.5), np.array([[H, W]] * 2)).cpu()
+    cart = s.coords.cartesian.cpu()
+    coord = cart[:, 1] if axis == "rows" else cart[:, 0]
+    margin = 2.0 / H      # one pixel in normalised units: clear of the lit edge (bilinear blends 1 px)
+    hi, lo = coord > margin, coord < -margin
+    assert hi.sum() > 1000 and lo.sum() > 1000
+    assert torch.all(out[:, :, hi] == 1.0), "points on the lit side did not sample 1"
+    assert torch.all(out[:, :, lo] == 0.0), "points on the dark side did not sample 0"
+    ref, _ = sampler_ref.sampler_forward(img, s.sampling_grid.cpu(), torch.full((2, 2), 0.5),
+                                         np.array([[H, W]] * 2), mode)
+    assert torch.all(ref[:, :, hi] == 1.0) and torch.all(ref[:, :, lo] == 0.0)
+
+
+def test_colour_decay_and_eval_grayscale():
+    """sigma: samples x exp(-r / sigma) per sensor point (r = the sampler's polar radius);
+    eval with no_color_val: 0.2989 R + 0.587 G + 0.114 B on all three channels (torchvision's
+    rgb_to_grayscale, reference retina.py:148-150). The reference's own decay expression
+    (x * decay.unsqueeze(1), retina.py:398-401) cannot broadcast [B, 3, N] against [N, 1]."""
+    g = torch.Generator().manual_seed(13)
+    img = torch.rand(3, 3, 128, 128, generator=g)
+    sigma = 0.35
+    rt = RetinalTransform(32, start_res=128, fov=16, cmf_a=2.78, style="logpolar", sampler="grid_bilinear",
+                          device="cuda", sigma=sigma, auto_match_cart_resources=0)
+    plain = RetinalTransform(32, start_res=128, fov=16, cmf_a=2.78, style="logpolar", sampler="grid_bilinear",
+                             device="cuda", auto_match_cart_resources=0)
+    base = plain(img.cuda(), (0.5, 0.5)).cpu()
+    r = rt.sampler.polar_radius.cpu()
+    decay = torch.exp(-r / sigma)
+    assert torch.equal(rt(img.cuda(), (0.5, 0.5)).cpu(), base * decay[None, None, :])
+    with pytest.raises(RuntimeError):
+        base * decay.unsqueeze(1)
+    gray = RetinalTransform(32, start_res=128, fov=16, cmf_a=2.78, style="logpolar", sampler="grid_bilinear",
+                            device="cuda", no_color_val=True, auto_match_cart_resources=0).eval()
+    y = gray(img.cuda(), (0.5, 0.5)).cpu()
+    want = 0.2989 * base[:, 0] + 0.587 * base[:, 1] + 0.114 * base[:, 2]
+    for c in range(3):
+        assert torch.equal(y[:, c], want)
+    assert torch.equal(gray.train()(img.cuda(), (0.5, 0.5)).cpu(), base)
