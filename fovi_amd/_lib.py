@@ -14,7 +14,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
 
-ABI_VERSION = 21
+ABI_VERSION = 22
 F32, BF16, F8E4M3 = 0, 1, 2
 NEAREST, BILINEAR = 0, 1
 PAD_ZEROS, PAD_BORDER = 0, 1
@@ -29,7 +29,8 @@ EXPORTED = ("fovi_abi_version", "fovi_last_error", "fovi_sampler_fwd", "fovi_knn
             "fovi_knnconv_pack_weight", "fovi_knnconv_weight_mfma_elems", "fovi_knnconv_pack_weight_mfma",
             "fovi_quantize_e4m3", "fovi_knnpool_fwd", "fovi_knnconv_slotsum", "fovi_knnconv_bwd_x",
             "fovi_knn_logpolar_candidates", "fovi_knn_select", "fovi_knnconv_dw_workspace_bytes",
-            "fovi_knnconv_dw", "fovi_knnpool_bwd", "fovi_knnconv_last_path")
+            "fovi_knnconv_dw", "fovi_knnpool_bwd", "fovi_knnconv_last_path",
+            "fovi_knnconv_fwd_noalloc")
 
 
 class SamplerArgs(C.Structure):
@@ -182,6 +183,8 @@ def load(path: str = LIB_PATH):
     lib.fovi_sampler_fwd.restype = C.c_int
     lib.fovi_knnconv_fwd.argtypes = [C.POINTER(KnnConvArgs), C.c_void_p]
     lib.fovi_knnconv_fwd.restype = C.c_int
+    lib.fovi_knnconv_fwd_noalloc.argtypes = [C.POINTER(KnnConvArgs), C.c_void_p]
+    lib.fovi_knnconv_fwd_noalloc.restype = C.c_int
     lib.fovi_knnconv_pack_weight.argtypes = [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_void_p,
                                              C.c_int32, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p]
     lib.fovi_knnconv_pack_weight.restype = C.c_int

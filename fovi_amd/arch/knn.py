@@ -446,6 +446,17 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         raise TypeError(f"KNNConvLayer: unsupported input dtype {x.dtype}")
 
     def _launch(self, x, activation=None):
+        a, y, _keep = self.launch_args(x, activation)
+        lib = _lib.load()
+        _lib.check(lib.fovi_knnconv_fwd(a, _lib.stream_handle(x.device)), "fovi_knnconv_fwd")
+        return y.transpose(1, 2)
+
+    def launch_args(self, x, activation=None, workspace=True):
+        """The ``fovi_knnconv_args`` of a forward of ``x`` (fp32 or bf16): ``(args, y, keep)``
+        with ``y`` the channels-last ``[B, N_out, C_out]`` output it writes and ``keep`` the
+        tensors its pointers name (hold them until the call has run). ``workspace=False``
+        leaves the few-channel path's slot-sum workspace out (``fovi_knnconv_fwd_noalloc``
+        takes none)."""
         _lib.require_device(x, self.weight)
         if x.dim() != 3 or x.shape[1] != self.in_channels or x.shape[2] != self.in_coords.shape[0]:
             raise ValueError(f"KNNConvLayer: expected [B, {self.in_channels}, {self.in_coords.shape[0]}], "
@@ -486,7 +497,7 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         a.activation = _lib.ACT_RELU if activation == "relu" else _lib.ACT_NONE
         a.w_c_slot = c_slot
         ws = None
-        if cp is not None and self.two_pass_few_channels:
+        if cp is not None and self.two_pass_few_channels and workspace:
             # slot-sum rows for the two-pass few-channel path (caller-owned scratch)
             ws = torch.empty(bsz * n_out * w.shape[1], dtype=torch.bfloat16, device=x.device)
             a.workspace = ws.data_ptr(); a.workspace_bytes = ws.numel() * 2
@@ -498,9 +509,7 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
             a.zero_row = self._zero_row
         if mfma:
             self._set_wide_tables(a)
-        lib = _lib.load()
-        _lib.check(lib.fovi_knnconv_fwd(a, _lib.stream_handle(x.device)), "fovi_knnconv_fwd")
-        return y.transpose(1, 2)
+        return a, y, (x, w, bias, ws)
 
     def _set_wide_tables(self, a):
         """The fragment-order kernel's tables, into the ``fovi_knnconv_args`` ``a``."""

@@ -26,6 +26,9 @@
 //    (row, 8 channels). Generic loader: any strides / c_in, element gathers.
 #include "knnconv_internal.h"
 
+#include <algorithm>
+#include <mutex>
+
 namespace fovi {
 
 // ---------------------------------------------------------------------------
@@ -1278,6 +1281,19 @@ extern "C" int fovi_knnconv_pack_weight(const float* w_ref, int64_t c_out, int64
   return check_launch("fovi_knnconv_pack_weight");
 }
 
+namespace fovi {
+
+// The few-channel bf16 path: a weight packed with w_c_slot = 4 or 8 > c_in channels per slot and
+// channels-last input rows padded to w_c_slot channels.
+static bool few_channel_rows(const fovi_knnconv_args* a) {
+  const int64_t cp = a->w_c_slot;
+  return a->x_dtype == FOVI_BF16 && a->w_dtype == FOVI_BF16 && a->w_layout == FOVI_W_ROWS &&
+         (cp == 4 || cp == 8) && cp > a->c_in && a->x_stride[1] == 1 && a->x_stride[2] == cp &&
+         a->x_stride[0] % cp == 0 && reinterpret_cast<uintptr_t>(a->x) % (2 * cp) == 0;
+}
+
+}  // namespace fovi
+
 extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
   using namespace fovi;
   clear_error();
@@ -1367,9 +1383,8 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
   }
   if (a->x_dtype == FOVI_BF16 && a->w_dtype == FOVI_BF16 && p.w_c_slot != p.C) {
     // packed weight with padded slots: only the small-channel kernel reads it
-    const uintptr_t xa = reinterpret_cast<uintptr_t>(a->x);
     const int cp = p.w_c_slot;
-    if ((cp == 4 || cp == 8) && p.xs1 == 1 && p.xs2 == cp && p.xs0 % cp == 0 && xa % (2 * cp) == 0) {
+    if (few_channel_rows(a)) {
       const uint64_t need = static_cast<uint64_t>(p.B) * static_cast<uint64_t>(p.Nout) *
                             static_cast<uint64_t>(p.Kpad) * 2u;
       if (a->workspace && static_cast<uint64_t>(a->workspace_bytes) >= need &&
@@ -1428,4 +1443,84 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
   }
   set_error("fovi_knnconv_fwd: unsupported dtypes x=%d w=%d", a->x_dtype, a->w_dtype);
   return 1;
+}
+
+// ---------------------------------------------------------------------------
+// fovi_knnconv_fwd_noalloc: the forward with the library's static scratch
+// ---------------------------------------------------------------------------
+namespace fovi {
+
+// Slot-sum rows of the few-channel two-pass path for callers that cannot allocate. One copy per
+// GPU (a file-scope __device__ array lives in every device's copy of the code object), held
+// until the process ends. Host code names it only through the per-device address below.
+constexpr int64_t kNoAllocScratchBytes = int64_t(64) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the current device, looked up once per device (with that
+// device current) and kept.
+static int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("fovi_knnconv_fwd_noalloc: no current device (%s)", hipGetErrorString(e));
+    return 1;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      set_error("fovi_knnconv_fwd_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                hipGetErrorString(e));
+      return 1;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+}  // namespace fovi
+
+extern "C" int fovi_knnconv_fwd_noalloc(const fovi_knnconv_args* a, void* stream) {
+  using namespace fovi;
+  clear_error();
+  note_path("");
+  if (!a) { set_error("fovi_knnconv_fwd_noalloc: null args"); return 1; }
+  if (a->workspace || a->workspace_bytes) {
+    set_error("fovi_knnconv_fwd_noalloc: takes no workspace (its scratch is the library's own)");
+    return 1;
+  }
+  if (!few_channel_rows(a)) return fovi_knnconv_fwd(a, stream);   // a path without scratch
+  if (!a->x || !a->y) { set_error("fovi_knnconv_fwd_noalloc: null pointer argument"); return 1; }
+  if (a->batch <= 0 || a->n_out <= 0 || a->k_pad <= 0) { set_error("fovi_knnconv_fwd_noalloc: bad sizes"); return 1; }
+  if (a->y_dtype != FOVI_F32 && a->y_dtype != FOVI_BF16) {
+    set_error("fovi_knnconv_fwd_noalloc: bad y dtype"); return 1;
+  }
+  // one image's slot-sum rows must fit the scratch; images are then taken in chunks that fit
+  const int64_t per_image = a->n_out * a->k_pad * 2;
+  if (a->n_out > kNoAllocScratchBytes || a->k_pad > kNoAllocScratchBytes || per_image > kNoAllocScratchBytes) {
+    set_error("fovi_knnconv_fwd_noalloc: one image's slot sums (n_out=%lld x k_pad=%lld bf16 = %lld bytes) "
+              "exceed the %lld-byte scratch", (long long)a->n_out, (long long)a->k_pad, (long long)per_image,
+              (long long)kNoAllocScratchBytes);
+    return 1;
+  }
+  void* ws = nullptr;
+  if (scratch_address(&ws)) return 1;
+  const int64_t chunk = kNoAllocScratchBytes / per_image;
+  const int64_t y_esize = a->y_dtype == FOVI_F32 ? 4 : 2;
+  fovi_knnconv_args b = *a;
+  for (int64_t b0 = 0; b0 < a->batch; b0 += chunk) {
+    b.batch = std::min(chunk, a->batch - b0);
+    b.x = static_cast<const char*>(a->x) + b0 * a->x_stride[0] * 2;
+    b.y = static_cast<char*>(a->y) + b0 * a->y_stride[0] * y_esize;
+    b.workspace = ws;
+    b.workspace_bytes = kNoAllocScratchBytes;
+    if (fovi_knnconv_fwd(&b, stream) != 0) return 1;
+  }
+  return 0;
 }

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 21
+#define FOVI_ABI_VERSION 22
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -195,6 +195,29 @@ typedef struct fovi_knnconv_args {
 } fovi_knnconv_args;
 
 int fovi_knnconv_fwd(const fovi_knnconv_args* args, void* stream);
+
+/*
+ * fovi_knnconv_fwd for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference, whose forward allocates its intermediates
+ * (fovi/arch/knn.py:484-557).
+ *
+ * Runs what fovi_knnconv_fwd runs for the same arguments, except that the
+ * few-channel two-pass path (bf16, a weight packed with w_c_slot = 4 or 8
+ * channels per slot > c_in, channels-last input rows padded to w_c_slot) keeps
+ * its slot-sum rows in the library's own scratch instead of a caller
+ * workspace: a static 64 MiB device array per GPU, held until the process
+ * ends, filled and read one chunk of whole images at a time (the same kernels
+ * per image, so results equal fovi_knnconv_fwd's with a workspace bit for
+ * bit). The other paths use no scratch. Calls no hipMalloc or hipFree.
+ *   - workspace must be NULL and workspace_bytes 0;
+ *   - one image's slot sums, n_out * k_pad * 2 bytes, must fit the 64 MiB
+ *     scratch, or the call fails with an error (no launch);
+ *   - every call on a GPU shares that GPU's scratch: calls that overlap on one
+ *     GPU (different streams or threads) race. Each chunk's rows are written
+ *     in full before they are read, so nothing needs clearing between calls.
+ */
+int fovi_knnconv_fwd_noalloc(const fovi_knnconv_args* args, void* stream);
 
 /*
  * The kernel path the last successful fovi_knnconv_fwd call on this thread
