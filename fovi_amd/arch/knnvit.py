@@ -24,12 +24,15 @@ from .knn import KNNConvLayer, get_in_out_coords
 __all__ = ["KNNPatchEmbedding", "PartitioningPatchEmbedding", "KNNPartitioningPatchEmbedding"]
 
 
-def _partition(distances, n_in, n_out):
+def _partition(distances, n_in, n_out, allow_empty=False):
     """Nearest token centre of every input point (first index on ties), from the distance
-    rows of the sensor points (the pad ring takes no part)."""
+    rows of the sensor points (the pad ring takes no part). A centre nearest to no point has
+    an empty group: ``PartitioningPatchEmbedding`` gives it an all -1 column, as the
+    reference does (``knnvit.py:176-186``); ``KNNPartitioningPatchEmbedding`` cannot size its
+    neighbourhood (the reference fails on the empty group's ``max``, ``knnvit.py:272-276``)."""
     part = torch.argmin(distances[:n_in], 1)
     sizes = torch.bincount(part, minlength=n_out)
-    if int(sizes.min()) == 0:
+    if not allow_empty and int(sizes.min()) == 0:
         raise ValueError("a token centre is nearest to no input point")
     return part, sizes
 
@@ -56,7 +59,7 @@ class KNNPatchEmbedding(KNNConvLayer):
             if out_cart_res is None:
                 raise ValueError("k from the patch size needs a matched cartesian resolution "
                                  "(auto_match_cart_resources with in_cart_res) or new_parameterization=True")
-            k = int((cart_patch_size * out_cart_res / np.sqrt(len(out_coords)) * patch_overlap_factor) ** 2)
+            k = int((cart_patch_size * out_cart_res / np.sqrt(out_coords.shape[0]) * patch_overlap_factor) ** 2)
         super().__init__(in_channels, embed_dim, k, in_coords, out_coords, device=device,
                          sample_cortex=sample_cortex, ref_frame_side_length=ref_frame_side_length, **kwargs)
         self.transposed = transposed
@@ -94,10 +97,10 @@ class PartitioningPatchEmbedding(KNNPatchEmbedding):
         self.device, self.arch_flag, self.sample_cortex = device, arch_flag, sample_cortex
         self.ref_frame_side_length = ref_frame_side_length
         self.batch_size = None
-        n_in, n_out = len(in_coords), len(out_coords)
+        n_in, n_out = in_coords.shape[0], out_coords.shape[0]
         self.k = int(n_in / n_out)
         self.distances = self._compute_all_distances()
-        self.partitioning, sizes = _partition(self.distances, n_in, n_out)
+        self.partitioning, sizes = _partition(self.distances, n_in, n_out, allow_empty=True)
         max_len = int(sizes.max())
         # rows of each group in increasing input index, -1 below
         order = torch.argsort(self.partitioning, stable=True)
@@ -131,7 +134,7 @@ class KNNPartitioningPatchEmbedding(KNNPatchEmbedding):
             max_out_coord_val=max_coord_val)
         nn.Module.__init__(self)
         self.in_coords, self.out_coords, self.sample_cortex = in_coords, out_coords, sample_cortex
-        n_in, n_out = len(in_coords), len(out_coords)
+        n_in, n_out = in_coords.shape[0], out_coords.shape[0]
         distances = self._compute_all_distances()
         part, _ = _partition(distances, n_in, n_out)
         own = distances[torch.arange(n_in), part]

@@ -388,3 +388,27 @@ def test_oracle_pads_negative_indices_like_the_pad_token():
     got = knnconv_ref.knnconv_forward(x, idx, 10, rf, w)
     want = knnconv_ref.knnconv_bruteforce(x, idx, slots, 10, w)
     assert np.allclose(got.numpy(), want, rtol=1e-5, atol=1e-5)
+
+
+def test_partitioning_keeps_an_empty_group_as_padding():
+    """A token centre nearest to no input point gets an all -1 column (no input), as the
+    reference's partition loop leaves it (knnvit.py:176-186); the k-nearest variant refuses."""
+    import types
+
+    import torch
+
+    from fovi_amd.arch.knnvit import PartitioningPatchEmbedding, _partition
+    from fovi_amd.sensing.coords import SamplingCoords
+    cin = SamplingCoords(16, 2.78, 8, style="logpolar")
+    cart = torch.tensor([[0.0, 0.0], [0.5, 0.0], [5.0, 5.0]])
+    cout = types.SimpleNamespace(cartesian=cart, cortical=None, polar=torch.zeros_like(cart), shape=cart.shape,
+                                 style="logpolar", dtype=torch.float32)
+    pe = PartitioningPatchEmbedding(3, 8, None, 16, 2.78, in_coords=cin, out_coords=cout, sample_cortex=False,
+                                    device="cpu")
+    idx = pe.knn_indices.cpu()
+    assert idx.shape[1] == 3 and bool((idx[:, 2] == -1).all())
+    covered = torch.sort(idx[:, :2][idx[:, :2] >= 0]).values
+    assert torch.equal(covered, torch.arange(cin.shape[0]))
+    assert int((pe.slot_ptr.cpu()[2] & 0xFFFF).sum()) == 0          # no neighbour in any slot
+    with pytest.raises(ValueError, match="nearest to no input point"):
+        _partition(pe.distances, cin.shape[0], 3)
