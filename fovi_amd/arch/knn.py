@@ -247,6 +247,25 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         if tiles is not None:
             order = T.stream_slot_order(T.slot_stream_units(tiles))
         self.set_slot_order(order)
+        # tables of the fused few-channel kernel (c_in <= 8): the largest tile whose LDS fits
+        self._fc = None
+        cp = 4 if self.in_channels <= 4 else (8 if self.in_channels <= 8 else None)
+        fc = None
+        if cp is not None:
+            k_pad = -(-cp * n_ref // _KCHUNK) * _KCHUNK
+            for tile in (256, 128):
+                fc = T.few_channel_tables(knn_indices, slots, n_in, n_ref, cp, k_pad, tile)
+                if fc is not None and T.few_channel_lds_bytes(fc, self.out_channels, cp) <= 160 * 1024:
+                    break
+                fc = None
+        for name, field in (("fc_lo", "lo"), ("fc_span", "span"), ("fc_item", "item"), ("fc_xlist", "xlist"),
+                            ("fc_xoff", "xoff")):
+            self.register_buffer(name, None if fc is None else getattr(fc, field).to(device), persistent=False)
+        if fc is not None:
+            self._fc = (fc.tile, fc.zero_row, fc.xmax)
+        # few-channel layers: the fused kernel when its tables fit (False: the slot sums through
+        # a workspace and a dense GEMM, or the single-pass kernel)
+        self.few_channel_fused = True
         # slot-sum headroom of the fp8 path: the largest neighbour count of a slot
         self._max_slot_count = int((slot_ptr & 0xFFFF).max()) if slot_ptr.numel() else 1
         # quantize every input to e4m3 and run the fp8 kernel
@@ -496,8 +515,14 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
             raise ValueError(f"activation must be None or 'relu', got {activation!r}")
         a.activation = _lib.ACT_RELU if activation == "relu" else _lib.ACT_NONE
         a.w_c_slot = c_slot
+        fused = cp is not None and self.few_channel_fused and self._fc is not None
+        if fused:
+            a.fc_lo = self.fc_lo.data_ptr(); a.fc_span = self.fc_span.data_ptr()
+            a.fc_item = self.fc_item.data_ptr(); a.fc_xlist = self.fc_xlist.data_ptr()
+            a.fc_xoff = self.fc_xoff.data_ptr()
+            a.fc_tile_points, a.fc_zero_row, a.fc_xmax = self._fc
         ws = None
-        if cp is not None and self.two_pass_few_channels and workspace:
+        if cp is not None and self.two_pass_few_channels and workspace and not fused:
             # slot-sum rows for the two-pass few-channel path (caller-owned scratch)
             ws = torch.empty(bsz * n_out * w.shape[1], dtype=torch.bfloat16, device=x.device)
             a.workspace = ws.data_ptr(); a.workspace_bytes = ws.numel() * 2

@@ -41,6 +41,8 @@ __all__ = [
     "tile_tables",
     "direct_tables",
     "TILE_POINTS",
+    "few_channel_tables",
+    "few_channel_lds_bytes",
 ]
 
 _PAIR_BUDGET = 500_000_000  # distance-matrix elements per chunk (reference knn.py:43-49)
@@ -441,6 +443,128 @@ def direct_tables(knn_idx, slots, n_in, n_ref, tile=TILE_POINTS):
             coll_n[t, v] = len(rows)
     return (lo, span, torch.from_numpy(e.astype(np.uint32).view(np.int32)), nbr,
             torch.from_numpy(coll), torch.from_numpy(coll_n), zero_row)
+
+
+class FewChannelTables(NamedTuple):
+    lo: torch.Tensor         # [T] int32 first staged input row of tile t
+    span: torch.Tensor       # [T] int32 staged rows
+    item: torch.Tensor       # [T, n_chunks, tile * spc, 2] int32 (uint32 words)
+    xlist: torch.Tensor      # [total] int16 (uint16 S rows), per (tile, chunk) blocks of multiples of 8
+    xoff: torch.Tensor       # [T * n_chunks + 1] int32 block starts
+    tile: int
+    zero_row: int
+    xmax: int
+
+
+FC_CHUNK = 64      # reduction columns per chunk of the fused few-channel kernel
+FC_THREADS = 512   # threads of its workgroup
+
+
+def few_channel_tables(knn_idx, slots, n_in, n_ref, cp, k_pad, tile):
+    """Tables of the fused few-channel kernel (``knnconv_fewc.hip``; ``fc_*`` in the C-ABI).
+
+    Output points are cut into tiles of ``tile`` (128 or 256) consecutive points; a tile
+    stages input rows ``[lo, lo + span)`` and a zero row ``zero_row`` (the largest span).
+    The reduction runs in chunks of 64 columns, ``64 // cp`` slots each. Every (row, slot)
+    of a chunk is one item, two uint32 words: ``first << 16 | count`` (``first`` = the S
+    row of the slot's first neighbour, ``zero_row`` when empty) and ``dest << 16 | xoff``
+    (``dest = row * spc + slot within the chunk``; the further ``count - 1`` neighbours, in
+    the CSR list order of ``csr_tables``, sit at ``xoff`` in the chunk's extras block).
+    Items are sorted by count (largest first) and dealt in a snake over the 512 threads (item
+    ``j * 512 + thread``; a wave holds items of similar counts). Returns
+    ``None`` when a span, a count or an extras block does not fit 16 bits.
+    """
+    k, n_out = knn_idx.shape
+    spc = FC_CHUNK // cp
+    n_chunks = k_pad // FC_CHUNK
+    per_chunk = tile * spc
+    if k_pad % FC_CHUNK or per_chunk % FC_THREADS or n_chunks * spc < n_ref:
+        return None
+    ptr, nbr = csr_tables(knn_idx, slots, n_in, n_ref)
+    ptr = ptr.numpy().astype(np.int64)
+    nbr = nbr.numpy().astype(np.int64)
+    n_tiles = -(-n_out // tile)
+    lo = np.zeros(n_tiles, np.int64)
+    span = np.zeros(n_tiles, np.int64)
+    for t in range(n_tiles):
+        blk = nbr[t * tile:(t + 1) * tile]
+        valid = blk >= 0
+        if valid.any():
+            lo[t] = blk[valid].min()
+            span[t] = blk[valid].max() - lo[t] + 1
+    zero_row = int(span.max())
+    if zero_row >= 0xFFFF:
+        return None
+    # per (point, padded slot): count, begin
+    vpad = n_chunks * spc
+    cnt = np.zeros((n_tiles * tile, vpad), np.int64)
+    beg = np.zeros((n_tiles * tile, vpad), np.int64)
+    cnt[:n_out, :n_ref] = ptr & 0xFFFF
+    beg[:n_out, :n_ref] = ptr >> 16
+    nbr_pad = np.full((n_tiles * tile, k), -1, np.int64)
+    nbr_pad[:n_out] = nbr
+    rows_lo = np.repeat(lo, tile)[:, None]
+    nbr_rel = np.where(nbr_pad >= 0, nbr_pad - rows_lo, 0)
+    first = np.take_along_axis(nbr_rel, np.minimum(beg, k - 1), axis=1)
+    first = np.where(cnt > 0, first, zero_row)
+    # item slot of each count rank: round j = rank // 512 fills slots j * 512 + thread, odd rounds
+    # backwards (a snake). A wave runs as long as its slowest lane: consecutive ranks share a
+    # wave, and a wave that takes the heaviest items of one round takes light ones in the next
+    rank = np.arange(per_chunk)
+    rnd, pos = rank // FC_THREADS, rank % FC_THREADS
+    slot_of_rank = rnd * FC_THREADS + np.where(rnd % 2 == 0, pos, FC_THREADS - 1 - pos)
+    item = np.zeros((n_tiles, n_chunks, per_chunk, 2), np.int64)
+    blocks, xoff, off = [], [0], 0
+    xmax = 0
+    for t in range(n_tiles):
+        rows = slice(t * tile, (t + 1) * tile)
+        for c in range(n_chunks):
+            cols = slice(c * spc, (c + 1) * spc)
+            cc = cnt[rows, cols].reshape(-1)            # dest = row * spc + slot
+            ff = first[rows, cols].reshape(-1)
+            bb = beg[rows, cols].reshape(-1)
+            order = np.argsort(-cc, kind="stable")      # dests by decreasing count
+            extra_n = np.maximum(cc[order] - 1, 0)
+            starts = np.cumsum(extra_n) - extra_n
+            total = int(extra_n.sum())
+            if total > 0xFFFF or cc.max(initial=0) > 0xFFFF:
+                return None
+            xl = np.zeros(-(-total // 8) * 8, np.int64)
+            nrel = nbr_rel[rows]
+            for d, st, ne in zip(order[extra_n > 0], starts[extra_n > 0], extra_n[extra_n > 0]):
+                r = d // spc
+                xl[st:st + ne] = nrel[r, bb[d] + 1:bb[d] + 1 + ne]
+            item[t, c, slot_of_rank, 0] = (ff[order] << 16) | cc[order]
+            item[t, c, slot_of_rank, 1] = (order << 16) | starts
+            blocks.append(xl)
+            off += len(xl)
+            xoff.append(off)
+            xmax = max(xmax, len(xl))
+    xlist = np.concatenate(blocks) if blocks else np.zeros(0, np.int64)
+    if len(xlist) == 0:
+        xlist = np.zeros(8, np.int64)
+    return FewChannelTables(
+        torch.from_numpy(lo.astype(np.int32)), torch.from_numpy(span.astype(np.int32)),
+        torch.from_numpy(item.astype(np.uint32).view(np.int32)),
+        torch.from_numpy(xlist.astype(np.uint16).view(np.int16)),
+        torch.from_numpy(np.asarray(xoff, np.int32)), tile, zero_row, xmax)
+
+
+def few_channel_lds_bytes(tables, c_out, cp):
+    """LDS bytes the fused few-channel kernel needs for these tables and ``c_out`` (its
+    layout: staged rows and the zero row, two A chunks, the weight chunk of ``c_out`` rounded
+    up to 64 columns, the extras block, at least the epilogue's transposition buffers; more
+    than 160 KB when no wave tiling of the kernel covers ``c_out`` at this tile size)."""
+    ntp = -(-c_out // 64) * 64
+    # the kernel's wave tilings: 2 x 4 or 4 x 2 waves of rb x cb blocks of 32 x 32, cb <= 4,
+    # rb * cb <= 8; extras blocks of at most 4 pieces of 16 bytes per thread
+    tilings = [(tables.tile // (32 * wm), ntp // (32 * (8 // wm))) for wm in (2, 4)
+               if ntp % (32 * (8 // wm)) == 0]
+    if not any(1 <= cb <= 4 and rb * cb <= 8 for rb, cb in tilings) or tables.xmax > 4 * 512 * 8:
+        return 1 << 30
+    s = ((tables.zero_row + 1) * cp * 2 + 15) & ~15
+    body = s + 2 * tables.tile * 128 + ntp * 128 + tables.xmax * 2
+    return max(body, tables.tile * ntp * 2)
 
 
 def _row_offset(r):

@@ -1283,12 +1283,12 @@ extern "C" int fovi_knnconv_pack_weight(const float* w_ref, int64_t c_out, int64
 
 namespace fovi {
 
-// The few-channel bf16 path: a weight packed with w_c_slot = 4 or 8 > c_in channels per slot and
+// The few-channel bf16 path: a weight packed with w_c_slot = 4 or 8 >= c_in channels per slot and
 // channels-last input rows padded to w_c_slot channels.
 static bool few_channel_rows(const fovi_knnconv_args* a) {
   const int64_t cp = a->w_c_slot;
   return a->x_dtype == FOVI_BF16 && a->w_dtype == FOVI_BF16 && a->w_layout == FOVI_W_ROWS &&
-         (cp == 4 || cp == 8) && cp > a->c_in && a->x_stride[1] == 1 && a->x_stride[2] == cp &&
+         (cp == 4 || cp == 8) && cp >= a->c_in && a->x_stride[1] == 1 && a->x_stride[2] == cp &&
          a->x_stride[0] % cp == 0 && reinterpret_cast<uintptr_t>(a->x) % (2 * cp) == 0;
 }
 
@@ -1381,10 +1381,14 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
     note_path("fp8 rows");
     return launch_knnconv_fp8(p, a->y_dtype, s);
   }
-  if (a->x_dtype == FOVI_BF16 && a->w_dtype == FOVI_BF16 && p.w_c_slot != p.C) {
-    // packed weight with padded slots: only the small-channel kernel reads it
+  if (a->x_dtype == FOVI_BF16 && a->w_dtype == FOVI_BF16 && (p.w_c_slot != p.C || few_channel_rows(a))) {
+    // packed weight with padded slots: only the few-channel kernels read it
     const int cp = p.w_c_slot;
     if (few_channel_rows(a)) {
+      if (launch_knnconv_fewc(p, a, cp, s)) {
+        note_path("bf16 few-channel fused");
+        return check_launch("fovi_knnconv_fwd(bf16 few-channel fused)");
+      }
       const uint64_t need = static_cast<uint64_t>(p.B) * static_cast<uint64_t>(p.Nout) *
                             static_cast<uint64_t>(p.Kpad) * 2u;
       if (a->workspace && static_cast<uint64_t>(a->workspace_bytes) >= need &&

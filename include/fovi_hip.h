@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 22
+#define FOVI_ABI_VERSION 23
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -192,6 +192,30 @@ typedef struct fovi_knnconv_args {
   const uint16_t* tile_hlist;
   int32_t heavy_stride;       /* heavy entries per tile, even, >= 2 */
   int32_t hlist_stride;       /* multiple of 8, >= 8 */
+  /* Tables of the fused few-channel kernel (the few-channel path: bf16, w_c_slot = 4 or 8 >=
+   * c_in, channels-last rows padded to w_c_slot; all NULL to leave it out). Output points are
+   * cut into tiles of fc_tile_points (128 or 256) consecutive points; tile t stages input rows
+   * fc_lo[t] .. fc_lo[t] + fc_span[t] - 1 (S rows 0 .. span - 1) and a zero row fc_zero_row
+   * (>= every span, < 65536). The reduction runs in chunks of 64 columns (64 / w_c_slot slots;
+   * k_pad / 64 chunks). Chunk c of tile t has fc_tile_points * 64 / w_c_slot items, two words
+   * each, at fc_item[((t * n_chunks + c) * items + j * 512 + thread) * 2]:
+   *   word 0 = (S row of the first neighbour, or fc_zero_row) << 16 | neighbour count;
+   *   word 1 = destination (row * (64 / w_c_slot) + slot within the chunk) << 16 | offset of the
+   *            further neighbours (count - 1 S rows, list order) in the chunk's extras block,
+   * every (row, slot) of the chunk exactly once (counts 0 for points past n_out and slots past
+   * n_ref). Extras block (t, c) is fc_xlist[fc_xoff[t * n_chunks + c] ..
+   * fc_xoff[t * n_chunks + c + 1]) (uint16, multiples of 8; fc_xmax = the longest). The slot
+   * sums (fp32 in list order from +0, one rounding to bf16) and the MFMA order equal the
+   * two-pass path's. */
+  const int32_t* fc_lo;
+  const int32_t* fc_span;
+  const uint32_t* fc_item;
+  const uint16_t* fc_xlist;
+  const int32_t* fc_xoff;
+  int32_t fc_tile_points;
+  int32_t fc_zero_row;
+  int32_t fc_xmax;
+  int32_t reserved6;
 } fovi_knnconv_args;
 
 int fovi_knnconv_fwd(const fovi_knnconv_args* args, void* stream);
@@ -204,7 +228,7 @@ int fovi_knnconv_fwd(const fovi_knnconv_args* args, void* stream);
  *
  * Runs what fovi_knnconv_fwd runs for the same arguments, except that the
  * few-channel two-pass path (bf16, a weight packed with w_c_slot = 4 or 8
- * channels per slot > c_in, channels-last input rows padded to w_c_slot) keeps
+ * channels per slot >= c_in, channels-last input rows padded to w_c_slot) keeps
  * its slot-sum rows in the library's own scratch instead of a caller
  * workspace: a static 64 MiB device array per GPU, held until the process
  * ends, filled and read one chunk of whole images at a time (the same kernels
@@ -222,8 +246,8 @@ int fovi_knnconv_fwd_noalloc(const fovi_knnconv_args* args, void* stream);
 /*
  * The kernel path the last successful fovi_knnconv_fwd call on this thread
  * took ("" before any, or after a failed call): "f32", "bf16 v5", "fp8 v5",
- * "fp8 rows", "bf16 v4", "bf16 v2", "bf16 few-channel", "bf16 few-channel
- * two-pass", "bf16 generic (rows)" or "bf16 generic". Diagnostics only (no
+ * "fp8 rows", "bf16 v4", "bf16 v2", "bf16 few-channel fused", "bf16 few-channel",
+ * "bf16 few-channel two-pass", "bf16 generic (rows)" or "bf16 generic". Diagnostics only (no
  * counterpart in the reference, whose forward is a fixed op sequence,
  * fovi/arch/knn.py:538-557); tests use it to check which kernel a layer
  * geometry selects.

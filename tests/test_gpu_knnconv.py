@@ -209,24 +209,57 @@ def test_alexnet_chain_c2_geometry():
     assert_close_rel(y.float().cpu(), h.float(), 2e-2)
 
 
-@pytest.mark.parametrize("c_in,k,side", [(3, 49, None), (1, 9, None), (4, 25, None), (6, 25, None), (3, 256, 16)])
-def test_bf16_few_channels_padded_rows(c_in, k, side):
-    """Few-channel kernel: rows padded to 4/8 channels by the producer (no copy) or by the layer."""
+@pytest.mark.parametrize("c_in,k,side,c_out", [(3, 49, None, 96), (1, 9, None, 96), (4, 25, None, 96),
+                                               (6, 25, None, 96), (3, 256, 16, 96), (3, 49, None, 64),
+                                               (3, 256, 16, 384), (5, 9, None, 200)])
+def test_bf16_few_channels_padded_rows(c_in, k, side, c_out):
+    """Few-channel layers, rows padded to 4/8 channels by the producer (no copy) or by the
+    layer: the fused kernel (default), the two-pass path (slot sums through a workspace, then a
+    dense GEMM) and the single-pass kernel. The fused kernel sums slots in the same order and
+    runs the same MFMA sequence as the two-pass path: bit-identical."""
+    from fovi_amd import _lib
     res_out = 4 if k == 256 else 16
-    layer = _layer(32, res_out, k, c_in, 96, side, bias=True, seed=7)
-    x = torch.randn(2, c_in, 1024, generator=torch.Generator().manual_seed(11)).bfloat16()
-    buf, view = layer.padded_input(2)
+    layer = _layer(32, res_out, k, c_in, c_out, side, bias=True, seed=7)
+    x = torch.randn(3, c_in, 1024, generator=torch.Generator().manual_seed(11)).bfloat16()
+    buf, view = layer.padded_input(3)
     view.copy_(x.cuda())
     buf[..., c_in:] = torch.nan          # padding channels must not leak into the result
     with torch.no_grad():
         y_view = layer(view)
+        assert _lib.knnconv_last_path() == "bf16 few-channel fused"
         y_copy = layer(x.cuda())
-        layer.two_pass_few_channels = False      # single fused kernel, no workspace
-        y_fused = layer(view)
+        layer.few_channel_fused = False
+        y_two = layer(view)
+        assert _lib.knnconv_last_path() == "bf16 few-channel two-pass"
+        layer.two_pass_few_channels = False      # single-pass kernel, no workspace
+        y_one = layer(view)
+        assert _lib.knnconv_last_path() == "bf16 few-channel"
     ref = _oracle(layer, x, layer.weight.detach().cpu().bfloat16().float())
     assert_close_rel(y_view.float().cpu(), ref, 1e-2)
     assert torch.equal(y_view, y_copy)
-    assert_close_rel(y_fused.float().cpu(), ref, 1e-2)
+    assert torch.equal(y_view, y_two), "fused and two-pass few-channel paths differ"
+    assert_close_rel(y_one.float().cpu(), ref, 1e-2)
+
+
+def test_few_channel_fused_c4_patch_embedding_geometry():
+    """C4 patch embedding (16384 -> 256 log-polar points, k = 256, 16 x 16 ref grid, 3 -> 384,
+    bias) at 64 views: the fused kernel (128-point tiles) equals the two-pass path bit for bit,
+    and views 0 and 63 match the oracle."""
+    from fovi_amd import _lib
+    layer = _layer(128, 16, 256, 3, 384, 16, bias=True, seed=9)
+    assert layer._fc is not None and layer._fc[0] == 128
+    x = torch.rand(64, 3, 16384, generator=torch.Generator().manual_seed(12)).bfloat16()
+    _, view = layer.padded_input(64)
+    view.copy_(x.cuda())
+    with torch.no_grad():
+        y = layer(view)
+        assert _lib.knnconv_last_path() == "bf16 few-channel fused"
+        layer.few_channel_fused = False
+        y_two = layer(view)
+    assert torch.equal(y, y_two)
+    w = layer.weight.detach().cpu().bfloat16().float()
+    for v in (0, 63):
+        assert_close_rel(y[v:v + 1].float().cpu(), _oracle(layer, x[v:v + 1], w), 1e-2, f"view {v}")
 
 
 @pytest.mark.parametrize("res_in,res_out,k,c_in,c_out,bias,act,batch", [
@@ -285,14 +318,14 @@ def test_fragment_order_kernel_falls_back_when_tables_exceed_lds():
 _SELECTION = [
     # name, (res_in, res_out, k, c_in, c_out, side), input, expected path
     ("C1 fp32", (64, 64, 9, 3, 64, None), "f32", "f32"),
-    ("C1 bf16", (64, 64, 9, 3, 64, None), "bf16", "bf16 few-channel two-pass"),
-    ("C2 layer 1", (64, 32, 49, 3, 64, None), "bf16", "bf16 few-channel two-pass"),
+    ("C1 bf16", (64, 64, 9, 3, 64, None), "bf16", "bf16 few-channel fused"),
+    ("C2 layer 1", (64, 32, 49, 3, 64, None), "bf16", "bf16 few-channel fused"),
     ("C2 layer 2", (32, 16, 25, 64, 192, None), "bf16", "bf16 v4"),
     ("C2 layer 3", (16, 16, 9, 192, 384, None), "bf16", "bf16 v5"),
     ("C2 layer 4", (16, 16, 9, 384, 256, None), "bf16", "bf16 v5"),
     ("C2 layer 5", (16, 16, 9, 256, 256, None), "bf16", "bf16 v5"),
     ("C3", (128, 128, 25, 256, 256, None), "bf16", "bf16 v5"),
-    ("C4 patch embedding", (128, 16, 256, 3, 384, 16), "bf16", "bf16 few-channel two-pass"),
+    ("C4 patch embedding", (128, 16, 256, 3, 384, 16), "bf16", "bf16 few-channel fused"),
     ("C5", (128, 128, 25, 256, 256, None), "fp8", "fp8 v5"),
     ("fp8, narrow output", (32, 16, 25, 64, 64, None), "fp8", "fp8 rows"),
     ("bf16 channel-major", (32, 16, 25, 64, 192, None), "bf16 channel-major", "bf16 generic"),

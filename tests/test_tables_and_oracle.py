@@ -315,3 +315,59 @@ def test_stream_slot_order_is_a_permutation_that_lowers_serial_work():
             bpos = np.minimum(np.maximum(bpos, off[:, v + 1]) + rate, off[:, min(v + ahead, u.shape[1])])
         return tot
     assert serial(order) < 0.5 * serial(list(range(t["V"])))
+
+
+@pytest.mark.parametrize("res_in,res_out,k,side,cp,tile", [
+    (128, 16, 256, 16, 4, 128),     # C4 patch embedding
+    (64, 32, 49, None, 4, 256),     # C2 layer 1
+    (32, 16, 25, None, 8, 128),     # eight-channel rows
+    (24, 12, 30, None, 4, 128),     # ragged: partial tile, padding slots in the last chunk
+])
+def test_few_channel_tables_rebuild_the_slot_sums(res_in, res_out, k, side, cp, tile):
+    """Emulates the fused few-channel kernel's use of its tables in float64: every (row, slot)
+    of a chunk is written exactly once, every S row it reads is a staged row or the zero row,
+    and the rebuilt A chunks equal the slot sums of the CSR lists."""
+    import numpy as np
+
+    from fovi_amd.arch import knn_tables as T
+    t = layer_tables(res_in, res_out, k, side=side)
+    V, n_in, n_out = t["V"], t["n_in"], t["n_out"]
+    k_pad = -(-V * cp // 64) * 64
+    ft = T.few_channel_tables(t["idx"], t["slots"], n_in, V, cp, k_pad, tile)
+    assert ft is not None
+    spc, nc = 64 // cp, k_pad // 64
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((n_in, cp))
+    # reference slot sums [n_out, V, cp] from the CSR lists
+    ptr, nbr = t["ptr"].numpy(), t["nbr"].numpy()
+    want = np.zeros((n_out, nc * spc, cp))
+    for n in range(n_out):
+        for v in range(V):
+            b, c = ptr[n, v] >> 16, ptr[n, v] & 0xFFFF
+            if c:
+                want[n, v] = x[nbr[n, b:b + c]].sum(0)
+    item = ft.item.numpy().view(np.uint32)
+    xl = ft.xlist.numpy().view(np.uint16).astype(np.int64)
+    xoff = ft.xoff.numpy()
+    for ti in range(ft.lo.shape[0]):
+        lo, span = int(ft.lo[ti]), int(ft.span[ti])
+        S = np.zeros((ft.zero_row + 1, cp))
+        S[:span] = x[lo:lo + span]
+        for c in range(nc):
+            blk = xl[xoff[ti * nc + c]:xoff[ti * nc + c + 1]]
+            assert len(blk) <= ft.xmax and len(blk) % 8 == 0
+            got = np.full((tile * spc, cp), np.nan)
+            for w0, w1 in item[ti, c]:
+                cnt, first, dest, off = int(w0 & 0xFFFF), int(w0 >> 16), int(w1 >> 16), int(w1 & 0xFFFF)
+                assert first <= ft.zero_row and (cnt > 0 or first == ft.zero_row)
+                rows = [first] + list(blk[off:off + cnt - 1]) if cnt > 1 else [first]
+                assert off + max(cnt - 1, 0) <= len(blk)
+                assert all(r < span or r == ft.zero_row for r in rows)
+                assert np.isnan(got[dest]).all(), "a (row, slot) is written twice"
+                got[dest] = S[rows].sum(0)
+            assert not np.isnan(got).any(), "a (row, slot) is never written"
+            got = got.reshape(tile, spc, cp)
+            rows = slice(ti * tile, min((ti + 1) * tile, n_out))
+            m = rows.stop - rows.start
+            np.testing.assert_allclose(got[:m], want[rows, c * spc:(c + 1) * spc], rtol=1e-12, atol=1e-12)
+            assert not got[m:].any(), "rows past n_out must be zero"
