@@ -14,7 +14,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
 
-ABI_VERSION = 23
+ABI_VERSION = 25
 F32, BF16, F8E4M3 = 0, 1, 2
 NEAREST, BILINEAR = 0, 1
 PAD_ZEROS, PAD_BORDER = 0, 1
@@ -76,7 +76,7 @@ class KnnConvArgs(C.Structure):
         ("hlist_stride", C.c_int32),
         ("fc_lo", C.c_void_p), ("fc_span", C.c_void_p), ("fc_item", C.c_void_p), ("fc_xlist", C.c_void_p),
         ("fc_xoff", C.c_void_p), ("fc_tile_points", C.c_int32), ("fc_zero_row", C.c_int32),
-        ("fc_xmax", C.c_int32), ("reserved6", C.c_int32),
+        ("fc_xmax", C.c_int32), ("wide_units", C.c_int32),
     ]
 
 

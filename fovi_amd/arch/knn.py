@@ -369,6 +369,7 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         tiles = self._direct_tables
         wide = T.wide_tables(tiles, self._k, order) if tiles is not None else None
         self._cent_stride = self._coll_off_stride = self._heavy_stride = self._hlist_stride = 0
+        self._wide_units = bool(wide.units) if wide is not None else False
         dev = self.weight.device
         for name, field in (("tile_src", "src"), ("tile_cent", "coll"), ("tile_coll_off", "coll_off"),
                             ("tile_heavy", "heavy"), ("tile_hlist", "hlist")):
@@ -433,7 +434,7 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         return (self.mfma_weights and chunk > 0 and self.in_channels % chunk == 0
                 and self._mfma_lds_bytes() <= 160 * 1024
                 and self.out_channels % 8 == 0 and self._mfma_column_use() >= 0.75
-                and self.tile_src is not None and 0 < self._zero_row <= 1023
+                and self.tile_src is not None and 0 < self._zero_row <= T.WIDE_MAX_ROWS
                 and self._k <= 255 and x.stride(1) == 1 and x.stride(2) % align == 0
                 and x.stride(0) % align == 0 and x.data_ptr() % 16 == 0)
 
@@ -543,6 +544,7 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         a.coll_off_stride = self._coll_off_stride; a.cent_stride = self._cent_stride
         a.tile_heavy = self.tile_heavy.data_ptr(); a.tile_hlist = self.tile_hlist.data_ptr()
         a.heavy_stride = self._heavy_stride; a.hlist_stride = self._hlist_stride
+        a.wide_units = int(self._wide_units)
 
     # -- backward --------------------------------------------------------------
     def _backward(self, x, weight, dy, need_x, need_w):

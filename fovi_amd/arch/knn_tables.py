@@ -584,6 +584,8 @@ STREAM_MAX_COUNT = 6
 # LDS bytes of one collision tile of the wide-layer kernel (256 rows x 64 bytes)
 WIDE_TILE_BYTES = 256 * 64
 WIDE_TILES = 3
+# staged rows the wide-layer kernel holds (four 16-byte pieces per thread and row, 16 per thread)
+WIDE_MAX_ROWS = 1024
 
 
 class WideTables(NamedTuple):
@@ -595,16 +597,19 @@ class WideTables(NamedTuple):
     heavy_stride: int
     hlist: torch.Tensor      # [T, hlist_stride] int16 (uint16 offsets)
     hlist_stride: int
+    units: bool              # row offsets in 16-byte units (True) or bytes (False)
 
 
 def wide_tables(direct, k, order=None):
     """Tables of the wide-layer (fragment-order) kernel, derived from ``direct_tables``.
 
     Laid out in the kernel's LDS order (16-byte copies) and holding swizzled
-    LDS byte offsets (``_row_offset``) rather than row numbers, so the kernel
-    forms every address with one XOR. The kernel's LDS starts with the staged
-    rows and the zero row (``zero_row + 1`` rows of 64 bytes), followed by
-    ``heavy_stride`` rows of heavy sums.
+    LDS offsets of rows (``_row_offset``) rather than row numbers, so the
+    kernel forms every address with one XOR: byte offsets when they fit 16
+    bits (up to 1023 staged rows), else 16-byte units (every row part is
+    16-byte aligned; ``units``), which the kernel shifts back. The kernel's
+    LDS starts with the staged rows and the zero row (``zero_row + 1`` rows of
+    64 bytes), followed by ``heavy_stride`` rows of heavy sums.
 
     * ``src [T, V, tile] uint16``: per (slot, row) the offset of the 64-byte
       row the MFMA lanes read for that slot: the neighbour's staged row when
@@ -614,27 +619,27 @@ def wide_tables(direct, k, order=None):
     * ``coll [T, stride, 4] uint32``: one 16-byte stream entry per (slot,
       collision row with 2 .. ``STREAM_MAX_COUNT`` neighbours), grouped by slot
       position and within a slot by decreasing count. Word 0: bits 0-15 the
-      destination, relative to the first collision tile (tile ``p % 3`` of slot
-      position p, then the row's offset), bits 16-23 the count; words 1-3:
-      offsets of the staged rows of neighbours 1-6, two per word (low half
-      first; the zero row past the count).
+      destination in bytes, relative to the first collision tile (tile ``p % 3``
+      of slot position p, then the row's offset), bits 16-23 the count; words
+      1-3: offsets of the staged rows of neighbours 1-6, two per word (low
+      half first; the zero row past the count).
     * ``coll_off [T, V + 1 rounded up to 4] int32``: slot position p's entries
       are ``coll[t, coll_off[t, p]:coll_off[t, p + 1]]``.
     * ``heavy [T, heavy_stride, 2] uint32``: one entry per heavy (slot, row):
       word 0 bits 0-15 the offset of its heavy-sum row, bits 16-23 the count
       (0 = padding); word 1 the index of its first neighbour in ``hlist``.
-    * ``hlist [T, hlist_stride] uint16``: the heavy entries' neighbour offsets,
-      in list order.
+    * ``hlist [T, hlist_stride] uint16``: the heavy entries' neighbour
+      offsets, in list order.
 
     ``order`` (default: slot order) is the order in which the kernel visits
     the slots (``stream_slot_order``): the tables are laid out by position p
     in that order, slot ``order[p]``.
 
-    Returns a ``WideTables``, or ``None`` when the offsets do not fit 16 bits
-    (more than 1023 staged rows, or heavy rows past 64 KB) or k exceeds 255.
+    Returns a ``WideTables``, or ``None`` when the kernel cannot stage the rows
+    (more than 1024 staged rows) or k exceeds 255.
     """
     lo, span, ent, nbr, coll, coll_n, zero_row = direct
-    if zero_row > 1023 or k > 255:
+    if zero_row > WIDE_MAX_ROWS or k > 255:
         return None
     e = ent.numpy().view(np.uint32).astype(np.int64)          # [T*tile, V]
     n_tiles, n_ref, tile = coll.shape
@@ -646,11 +651,14 @@ def wide_tables(direct, k, order=None):
     heavy_mask = cnt > STREAM_MAX_COUNT                        # [T, tile, V]
     n_heavy = heavy_mask.sum(axis=(1, 2))
     heavy_stride = max(2, -(-int(n_heavy.max(initial=0)) // 2) * 2)
-    heavy_base = (zero_row + 1) * 64
-    if heavy_base + heavy_stride * 64 > 0xFFFF:
+    units = zero_row > 1023
+    sh = 4 if units else 0                                    # offset = byte offset >> sh
+    row_b = 64 >> sh
+    heavy_base = (zero_row + 1) * row_b
+    if heavy_base + heavy_stride * row_b >= 0xFFFF:           # 0xFFFF marks a stream-built sum
         return None
     nb = nbr.numpy().astype(np.int64).reshape(n_tiles, tile, k)
-    zoff = int(_row_offset(zero_row))
+    zoff = int(_row_offset(zero_row)) >> sh
 
     # heavy entries: in (slot, row) order of each tile
     heavy_row = np.full((n_tiles, tile, n_ref), -1, np.int64)
@@ -671,13 +679,13 @@ def wide_tables(direct, k, order=None):
         pos = 0
         for h, (r, v) in enumerate(zip(rr, vv)):
             c, b0 = int(cnt[t, r, v]), int(begin[t, r, v])
-            heavy[t, h, 0] = (heavy_base + 64 * h) | (c << 16)
+            heavy[t, h, 0] = (heavy_base + row_b * h) | (c << 16)
             heavy[t, h, 1] = pos
-            hlist[t, pos:pos + c] = _row_offset(nb[t, r, b0:b0 + c])
+            hlist[t, pos:pos + c] = _row_offset(nb[t, r, b0:b0 + c]) >> sh
             pos += c
 
-    src = np.where(cnt >= 2, 0xFFFF, _row_offset(first))
-    src = np.where(heavy_mask, heavy_base + 64 * heavy_row, src).astype(np.uint16)
+    src = np.where(cnt >= 2, 0xFFFF, _row_offset(first) >> sh)
+    src = np.where(heavy_mask, heavy_base + row_b * heavy_row, src).astype(np.uint16)
     src = src.transpose(0, 2, 1)[:, order].copy()              # [T, V (position), tile]
 
     # stream entries: collision rows of each slot with 2 .. STREAM_MAX_COUNT neighbours
@@ -708,7 +716,7 @@ def wide_tables(direct, k, order=None):
         nbo = []
         for j in range(STREAM_MAX_COUNT):
             r = nb[t, rows, np.minimum(b0 + j, k - 1)]
-            nbo.append(np.where(j < c, _row_offset(r), zoff))
+            nbo.append(np.where(j < c, _row_offset(r) >> sh, zoff))
         n_e = off[-1]
         dst = (pos % WIDE_TILES) * WIDE_TILE_BYTES + _row_offset(rows)
         out[t, :n_e, 0] = (dst | (c << 16)).astype(np.uint32)
@@ -716,7 +724,7 @@ def wide_tables(direct, k, order=None):
             out[t, :n_e, 1 + w] = (nbo[2 * w] | (nbo[2 * w + 1] << 16)).astype(np.uint32)
     return WideTables(torch.from_numpy(src), torch.from_numpy(out.view(np.int32)), torch.from_numpy(coll_off),
                       stride, torch.from_numpy(heavy.view(np.int32)), heavy_stride,
-                      torch.from_numpy(hlist.view(np.int16)), hlist_stride)
+                      torch.from_numpy(hlist.view(np.int16)), hlist_stride, units)
 
 
 def slot_stream_units(direct):

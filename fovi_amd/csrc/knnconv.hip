@@ -1331,6 +1331,7 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
   p.coll_off_stride = a->coll_off_stride; p.cent_stride = a->cent_stride;
   p.tile_heavy = a->tile_heavy; p.tile_hlist = a->tile_hlist;
   p.heavy_stride = a->heavy_stride; p.hlist_stride = a->hlist_stride;
+  p.wide_units = a->wide_units ? 1 : 0;
   p.w_c_slot = a->w_c_slot > 0 ? a->w_c_slot : static_cast<int>(a->c_in);
   if (p.w_c_slot < p.C || a->k_pad < p.w_c_slot * p.V) {
     set_error("fovi_knnconv_fwd: w_c_slot=%d must be >= c_in and k_pad >= w_c_slot * n_ref", p.w_c_slot);
@@ -1351,7 +1352,7 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
     }
     if (!v5_applies(p, f8)) {
       set_error("fovi_knnconv_fwd: fragment-order weights need c_in %% %d == 0, channels-last 16-byte input "
-                "rows, the wide-layer tables within 160 KB of LDS (zero_row <= 1023)%s", f8 ? 64 : 32,
+                "rows, the wide-layer tables within 160 KB of LDS (zero_row <= 1024)%s", f8 ? 64 : 32,
                 f8 ? " and w_scale" : "");
       return 1;
     }

@@ -41,6 +41,7 @@ struct KnnParams {
   const uint16_t* tile_hlist;
   int heavy_stride;
   int hlist_stride;
+  int wide_units;   // wide-layer tables in 16-byte units (1) or bytes (0)
 };
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));

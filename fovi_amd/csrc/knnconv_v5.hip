@@ -117,7 +117,9 @@ __host__ __device__ inline int64_t v5_frag(int64_t it, int64_t ncb, int64_t cb, 
   return (it * ncb + cb) * 2 + ks;
 }
 
-template <int SV, typename OutT, bool F8>
+// SH: the tables name staged and heavy rows by byte offsets (0) or in 16-byte units (4, for
+// more than 1023 staged rows); byte offset = value << SH.
+template <int SV, typename OutT, bool F8, int SH>
 __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t tiles_per_b, int64_t n_tiles_n,
                                         int64_t total_tiles, int64_t padded_tiles, int vec_out) {
   typedef V5Elem<F8> E;
@@ -232,16 +234,16 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
   // and 6 from word 3 (missing ones are the zero row).
   auto unit_sum4 = [&](const u32x4 ce, uint32_t pq) {
     Sum a = {};
-    E::acc(a, lds16(smem, (ce[1] & 0xffffu) ^ pq));
-    E::acc(a, lds16(smem, (ce[1] >> 16) ^ pq));
-    E::acc(a, lds16(smem, (ce[2] & 0xffffu) ^ pq));
-    E::acc(a, lds16(smem, (ce[2] >> 16) ^ pq));
+    E::acc(a, lds16(smem, ((ce[1] & 0xffffu) << SH) ^ pq));
+    E::acc(a, lds16(smem, ((ce[1] >> 16) << SH) ^ pq));
+    E::acc(a, lds16(smem, ((ce[2] & 0xffffu) << SH) ^ pq));
+    E::acc(a, lds16(smem, ((ce[2] >> 16) << SH) ^ pq));
     return a;
   };
   auto unit_rest = [&](Sum& a, const u32x4 ce, uint32_t pq) {
     if (((ce[0] >> 16) & 0xffu) > 4) {
-      E::acc(a, lds16(smem, (ce[3] & 0xffffu) ^ pq));
-      E::acc(a, lds16(smem, (ce[3] >> 16) ^ pq));
+      E::acc(a, lds16(smem, ((ce[3] & 0xffffu) << SH) ^ pq));
+      E::acc(a, lds16(smem, ((ce[3] >> 16) << SH) ^ pq));
     }
   };
   // collision tile offset of a unit (the entry holds tile and row)
@@ -260,11 +262,11 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
       for (int j = 0; j < cnt; j += 4) {
         uint32_t r[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) r[q] = j + q < cnt ? hlist[w1 + j + q] : zoff;
+        for (int q = 0; q < 4; ++q) r[q] = j + q < cnt ? static_cast<uint32_t>(hlist[w1 + j + q]) << SH : zoff;
 #pragma unroll
         for (int q = 0; q < 4; ++q) E::acc(a, lds16(smem, r[q] ^ pq));
       }
-      *reinterpret_cast<u32x4*>(smem + ((w0 & 0xffffu) ^ pq)) = E::pack(a);
+      *reinterpret_cast<u32x4*>(smem + (((w0 & 0xffffu) << SH) ^ pq)) = E::pack(a);
     }
   };
   // units [from, to) of the tile's unit stream (the entry list in slot order,
@@ -340,7 +342,7 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
     u32x4 af[2][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t a = ecur[i] == 0xffffu ? rowm_off[i] + vb * V5_TILE_BYTES : ecur[i];
+      const uint32_t a = ecur[i] == 0xffffu ? rowm_off[i] + vb * V5_TILE_BYTES : ecur[i] << SH;
       af[0][i] = lds16(smem, a ^ qx0);
       af[1][i] = lds16(smem, a ^ qx1);
     }
@@ -462,35 +464,35 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
   }
 }
 
-template <int SV, typename OutT>
+template <int SV, typename OutT, int SH = 0>
 __global__ __launch_bounds__(256, 1) void knnconv_bf16_v5_kernel(KnnParams p, int ncb, int64_t tiles_per_b,
                                                                  int64_t n_tiles_n, int64_t total_tiles,
                                                                  int64_t padded_tiles, int vec_out) {
-  v5_body<SV, OutT, false>(p, ncb, tiles_per_b, n_tiles_n, total_tiles, padded_tiles, vec_out);
+  v5_body<SV, OutT, false, SH>(p, ncb, tiles_per_b, n_tiles_n, total_tiles, padded_tiles, vec_out);
 }
 
-template <int SV, typename OutT>
+template <int SV, typename OutT, int SH = 0>
 __global__ __launch_bounds__(256, 1) void knnconv_fp8_v5_kernel(KnnParams p, int ncb, int64_t tiles_per_b,
                                                                 int64_t n_tiles_n, int64_t total_tiles,
                                                                 int64_t padded_tiles, int vec_out) {
-  v5_body<SV, OutT, true>(p, ncb, tiles_per_b, n_tiles_n, total_tiles, padded_tiles, vec_out);
+  v5_body<SV, OutT, true, SH>(p, ncb, tiles_per_b, n_tiles_n, total_tiles, padded_tiles, vec_out);
 }
 
-template <int SV, bool F8, typename OutT>
+template <int SV, bool F8, typename OutT, int SH>
 static void launch_v5_kernel(const KnnParams& p, hipStream_t s, size_t lds, dim3 grid, int ncb, int64_t tiles_per_b,
                              int64_t n_tiles_n, int64_t total, int64_t padded, int vec_out) {
-  const void* fn = F8 ? reinterpret_cast<const void*>(&knnconv_fp8_v5_kernel<SV, OutT>)
-                      : reinterpret_cast<const void*>(&knnconv_bf16_v5_kernel<SV, OutT>);
+  const void* fn = F8 ? reinterpret_cast<const void*>(&knnconv_fp8_v5_kernel<SV, OutT, SH>)
+                      : reinterpret_cast<const void*>(&knnconv_bf16_v5_kernel<SV, OutT, SH>);
   (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
   if constexpr (F8)
-    hipLaunchKernelGGL((knnconv_fp8_v5_kernel<SV, OutT>), grid, dim3(256), lds, s, p, ncb, tiles_per_b, n_tiles_n,
+    hipLaunchKernelGGL((knnconv_fp8_v5_kernel<SV, OutT, SH>), grid, dim3(256), lds, s, p, ncb, tiles_per_b, n_tiles_n,
                        total, padded, vec_out);
   else
-    hipLaunchKernelGGL((knnconv_bf16_v5_kernel<SV, OutT>), grid, dim3(256), lds, s, p, ncb, tiles_per_b, n_tiles_n,
+    hipLaunchKernelGGL((knnconv_bf16_v5_kernel<SV, OutT, SH>), grid, dim3(256), lds, s, p, ncb, tiles_per_b, n_tiles_n,
                        total, padded, vec_out);
 }
 
-template <int SV, bool F8>
+template <int SV, bool F8, int SH = 0>
 static void launch_v5_sv(const KnnParams& p, int out_t, hipStream_t s) {
   const int64_t tiles_per_b = (p.Nout + V5_MT - 1) / V5_MT;
   const int64_t n_tiles_n = (p.Cout + V5_NT - 1) / V5_NT;
@@ -504,20 +506,21 @@ static void launch_v5_sv(const KnnParams& p, int out_t, hipStream_t s) {
                       reinterpret_cast<uintptr_t>(p.y) % 16 == 0;
   const dim3 grid(static_cast<unsigned>(padded));
   if (out_t == FOVI_BF16)
-    launch_v5_kernel<SV, F8, uint16_t>(p, s, lds, grid, ncb, tiles_per_b, n_tiles_n, total, padded, vec_out);
+    launch_v5_kernel<SV, F8, uint16_t, SH>(p, s, lds, grid, ncb, tiles_per_b, n_tiles_n, total, padded, vec_out);
   else
-    launch_v5_kernel<SV, F8, float>(p, s, lds, grid, ncb, tiles_per_b, n_tiles_n, total, padded, 0);
+    launch_v5_kernel<SV, F8, float, SH>(p, s, lds, grid, ncb, tiles_per_b, n_tiles_n, total, padded, 0);
 }
 
 int v5_applies(const KnnParams& p, int f8) {
   if (p.w_layout != FOVI_W_MFMA) return 0;
-  if (p.C % (f8 ? V5Elem<true>::CC : V5Elem<false>::CC) != 0 || p.zero_row <= 0 || p.zero_row > 1023 ||
+  if (p.C % (f8 ? V5Elem<true>::CC : V5Elem<false>::CC) != 0 || p.zero_row <= 0 || p.zero_row > 1024 ||
       !p.tile_lo || !p.tile_src || !p.tile_coll_off || !p.tile_cent || !p.tile_heavy || !p.tile_hlist || p.V > 255)
     return 0;
   if (f8 && !p.w_scale) return 0;
   if (p.coll_off_stride <= p.V || p.coll_off_stride % 4 != 0 || p.cent_stride < 1) return 0;
   if (p.heavy_stride < 2 || p.heavy_stride % 2 != 0 || p.hlist_stride < 8 || p.hlist_stride % 8 != 0) return 0;
-  if ((p.zero_row + 1 + p.heavy_stride) * V5_ROW > 0xffff) return 0;   // 16-bit row offsets
+  // 16-bit row offsets (bytes, or 16-byte units), below the 0xFFFF marker of stream-built sums
+  if ((p.zero_row + 1 + p.heavy_stride) * (p.wide_units ? V5_ROW / 16 : V5_ROW) >= 0xffff) return 0;
   if ((reinterpret_cast<uintptr_t>(p.tile_src) | reinterpret_cast<uintptr_t>(p.tile_coll_off) |
        reinterpret_cast<uintptr_t>(p.tile_cent) | reinterpret_cast<uintptr_t>(p.tile_heavy) |
        reinterpret_cast<uintptr_t>(p.tile_hlist)) % 16 != 0)
@@ -533,6 +536,11 @@ int v5_applies(const KnnParams& p, int f8) {
 template <bool F8>
 static int launch_v5(const KnnParams& p, int out_t, hipStream_t s) {
   const int sv = (p.zero_row * 4 + 255) / 256;
+  if (p.wide_units) {                 // 16-byte-unit tables: more than 1023 staged rows
+    if (sv > 16) return 1;
+    launch_v5_sv<16, F8, 4>(p, out_t, s);
+    return 0;
+  }
   if (sv <= 4) launch_v5_sv<4, F8>(p, out_t, s);
   else if (sv <= 8) launch_v5_sv<8, F8>(p, out_t, s);
   else if (sv <= 12) launch_v5_sv<12, F8>(p, out_t, s);

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 23
+#define FOVI_ABI_VERSION 25
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -168,20 +168,23 @@ typedef struct fovi_knnconv_args {
                                  fovi_quantize_e4m3 writes; used instead of x_scale when non-NULL */
   /* Tables of the wide-layer kernel (w_layout = FOVI_W_MFMA), in its LDS order and in the
    * slot visit order (position p visits slot slot_order[p], see fovi_knnconv_pack_weight_mfma).
-   * 64-byte rows are named by LDS byte offsets; staged row r (relative to tile_lo[t]) is at
-   * off(r) = 64 r + 16 g(r), g(r) = (bit1(r) ^ bit3(r)) | bit2(r) << 1 (16-byte part q at
-   * off(r) ^ 16 q); zero_row must be below 1024. Heavy-sum row h is at 64 (zero_row + 1 + h).
-   *   tile_src[(t * n_ref + p) * tile_points + r]: the row the MFMA reads for position p of
-   *     output row r: the neighbour's staged row (one neighbour), the zero row (none), the
-   *     row's heavy sum (more than 6), or 0xFFFF (2 to 6: summed by the kernel's stream);
+   * 64-byte rows are named by LDS offsets u(r): byte offsets off(r) (wide_units = 0), or in
+   * 16-byte units off(r) / 16 (wide_units = 1, needed past 1023 staged rows): staged row r
+   * (relative to tile_lo[t]) is at byte off(r) = 64 r + 16 g(r), g(r) = (bit1(r) ^ bit3(r)) |
+   * bit2(r) << 1 (16-byte part q at off(r) ^ 16 q); zero_row must be at most 1024. Heavy-sum
+   * row h is at byte 64 (zero_row + 1 + h). Collision-tile destinations are in bytes.
+   *   tile_src[(t * n_ref + p) * tile_points + r]: the row (unit offset) the MFMA reads for
+   *     position p of output row r: the neighbour's staged row (one neighbour), the zero row
+   *     (none), the row's heavy sum (more than 6), or 0xFFFF (2 to 6: summed by the stream);
    *   tile_cent[(t * cent_stride + i) * 4 + 0..3], i in [tile_coll_off[t * coll_off_stride + p],
    *     tile_coll_off[t * coll_off_stride + p + 1]): one 16-byte entry per (position p, row
    *     with 2 to 6 neighbours), decreasing count within a position: word 0 = destination
-   *     ((p % 3) * 16384 + off(row)) | count << 16; words 1-3 = off() of the staged rows of
-   *     neighbours 1-6 in list order, two 16-bit halves each (the zero row past the count);
+   *     ((p % 3) * 16384 + off(row), bytes) | count << 16; words 1-3 = u() of the staged
+   *     rows of neighbours 1-6 in list order, two 16-bit halves each (the zero row past the
+   *     count);
    *   tile_heavy[(t * heavy_stride + h) * 2 + 0..1]: heavy entry h (more than 6 neighbours):
-   *     word 0 = its heavy-sum row's offset | count << 16 (count 0: padding); word 1 = the
-   *     index of its first neighbour in tile_hlist[t * hlist_stride ...] (off() values, in
+   *     word 0 = its heavy-sum row's unit offset | count << 16 (count 0: padding); word 1 =
+   *     the index of its first neighbour in tile_hlist[t * hlist_stride ...] (u() values, in
    *     list order). */
   const uint16_t* tile_src;
   const int32_t* tile_coll_off;
@@ -215,7 +218,9 @@ typedef struct fovi_knnconv_args {
   int32_t fc_tile_points;
   int32_t fc_zero_row;
   int32_t fc_xmax;
-  int32_t reserved6;
+  int32_t wide_units;         /* 1: the wide-layer tables (tile_src, tile_cent words 1-3, tile_heavy
+                                 word 0, tile_hlist) name staged and heavy rows in 16-byte units
+                                 (needed past 1023 staged rows); 0: in bytes */
 } fovi_knnconv_args;
 
 int fovi_knnconv_fwd(const fovi_knnconv_args* args, void* stream);

@@ -270,6 +270,7 @@ def test_few_channel_fused_c4_patch_embedding_geometry():
     (128, 128, 25, 256, 256, False, None, 2), # C3 geometry
     (24, 12, 25, 64, 192, True, "relu", 4),   # one 256-channel tile, 192 real channels
     (16, 16, 9, 192, 384, False, None, 3),    # C2 layer 3: two tiles, 384 real
+    (32, 16, 25, 64, 192, True, "relu", 3),   # C2 layer 2: one tile reads all 1024 input rows
 ])
 def test_fragment_order_kernel(res_in, res_out, k, c_in, c_out, bias, act, batch):
     """Wide bf16 layers take the fragment-order (256 x 256 tile) kernel; it matches the oracle
@@ -320,7 +321,8 @@ _SELECTION = [
     ("C1 fp32", (64, 64, 9, 3, 64, None), "f32", "f32"),
     ("C1 bf16", (64, 64, 9, 3, 64, None), "bf16", "bf16 few-channel fused"),
     ("C2 layer 1", (64, 32, 49, 3, 64, None), "bf16", "bf16 few-channel fused"),
-    ("C2 layer 2", (32, 16, 25, 64, 192, None), "bf16", "bf16 v4"),
+    ("C2 layer 2", (32, 16, 25, 64, 192, None), "bf16", "bf16 v5"),
+    ("bf16 rows, no wide tables", (32, 16, 25, 64, 64, None), "bf16", "bf16 v4"),
     ("C2 layer 3", (16, 16, 9, 192, 384, None), "bf16", "bf16 v5"),
     ("C2 layer 4", (16, 16, 9, 384, 256, None), "bf16", "bf16 v5"),
     ("C2 layer 5", (16, 16, 9, 256, 256, None), "bf16", "bf16 v5"),
@@ -342,6 +344,7 @@ def test_kernel_selection(name, geom, mode, path):
     layer = _layer(res_in, res_out, k, c_in, c_out, side, bias=True)
     if mode == "bf16 no tiles":
         layer.tile_lo = None            # a caller without the tile tables
+        layer.mfma_weights = False
     x = torch.randn(1, c_in, res_in * res_in, generator=torch.Generator().manual_seed(21))
     xd = x.cuda()
     if mode == "f32":

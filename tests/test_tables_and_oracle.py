@@ -224,7 +224,8 @@ def test_direct_tables_lists_and_zero_row(res_in, res_out, k):
 
 
 @pytest.mark.parametrize("res_in,res_out,k,permute", [(32, 32, 25, False), (64, 32, 49, False), (16, 16, 9, False),
-                                                      (128, 128, 25, False), (32, 32, 25, True)])
+                                                      (128, 128, 25, False), (32, 32, 25, True),
+                                                      (32, 16, 25, False)])   # C2 layer 2: 1024 staged rows
 def test_wide_tables_decode_to_the_csr_lists(res_in, res_out, k, permute):
     """Fragment-order kernel tables: every (slot, row) source, stream entry and heavy entry
     decodes back to the slot-major CSR lists (global input index = staged row + tile_lo)."""
@@ -233,15 +234,19 @@ def test_wide_tables_decode_to_the_csr_lists(res_in, res_out, k, permute):
     lo, span, ent, nbr, coll, coll_n, zr = direct
     order = list(np.random.default_rng(3).permutation(t["V"])) if permute else list(range(t["V"]))
     wide = T.wide_tables(direct, t["k"], order if permute else None)
-    if wide is None:                      # staged-row offsets need 16 bits
-        assert zr > 1023
+    if wide is None:                      # more rows than the kernel stages
+        assert zr > T.WIDE_MAX_ROWS
         return
     src, cent, coll_off = wide.src.numpy().astype(np.int64), wide.coll.numpy().view(np.uint32), wide.coll_off.numpy()
     heavy, hlist = wide.heavy.numpy().view(np.uint32), wide.hlist.numpy().view(np.uint16)
-    # offset -> row: 64-byte rows, swizzle bits only in bits 4-5
-    row_of = {int(T._row_offset(r)): r for r in range(zr + 1)}
-    assert len(row_of) == zr + 1 and all(o & 15 == 0 for o in row_of)
-    heavy_base = (zr + 1) * 64
+    # byte offset -> row: 64-byte rows, swizzle bits only in bits 4-5; the tables hold staged
+    # and heavy rows in bytes or 16-byte units, collision-tile destinations in bytes
+    row_of_byte = {int(T._row_offset(r)): r for r in range(zr + 1)}
+    assert len(row_of_byte) == zr + 1 and all(o & 15 == 0 for o in row_of_byte)
+    sh = 4 if wide.units else 0
+    assert wide.units == (zr > 1023)
+    row_of = {o >> sh: r for o, r in row_of_byte.items()}
+    heavy_base = (zr + 1) * (64 >> sh)
     ptr, gnbr = t["ptr"].numpy(), t["nbr"].numpy()
     lo = lo.numpy().astype(np.int64)
     n_tiles, V = src.shape[0], t["V"]
@@ -258,7 +263,7 @@ def test_wide_tables_decode_to_the_csr_lists(res_in, res_out, k, permute):
                 dst, cnt = w0 & 0xFFFF, (w0 >> 16) & 0xFF
                 assert w0 >> 24 == 0
                 assert dst // T.WIDE_TILE_BYTES == pos % T.WIDE_TILES
-                row = row_of[dst % T.WIDE_TILE_BYTES]
+                row = row_of_byte[dst % T.WIDE_TILE_BYTES]
                 n = tt * 256 + row
                 assert 2 <= cnt <= T.STREAM_MAX_COUNT and cnt == (ptr[n, v] & 0xFFFF)
                 beg = ptr[n, v] >> 16
@@ -278,7 +283,7 @@ def test_wide_tables_decode_to_the_csr_lists(res_in, res_out, k, permute):
                     continue
                 cnt = ptr[n, v] & 0xFFFF
                 if cnt > T.STREAM_MAX_COUNT:       # heavy: its own row, summed once per chunk
-                    h, r = divmod(int(src[tt, pos, row]) - heavy_base, 64)
+                    h, r = divmod(int(src[tt, pos, row]) - heavy_base, 64 >> sh)
                     assert r == 0 and 0 <= h < wide.heavy_stride
                     w0, w1 = (int(x) for x in heavy[tt, h])
                     assert w0 & 0xFFFF == src[tt, pos, row] and (w0 >> 16) & 0xFF == cnt
