@@ -305,11 +305,21 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         self.ref_coords = ref.to(self.device, dtype=getattr(self.in_coords, "dtype", torch.float32))
 
     def compute_local_rf_slots(self, knn_indices):
+        """Ref slot ``[N_out, k]`` of every neighbour (reference ``knn.py:599-647``), on the CPU;
+        for a CUDA layer the per-neighbour arithmetic runs on the GPU and only the points
+        it flags as near a tie are recomputed here (``knn_tables.local_rf_slots_device``,
+        the same slots bit for bit)."""
+        ref = self.ref_coords.cpu()
         if not self.sample_cortex:
-            return T.visual_rf_slots(knn_indices, self.sample_coords, self.ref_coords.cpu())
-        return T.local_rf_slots(knn_indices, self.sample_coords, self.sample_coords_cart,
-                                self.out_coords.cortical.cpu(), self.out_coords.cartesian.cpu(),
-                                self.ref_coords.cpu())
+            return T.visual_rf_slots(knn_indices, self.sample_coords, ref)
+        args = (knn_indices, self.sample_coords, self.sample_coords_cart, self.out_coords.cortical.cpu(),
+                self.out_coords.cartesian.cpu(), ref)
+        dev = torch.device(self.device) if not isinstance(self.device, torch.device) else self.device
+        if (dev.type == "cuda" and torch.cuda.is_available()
+                and T.local_rf_slots_device_ok(knn_indices, self.sample_coords, ref)):
+            slots, self.slots_recomputed = T.local_rf_slots_device(*args, device=dev)
+            return slots
+        return T.local_rf_slots(*args)
 
     @property
     def local_rf(self):

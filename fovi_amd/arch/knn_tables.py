@@ -213,6 +213,101 @@ def local_rf_slots(knn_idx, src_cortical, src_cart, out_cortical, out_cart, ref_
     return nearest.t().contiguous()
 
 
+def local_rf_slots_rows(knn_idx, src_cortical, src_cart, out_cortical, out_cart, ref_coords, rows):
+    """``local_rf_slots`` for the output points ``rows`` only: ``[len(rows), k]``, equal to
+    those rows of the full computation. Every step is per output point (the per-point
+    ``cdist``, ``arctan2``/``cos``/``sin`` element by element, the min-max over a point's
+    neighbours) except the final ``cdist`` to the ref grid, whose formula depends on the row
+    count (a matrix product above 25 rows): it runs on at least 26 rows, the subset padded
+    with copies of its first row, as the full call does for more than 25 output points."""
+    rows = torch.as_tensor(rows, dtype=torch.long)
+    k, n_out = knn_idx.shape
+    if rows.numel() == 0:
+        return torch.zeros(0, k, dtype=torch.long)
+    sub = knn_idx[:, rows]
+    nb = src_cortical[sub]
+    nb_cart = src_cart[sub]
+    oc, ocart = out_cortical[rows], out_cart[rows]
+    theta = torch.arctan2(nb_cart[:, :, 1] - ocart[:, 1], nb_cart[:, :, 0] - ocart[:, 0])
+    m = rows.numel()
+    radial = torch.empty(m, k, dtype=nb.dtype)
+    for i in range(m):
+        radial[i] = torch.cdist(oc[i].unsqueeze(0), nb[:, i]).squeeze(0)
+    radial = radial.t()
+    radial[sub < 0] = 0
+    local = torch.stack([radial * torch.cos(theta), radial * torch.sin(theta)], dim=2)
+    lo = local.min(dim=0, keepdim=True)[0]
+    hi = local.max(dim=0, keepdim=True)[0]
+    local = 2 * (local - lo) / (hi - lo + 1e-6) - 1
+    pad = 0
+    if n_out > 25 and m <= 25:
+        pad = 26 - m
+        local = torch.cat([local, local[:, :1].expand(k, pad, 2)], dim=1)
+    nearest = torch.argmin(torch.cdist(local, ref_coords), dim=2)
+    return nearest[:, :m].t().contiguous()
+
+
+def local_rf_slots_device_ok(knn_idx, src_cortical, ref_coords):
+    """Whether ``local_rf_slots_device`` applies: fp32 coordinates of 1 to 3 dimensions,
+    k <= 256 neighbours, at most 65536 ref points."""
+    k = knn_idx.shape[0]
+    return (src_cortical.dtype == torch.float32 and ref_coords.dtype == torch.float32
+            and 1 <= src_cortical.shape[1] <= 3 and 1 <= k <= 256 and 1 <= ref_coords.shape[0] <= 65536)
+
+
+def local_rf_slots_device(knn_idx, src_cortical, src_cart, out_cortical, out_cart, ref_coords, device,
+                          tol=1e-4):
+    """``local_rf_slots`` with the per-neighbour arithmetic on the GPU: the same ``[N_out, k]``
+    int64 slots, bit for bit, on the CPU, and the number of output points recomputed here.
+
+    ``fovi_local_rf_slots`` assigns every neighbour in fp32 and flags each output point where
+    some neighbour's two nearest ref points are closer than ``tol`` plus its bound on the
+    kernel's difference from this host's arithmetic (its transcendental functions and the
+    matrix-product ``cdist`` round differently); those points are recomputed here with
+    ``local_rf_slots_rows``, the reference's own calls."""
+    from .. import _lib
+    if not local_rf_slots_device_ok(knn_idx, src_cortical, ref_coords):
+        raise ValueError("local_rf_slots_device: needs fp32 coordinates of 1 to 3 dimensions, k <= 256, "
+                         "n_ref <= 65536")
+    k, n_out = knn_idx.shape
+    lib = _lib.load()
+    dev = torch.device(device)
+    stream = _lib.stream_handle(dev)
+    dim = src_cortical.shape[1]
+
+    def put(t, cols):
+        t = t.to(device=dev, dtype=torch.float32).contiguous()
+        if t.dim() != 2 or t.shape[1] != cols:
+            raise ValueError(f"local_rf_slots_device: coordinate rows of {cols} expected, got {tuple(t.shape)}")
+        return t
+
+    sc, scart = put(src_cortical, dim), put(src_cart, 2)
+    oc, ocart = put(out_cortical, dim), put(out_cart, 2)
+    # the visual-field set may be longer (log-polar layers: the pad ring follows the points)
+    if scart.shape[0] < sc.shape[0] or ocart.shape[0] != n_out or oc.shape[0] != n_out:
+        raise ValueError("local_rf_slots_device: point counts of the coordinate sets disagree")
+    n_src = sc.shape[0]
+    if knn_idx.numel() and (int(knn_idx.max()) >= n_src or int(knn_idx.min()) < -1):
+        raise ValueError("local_rf_slots_device: neighbour index out of range")
+    idx = knn_idx.to(device=dev, dtype=torch.int32).contiguous()
+    ref = put(ref_coords, 2)
+    slots = torch.empty(n_out, k, dtype=torch.int32, device=dev)
+    flags = torch.empty(n_out, dtype=torch.int32, device=dev)
+    a = _lib.LocalRfArgs()
+    a.src_cortical, a.src_cart, a.n_src, a.dim = sc.data_ptr(), scart.data_ptr(), n_src, dim
+    a.out_cortical, a.out_cart, a.n_out = oc.data_ptr(), ocart.data_ptr(), n_out
+    a.knn_idx, a.k, a.ref, a.n_ref = idx.data_ptr(), k, ref.data_ptr(), ref.shape[0]
+    a.tol = float(tol)
+    a.slots, a.flags = slots.data_ptr(), flags.data_ptr()
+    _lib.check(lib.fovi_local_rf_slots(a, stream), "fovi_local_rf_slots")
+    out = slots.cpu().long()
+    rows = torch.nonzero(flags.cpu(), as_tuple=True)[0]
+    if rows.numel():
+        out[rows] = local_rf_slots_rows(knn_idx, src_cortical, src_cart, out_cortical, out_cart, ref_coords,
+                                        rows)
+    return out, int(rows.numel())
+
+
 def visual_rf_slots(knn_idx, src_cart, ref_coords):
     """Ref slot id ``[N_out, k]`` (int64) of every neighbour for visual-field neighbourhoods
     (``sample_cortex=False``): the neighbours' visual (x, y), min-max normalised to [-1, 1]

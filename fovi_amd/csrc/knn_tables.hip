@@ -197,10 +197,175 @@ static int reserve_lds(const void* kernel, size_t lds, const char* what) {
   return 0;
 }
 
+// ---------------------------------------------------------------------------
+// Ref-slot assignment of every neighbour (KNNConvLayer.compute_local_rf,
+// fovi/arch/knn.py:599-647), one wave per output point, candidate-and-verify:
+// the kernel follows the reference's formulas in fp32 and flags each output
+// point where some neighbour's nearest and second-nearest ref points lie
+// within `tol`; the host recomputes the flagged points with the reference's
+// own torch calls (their transcendental functions and the matrix-product
+// cdist round differently from these), so the combined table is the host's.
+//  * angle theta = atan2(y_j - y_n, x_j - x_n) on the visual-field points;
+//  * radial distance r = cdist(cortical_n, cortical_j): the direct form
+//    sqrt(sum (a - b)^2), or for k > 25 the matrix-product form torch's cdist
+//    switches to, sqrt(max(|a|^2 + |b|^2 - 2 a.b, 0)); r = 0 for a padding
+//    index (< 0), whose coordinates are the last point's (Python indexing);
+//  * local point (r cos theta, r sin theta), min-max normalised over the
+//    point's neighbours to 2 (p - lo) / (hi - lo + 1e-6) - 1;
+//  * the nearest ref point (first index among equals), distances in the
+//    direct form, or the matrix-product form for more than 25 output points.
+// ---------------------------------------------------------------------------
+constexpr int RF_LANES = 64;
+constexpr int RF_PER_LANE = 4;   // k <= 256
+
+struct RfParams {
+  const float* src_cort;
+  const float* src_cart;
+  int64_t n_src;
+  int dim;
+  const float* out_cort;
+  const float* out_cart;
+  int64_t n_out;
+  const int32_t* knn;
+  int k;
+  const float* ref;
+  int V;
+  int mm_radial, mm_ref;
+  float tol;
+  int32_t* slots;
+  int32_t* flags;
+};
+
+// Radial distance and a bound on its difference from the host's value: the
+// direct form differs by a few ulps of r; the matrix-product form by a few ulps
+// of the terms it sums, which near r = 0 is sqrt of that (cancellation).
+__device__ __forceinline__ float rf_radial(const float* a, const float* b, int dim, int mm, float* err) {
+  if (!mm) {
+    float s = 0.0f;
+    for (int d = 0; d < dim; ++d) {
+      const float t = a[d] - b[d];
+      s = s + t * t;
+    }
+    const float r = sqrtf(s);
+    *err = r * 0x1p-20f;
+    return r;
+  }
+  float na = 0.0f, nb = 0.0f, dot = 0.0f;
+  for (int d = 0; d < dim; ++d) {
+    na = na + a[d] * a[d];
+    nb = nb + b[d] * b[d];
+    dot = dot + (-2.0f * a[d]) * b[d];
+  }
+  const float r = sqrtf(fmaxf(dot + na + nb, 0.0f));
+  const float e2 = (na + nb + fabsf(dot)) * 0x1p-20f;
+  *err = e2 / (r + sqrtf(e2));
+  return r;
+}
+
+__global__ __launch_bounds__(RF_LANES) void local_rf_slots_kernel(RfParams p) {
+  const int64_t n = blockIdx.x;
+  const int lane = threadIdx.x;
+  float oc[3] = {0.0f, 0.0f, 0.0f};
+  for (int d = 0; d < p.dim; ++d) oc[d] = p.out_cort[n * p.dim + d];
+  const float ox = p.out_cart[2 * n], oy = p.out_cart[2 * n + 1];
+  float lx[RF_PER_LANE], ly[RF_PER_LANE];
+  float mnx = __builtin_inff(), mny = __builtin_inff(), mxx = -__builtin_inff(), mxy = -__builtin_inff();
+  float emax = 0.0f;
+#pragma unroll
+  for (int m = 0; m < RF_PER_LANE; ++m) {
+    const int i = lane + RF_LANES * m;
+    lx[m] = ly[m] = 0.0f;
+    if (i >= p.k) continue;
+    const int32_t j = p.knn[static_cast<int64_t>(i) * p.n_out + n];
+    const int64_t jj = j < 0 ? p.n_src - 1 : j;
+    float sc[3] = {0.0f, 0.0f, 0.0f};
+    for (int d = 0; d < p.dim; ++d) sc[d] = p.src_cort[jj * p.dim + d];
+    const float th = atan2f(p.src_cart[2 * jj + 1] - oy, p.src_cart[2 * jj] - ox);
+    float er = 0.0f;
+    float r = rf_radial(oc, sc, p.dim, p.mm_radial, &er);
+    if (j < 0) r = er = 0.0f;
+    lx[m] = r * cosf(th);
+    ly[m] = r * sinf(th);
+    // the angle and its cosine and sine differ from the host's by a few ulps
+    emax = fmaxf(emax, er + r * 0x1p-19f);
+    mnx = fminf(mnx, lx[m]); mxx = fmaxf(mxx, lx[m]);
+    mny = fminf(mny, ly[m]); mxy = fmaxf(mxy, ly[m]);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    mnx = fminf(mnx, __shfl_xor(mnx, off)); mxx = fmaxf(mxx, __shfl_xor(mxx, off));
+    mny = fminf(mny, __shfl_xor(mny, off)); mxy = fmaxf(mxy, __shfl_xor(mxy, off));
+    emax = fmaxf(emax, __shfl_xor(emax, off));
+  }
+  const float dx = (mxx - mnx) + 1e-6f, dy = (mxy - mny) + 1e-6f;
+  // an error e in the local points moves a normalised coordinate by at most
+  // 8 e / span (the point, lo and hi each move); a distance comparison sees
+  // twice the sum over both axes
+  const float tol = p.tol + 16.0f * emax * (1.0f / dx + 1.0f / dy);
+  bool near = !(tol < 0.5f);
+#pragma unroll
+  for (int m = 0; m < RF_PER_LANE; ++m) {
+    const int i = lane + RF_LANES * m;
+    if (i >= p.k) continue;
+    const float x = (2.0f * (lx[m] - mnx)) / dx - 1.0f;
+    const float y = (2.0f * (ly[m] - mny)) / dy - 1.0f;
+    const float xn = x * x + y * y;
+    float best = __builtin_inff(), second = __builtin_inff();
+    int bv = 0;
+    for (int v = 0; v < p.V; ++v) {
+      const float rx = p.ref[2 * v], ry = p.ref[2 * v + 1];
+      float dist;
+      if (p.mm_ref) {
+        dist = sqrtf(fmaxf((-2.0f * x) * rx + (-2.0f * y) * ry + xn + (rx * rx + ry * ry), 0.0f));
+      } else {
+        const float tx = x - rx, ty = y - ry;
+        dist = sqrtf(tx * tx + ty * ty);
+      }
+      if (dist < best) {
+        second = best;
+        best = dist;
+        bv = v;
+      } else if (dist < second) {
+        second = dist;
+      }
+    }
+    p.slots[n * p.k + i] = bv;
+    near |= !(second - best > tol);
+  }
+  const bool any = __builtin_amdgcn_ballot_w64(near) != 0;
+  if (lane == 0) p.flags[n] = any ? 1 : 0;
+}
+
 }  // namespace
 }  // namespace fovi
 
 using namespace fovi;
+
+extern "C" int fovi_local_rf_slots(const fovi_local_rf_args* a, void* stream) {
+  clear_error();
+  if (!a || !a->src_cortical || !a->src_cart || !a->out_cortical || !a->out_cart || !a->knn_idx || !a->ref ||
+      !a->slots || !a->flags) {
+    set_error("fovi_local_rf_slots: null pointer");
+    return 1;
+  }
+  if (a->dim < 1 || a->dim > 3 || a->k < 1 || a->k > RF_LANES * RF_PER_LANE || a->n_ref < 1 ||
+      a->n_ref > 65536 || a->n_out < 0 || a->n_src < 1 || !(a->tol >= 0.0f)) {
+    set_error("fovi_local_rf_slots: need 1 <= dim <= 3, 1 <= k <= %d, 1 <= n_ref <= 65536, n_src >= 1, tol >= 0 "
+              "(dim=%d k=%lld n_ref=%lld)", RF_LANES * RF_PER_LANE, a->dim, (long long)a->k, (long long)a->n_ref);
+    return 1;
+  }
+  if (a->n_out == 0) return 0;
+  if (a->n_out > INT32_MAX) { set_error("fovi_local_rf_slots: n_out too large"); return 1; }
+  RfParams p;
+  p.src_cort = a->src_cortical; p.src_cart = a->src_cart; p.n_src = a->n_src; p.dim = a->dim;
+  p.out_cort = a->out_cortical; p.out_cart = a->out_cart; p.n_out = a->n_out;
+  p.knn = a->knn_idx; p.k = static_cast<int>(a->k); p.ref = a->ref; p.V = static_cast<int>(a->n_ref);
+  p.mm_radial = a->k > 25; p.mm_ref = a->n_out > 25 || a->n_ref > 25; p.tol = a->tol;
+  p.slots = a->slots; p.flags = a->flags;
+  hipLaunchKernelGGL(local_rf_slots_kernel, dim3(static_cast<unsigned>(a->n_out)), dim3(RF_LANES), 0,
+                     static_cast<hipStream_t>(stream), p);
+  return check_launch("fovi_local_rf_slots");
+}
 
 static bool knn_sizes_ok(int64_t k, int64_t n_in, int64_t n_out, const char* what) {
   if (k < 1 || k > KNN_MAX_K || n_out < 0 || n_in < k * 64 || n_in > INT32_MAX) {

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 25
+#define FOVI_ABI_VERSION 26
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -497,6 +497,43 @@ typedef struct fovi_knn_select_args {
 } fovi_knn_select_args;
 
 int fovi_knn_select(const fovi_knn_select_args* args, void* stream);
+
+/*
+ * Ref slot of every neighbour, replacing the host loop of
+ * KNNConvLayer.compute_local_rf (fovi/arch/knn.py:599-647, sample_cortex=True):
+ * per output point n and neighbour i (j = knn_idx[i * n_out + n], k-major as
+ * knn_indices; j < 0 reads point n_src - 1 and has radius 0):
+ *   theta = atan2(y_j - y_n, x_j - x_n) on the visual-field points (cart),
+ *   r = |cortical_n - cortical_j| (the matrix-product form torch's cdist
+ *   uses for k > 25), local = (r cos theta, r sin theta), min-max normalised
+ *   over the point's neighbours to 2 (p - lo) / (hi - lo + 1e-6) - 1, and
+ *   slots[n * k + i] = the nearest ref point (first among equals; the
+ *   matrix-product form for n_out > 25 or n_ref > 25).
+ * fp32 throughout; flags[n] = 1 where, for some neighbour, the nearest and
+ * second-nearest ref points lie within tol plus a bound on the kernel's
+ * difference from the host's arithmetic: those points' slots must be
+ * recomputed on the host (candidate and verify); flags[n] = 0 means the
+ * slots equal the host's. Needs 1 <= dim <= 3, 1 <= k <= 256,
+ * 1 <= n_ref <= 65536, tol >= 0.
+ */
+typedef struct fovi_local_rf_args {
+  const float* src_cortical;  /* [n_src, dim] */
+  const float* src_cart;      /* [n_src, 2] */
+  int64_t n_src;
+  int dim;
+  const float* out_cortical;  /* [n_out, dim] */
+  const float* out_cart;      /* [n_out, 2] */
+  int64_t n_out;
+  const int32_t* knn_idx;     /* [k, n_out] */
+  int64_t k;
+  const float* ref;           /* [n_ref, 2] */
+  int64_t n_ref;
+  float tol;
+  int32_t* slots;             /* [n_out, k] */
+  int32_t* flags;             /* [n_out] */
+} fovi_local_rf_args;
+
+int fovi_local_rf_slots(const fovi_local_rf_args* args, void* stream);
 
 /*
  * Weight gradient of the kNN convolution without the slot-sum matrix (the

@@ -101,3 +101,80 @@ def test_layer_tables_built_on_the_gpu_equal_the_host_build():
     assert torch.equal(gpu.slots, cpu.slots)
     with pytest.raises(ValueError):
         T.knn_logpolar_device(ci.cortical, co.cortical, 65, "cuda")     # 65 * 64 > 4096
+
+
+# -------------------------------------------------- ref slots (fovi_local_rf_slots) ---
+def _logpolar_case(res_in, res_out, k):
+    ci = SamplingCoords(16, 2.78, res_in, style="logpolar")
+    co = SamplingCoords(16, 2.78, res_out, style="logpolar")
+    idx, _, src = T.knn_logpolar(ci.cortical, co.cortical, k)
+    ref, _ = T.reference_grid(k)
+    return idx, src, ci.cartesian, co.cortical, co.cartesian, ref
+
+
+def test_device_slots_eligibility():
+    idx = torch.zeros(25, 10, dtype=torch.long)
+    assert T.local_rf_slots_device_ok(idx, torch.zeros(5, 2), torch.zeros(25, 2))
+    assert T.local_rf_slots_device_ok(idx, torch.zeros(5, 3), torch.zeros(25, 2))
+    assert not T.local_rf_slots_device_ok(idx, torch.zeros(5, 2, dtype=torch.float64), torch.zeros(25, 2))
+    assert not T.local_rf_slots_device_ok(torch.zeros(257, 10, dtype=torch.long), torch.zeros(5, 2),
+                                          torch.zeros(25, 2))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("res_in,res_out,k", [(64, 64, 9), (64, 32, 49), (32, 16, 25), (16, 8, 9),
+                                              (128, 128, 25), (128, 16, 256), (24, 12, 7), (8, 4, 9)])
+def test_device_slots_equal_host(res_in, res_out, k):
+    """Log-polar layers of C1-C4's shapes, both cdist forms of the radius (k <= 25, k > 25) and
+    of the ref distances (N_out and V on either side of 25)."""
+    args = _logpolar_case(res_in, res_out, k)
+    want = T.local_rf_slots(*args)
+    got, redone = T.local_rf_slots_device(*args, device="cuda")
+    print(f"\n{res_in}->{res_out} k={k}: {redone} of {want.shape[0]} points recomputed on the host")
+    assert got.dtype == want.dtype and got.shape == want.shape
+    assert torch.equal(got, want), f"slots differ at {int((got != want).sum())} entries"
+
+
+@pytest.mark.gpu
+def test_device_slots_with_padding_entries():
+    """Entries < 0 (a partition's padding) read the last point and have radius 0."""
+    idx, *rest = _logpolar_case(32, 16, 49)
+    g = torch.Generator().manual_seed(5)
+    idx = idx.clone()
+    cut = torch.randint(20, 50, (idx.shape[1],), generator=g)
+    idx[torch.arange(idx.shape[0]).unsqueeze(1) >= cut.unsqueeze(0)] = -1
+    want = T.local_rf_slots(idx, *rest)
+    got, _ = T.local_rf_slots_device(idx, *rest, device="cuda")
+    assert torch.equal(got, want), f"slots differ at {int((got != want).sum())} entries"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", [0, 1])
+def test_device_slots_tie_heavy(seed):
+    """Points on a coarse lattice: many neighbours fall exactly between two ref points, so the
+    host recomputation has work to do."""
+    g = torch.Generator().manual_seed(seed)
+    src = torch.randint(0, 9, (600, 2), generator=g).float() / 8
+    out = torch.randint(0, 9, (80, 2), generator=g).float() / 8
+    idx, _, norm = T.knn_logpolar(src, out, 16)
+    ref, _ = T.reference_grid(16)
+    want = T.local_rf_slots(idx, norm, src, out, out, ref)
+    got, redone = T.local_rf_slots_device(idx, norm, src, out, out, ref, device="cuda")
+    assert redone > 0
+    assert torch.equal(got, want), f"slots differ at {int((got != want).sum())} entries"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["iso_16_8", "iso_24_12", "iso_16_16"])
+def test_device_slots_isotropic_equal_host_build(name):
+    """Isotropic layers (3-D cortical coordinates, pad-ring neighbours) built on the GPU: slots
+    equal the host build's (which the CPU tests pin to the reference's tests/golden/isotropic.npz
+    on the host that wrote it)."""
+    from fovi_amd.arch.knn import KNNConvLayer
+    r_in, r_out, k = {"iso_16_8": (16, 8, 9), "iso_24_12": (24, 12, 25), "iso_16_16": (16, 16, 9)}[name]
+    ci = SamplingCoords(16, 2.78, r_in, style="isotropic")
+    co = SamplingCoords(16, 2.78, r_out, style="isotropic")
+    layer = KNNConvLayer(1, 1, k, ci, co, device="cuda")
+    assert hasattr(layer, "slots_recomputed")
+    cpu = KNNConvLayer(1, 1, k, ci, co, device="cpu")
+    assert torch.equal(layer.slots, cpu.slots)

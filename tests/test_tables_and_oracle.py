@@ -376,3 +376,23 @@ def test_few_channel_tables_rebuild_the_slot_sums(res_in, res_out, k, side, cp, 
             m = rows.stop - rows.start
             np.testing.assert_allclose(got[:m], want[rows, c * spc:(c + 1) * spc], rtol=1e-12, atol=1e-12)
             assert not got[m:].any(), "rows past n_out must be zero"
+
+
+@pytest.mark.parametrize("res_in,res_out,k,side", [(64, 64, 9, None), (64, 32, 49, None), (32, 16, 25, None),
+                                                    (128, 16, 256, 16), (24, 12, 30, None)])
+def test_local_rf_slots_of_a_subset_equal_the_full_computation(res_in, res_out, k, side):
+    """The host recomputation of flagged output points (local_rf_slots_rows) equals the full
+    computation's rows bit for bit, for subsets of 1, 7, 25 and 100 points."""
+    import numpy as np
+
+    from fovi_amd.arch import knn_tables as T
+    t = layer_tables(res_in, res_out, k, side=side)
+    src = t["cin"].cortical
+    ref, _ = T.reference_grid(t["k"], side_length=side)
+    full = t["slots"]
+    rng = np.random.default_rng(1)
+    for m in (1, 7, 25, 100):
+        rows = torch.from_numpy(np.sort(rng.choice(t["n_out"], size=min(m, t["n_out"]), replace=False)))
+        got = T.local_rf_slots_rows(t["idx"], src, t["cin"].cartesian, t["cout"].cortical, t["cout"].cartesian, ref,
+                                    rows)
+        assert torch.equal(got, full[rows]), m
