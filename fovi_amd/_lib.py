@@ -14,7 +14,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
 
-ABI_VERSION = 26
+ABI_VERSION = 27
 F32, BF16, F8E4M3 = 0, 1, 2
 NEAREST, BILINEAR = 0, 1
 PAD_ZEROS, PAD_BORDER = 0, 1
@@ -28,7 +28,7 @@ _DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float8_e4m3fn: F8
 EXPORTED = ("fovi_abi_version", "fovi_last_error", "fovi_sampler_fwd", "fovi_knnconv_fwd",
             "fovi_knnconv_pack_weight", "fovi_knnconv_weight_mfma_elems", "fovi_knnconv_pack_weight_mfma",
             "fovi_quantize_e4m3", "fovi_knnpool_fwd", "fovi_knnconv_slotsum", "fovi_knnconv_bwd_x",
-            "fovi_knn_logpolar_candidates", "fovi_knn_select", "fovi_local_rf_slots", "fovi_knnconv_dw_workspace_bytes",
+            "fovi_knn_logpolar_candidates", "fovi_knn_select", "fovi_knn_euclid_candidates", "fovi_local_rf_slots", "fovi_knnconv_dw_workspace_bytes",
             "fovi_knnconv_dw", "fovi_knnpool_bwd", "fovi_knnconv_last_path",
             "fovi_knnconv_fwd_noalloc")
 
@@ -147,6 +147,15 @@ class KnnLogpolarArgs(C.Structure):
     ]
 
 
+class KnnEuclidArgs(C.Structure):
+    _fields_ = [
+        ("src", C.c_void_p), ("dst", C.c_void_p),
+        ("n_in", C.c_int64), ("n_out", C.c_int64), ("k", C.c_int64),
+        ("dim", C.c_int32), ("src_norm_max", C.c_float),
+        ("cap", C.c_int64), ("cand_idx", C.c_void_p), ("cand_sq", C.c_void_p), ("cand_n", C.c_void_p),
+    ]
+
+
 class KnnSelectArgs(C.Structure):
     _fields_ = [
         ("n_out", C.c_int64), ("k", C.c_int64), ("cap", C.c_int64),
@@ -217,6 +226,8 @@ def load(path: str = LIB_PATH):
     lib.fovi_knn_logpolar_candidates.restype = C.c_int
     lib.fovi_knn_select.argtypes = [C.POINTER(KnnSelectArgs), C.c_void_p]
     lib.fovi_knn_select.restype = C.c_int
+    lib.fovi_knn_euclid_candidates.argtypes = [C.POINTER(KnnEuclidArgs), C.c_void_p]
+    lib.fovi_knn_euclid_candidates.restype = C.c_int
     lib.fovi_local_rf_slots.argtypes = [C.POINTER(LocalRfArgs), C.c_void_p]
     lib.fovi_local_rf_slots.restype = C.c_int
     lib.fovi_knnconv_dw_workspace_bytes.argtypes = [C.c_int64] * 6

@@ -99,7 +99,7 @@ class KNNBaseLayer:
         self.sample_coords_cart = torch.cat([in_c.cartesian.cpu(), pads], 0)
         if not self.sample_cortex:
             self.sample_coords = self.sample_coords_cart
-            return T.knn_euclidean(self.sample_coords, out_c.cartesian.cpu(), self._k, batch_size)
+            return self._knn_euclidean(out_c.cartesian.cpu(), batch_size)
         if in_c.style in ("image", "logpolar"):
             assert out_c.style == in_c.style
             if self._gpu_tables(in_c.shape[0]):
@@ -112,7 +112,20 @@ class KNNBaseLayer:
         if in_c.cortical is None:
             raise ValueError(f"style {in_c.style!r} has no cortical coordinates: use sample_cortex=False")
         self.sample_coords = torch.cat([in_c.cortical.cpu(), _pad_coords(in_c, "cortical_pad_coords")], 0)
-        return T.knn_euclidean(self.sample_coords, out_c.cortical.cpu(), self._k, batch_size)
+        return self._knn_euclidean(out_c.cortical.cpu(), batch_size)
+
+    def _knn_euclidean(self, out_pts, batch_size):
+        """``cdist`` + ``topk`` neighbours of ``out_pts`` among ``self.sample_coords``: the GPU
+        scan with host-verified candidates for a CUDA layer where it applies
+        (``knn_tables.knn_euclidean_device``, the host's results bit for bit), else the host."""
+        if self._on_gpu() and T.knn_euclidean_device_ok(self.sample_coords, self._k) \
+                and out_pts.dtype == torch.float32:
+            return T.knn_euclidean_device(self.sample_coords, out_pts, self._k, self.device, batch_size)
+        return T.knn_euclidean(self.sample_coords, out_pts, self._k, batch_size)
+
+    def _on_gpu(self):
+        dev = torch.device(self.device) if not isinstance(self.device, torch.device) else self.device
+        return dev.type == "cuda" and torch.cuda.is_available()
 
     def _compute_all_distances(self):
         """Distances ``[N_in + P, N_out]`` between every input point (pad ring included) and
@@ -135,8 +148,7 @@ class KNNBaseLayer:
     def _gpu_tables(self, n_in):
         """Whether the neighbour search runs on the GPU (``knn_tables.knn_logpolar_device``, the
         host's results bit for bit): a CUDA layer where the GPU search applies."""
-        dev = torch.device(self.device) if not isinstance(self.device, torch.device) else self.device
-        return dev.type == "cuda" and torch.cuda.is_available() and T.knn_logpolar_device_ok(n_in, self._k)
+        return self._on_gpu() and T.knn_logpolar_device_ok(n_in, self._k)
 
 
 class _KnnConvFn(torch.autograd.Function):
@@ -314,10 +326,8 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
             return T.visual_rf_slots(knn_indices, self.sample_coords, ref)
         args = (knn_indices, self.sample_coords, self.sample_coords_cart, self.out_coords.cortical.cpu(),
                 self.out_coords.cartesian.cpu(), ref)
-        dev = torch.device(self.device) if not isinstance(self.device, torch.device) else self.device
-        if (dev.type == "cuda" and torch.cuda.is_available()
-                and T.local_rf_slots_device_ok(knn_indices, self.sample_coords, ref)):
-            slots, self.slots_recomputed = T.local_rf_slots_device(*args, device=dev)
+        if self._on_gpu() and T.local_rf_slots_device_ok(knn_indices, self.sample_coords, ref):
+            slots, self.slots_recomputed = T.local_rf_slots_device(*args, device=self.device)
             return slots
         return T.local_rf_slots(*args)
 

@@ -82,58 +82,146 @@ def knn_logpolar_device_ok(n_in, k):
     return 1 <= k <= 256 and k * 64 <= n_in
 
 
-def knn_logpolar_device(in_cortical, out_cortical, k, device, max_bytes=2 << 30):
+def _deciding(sq, mask, k, gap_abs, gap_rel, exact_values=False):
+    """Candidates whose host distance can decide the selection: ``[m, cap]`` bool.
+
+    ``sq`` holds the kernel's squared distances, each within ``gap / 4`` (``gap = gap_abs +
+    gap_rel * value``, ``gap_abs`` per row) of what the host's distance squares to. A candidate
+    whose value is more than ``gap`` away from every other candidate's compares with each of
+    them as the host's values do, and one more than ``gap`` above the k-th smallest is not
+    selected: such candidates may take any value that keeps those comparisons (the kernel's
+    own, square rooted). The rest -- the k smallest and any within ``gap`` of them, and every
+    pair within ``gap`` of each other -- take the host's distances. With ``exact_values`` the
+    host's distance is a function of the kernel's value (its square root), so equal values
+    stay equal either way and only distinct values within ``gap`` count as close (every copy
+    of such a value is taken, so that equal values are treated alike)."""
+    v = sq.masked_fill(~mask, float("inf"))
+    sv, order = v.sort(dim=1)
+    g = gap_abs.unsqueeze(1)
+    kth = sv[:, k - 1:k]
+    need = v <= kth + g + gap_rel * kth
+    step = sv[:, 1:] - sv[:, :-1]
+    close = (step <= g + gap_rel * sv[:, 1:]) & torch.isfinite(sv[:, 1:])
+    if exact_values:
+        close &= step > 0
+    near = torch.zeros_like(need)
+    near[:, 1:] |= close
+    near[:, :-1] |= close
+    if exact_values:
+        # every copy of a value marked close: a running id of the distinct values in each row
+        run = torch.zeros_like(sv, dtype=torch.long)
+        run[:, 1:] = torch.cumsum(step != 0, dim=1)
+        run += torch.arange(sv.shape[0], device=sv.device).unsqueeze(1) * sv.shape[1]
+        marked = torch.zeros(sv.numel(), dtype=torch.bool, device=sv.device)
+        marked[run[near]] = True
+        near = marked[run]
+    need |= torch.zeros_like(need).scatter_(1, order, near)
+    return need & mask
+
+
+def _device_search(run, dst, n_in, k, distances, gap_rel, max_bytes, exact_values=False):
+    """Driver of the candidate-and-select GPU searches: ``(indices [k, N_out] int64, distances
+    [k, N_out] fp32)`` on the CPU.
+
+    ``run(dst_rows, cap)`` launches a candidate kernel for the output points ``dst_rows`` (a
+    device tensor) with room for ``cap`` candidates per point and returns ``(cand_idx [m, cap],
+    cand_n [m], cand_sq [m, cap], gap_abs [m])``; ``distances(flat, owner, sq)`` gives the host's
+    distances of candidate pairs (input ``flat[j]``, output ``owner[j]``, in output then index
+    order, kernel value ``sq[j]``), taken for the candidates ``_deciding`` picks; the others
+    keep the square root of the kernel's value. ``fovi_knn_select`` then replays the host's
+    selection. The scan emits every input below its running k-th smallest, so a point far in
+    index order from the first inputs collects a few hundred: every point first gets room for
+    ``max(8k, 4096)`` candidates, and any whose count exceeds that runs again with room for
+    every input, so no candidate is ever dropped. Rows go in chunks of at most ``max_bytes``
+    of candidate storage."""
+    from .. import _lib
+    n_out = dst.shape[0]
+    dev = dst.device
+    idx = torch.empty(k, n_out, dtype=torch.int32)
+    dist = torch.empty(k, n_out, dtype=torch.float32)
+    lib = _lib.load()
+    stream = _lib.stream_handle(dev)
+
+    def one(rows, cap):
+        over = []
+        chunk = max(1, min(rows.numel(), max_bytes // (cap * 24)))
+        lanes = torch.arange(cap, device=dev)
+        for a0 in range(0, rows.numel(), chunk):
+            r = rows[a0:a0 + chunk]
+            m = r.numel()
+            contiguous = int(r[-1]) - int(r[0]) + 1 == m
+            d_rows = dst[int(r[0]):int(r[0]) + m] if contiguous else dst[r.to(dev)].contiguous()
+            cand_idx, cand_n, cand_sq, gap_abs = run(d_rows, cap)
+            mask = lanes.unsqueeze(0) < cand_n.unsqueeze(1)
+            need = _deciding(cand_sq, mask, k, gap_abs, gap_rel, exact_values)
+            counts = need.sum(dim=1).cpu().numpy()
+            owner = torch.from_numpy(np.repeat(r.numpy(), counts))
+            cand_d = cand_sq.sqrt()
+            cand_d[need] = distances(cand_idx[need].cpu().long(), owner, cand_sq[need].cpu()).to(dev)
+            del cand_sq, need
+            out_i = torch.empty(k, m, dtype=torch.int32, device=dev)
+            out_d = torch.empty(k, m, dtype=torch.float32, device=dev)
+            sa = _lib.KnnSelectArgs()
+            sa.n_out, sa.k, sa.cap = m, k, cap
+            sa.cand_idx, sa.cand_d, sa.cand_n = cand_idx.data_ptr(), cand_d.data_ptr(), cand_n.data_ptr()
+            sa.idx, sa.dist = out_i.data_ptr(), out_d.data_ptr()
+            _lib.check(lib.fovi_knn_select(sa, stream), "fovi_knn_select")
+            if contiguous:
+                idx[:, int(r[0]):int(r[0]) + m] = out_i.cpu()
+                dist[:, int(r[0]):int(r[0]) + m] = out_d.cpu()
+            else:
+                idx[:, r] = out_i.cpu()
+                dist[:, r] = out_d.cpu()
+            over.append(r[cand_n.cpu() > cap])
+        return torch.cat(over) if over else torch.zeros(0, dtype=torch.long)
+
+    if n_out:
+        over = one(torch.arange(n_out), min(n_in, max(8 * k, 4096)))
+        if over.numel():
+            one(over, n_in)
+    return idx.long(), dist
+
+
+def knn_logpolar_device(in_cortical, out_cortical, k, device, max_bytes=8 << 30):
     """``knn_logpolar`` with the O(N_in N_out) scan on the GPU: the same ``(indices [k, N_out]
     int64, distances [k, N_out] fp32, normalised input coords)``, bit for bit, on the CPU.
 
     ``fovi_knn_logpolar_candidates`` emits per output point the inputs the host's heap
     selection could admit, with their exact squared distances; their square roots are taken
     here with the host builder's own call (``** (1 / 2)`` on a CPU tensor, whose rounding is
-    not always IEEE); ``fovi_knn_select`` replays the selection over them. Output points go
-    in chunks of at most ``max_bytes`` of candidate storage (``n_in`` slots per point, so no
-    row can overflow).
+    not always IEEE); ``fovi_knn_select`` replays the selection over them (``_device_search``).
     """
     from .. import _lib
     src, dst, theta_hi, theta_half = _logpolar_prep(in_cortical, out_cortical)
-    n_in, n_out = src.shape[0], dst.shape[0]
+    n_in = src.shape[0]
     if not knn_logpolar_device_ok(n_in, k):
         raise ValueError(f"knn_logpolar_device: needs 1 <= k <= 256 and k * 64 <= n_in (k={k}, n_in={n_in})")
     s_d = src.to(device=device, dtype=torch.float32).contiguous()
     d_d = dst.to(device=device, dtype=torch.float32).contiguous()
-    dev = s_d.device
-    cap = n_in
-    chunk = max(1, min(n_out, max_bytes // (cap * 12)))
-    idx = torch.empty(k, n_out, dtype=torch.int32)
-    dist = torch.empty(k, n_out, dtype=torch.float32)
     lib = _lib.load()
-    stream = _lib.stream_handle(dev)
-    slots = torch.arange(cap, device=dev)
-    for s0 in range(0, n_out, chunk):
-        m = min(chunk, n_out - s0)
-        cand_idx = torch.empty(m, cap, dtype=torch.int32, device=dev)
-        cand_sq = torch.empty(m, cap, dtype=torch.float32, device=dev)
-        cand_n = torch.empty(m, dtype=torch.int32, device=dev)
+    stream = _lib.stream_handle(s_d.device)
+
+    def run(rows, cap):
+        m = rows.shape[0]
+        cand_idx = torch.empty(m, cap, dtype=torch.int32, device=rows.device)
+        cand_sq = torch.empty(m, cap, dtype=torch.float32, device=rows.device)
+        cand_n = torch.empty(m, dtype=torch.int32, device=rows.device)
         a = _lib.KnnLogpolarArgs()
-        a.src, a.dst = s_d.data_ptr(), d_d[s0:s0 + m].data_ptr()
+        a.src, a.dst = s_d.data_ptr(), rows.data_ptr()
         a.n_in, a.n_out, a.k = n_in, m, k
         a.theta_hi, a.theta_half = float(theta_hi), float(theta_half)
         a.cap = cap
         a.cand_idx, a.cand_sq, a.cand_n = cand_idx.data_ptr(), cand_sq.data_ptr(), cand_n.data_ptr()
         _lib.check(lib.fovi_knn_logpolar_candidates(a, stream), "fovi_knn_logpolar_candidates")
-        mask = slots.unsqueeze(0) < cand_n.unsqueeze(1)
-        cand_d = torch.empty_like(cand_sq)
-        cand_d[mask] = (cand_sq[mask].cpu() ** (1 / 2)).to(dev)          # the host builder's square root
-        del cand_sq
-        out_i = torch.empty(k, m, dtype=torch.int32, device=dev)
-        out_d = torch.empty(k, m, dtype=torch.float32, device=dev)
-        sa = _lib.KnnSelectArgs()
-        sa.n_out, sa.k, sa.cap = m, k, cap
-        sa.cand_idx, sa.cand_d, sa.cand_n = cand_idx.data_ptr(), cand_d.data_ptr(), cand_n.data_ptr()
-        sa.idx, sa.dist = out_i.data_ptr(), out_d.data_ptr()
-        _lib.check(lib.fovi_knn_select(sa, stream), "fovi_knn_select")
-        idx[:, s0:s0 + m] = out_i.cpu()
-        dist[:, s0:s0 + m] = out_d.cpu()
-    return idx.long(), dist, src
+        return cand_idx, cand_n, cand_sq, torch.zeros(m, device=rows.device)
+
+    def distances(flat, owner, sq):
+        return sq ** (1 / 2)                                   # the host builder's square root
+
+    # the squared distances are exact on both sides and the square roots differ by an ulp or
+    # so: values 2^-19 apart (8 ulps of the distance) stay strictly ordered
+    idx, dist = _device_search(run, d_d, n_in, k, distances, 2 ** -19, max_bytes, exact_values=True)
+    return idx, dist, src
 
 
 def knn_logpolar(in_cortical, out_cortical, k, batch_size=None):
@@ -174,6 +262,106 @@ def knn_euclidean(in_pts, out_pts, k, batch_size=None):
         idx[:, s:e] = inds
         dist[:, s:e] = vals
     return idx, dist
+
+
+def knn_euclidean_device_ok(in_pts, k):
+    """Whether ``knn_euclidean_device`` applies: fp32 points of 1 to 3 dimensions, 1 <= k <= 256
+    and k * 64 <= N_in (where torch's CPU topk runs the heap selection the GPU replays)."""
+    return (in_pts.dtype == torch.float32 and in_pts.dim() == 2 and 1 <= in_pts.shape[1] <= 3
+            and 1 <= k <= 256 and k * 64 <= in_pts.shape[0])
+
+
+def _candidate_distances(in_pts, out_pts, flat, owner, s, e, group=256):
+    """Host distances of candidate pairs (input ``flat[j]``, output ``owner[j]``), all owners in
+    the reference chunk ``[s, e)``, equal to the entries of that chunk's ``cdist(in_pts,
+    out_pts[s:e])``: a chunk of fewer than ``group`` outputs is computed whole with that call;
+    otherwise each ``group`` consecutive outputs take one ``cdist`` over the union of their
+    candidates (at least ``group`` rows and columns, padded with repeats): at such shapes the
+    matrix-product form rounds every entry as the whole chunk's call does (a single column or a
+    few rows take other BLAS paths, which round differently)."""
+    out = torch.empty(flat.numel(), dtype=torch.float32)
+    if flat.numel() == 0:
+        return out
+    if e - s < group:
+        d = torch.cdist(in_pts, out_pts[s:e])
+        return d[flat, owner - s]
+    bounds = np.searchsorted(owner.numpy(), np.minimum(np.arange(s, e + group, group), e))
+    flat_np = flat.numpy()
+    seen = np.zeros(in_pts.shape[0], dtype=bool)
+    where = np.empty(in_pts.shape[0], dtype=np.int64)
+    for g, g0 in enumerate(range(s, e, group)):
+        a, b = int(bounds[g]), int(bounds[g + 1])
+        if a == b:
+            continue
+        seg = flat_np[a:b]
+        seen[seg] = True
+        rows = np.flatnonzero(seen)                      # the group's inputs, ascending
+        seen[rows] = False
+        where[rows] = np.arange(rows.size)
+        g1 = min(g0 + group, e)
+        cols = np.arange(g0, g0 + group).clip(max=g1 - 1)
+        r = rows if rows.size >= group else np.concatenate([rows, np.repeat(rows[:1], group - rows.size)])
+        d = torch.cdist(in_pts[torch.from_numpy(r)], out_pts[torch.from_numpy(cols)])
+        out[a:b] = d[torch.from_numpy(where[seg]), owner[a:b] - g0]
+    return out
+
+
+def knn_euclidean_device(in_pts, out_pts, k, device, batch_size=None, max_bytes=8 << 30):
+    """``knn_euclidean`` with the O(N_in N_out) scan on the GPU: the same ``(indices [k, N_out]
+    int64, distances [k, N_out] fp32)``, bit for bit, on the CPU.
+
+    ``fovi_knn_euclid_candidates`` emits per output point, in index order, every input the
+    host's heap selection could admit given how far torch's matrix-product ``cdist`` can round
+    from the direct distance; their distances are taken here with the host's ``cdist``
+    (``_candidate_distances``, over the reference's chunks of ``batch_size`` outputs); and
+    ``fovi_knn_select`` replays the selection over them (``_device_search``)."""
+    from .. import _lib
+    if not knn_euclidean_device_ok(in_pts, k) or out_pts.dtype != torch.float32 or \
+            out_pts.shape[-1] != in_pts.shape[1]:
+        raise ValueError(f"knn_euclidean_device: needs fp32 points of 1 to 3 dimensions, 1 <= k <= 256 and "
+                         f"k * 64 <= n_in (k={k}, n_in={in_pts.shape[0]})")
+    in_pts, out_pts = in_pts.contiguous(), out_pts.contiguous()
+    if not (torch.isfinite(in_pts).all() and torch.isfinite(out_pts).all()):
+        raise ValueError("knn_euclidean_device: coordinates must be finite")
+    n_in, n_out, dim = in_pts.shape[0], out_pts.shape[0], in_pts.shape[1]
+    s_d = in_pts.to(device)
+    d_d = out_pts.to(device)
+    src_norm = (torch.linalg.vector_norm(in_pts.double(), dim=1) * (1 + 2 ** -20)).to(device)
+    norm_max = float(src_norm.max())
+    step = _chunk(n_in, n_out, batch_size)
+    lib = _lib.load()
+    stream = _lib.stream_handle(s_d.device)
+
+    def run(rows, cap):
+        m = rows.shape[0]
+        cand_idx = torch.empty(m, cap, dtype=torch.int32, device=rows.device)
+        cand_sq = torch.empty(m, cap, dtype=torch.float32, device=rows.device)
+        cand_n = torch.empty(m, dtype=torch.int32, device=rows.device)
+        a = _lib.KnnEuclidArgs()
+        a.src, a.dst = s_d.data_ptr(), rows.data_ptr()
+        a.n_in, a.n_out, a.k, a.dim, a.src_norm_max = n_in, m, k, dim, norm_max
+        a.cap, a.cand_idx, a.cand_sq, a.cand_n = cap, cand_idx.data_ptr(), cand_sq.data_ptr(), cand_n.data_ptr()
+        _lib.check(lib.fovi_knn_euclid_candidates(a, stream), "fovi_knn_euclid_candidates")
+        # four times the bound on the matrix-product form's difference, 2^-20 (|x| + |y|)^2, with
+        # |x| the row's largest candidate: two values that far apart stay strictly ordered,
+        # square roots included
+        held = torch.arange(cap, device=rows.device).unsqueeze(0) < cand_n.unsqueeze(1)
+        xn = src_norm[cand_idx.clamp(0, n_in - 1).long()].masked_fill(~held, 0).amax(dim=1)
+        reach = xn + torch.linalg.vector_norm(rows.double(), dim=1)
+        return cand_idx, cand_n, cand_sq, (4.0 * 2 ** -20 * reach * reach).float() * (1 + 2 ** -10)
+
+    def distances(flat, owner, sq):
+        out = torch.empty(flat.numel(), dtype=torch.float32)
+        if flat.numel() == 0:
+            return out
+        for s in range((int(owner[0]) // step) * step, int(owner[-1]) + 1, step):
+            e = min(s + step, n_out)
+            a_, b_ = int(torch.searchsorted(owner, s)), int(torch.searchsorted(owner, e))
+            out[a_:b_] = _candidate_distances(in_pts, out_pts, flat[a_:b_], owner[a_:b_], s, e)
+        return out
+
+    # the direct form's own rounding, 2^-20 of the value per candidate, four times over
+    return _device_search(run, d_d, n_in, k, distances, 2 ** -18, max_bytes)
 
 
 def reference_grid(k, side_length=None, doubleres=False, dtype=torch.float32):

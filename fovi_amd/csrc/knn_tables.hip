@@ -188,6 +188,84 @@ __global__ __launch_bounds__(KNN_THREADS) void knn_select_kernel(int64_t n_out, 
   }
 }
 
+// Euclidean search (fovi/arch/knn.py:119-152 for isotropic cortical and visual-field points):
+// the host builder's distances are torch's CPU cdist in its matrix-product form, whose rounding
+// (|x|^2 + |y|^2 - 2 x.y summed by the BLAS kernel, then clamped and square-rooted) this kernel
+// does not reproduce. So the scan runs on the direct form sum (x - y)^2, accurate to a few ulps,
+// and emits every input whose squared distance lies within a margin of the running k-th
+// smallest: the matrix-product form differs from the exact value by at most 16 ulps of
+// (|x| + |y|)^2 (five products and sums, each rounded once), so margin = 2 * 2^-20 *
+// (r_src + |y|)^2 with r_src the largest |x|, plus 2^-20 of the running value for the direct
+// form's own rounding. An input outside the margin has a host value at or above the host's
+// running k-th smallest, which the heap never admits (it admits strictly smaller values).
+// Emits (index, direct squared distance); the host takes the distances of the candidates
+// that can decide the result with its own cdist.
+struct KnnEuParams {
+  const float* src;
+  const float* dst;
+  int64_t n_in, n_out;
+  int k, dim;
+  float src_norm_max;
+};
+
+__device__ __forceinline__ float eu_sq(const float* src, int64_t i, const float* y, int dim) {
+  float s = 0.0f;
+  for (int d = 0; d < dim; ++d) {
+    const float t = src[i * dim + d] - y[d];
+    s = s + t * t;
+  }
+  return s;
+}
+
+__global__ __launch_bounds__(KNN_THREADS) void knn_eu_candidates_kernel(KnnEuParams p, int64_t cap,
+                                                                        int32_t* cand_idx, float* cand_sq,
+                                                                        int32_t* cand_n) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  constexpr int T = KNN_THREADS;
+  const int t = threadIdx.x;
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * T + t;
+  if (n >= p.n_out) return;                      // no block-wide synchronisation below
+  float* hv = reinterpret_cast<float*>(smem) + t;
+  int32_t* hi = reinterpret_cast<int32_t*>(smem + static_cast<size_t>(p.k) * T * sizeof(float)) + t;
+  float y[3] = {0.0f, 0.0f, 0.0f};
+  float yn = 0.0f;
+  for (int d = 0; d < p.dim; ++d) {
+    y[d] = p.dst[n * p.dim + d];
+    yn = yn + y[d] * y[d];
+  }
+  const float reach = p.src_norm_max + sqrtf(yn);
+  const float m2 = 2.0f * 0x1p-20f * reach * reach;
+  const int k = p.k;
+  int32_t* ci = cand_idx + n * cap;
+  float* cs = cand_sq + n * cap;
+  int64_t m = 0;
+  for (int j = 0; j < k; ++j) {
+    const float sq = eu_sq(p.src, j, y, p.dim);
+    hv[j * T] = sq;
+    hi[j * T] = j;
+    ci[m] = j;
+    cs[m] = sq;
+    ++m;
+  }
+  heap_make(hv, hi, k);
+  float top = hv[0];
+  for (int64_t i = k; i < p.n_in; ++i) {
+    const float sq = eu_sq(p.src, i, y, p.dim);
+    if (sq < top + (m2 + top * 0x1p-20f)) {
+      if (m < cap) {
+        ci[m] = static_cast<int32_t>(i);
+        cs[m] = sq;
+      }
+      ++m;
+    }
+    if (knn_less(sq, top)) {
+      heap_adjust(hv, hi, 0, k, sq, static_cast<int32_t>(i));
+      top = hv[0];
+    }
+  }
+  cand_n[n] = static_cast<int32_t>(m < INT32_MAX ? m : INT32_MAX);
+}
+
 static int reserve_lds(const void* kernel, size_t lds, const char* what) {
   if (lds > 64 * 1024 &&
       hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess) {
@@ -398,6 +476,34 @@ extern "C" int fovi_knn_logpolar_candidates(const fovi_knn_logpolar_args* a, voi
   hipLaunchKernelGGL(knn_lp_candidates_kernel, dim3(blocks), dim3(KNN_THREADS), lds,
                      static_cast<hipStream_t>(stream), p, a->cap, a->cand_idx, a->cand_sq, a->cand_n);
   return check_launch("fovi_knn_logpolar_candidates");
+}
+
+extern "C" int fovi_knn_euclid_candidates(const fovi_knn_euclid_args* a, void* stream) {
+  clear_error();
+  if (!a || !a->src || !a->dst || !a->cand_idx || !a->cand_sq || !a->cand_n) {
+    set_error("fovi_knn_euclid_candidates: null pointer");
+    return 1;
+  }
+  if (!knn_sizes_ok(a->k, a->n_in, a->n_out, "fovi_knn_euclid_candidates")) return 1;
+  if (a->dim < 1 || a->dim > 3 || !(a->src_norm_max >= 0.0f) || !__builtin_isfinite(a->src_norm_max)) {
+    set_error("fovi_knn_euclid_candidates: need 1 <= dim <= 3 and a finite src_norm_max >= 0 (dim=%d)", a->dim);
+    return 1;
+  }
+  if (a->cap < a->k) {
+    set_error("fovi_knn_euclid_candidates: cap %lld < k %lld", (long long)a->cap, (long long)a->k);
+    return 1;
+  }
+  if (a->n_out == 0) return 0;
+  KnnEuParams p;
+  p.src = a->src; p.dst = a->dst; p.n_in = a->n_in; p.n_out = a->n_out; p.k = static_cast<int>(a->k);
+  p.dim = a->dim; p.src_norm_max = a->src_norm_max;
+  const size_t lds = static_cast<size_t>(p.k) * KNN_THREADS * (sizeof(float) + sizeof(int32_t));
+  if (reserve_lds(reinterpret_cast<const void*>(&knn_eu_candidates_kernel), lds, "fovi_knn_euclid_candidates"))
+    return 1;
+  const unsigned blocks = static_cast<unsigned>((a->n_out + KNN_THREADS - 1) / KNN_THREADS);
+  hipLaunchKernelGGL(knn_eu_candidates_kernel, dim3(blocks), dim3(KNN_THREADS), lds,
+                     static_cast<hipStream_t>(stream), p, a->cap, a->cand_idx, a->cand_sq, a->cand_n);
+  return check_launch("fovi_knn_euclid_candidates");
 }
 
 extern "C" int fovi_knn_select(const fovi_knn_select_args* a, void* stream) {

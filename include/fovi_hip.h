@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 26
+#define FOVI_ABI_VERSION 27
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -465,7 +465,8 @@ int fovi_knnconv_bwd_x(const fovi_knnconv_bwd_x_args* args, void* stream);
  *     IEEE distance sqrt(sq) is below (1 + 2^-20) times the running k-th
  *     smallest, in index order, and their number to cand_n[n] (entries past
  *     cap are counted, not written: cand_n[n] > cap means the row overflowed).
- *   (host) cand_d = sqrt(cand_sq) with the host builder's own square root.
+ *   (host) cand_d = sqrt(cand_sq) with the host builder's own square root for
+ *     the candidates that can decide the selection, any square root for the rest.
  *   fovi_knn_select: per output point, the k smallest of its candidates in
  *     the order torch's CPU topk(largest=False) returns them for k * 64 <= n_in
  *     (a size-k max-heap over the candidates in index order that admits
@@ -486,6 +487,40 @@ typedef struct fovi_knn_logpolar_args {
 } fovi_knn_logpolar_args;
 
 int fovi_knn_logpolar_candidates(const fovi_knn_logpolar_args* args, void* stream);
+
+/*
+ * Candidate pass of the Euclidean kNN search (fovi/arch/knn.py:119-152, the
+ * torch.cdist + topk branch: isotropic cortical points, visual-field points),
+ * for the host builder's results bit for bit together with a host step and
+ * fovi_knn_select:
+ *   fovi_knn_euclid_candidates: per output point n, the scan over the inputs
+ *     in index order of the direct squared distance sum_d (src_i,d - dst_n,d)^2
+ *     in fp32 (src: [n_in, dim], dst: [n_out, dim]), writing cand_idx[n * cap + j]
+ *     for the first k inputs and every later input whose squared distance is
+ *     below the running k-th smallest plus 2^-19 (src_norm_max + |dst_n|)^2 plus
+ *     2^-20 of that running value (a bound on the difference from the
+ *     matrix-product form torch's cdist rounds in; src_norm_max >= every |src_i|),
+ *     with that squared distance in cand_sq[n * cap + j], in index order, and
+ *     their number to cand_n[n] (entries past cap are counted, not written).
+ *   (host) the distances of the candidates that can decide the selection (the
+ *     k smallest within the margin, and any two within the margin of each
+ *     other) with the host's own cdist; the square root of cand_sq for the rest.
+ *   fovi_knn_select: the heap selection over them (below).
+ * Needs 1 <= k <= 256, k * 64 <= n_in < 2^31, 1 <= dim <= 3 and cap >= k.
+ */
+typedef struct fovi_knn_euclid_args {
+  const float* src;           /* [n_in, dim] */
+  const float* dst;           /* [n_out, dim] */
+  int64_t n_in, n_out, k;
+  int32_t dim;
+  float src_norm_max;
+  int64_t cap;                /* candidates per output row */
+  int32_t* cand_idx;          /* [n_out, cap] */
+  float* cand_sq;             /* [n_out, cap] direct squared distances */
+  int32_t* cand_n;            /* [n_out] */
+} fovi_knn_euclid_args;
+
+int fovi_knn_euclid_candidates(const fovi_knn_euclid_args* args, void* stream);
 
 typedef struct fovi_knn_select_args {
   int64_t n_out, k, cap;

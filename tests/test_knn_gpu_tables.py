@@ -178,3 +178,158 @@ def test_device_slots_isotropic_equal_host_build(name):
     assert hasattr(layer, "slots_recomputed")
     cpu = KNNConvLayer(1, 1, k, ci, co, device="cpu")
     assert torch.equal(layer.slots, cpu.slots)
+
+
+# ------------------------------------------- Euclidean search (fovi_knn_euclid_candidates) ---
+def _iso_points(res):
+    c = SamplingCoords(16, 2.78, res, style="isotropic")
+    return torch.cat([c.cortical, c.cortical_pad_coords], 0), c.cortical
+
+
+def _eu_candidates(src, dst, k):
+    """The candidate scan restated on the CPU (fp32 steps as the kernel takes them)."""
+    import heapq
+    s32, d32 = src.numpy().astype(np.float32), dst.numpy().astype(np.float32)
+    norm_max = np.float32(float(torch.linalg.vector_norm(src.double(), dim=1).max()) * (1 + 2 ** -20))
+    out = []
+    for n in range(d32.shape[0]):
+        y = d32[n]
+        yn = np.float32(0)
+        for t in y:
+            yn = np.float32(yn + np.float32(t * t))
+        reach = np.float32(norm_max + np.float32(np.sqrt(yn)))
+        m2 = np.float32(np.float32(2.0 * 2 ** -20) * reach * reach)
+        diff = s32 - y
+        sq = np.zeros(s32.shape[0], dtype=np.float32)
+        for d in range(s32.shape[1]):
+            sq = (sq + diff[:, d] * diff[:, d]).astype(np.float32)
+        heap = [-float(v) for v in sq[:k]]
+        heapq.heapify(heap)
+        cand = list(range(k))
+        for i in range(k, sq.shape[0]):
+            top = np.float32(-heap[0])
+            if sq[i] < np.float32(top + np.float32(m2 + np.float32(top * np.float32(2 ** -20)))):
+                cand.append(i)
+            if sq[i] < top:
+                heapq.heapreplace(heap, -float(sq[i]))
+        reach2 = (float(norm_max) + float(np.sqrt(np.float64(y) @ np.float64(y)))) ** 2
+        out.append((cand, sq[cand], 4.0 * 2 ** -20 * reach2 * (1 + 2 ** -10)))
+    return out
+
+
+def test_candidate_distances_equal_the_chunk_cdist():
+    """Distances of candidate pairs from the grouped host cdist equal the whole chunk's call,
+    for chunks above and below the group size (a chunk of one output included)."""
+    src, dst = _iso_points(24)
+    g = torch.Generator().manual_seed(0)
+    n_out = dst.shape[0]
+    for step in (n_out, 200, 63, 1):
+        for s in range(0, n_out, step)[:6]:
+            e = min(s + step, n_out)
+            owner = torch.sort(torch.randint(s, e, (400,), generator=g))[0]
+            flat = torch.randint(0, src.shape[0], (400,), generator=g)
+            got = T._candidate_distances(src, dst, flat, owner, s, e)
+            want = torch.cdist(src, dst[s:e])[flat, owner - s]
+            assert torch.equal(got, want), (step, s, int((got != want).sum()))
+
+
+@pytest.mark.parametrize("case", ["iso", "ties"])
+def test_euclid_candidates_and_selection_equal_host_topk(case):
+    """The candidate scan (restated) keeps every input the host heap admits, and the selection
+    replayed over the candidates -- with the host's distances for those _deciding picks and the
+    scan's own square-rooted values for the rest -- gives the host's topk bit for bit."""
+    if case == "iso":
+        src, dst = _iso_points(16)
+        dst = dst[::3]
+        k = 9
+    else:
+        g = torch.Generator().manual_seed(3)
+        src = torch.randint(0, 5, (1300, 3), generator=g).float() / 4
+        dst = torch.randint(0, 5, (40, 3), generator=g).float() / 4
+        k = 20
+    hi, hd = T.knn_euclidean(src, dst, k)
+    full = torch.cdist(src, dst)
+    taken = total = 0
+    for n, (c, sq, gap) in enumerate(_eu_candidates(src, dst, k)):
+        c = torch.tensor(c)
+        sq = torch.from_numpy(sq).unsqueeze(0)
+        need = T._deciding(sq, torch.ones_like(sq, dtype=torch.bool), k, torch.tensor([gap]), 2 ** -18)[0]
+        taken, total = taken + int(need.sum()), total + c.numel()
+        # the host's distances where they can decide, the kernel's square-rooted elsewhere
+        d = torch.where(need, full[c, n], sq[0].sqrt())
+        order = _heap_topk(d.numpy(), k)
+        assert c[order].tolist() == hi[:, n].tolist(), n
+        assert torch.equal(d[order], hd[:, n])
+    assert taken < total
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("res_in,res_out,k,batch", [(16, 8, 9, None), (24, 12, 25, None), (16, 16, 9, None),
+                                                    (64, 32, 9, None), (64, 64, 25, None), (96, 48, 49, None),
+                                                    (64, 32, 9, 500), (64, 32, 9, 1001)])
+def test_device_euclid_search_equals_host(res_in, res_out, k, batch):
+    """Isotropic cortical points (3-D, pad ring included), the reference's default output
+    batching and batchings that leave a short last chunk."""
+    src, _ = _iso_points(res_in)
+    _, dst = _iso_points(res_out)
+    hi, hd = T.knn_euclidean(src, dst, k, batch)
+    gi, gd = T.knn_euclidean_device(src, dst, k, "cuda", batch)
+    assert torch.equal(gi, hi), f"indices differ at {int((gi != hi).sum())} entries"
+    assert torch.equal(gd, hd)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", [0, 1])
+def test_device_euclid_search_tie_heavy(seed):
+    g = torch.Generator().manual_seed(seed)
+    src = torch.randint(0, 5, (3000, 3), generator=g).float() / 4
+    dst = torch.randint(0, 5, (500, 3), generator=g).float() / 4
+    hi, hd = T.knn_euclidean(src, dst, 40)
+    gi, gd = T.knn_euclidean_device(src, dst, 40, "cuda")
+    assert torch.equal(gd, hd)
+    assert torch.equal(gi, hi), f"indices differ at {int((gi != hi).sum())} entries"
+
+
+@pytest.mark.gpu
+def test_device_euclid_search_visual_field():
+    """2-D visual-field points (sample_cortex=False layers)."""
+    ci = SamplingCoords(16, 2.78, 64, style="isotropic")
+    co = SamplingCoords(16, 2.78, 32, style="isotropic")
+    src = torch.cat([ci.cartesian, ci.cartesian_pad_coords], 0)
+    hi, hd = T.knn_euclidean(src, co.cartesian, 9)
+    gi, gd = T.knn_euclidean_device(src, co.cartesian, 9, "cuda")
+    assert torch.equal(gi, hi) and torch.equal(gd, hd)
+
+
+@pytest.mark.gpu
+def test_isotropic_layer_built_on_the_gpu_equals_the_host_build():
+    from fovi_amd.arch.knn import KNNConvLayer
+    ci = SamplingCoords(16, 2.78, 64, style="isotropic")
+    co = SamplingCoords(16, 2.78, 32, style="isotropic")
+    gpu = KNNConvLayer(8, 16, 25, ci, co, device="cuda")
+    cpu = KNNConvLayer(8, 16, 25, ci, co, device="cpu")
+    assert torch.equal(gpu.knn_indices.cpu(), cpu.knn_indices)
+    assert torch.equal(gpu.knn_distances.cpu(), cpu.knn_distances)
+    assert torch.equal(gpu.slots, cpu.slots)
+    assert torch.equal(gpu.slot_ptr.cpu(), cpu.slot_ptr.cpu())
+
+
+def test_deciding_candidates():
+    """The k smallest and everything within the gap of them, and every pair within the gap of
+    each other (equal values included), are taken; isolated values above them are not."""
+    sq = torch.tensor([[5.0, 1.0, 9.0, 3.0, 3.0, 20.0, 30.0, 30.05, 50.0, 2.05, 0.0]])
+    mask = torch.ones_like(sq, dtype=torch.bool)
+    mask[0, -1] = False                                   # past the row's count
+    need = T._deciding(sq, mask, 2, torch.tensor([0.1]), 0.0)[0].tolist()
+    #        5.0    1.0   9.0    3.0   3.0   20.0   30.0  30.05  50.0  2.05   (unused)
+    assert need == [False, True, False, True, True, False, True, True, False, True, False]
+
+
+def test_deciding_candidates_exact_values():
+    """Host distance a function of the kernel's value: copies of one value need not be taken,
+    but every copy of a value close to a distinct other value is."""
+    sq = torch.tensor([[5.0, 1.0, 9.0, 3.0, 3.0, 20.0, 30.0, 30.0, 50.0, 2.05, 0.0, 30.000002, 9.0]])
+    mask = torch.ones_like(sq, dtype=torch.bool)
+    mask[0, 10] = False
+    need = T._deciding(sq, mask, 2, torch.tensor([0.0]), 2 ** -19, exact_values=True)[0].tolist()
+    assert need == [False, True, False, False, False, False, True, True, False, True, False, True, False]
