@@ -172,13 +172,17 @@ def sampler_algorithmic_bytes(sampler, img, fix, sizes, vmap, mode):
     return out_bytes + distinct * C * es, out_bytes, distinct
 
 
-def bench_c4_sampler(steps, warmup, dev, mode="nearest"):
+def bench_c4_sampler(steps, warmup, dev, mode="nearest", channels_last=False):
+    """C4 sampler; ``channels_last``: the same images in torch's channels-last memory format
+    (the layout image decoders produce), whose taps read all channels of a pixel at once."""
     import numpy as np
     import torch
     from fovi_amd.sensing.samplers import GridSampler
     B, Fx, RES, S = 128, 4, 128, 512
     # two image sets (2 x 201 MB) rotated so the 256 MB MALL cannot hold the input
     imgs = [cpu_rand((B, 3, S, S), i, torch.bfloat16, dev) for i in range(2)]
+    if channels_last:
+        imgs = [x.contiguous(memory_format=torch.channels_last) for x in imgs]
     gf = torch.Generator().manual_seed(2)
     fix = 0.25 + 0.5 * torch.rand(B * Fx, 2, generator=gf)
     sizes = np.array([[S, S]] * (B * Fx))
@@ -197,7 +201,7 @@ def bench_c4_sampler(steps, warmup, dev, mode="nearest"):
         ms = time_steps(step, steps, warmup)
         nbytes, out_bytes, distinct = sampler_algorithmic_bytes(sampler, imgs[0], fix_d, sizes, vmap, mode)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    log(f"[c4 sampler {mode}] {ms:.3f} ms/step  {gbs:.0f} GB/s algorithmic "
+    log(f"[c4 sampler {mode}{' channels-last' if channels_last else ''}] {ms:.3f} ms/step  {gbs:.0f} GB/s algorithmic "
         f"({100 * gbs / PEAK_HBM_GBS:.1f}% of HBM peak); bytes {nbytes / 1e6:.1f} MB "
         f"(out {out_bytes / 1e6:.1f} MB, {distinct} distinct taps)")
     return dict(ms=ms, bytes=nbytes, gbs=gbs, images_per_s=B / (ms * 1e-3))
@@ -436,6 +440,8 @@ def main():
     bwd = bench_c3_backward(c3, args.steps, args.warmup) if "bwd" in legs else None
     c4 = None if args.no_sampler else bench_c4_sampler(args.steps, args.warmup, dev, "nearest")
     c4b = None if args.no_sampler else bench_c4_sampler(args.steps, args.warmup, dev, "bilinear")
+    c4cl = None if args.no_sampler else bench_c4_sampler(args.steps, args.warmup, dev, "nearest", True)
+    c4bcl = None if args.no_sampler else bench_c4_sampler(args.steps, args.warmup, dev, "bilinear", True)
     pool = bench_pool(args.steps, args.warmup, dev) if "pool" in legs else None
     c2 = None if args.no_e2e or "c2" not in legs else bench_c2(args.steps, args.warmup, dev)
     c4e = None if args.no_e2e or "c4" not in legs else bench_c4_frontend(args.steps, args.warmup, dev)
@@ -489,6 +495,11 @@ def main():
                         "ms": round(c4["ms"], 4), "images/s": round(c4["images_per_s"], 1)},
             "bilinear": {"GB/s": round(c4b["gbs"], 1), "frac": round(c4b["gbs"] / PEAK_HBM_GBS, 4),
                          "ms": round(c4b["ms"], 4), "images/s": round(c4b["images_per_s"], 1)},
+            "channels_last_images": {
+                "nearest": {"GB/s": round(c4cl["gbs"], 1), "frac": round(c4cl["gbs"] / PEAK_HBM_GBS, 4),
+                            "ms": round(c4cl["ms"], 4)},
+                "bilinear": {"GB/s": round(c4bcl["gbs"], 1), "frac": round(c4bcl["gbs"] / PEAK_HBM_GBS, 4),
+                             "ms": round(c4bcl["ms"], 4)}},
             "roofline": {"bound": "hbm", "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "traffic": {"nearest": measured_traffic("sampler_rings_kernel<bf16,nearest>"),
                                      "bilinear": measured_traffic("sampler_rings_kernel<bf16,bilinear>")}},

@@ -18,6 +18,8 @@
 //    parts, blended as the chain fma(se, fma(sw, fma(ne, nw*v_nw)));
 //    out-of-image taps contribute zero. This matches that kernel bit for bit
 //    (checked on 20000 random points at a non-power-of-two size).
+#include <type_traits>
+
 #include "common.h"
 
 namespace fovi {
@@ -75,7 +77,7 @@ struct Taps {
   bool inb, y0, y1, pair;
   bool b_nw, b_ne, b_sw, b_se;
   Off off, o_nw, o_ne, o_sw, o_se;
-  Off cx;
+  Off cx, px;
   float w_nw, w_ne, w_sw, w_se;
 
   __device__ __forceinline__ Taps(const SamplerParams& p, int64_t v, int64_t pt) {
@@ -121,6 +123,7 @@ struct Taps {
       const Off ox = static_cast<Off>(fminf(fmaxf(rx, 0.0f), W - 1.0f));
       const Off oy = static_cast<Off>(fminf(fmaxf(ry, 0.0f), H - 1.0f));
       off = inb ? oy * static_cast<Off>(p.is2) + ox * static_cast<Off>(p.is3) : 0;
+      px = ox;
       return;
     }
     const float fx = floorf(ix);
@@ -164,6 +167,75 @@ struct Taps {
       v_se = b_se ? Elem<InT>::load(s + o_se) : 0.0f;
     }
     return __builtin_fmaf(v_se, w_se, __builtin_fmaf(v_sw, w_sw, __builtin_fmaf(v_ne, w_ne, v_nw * w_nw)));
+  }
+
+  // Channels-last bf16 images (channel stride 1, pixel stride NCH = 3 or 4, image base
+  // 4-byte aligned): the NCH channels of the tap at element offset e with one 8-byte load
+  // of the 4-byte-aligned words at or below it. Those 8 bytes hold the pixel whatever the
+  // alignment (NCH <= 4 - (e & 1)) and stay inside the row unless the pixel is the row's
+  // last and starts at an even element (then NCH = 3 reads two bytes of the next pixel):
+  // there the channels are loaded one by one. One load instead of NCH cuts the distinct
+  // cache lines a wave's gather touches by NCH.
+  template <int NCH>
+  __device__ __forceinline__ static void pixel_cl(const uint16_t* s, Off e, Off x, Off W, float (&v)[4]) {
+    if (NCH == 4 || (e & 1) || x + 1 < W) {
+      typedef uint32_t u32x2a4 __attribute__((ext_vector_type(2), aligned(4)));
+      const u32x2a4 w = *reinterpret_cast<const u32x2a4*>(s + (e & ~Off(1)));
+      const uint32_t h[4] = {w[0] << 16, w[0] & 0xffff0000u, w[1] << 16, w[1] & 0xffff0000u};
+      const int o = static_cast<int>(e & 1);
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) v[c] = __uint_as_float(h[o + c]);
+    } else {
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) v[c] = bf16_bits_to_f32(s[e + c]);
+    }
+  }
+
+  // The two horizontally adjacent pixels at e and e + NCH of a channels-last bf16 image with
+  // one 16-byte load of the 4-byte-aligned words at or below e; the caller checks that the
+  // load stays in the row (NCH = 4, or a third pixel follows).
+  template <int NCH>
+  __device__ __forceinline__ static void pair_cl(const uint16_t* s, Off e, float (&a)[4], float (&b)[4]) {
+    typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+    const u32x4a4 w = *reinterpret_cast<const u32x4a4*>(s + (e & ~Off(1)));
+    const uint32_t h[8] = {w[0] << 16, w[0] & 0xffff0000u, w[1] << 16, w[1] & 0xffff0000u,
+                           w[2] << 16, w[2] & 0xffff0000u, w[3] << 16, w[3] & 0xffff0000u};
+    const int o = static_cast<int>(e & 1);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      a[c] = __uint_as_float(h[o + c]);
+      b[c] = __uint_as_float(h[o + NCH + c]);
+    }
+  }
+
+  // Every channel of the sample from a channels-last bf16 image (see pixel_cl), blended in
+  // the order value() blends one channel plane: the same results bit for bit.
+  template <int NCH>
+  __device__ __forceinline__ void values_cl(const uint16_t* s, Off W, float (&out)[4]) const {
+    if (MODE == FOVI_NEAREST) {
+      if (inb) pixel_cl<NCH>(s, off, px, W, out);
+      else
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) out[c] = 0.0f;
+      return;
+    }
+    float nw[4] = {}, ne[4] = {}, sw[4] = {}, se[4] = {};
+    const bool row2 = NCH == 4 || cx + 2 < W;   // a row's two taps with one load
+    if (b_nw && b_ne && row2) {
+      pair_cl<NCH>(s, o_nw, nw, ne);
+    } else {
+      if (b_nw) pixel_cl<NCH>(s, o_nw, cx, W, nw);
+      if (b_ne) pixel_cl<NCH>(s, o_ne, cx + 1, W, ne);
+    }
+    if (b_sw && b_se && row2) {
+      pair_cl<NCH>(s, o_sw, sw, se);
+    } else {
+      if (b_sw) pixel_cl<NCH>(s, o_sw, cx, W, sw);
+      if (b_se) pixel_cl<NCH>(s, o_se, cx + 1, W, se);
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+      out[c] = __builtin_fmaf(se[c], w_se, __builtin_fmaf(sw[c], w_sw, __builtin_fmaf(ne[c], w_ne, nw[c] * w_nw)));
   }
 };
 
@@ -225,7 +297,9 @@ template <> struct Vec16Store<uint16_t> {
 // of the view is sampled exactly once whatever the geometry, so results do
 // not depend on it. Block indices and in-image / in-view offsets are 32-bit
 // (the host checks the extents).
-template <typename InT, typename OutT, int MODE, int PAD, bool PAIRS, int NC>
+// CL = 3 or 4: channels-last bf16 image with NC = CL channels, each tap's channels read with
+// one load (Taps::values_cl); 0: channel planes, one load per channel.
+template <typename InT, typename OutT, int MODE, int PAD, bool PAIRS, int NC, int CL = 0>
 __global__ __launch_bounds__(256) void sampler_rings_kernel(SamplerParams p, uint32_t blocks_per_view,
                                                             uint32_t total_blocks, uint32_t padded_blocks,
                                                             int vec_out) {
@@ -248,9 +322,15 @@ __global__ __launch_bounds__(256) void sampler_rings_kernel(SamplerParams p, uin
   float val[4];
   if (img >= 0 && img < p.n_img) {
     const InT* src = static_cast<const InT*>(p.img) + img * p.is0;
-    const int32_t is1 = static_cast<int32_t>(p.is1);
+    if constexpr (CL > 0) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) val[c] = c < C ? t.value(src + c * is1) : 0.0f;
+      for (int c = 0; c < 4; ++c) val[c] = 0.0f;
+      t.template values_cl<CL>(src, static_cast<int32_t>(p.W), val);
+    } else {
+      const int32_t is1 = static_cast<int32_t>(p.is1);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) val[c] = c < C ? t.value(src + c * is1) : 0.0f;
+    }
   } else {
 #pragma unroll
     for (int c = 0; c < 4; ++c) val[c] = 0.0f;
@@ -300,6 +380,19 @@ static void launch_rings(const SamplerParams& p, uint32_t bpv, uint32_t total, u
   constexpr int64_t VPL = 16 / sizeof(OutT);
   const int vec_out = p.os2 == 1 && p.os1 % VPL == 0 && p.os0 % VPL == 0 &&
                       reinterpret_cast<uintptr_t>(p.out) % 16 == 0;
+  if constexpr (std::is_same<InT, uint16_t>::value) {
+    // channels-last bf16 pixels of 3 or 4 channels, 4-byte aligned image starts
+    if (p.is1 == 1 && p.is3 == p.C && (p.C == 3 || p.C == 4) && p.is0 % 2 == 0 &&
+        reinterpret_cast<uintptr_t>(p.img) % 4 == 0) {
+      if (p.C == 3)
+        hipLaunchKernelGGL((sampler_rings_kernel<InT, OutT, MODE, PAD, false, 3, 3>), grid, dim3(256), 0, s, p, bpv,
+                           total, padded, vec_out);
+      else
+        hipLaunchKernelGGL((sampler_rings_kernel<InT, OutT, MODE, PAD, false, 4, 4>), grid, dim3(256), 0, s, p, bpv,
+                           total, padded, vec_out);
+      return;
+    }
+  }
   if (p.C == 3)
     hipLaunchKernelGGL((sampler_rings_kernel<InT, OutT, MODE, PAD, PAIRS, 3>), grid, dim3(256), 0, s, p, bpv, total,
                        padded, vec_out);

@@ -175,6 +175,27 @@ def test_ring_blocked_order_equals_point_order(mode, pad, dt, channels):
     assert_close_rel(blocked[2:3].float().cpu(), ref, 1e-5 if dt == torch.float32 else 1e-2)
 
 
+@pytest.mark.parametrize("mode", ["bilinear", "nearest"])
+@pytest.mark.parametrize("pad", ["zeros", "border"])
+@pytest.mark.parametrize("channels,width", [(3, 173), (3, 174), (4, 173)])
+def test_channels_last_images_equal_channel_planes(mode, pad, channels, width):
+    """bf16 images in the channels-last memory format (one load per tap for all channels)
+    give the channel-plane results bit for bit: odd and even widths, so taps start at odd and
+    even elements, and corner fixations with border padding, so taps hit each row's last
+    pixel (loaded channel by channel)."""
+    g = torch.Generator().manual_seed(12)
+    planar = torch.rand(3, channels, 150, width, generator=g).to(torch.bfloat16).cuda()
+    cl = planar.contiguous(memory_format=torch.channels_last)
+    assert cl.stride()[1] == 1 and cl.stride()[3] == channels
+    fix = torch.tensor([[0.5, 0.5], [0.05, 0.95], [0.9, 0.1], [0.3, 0.7], [0.6, 0.4], [0.99, 0.99]])
+    sizes = np.array([[150, width]] * 6)
+    vmap = torch.tensor([0, 0, 1, 1, 2, 2])
+    s = GridSampler(16, 2.78, 64, device="cuda", mode=mode, style="logpolar", padding_mode=pad)
+    want = s.sample_views(planar, fix, sizes, view_image=vmap)
+    got = s.sample_views(cl, fix, sizes, view_image=vmap)
+    assert torch.equal(got, want)
+
+
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "tables.npz")
 
 
