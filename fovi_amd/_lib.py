@@ -14,7 +14,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
 
-ABI_VERSION = 27
+ABI_VERSION = 28
 F32, BF16, F8E4M3 = 0, 1, 2
 NEAREST, BILINEAR = 0, 1
 PAD_ZEROS, PAD_BORDER = 0, 1
@@ -77,6 +77,7 @@ class KnnConvArgs(C.Structure):
         ("fc_lo", C.c_void_p), ("fc_span", C.c_void_p), ("fc_item", C.c_void_p), ("fc_xlist", C.c_void_p),
         ("fc_xoff", C.c_void_p), ("fc_tile_points", C.c_int32), ("fc_zero_row", C.c_int32),
         ("fc_xmax", C.c_int32), ("wide_units", C.c_int32),
+        ("fc_comb", C.c_void_p), ("fc_comb_off", C.c_void_p), ("fc_pmax", C.c_int32), ("reserved4", C.c_int32),
     ]
 
 

@@ -271,10 +271,10 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
                     break
                 fc = None
         for name, field in (("fc_lo", "lo"), ("fc_span", "span"), ("fc_item", "item"), ("fc_xlist", "xlist"),
-                            ("fc_xoff", "xoff")):
+                            ("fc_xoff", "xoff"), ("fc_comb", "comb"), ("fc_comb_off", "comb_off")):
             self.register_buffer(name, None if fc is None else getattr(fc, field).to(device), persistent=False)
         if fc is not None:
-            self._fc = (fc.tile, fc.zero_row, fc.xmax)
+            self._fc = (fc.tile, fc.zero_row, fc.xmax, fc.pmax)
         # few-channel layers: the fused kernel when its tables fit (False: the slot sums through
         # a workspace and a dense GEMM, or the single-pass kernel)
         self.few_channel_fused = True
@@ -541,7 +541,8 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
             a.fc_lo = self.fc_lo.data_ptr(); a.fc_span = self.fc_span.data_ptr()
             a.fc_item = self.fc_item.data_ptr(); a.fc_xlist = self.fc_xlist.data_ptr()
             a.fc_xoff = self.fc_xoff.data_ptr()
-            a.fc_tile_points, a.fc_zero_row, a.fc_xmax = self._fc
+            a.fc_comb = self.fc_comb.data_ptr(); a.fc_comb_off = self.fc_comb_off.data_ptr()
+            a.fc_tile_points, a.fc_zero_row, a.fc_xmax, a.fc_pmax = self._fc
         ws = None
         if cp is not None and self.two_pass_few_channels and workspace and not fused:
             # slot-sum rows for the two-pass few-channel path (caller-owned scratch)

@@ -737,10 +737,18 @@ class FewChannelTables(NamedTuple):
     tile: int
     zero_row: int
     xmax: int
+    comb: torch.Tensor       # [total] int32 (uint32 words): per (tile, chunk) combine entries
+    comb_off: torch.Tensor   # [T * n_chunks + 1] int32 block starts
+    pmax: int                # most partial sums of one chunk
 
 
 FC_CHUNK = 64      # reduction columns per chunk of the fused few-channel kernel
 FC_THREADS = 512   # threads of its workgroup
+# Slot sums of few-channel layers run over the neighbour list in groups of this many: each
+# group's fp32 sum in list order from +0, the groups' sums added in order (for up to this many
+# neighbours, the plain list order). The fused kernel sums the groups of one slot on different
+# lanes; the two-pass slot-sum kernel uses the same order.
+FC_GROUP = 8
 
 
 def few_channel_tables(knn_idx, slots, n_in, n_ref, cp, k_pad, tile):
@@ -748,20 +756,26 @@ def few_channel_tables(knn_idx, slots, n_in, n_ref, cp, k_pad, tile):
 
     Output points are cut into tiles of ``tile`` (128 or 256) consecutive points; a tile
     stages input rows ``[lo, lo + span)`` and a zero row ``zero_row`` (the largest span).
-    The reduction runs in chunks of 64 columns, ``64 // cp`` slots each. Every (row, slot)
-    of a chunk is one item, two uint32 words: ``first << 16 | count`` (``first`` = the S
-    row of the slot's first neighbour, ``zero_row`` when empty) and ``dest << 16 | xoff``
-    (``dest = row * spc + slot within the chunk``; the further ``count - 1`` neighbours, in
-    the CSR list order of ``csr_tables``, sit at ``xoff`` in the chunk's extras block).
-    Items are sorted by count (largest first) and dealt in a snake over the 512 threads (item
-    ``j * 512 + thread``; a wave holds items of similar counts). Returns
-    ``None`` when a span, a count or an extras block does not fit 16 bits.
+    The reduction runs in chunks of 64 columns, ``64 // cp`` slots each; the kernel clears a
+    chunk's A tile and writes only its non-empty (row, slot) sums. Each is built from items of
+    two uint32 words, ``first << 16 | partial << 15 | count`` and ``dest << 16 | xoff``: the
+    sum in list order of ``count`` (1 .. ``FC_GROUP``) neighbours, the S row of the first and
+    the further ``count - 1`` at ``xoff`` in the chunk's extras block (CSR list order of
+    ``csr_tables``). A slot of at most ``FC_GROUP`` neighbours is one item written to A at
+    ``dest = row * spc + slot``; a longer one is one item per group of ``FC_GROUP`` (partial
+    flag set) writing an fp32 partial sum to ``dest`` in the chunk's partial buffer, and a
+    combine entry ``dest | m << 12 | p0 << 20`` adds its ``m`` partials ``p0 ..`` in order
+    and writes A. Items are sorted by count (largest first) and dealt in a snake over the 512
+    threads (item ``j * 512 + thread``; a wave holds items of similar counts), the rest of the
+    ``tile * spc`` item slots being empty (count 0). Returns ``None`` when a span or an extras
+    block does not fit 16 bits, or a chunk has more items than slots, more than 512 combine
+    entries or more than 4095 partials.
     """
     k, n_out = knn_idx.shape
     spc = FC_CHUNK // cp
     n_chunks = k_pad // FC_CHUNK
     per_chunk = tile * spc
-    if k_pad % FC_CHUNK or per_chunk % FC_THREADS or n_chunks * spc < n_ref:
+    if k_pad % FC_CHUNK or per_chunk % FC_THREADS or n_chunks * spc < n_ref or per_chunk > 4096:
         return None
     ptr, nbr = csr_tables(knn_idx, slots, n_in, n_ref)
     ptr = ptr.numpy().astype(np.int64)
@@ -788,55 +802,93 @@ def few_channel_tables(knn_idx, slots, n_in, n_ref, cp, k_pad, tile):
     nbr_pad[:n_out] = nbr
     rows_lo = np.repeat(lo, tile)[:, None]
     nbr_rel = np.where(nbr_pad >= 0, nbr_pad - rows_lo, 0)
-    first = np.take_along_axis(nbr_rel, np.minimum(beg, k - 1), axis=1)
-    first = np.where(cnt > 0, first, zero_row)
     # item slot of each count rank: round j = rank // 512 fills slots j * 512 + thread, odd rounds
     # backwards (a snake). A wave runs as long as its slowest lane: consecutive ranks share a
     # wave, and a wave that takes the heaviest items of one round takes light ones in the next
     rank = np.arange(per_chunk)
     rnd, pos = rank // FC_THREADS, rank % FC_THREADS
     slot_of_rank = rnd * FC_THREADS + np.where(rnd % 2 == 0, pos, FC_THREADS - 1 - pos)
+    G = FC_GROUP
     item = np.zeros((n_tiles, n_chunks, per_chunk, 2), np.int64)
     blocks, xoff, off = [], [0], 0
-    xmax = 0
+    cblocks, coff = [], [0]
+    xmax = pmax = 0
     for t in range(n_tiles):
         rows = slice(t * tile, (t + 1) * tile)
+        nrel = nbr_rel[rows]
         for c in range(n_chunks):
             cols = slice(c * spc, (c + 1) * spc)
             cc = cnt[rows, cols].reshape(-1)            # dest = row * spc + slot
-            ff = first[rows, cols].reshape(-1)
             bb = beg[rows, cols].reshape(-1)
-            order = np.argsort(-cc, kind="stable")      # dests by decreasing count
-            extra_n = np.maximum(cc[order] - 1, 0)
+            dests = np.nonzero(cc)[0]
+            # items: (count, first, dest, partial, list start); groups of G for long lists
+            i_cnt, i_first, i_dest, i_part, i_beg = [], [], [], [], []
+            comb = []
+            n_part = 0
+            for d in dests:
+                n, b0 = int(cc[d]), int(bb[d])
+                r = d // spc
+                if n <= G:
+                    i_cnt.append(n); i_first.append(nrel[r, b0]); i_dest.append(d); i_part.append(0)
+                    i_beg.append((r, b0))
+                    continue
+                m = -(-n // G)
+                if m > 0xFF:
+                    return None
+                comb.append(int(d) | (m << 12) | (n_part << 20))
+                for g in range(m):
+                    gn = min(G, n - g * G)
+                    i_cnt.append(gn); i_first.append(nrel[r, b0 + g * G]); i_dest.append(n_part + g)
+                    i_part.append(1); i_beg.append((r, b0 + g * G))
+                n_part += m
+            n_items = len(i_cnt)
+            if n_items > per_chunk or len(comb) > FC_THREADS or n_part > 0xFFF:
+                return None
+            i_cnt = np.asarray(i_cnt, np.int64)
+            order = np.argsort(-i_cnt, kind="stable")
+            extra_n = np.maximum(i_cnt[order] - 1, 0)
             starts = np.cumsum(extra_n) - extra_n
             total = int(extra_n.sum())
-            if total > 0xFFFF or cc.max(initial=0) > 0xFFFF:
+            if total > 0xFFFF:
                 return None
             xl = np.zeros(-(-total // 8) * 8, np.int64)
-            nrel = nbr_rel[rows]
-            for d, st, ne in zip(order[extra_n > 0], starts[extra_n > 0], extra_n[extra_n > 0]):
-                r = d // spc
-                xl[st:st + ne] = nrel[r, bb[d] + 1:bb[d] + 1 + ne]
-            item[t, c, slot_of_rank, 0] = (ff[order] << 16) | cc[order]
-            item[t, c, slot_of_rank, 1] = (order << 16) | starts
+            for q, st, ne in zip(order, starts, extra_n):
+                if ne:
+                    r, b0 = i_beg[q]
+                    xl[st:st + ne] = nrel[r, b0 + 1:b0 + 1 + ne]
+            sl = slot_of_rank[:n_items]
+            first = np.asarray(i_first, np.int64)[order]
+            dest = np.asarray(i_dest, np.int64)[order]
+            part = np.asarray(i_part, np.int64)[order]
+            item[t, c, sl, 0] = (first << 16) | (part << 15) | i_cnt[order]
+            item[t, c, sl, 1] = (dest << 16) | starts
             blocks.append(xl)
             off += len(xl)
             xoff.append(off)
             xmax = max(xmax, len(xl))
+            cblocks.append(np.asarray(comb, np.int64))
+            coff.append(coff[-1] + len(comb))
+            pmax = max(pmax, n_part)
     xlist = np.concatenate(blocks) if blocks else np.zeros(0, np.int64)
     if len(xlist) == 0:
         xlist = np.zeros(8, np.int64)
+    comb_all = np.concatenate(cblocks) if cblocks else np.zeros(0, np.int64)
+    if len(comb_all) == 0:
+        comb_all = np.zeros(1, np.int64)
     return FewChannelTables(
         torch.from_numpy(lo.astype(np.int32)), torch.from_numpy(span.astype(np.int32)),
         torch.from_numpy(item.astype(np.uint32).view(np.int32)),
         torch.from_numpy(xlist.astype(np.uint16).view(np.int16)),
-        torch.from_numpy(np.asarray(xoff, np.int32)), tile, zero_row, xmax)
+        torch.from_numpy(np.asarray(xoff, np.int32)), tile, zero_row, xmax,
+        torch.from_numpy(comb_all.astype(np.uint32).view(np.int32)), torch.from_numpy(np.asarray(coff, np.int32)),
+        pmax)
 
 
 def few_channel_lds_bytes(tables, c_out, cp):
     """LDS bytes the fused few-channel kernel needs for these tables and ``c_out`` (its
     layout: staged rows and the zero row, two A chunks, the weight chunk of ``c_out`` rounded
-    up to 64 columns, the extras block, at least the epilogue's transposition buffers; more
+    up to 64 columns, the extras block, the partial sums, at least the epilogue's
+    transposition buffers; more
     than 160 KB when no wave tiling of the kernel covers ``c_out`` at this tile size)."""
     ntp = -(-c_out // 64) * 64
     # the kernel's wave tilings: 2 x 4 or 4 x 2 waves of rb x cb blocks of 32 x 32, cb <= 4,
@@ -846,7 +898,7 @@ def few_channel_lds_bytes(tables, c_out, cp):
     if not any(1 <= cb <= 4 and rb * cb <= 8 for rb, cb in tilings) or tables.xmax > 4 * 512 * 8:
         return 1 << 30
     s = ((tables.zero_row + 1) * cp * 2 + 15) & ~15
-    body = s + 2 * tables.tile * 128 + ntp * 128 + tables.xmax * 2
+    body = s + 2 * tables.tile * 128 + ntp * 128 + tables.xmax * 2 + tables.pmax * cp * 4
     return max(body, tables.tile * ntp * 2)
 
 

@@ -1009,8 +1009,9 @@ static void launch_bf16_smallc_nt(const KnnParams& p, int out_t, hipStream_t s) 
 // independent loads instead of a dependent chain per slot); neighbours after
 // the first, rare at one neighbour per slot on average, follow in list order.
 // The lane writes the point's slot-major reduction row A[b, n, v * CP + c] in
-// bf16 (fp32 sums in list order from +0, one RNE rounding), zero padded to
-// k_pad. Few registers, many waves in flight: the neighbour-list latency is
+// bf16 (fp32 sums, one RNE rounding; in list order from +0 over groups of
+// FC_GROUP neighbours, the groups' sums added in order, as the fused kernel
+// sums them), zero padded to k_pad. Few registers, many waves in flight: the neighbour-list latency is
 // hidden by occupancy, which the MFMA kernels (one 8-wave workgroup per CU)
 // cannot do. Pass 2 (dense_gemm_kernel): the MFMA tile core of the kernels
 // above with A rows read contiguously from the workspace.
@@ -1067,20 +1068,34 @@ __global__ __launch_bounds__(256) void slotsum_kernel(KnnParams p, uint16_t* A, 
       for (int c = 0; c < CP; ++c) acc[s][c] = 0.0f;
       add_row(acc[s], r[s]);
     }
-#pragma unroll
-    for (int s = 0; s < SL; ++s) {
-      const int cnt = e[s] & 0xffff;
-      const int32_t* nb = nbn + (e[s] >> 16);
-      for (int j0 = 1; j0 < cnt; j0 += 4) {
+    // neighbours [from, to) of a slot's list added to sum in list order, four reads in flight
+    auto add_range = [&](float* sum, const int32_t* nb, int from, int to) {
+      for (int j0 = from; j0 < to; j0 += 4) {
         int id4[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) id4[u] = j0 + u < cnt ? nb[j0 + u] : -1;
+        for (int u = 0; u < 4; ++u) id4[u] = j0 + u < to ? nb[j0 + u] : -1;
         RowT r4[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u)
           r4[u] = id4[u] >= 0 ? *reinterpret_cast<const RowT*>(xb + static_cast<int64_t>(id4[u]) * p.xs2) : zero;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) add_row(acc[s], r4[u]);
+        for (int u = 0; u < 4; ++u) add_row(sum, r4[u]);
+      }
+    };
+#pragma unroll
+    for (int s = 0; s < SL; ++s) {
+      const int cnt = e[s] & 0xffff;
+      const int32_t* nb = nbn + (e[s] >> 16);
+      // the first group of FC_GROUP (the first neighbour is in already), then each further
+      // group summed from +0 and added in order: the fused kernel's order
+      add_range(acc[s], nb, 1, cnt < FC_GROUP ? cnt : FC_GROUP);
+      for (int g0 = FC_GROUP; g0 < cnt; g0 += FC_GROUP) {
+        float part[CP];
+#pragma unroll
+        for (int c = 0; c < CP; ++c) part[c] = 0.0f;
+        add_range(part, nb, g0, cnt < g0 + FC_GROUP ? cnt : g0 + FC_GROUP);
+#pragma unroll
+        for (int c = 0; c < CP; ++c) acc[s][c] += part[c];
       }
     }
 #pragma unroll

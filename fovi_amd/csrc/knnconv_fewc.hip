@@ -11,21 +11,27 @@
 //    in LDS once (S, CP channels per row, channels >= c_in zeroed), plus a
 //    zero row.
 //  * The reduction runs in chunks of 64 columns (64 / CP slots). A chunk's A
-//    tile [TM x 64] is built in LDS from S by "items" (one per (point, slot)):
-//    the slot's neighbours summed in fp32 in list order from +0 and rounded
-//    once to bf16. Items come from a host table, sorted by neighbour count and
-//    dealt in a snake over the threads (lanes of a wave hold items of similar
-//    counts, heavy rounds alternate between waves); each is 8
-//    bytes (first neighbour's S row, count, destination, offset of the further
-//    neighbours in the chunk's extras list, which is staged in LDS). The slot
-//    sums therefore equal the two-pass path's (slotsum_kernel) bit for bit.
+//    tile [TM x 64] is cleared and its non-empty (point, slot) sums are built
+//    in LDS from S by "items": up to 8 neighbours summed in fp32 in list order
+//    from +0 and rounded once to bf16. A longer list (the fovea's slots hold
+//    up to ~120 neighbours) is one item per group of 8, each writing its fp32
+//    partial sum, and a combine entry adds the partials in order and rounds
+//    once: a long list no longer serialises its wave (and the barrier after
+//    the build) for its whole length. Items come from a host table, sorted by
+//    neighbour count and dealt in a snake over the threads (lanes of a wave
+//    hold items of similar counts); each is 8 bytes (first neighbour's S row,
+//    count, destination, offset of the further neighbours in the chunk's
+//    extras list, which is staged in LDS). The slot sums equal the two-pass
+//    path's (slotsum_kernel, same grouped order) bit for bit.
 //  * The weight chunk [NTP x 64] is staged in LDS once per workgroup and read
 //    by all waves; A and weight rows are 128 bytes, 16-byte parts XOR-swizzled
 //    by bits 1-3 of the row (conflict-free fragment reads).
 //  * Per chunk: the MFMAs of chunk c (32x32x16 bf16, ascending K, as the
 //    two-pass GEMM) and the build of chunk c + 1's A tile into the other A
-//    buffer, then the weight and extras of the next chunks (loaded into
-//    registers one chunk ahead) are stored; two barriers per chunk.
+//    buffer; after a barrier, chunk c + 1's long lists are combined, chunk c's
+//    buffer is cleared for chunk c + 2, and the weight and extras of the next
+//    chunks (loaded into registers one chunk ahead) are stored; two barriers
+//    per chunk.
 //  * Epilogue: bias and ReLU, each wave transposes its tile through LDS and
 //    stores 16-byte pieces of channels-last rows.
 #include "knnconv_internal.h"
@@ -41,22 +47,27 @@ struct FewcTables {
   const uint32_t* item;    // [n_tiles, n_chunks, TM * SPC] x 2 words
   const uint16_t* xlist;   // extras, per (tile, chunk) blocks
   const int32_t* xoff;     // [n_tiles * n_chunks + 1] block starts (uint16 units, multiples of 8)
+  const uint32_t* comb;    // combine entries, per (tile, chunk) blocks
+  const int32_t* comb_off; // [n_tiles * n_chunks + 1] block starts
   int zero_row;            // S row of zeros (>= every span)
   int xmax;                // largest extras block (uint16 units, multiple of 8)
+  int pmax;                // most partial sums of a chunk
   int n_chunks;
 };
 
 struct FewcLayout {
-  int s_off, a_off, w_off, x_off, total;
+  int s_off, a_off, w_off, x_off, p_off, total;
 };
 
-__host__ __device__ inline FewcLayout fewc_layout(int tm, int ntp, int cp, int zero_row, int xmax, int epi_bytes) {
+__host__ __device__ inline FewcLayout fewc_layout(int tm, int ntp, int cp, int zero_row, int xmax, int pmax,
+                                                  int epi_bytes) {
   FewcLayout l;
   int o = 0;
   l.s_off = o; o += ((zero_row + 1) * cp * 2 + 15) & ~15;
   l.a_off = o; o += 2 * tm * FC_ROWB;
   l.w_off = o; o += ntp * FC_ROWB;
-  l.x_off = o; o += xmax * 2;
+  l.x_off = o; o += (xmax * 2 + 15) & ~15;
+  l.p_off = o; o += pmax * cp * 4;
   l.total = o > epi_bytes ? o : epi_bytes;
   return l;
 }
@@ -120,7 +131,7 @@ __global__ __launch_bounds__(512, 1) void knnconv_fewc_kernel(KnnParams p, FewcT
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave % WM, wn = wave / WM;
   const int zr = ft.zero_row;
-  const FewcLayout L = fewc_layout(TM, NTP, CP, zr, ft.xmax, 0);
+  const FewcLayout L = fewc_layout(TM, NTP, CP, zr, ft.xmax, ft.pmax, 0);
   const int NC = ft.n_chunks;
 
   // Stage the tile's input rows (channels >= c_in zeroed) and the zero row.
@@ -201,23 +212,68 @@ __global__ __launch_bounds__(512, 1) void knnconv_fewc_kernel(KnnParams p, FewcT
   const uint16_t* X = reinterpret_cast<const uint16_t*>(smem + L.x_off);
   // Further neighbours in list order (a plain loop: the compiler pipelines its index and row
   // reads better than a hand-staged prefetch, measured).
+  // A-tile address of (row, slot) dest of a chunk in buffer A
+  auto a_addr = [&](uint8_t* A, int dest) {
+    const int r = dest / SPC, sl = dest - r * SPC;
+    const int byte = sl * CP * 2;
+    return reinterpret_cast<RowT*>(A + fc_off(r, byte >> 4) + (byte & 15));
+  };
+  float* P = reinterpret_cast<float*>(smem + L.p_off);
   auto build = [&](const uint2 (&it)[IT], int buf) {
     uint8_t* A = smem + L.a_off + buf * TM * FC_ROWB;
 #pragma unroll
     for (int j = 0; j < IT; ++j) {
       const uint32_t w0 = it[j].x, w1 = it[j].y;
-      const int extra = static_cast<int>(w0 & 0xffffu) - 1;
+      const int count = static_cast<int>(w0 & 0xfu);
+      if (count == 0) continue;            // no item in this slot: the A tile was cleared
       float a[CP];
 #pragma unroll
       for (int c = 0; c < CP; ++c) a[c] = 0.0f;
       R::acc(a, S[w0 >> 16]);
       const uint16_t* xl = X + (w1 & 0xffffu);
-      for (int q = 0; q < extra; ++q) R::acc(a, S[xl[q]]);
+      for (int q = 0; q < count - 1; ++q) R::acc(a, S[xl[q]]);
       const int dest = static_cast<int>(w1 >> 16);
-      const int r = dest / SPC, sl = dest - r * SPC;
-      const int byte = sl * CP * 2;
-      *reinterpret_cast<RowT*>(A + fc_off(r, byte >> 4) + (byte & 15)) = R::pack(a);
+      if (w0 & 0x8000u) {                  // one group of a long list: its fp32 partial sum
+#pragma unroll
+        for (int c = 0; c < CP; c += 4)
+          *reinterpret_cast<f32x4*>(P + dest * CP + c) = f32x4{a[c], a[c + 1], a[c + 2], a[c + 3]};
+      } else {
+        *a_addr(A, dest) = R::pack(a);
+      }
     }
+  };
+  // the long lists of a chunk: entry dest | m << 12 | p0 << 20 adds partials p0 .. p0 + m - 1
+  // in order (from the first, which an fp32 sum from +0 never leaves at -0) and writes A
+  auto combine = [&](uint32_t cw, int buf) {
+    if (cw == 0u) return;
+    uint8_t* A = smem + L.a_off + buf * TM * FC_ROWB;
+    const int dest = static_cast<int>(cw & 0xfffu), m = static_cast<int>((cw >> 12) & 0xffu);
+    const int p0 = static_cast<int>(cw >> 20);
+    float a[CP];
+#pragma unroll
+    for (int c = 0; c < CP; c += 4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(P + p0 * CP + c);
+      a[c] = v[0]; a[c + 1] = v[1]; a[c + 2] = v[2]; a[c + 3] = v[3];
+    }
+    for (int i = 1; i < m; ++i) {
+#pragma unroll
+      for (int c = 0; c < CP; c += 4) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(P + (p0 + i) * CP + c);
+        a[c] += v[0]; a[c + 1] += v[1]; a[c + 2] += v[2]; a[c + 3] += v[3];
+      }
+    }
+    *a_addr(A, dest) = R::pack(a);
+  };
+  auto load_comb = [&](int c) -> uint32_t {
+    const int64_t blk = static_cast<int64_t>(t) * NC + c;
+    const int beg = ft.comb_off[blk], n = ft.comb_off[blk + 1] - beg;
+    return tid < n ? ft.comb[beg + tid] : 0u;
+  };
+  // zero A buffer `buf` (TM rows of 128 bytes)
+  auto clear = [&](int buf) {
+    u32x4* A = reinterpret_cast<u32x4*>(smem + L.a_off + buf * TM * FC_ROWB);
+#pragma unroll
+    for (int j = 0; j < TM * FC_ROWB / 16 / 512; ++j) A[j * 512 + tid] = u32x4{0u, 0u, 0u, 0u};
   };
 
   uint2 it_a[IT], it_b[IT];
@@ -225,10 +281,13 @@ __global__ __launch_bounds__(512, 1) void knnconv_fewc_kernel(KnnParams p, FewcT
   int xn = 0;
   load_items(0, it_a);
   if (NC > 1) load_items(1, it_b);
+  uint32_t cw_a = load_comb(0), cw_b = NC > 1 ? load_comb(1) : 0u;
   load_w(0, wreg);
   load_x(0, xreg, xn);
   store_w(wreg);
   store_x(xreg, xn);
+  clear(0);
+  clear(1);
   if (NC > 1) {
     load_w(1, wreg);
     load_x(1, xreg, xn);
@@ -241,6 +300,9 @@ __global__ __launch_bounds__(512, 1) void knnconv_fewc_kernel(KnnParams p, FewcT
     if (NC > 2) load_items(2, it_b);
   }
   __syncthreads();
+  combine(cw_a, 0);
+  cw_a = cw_b;
+  cw_b = NC > 2 ? load_comb(2) : 0u;
   if (NC > 1) {
     store_x(xreg, xn);
     if (NC > 2) load_x(2, xreg, xn);
@@ -275,6 +337,12 @@ __global__ __launch_bounds__(512, 1) void knnconv_fewc_kernel(KnnParams p, FewcT
     }
     if (c + 1 < NC) build(it_a, (c + 1) & 1);
     __syncthreads();
+    // every wave is past chunk c's fragment reads and chunk c + 1's items: finish c + 1's long
+    // lists, clear c's buffer for chunk c + 2, stage the next weights and extras
+    if (c + 1 < NC) combine(cw_a, (c + 1) & 1);
+    if (c + 2 < NC) clear(c & 1);
+    cw_a = cw_b;
+    cw_b = c + 3 < NC ? load_comb(c + 3) : 0u;
     if (c + 1 < NC) store_w(wreg);
     if (c + 2 < NC) store_x(xreg, xn);
 #pragma unroll
@@ -340,7 +408,7 @@ struct FewcPlan {
   int tm, wm, rb, cb, xv, lds;
 };
 
-static bool fewc_plan(const KnnParams& p, int cp, int tm, int zero_row, int xmax, FewcPlan& pl) {
+static bool fewc_plan(const KnnParams& p, int cp, int tm, int zero_row, int xmax, int pmax, FewcPlan& pl) {
   if (tm != 128 && tm != 256) return false;
   // output columns padded to a multiple of 64 (zero weight columns, masked stores)
   const int ntp = static_cast<int>((p.Cout + 63) / 64 * 64);
@@ -354,7 +422,7 @@ static bool fewc_plan(const KnnParams& p, int cp, int tm, int zero_row, int xmax
     const int xv = (xmax / 8 + 511) / 512;
     if (xv > 4) return false;
     const int epi = 8 * rb * 32 * cb * 32 * 2;
-    const FewcLayout l = fewc_layout(tm, 32 * wn * cb, cp, zero_row, xmax, epi);
+    const FewcLayout l = fewc_layout(tm, 32 * wn * cb, cp, zero_row, xmax, pmax, epi);
     if (l.total > 160 * 1024) continue;
     pl = FewcPlan{tm, wm, rb, cb, xv < 1 ? 1 : xv, l.total};
     return true;
@@ -406,15 +474,19 @@ static int launch_fewc_cp(const KnnParams& p, const FewcTables& ft, const FewcPl
 
 // 1 if launched, 0 if the fused kernel does not take this call (caller falls back).
 int launch_knnconv_fewc(const KnnParams& p, const fovi_knnconv_args* a, int cp, hipStream_t s) {
-  if (!a->fc_lo || !a->fc_span || !a->fc_item || !a->fc_xoff || a->y_dtype != FOVI_BF16) return 0;
+  if (!a->fc_lo || !a->fc_span || !a->fc_item || !a->fc_xoff || !a->fc_comb || !a->fc_comb_off ||
+      a->y_dtype != FOVI_BF16)
+    return 0;
   if (a->fc_zero_row <= 0 || a->fc_zero_row > 0xffff || a->fc_xmax < 0 || a->fc_xmax % 8 != 0 ||
-      a->fc_xmax > 0xffff || a->k_pad % FC_KC != 0)
+      a->fc_xmax > 0xffff || a->fc_pmax < 0 || a->fc_pmax > 0xfff || a->k_pad % FC_KC != 0 ||
+      a->k_pad / cp > 4096)
     return 0;
   if (a->fc_xmax > 0 && !a->fc_xlist) return 0;
   FewcPlan pl;
-  if (!fewc_plan(p, cp, a->fc_tile_points, a->fc_zero_row, a->fc_xmax, pl)) return 0;
+  if (!fewc_plan(p, cp, a->fc_tile_points, a->fc_zero_row, a->fc_xmax, a->fc_pmax, pl)) return 0;
   FewcTables ft;
   ft.lo = a->fc_lo; ft.span = a->fc_span; ft.item = a->fc_item; ft.xlist = a->fc_xlist; ft.xoff = a->fc_xoff;
+  ft.comb = a->fc_comb; ft.comb_off = a->fc_comb_off; ft.pmax = a->fc_pmax;
   ft.zero_row = a->fc_zero_row; ft.xmax = a->fc_xmax; ft.n_chunks = static_cast<int>(a->k_pad / FC_KC);
   const int vec_out = p.ys1 == 1 && p.ys2 % 8 == 0 && p.ys0 % 8 == 0 && p.Cout % 8 == 0 &&
                       reinterpret_cast<uintptr_t>(p.y) % 16 == 0;

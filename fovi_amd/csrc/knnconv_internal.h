@@ -5,6 +5,11 @@
 
 namespace fovi {
 
+// Few-channel slot sums (the fused kernel and the two-pass slot-sum kernel) run over a slot's
+// neighbour list in groups of FC_GROUP: each group's fp32 sum in list order from +0, the
+// groups' sums added in order (for up to FC_GROUP neighbours, the plain list order).
+constexpr int FC_GROUP = 8;
+
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 struct KnnParams {

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 27
+#define FOVI_ABI_VERSION 28
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -200,16 +200,23 @@ typedef struct fovi_knnconv_args {
    * cut into tiles of fc_tile_points (128 or 256) consecutive points; tile t stages input rows
    * fc_lo[t] .. fc_lo[t] + fc_span[t] - 1 (S rows 0 .. span - 1) and a zero row fc_zero_row
    * (>= every span, < 65536). The reduction runs in chunks of 64 columns (64 / w_c_slot slots;
-   * k_pad / 64 chunks). Chunk c of tile t has fc_tile_points * 64 / w_c_slot items, two words
-   * each, at fc_item[((t * n_chunks + c) * items + j * 512 + thread) * 2]:
-   *   word 0 = (S row of the first neighbour, or fc_zero_row) << 16 | neighbour count;
-   *   word 1 = destination (row * (64 / w_c_slot) + slot within the chunk) << 16 | offset of the
-   *            further neighbours (count - 1 S rows, list order) in the chunk's extras block,
-   * every (row, slot) of the chunk exactly once (counts 0 for points past n_out and slots past
-   * n_ref). Extras block (t, c) is fc_xlist[fc_xoff[t * n_chunks + c] ..
-   * fc_xoff[t * n_chunks + c + 1]) (uint16, multiples of 8; fc_xmax = the longest). The slot
-   * sums (fp32 in list order from +0, one rounding to bf16) and the MFMA order equal the
-   * two-pass path's. */
+   * k_pad / 64 chunks, at most 4096 slots). The kernel clears chunk c's A tile and writes its
+   * non-empty (row, slot) sums from items, fc_tile_points * 64 / w_c_slot slots of two words
+   * at fc_item[((t * n_chunks + c) * items + j * 512 + thread) * 2]:
+   *   word 0 = (S row of the first neighbour) << 16 | partial << 15 | count (1 .. 8; 0 = no
+   *            item in this slot);
+   *   word 1 = destination << 16 | offset of the further neighbours (count - 1 S rows, list
+   *            order) in the chunk's extras block;
+   * the destination is row * (64 / w_c_slot) + slot within the chunk (the item's fp32 sum in
+   * list order from +0, rounded once to bf16) or, with the partial bit, an index below
+   * fc_pmax (<= 4095) of the chunk's fp32 partial sums. Combine entries (t, c), fc_comb[
+   * fc_comb_off[t * n_chunks + c] .. fc_comb_off[t * n_chunks + c + 1]) (at most 512), each
+   * destination | m << 12 | p0 << 20, write to A the partials p0 .. p0 + m - 1 added in order
+   * and rounded once. A (row, slot) of up to 8 neighbours is one item; a longer one is one
+   * partial per group of 8 consecutive neighbours and one combine entry. Extras block (t, c)
+   * is fc_xlist[fc_xoff[t * n_chunks + c] .. fc_xoff[t * n_chunks + c + 1]) (uint16, multiples
+   * of 8; fc_xmax = the longest). The slot sums (this grouped order) and the MFMA order equal
+   * the two-pass path's. */
   const int32_t* fc_lo;
   const int32_t* fc_span;
   const uint32_t* fc_item;
@@ -221,6 +228,10 @@ typedef struct fovi_knnconv_args {
   int32_t wide_units;         /* 1: the wide-layer tables (tile_src, tile_cent words 1-3, tile_heavy
                                  word 0, tile_hlist) name staged and heavy rows in 16-byte units
                                  (needed past 1023 staged rows); 0: in bytes */
+  const uint32_t* fc_comb;    /* the fused few-channel kernel's combine entries (above) */
+  const int32_t* fc_comb_off;
+  int32_t fc_pmax;
+  int32_t reserved4;
 } fovi_knnconv_args;
 
 int fovi_knnconv_fwd(const fovi_knnconv_args* args, void* stream);

@@ -329,9 +329,11 @@ def test_stream_slot_order_is_a_permutation_that_lowers_serial_work():
     (24, 12, 30, None, 4, 128),     # ragged: partial tile, padding slots in the last chunk
 ])
 def test_few_channel_tables_rebuild_the_slot_sums(res_in, res_out, k, side, cp, tile):
-    """Emulates the fused few-channel kernel's use of its tables in float64: every (row, slot)
-    of a chunk is written exactly once, every S row it reads is a staged row or the zero row,
-    and the rebuilt A chunks equal the slot sums of the CSR lists."""
+    """Emulates the fused few-channel kernel's use of its tables in float64: the A tile starts
+    cleared, every non-empty (row, slot) of a chunk is written exactly once (by an item of at
+    most FC_GROUP neighbours, or by a combine entry adding the partial sums of its groups of
+    FC_GROUP consecutive neighbours in order), every S row read is a staged row, and the
+    rebuilt A chunks equal the slot sums of the CSR lists."""
     import numpy as np
 
     from fovi_amd.arch import knn_tables as T
@@ -340,6 +342,7 @@ def test_few_channel_tables_rebuild_the_slot_sums(res_in, res_out, k, side, cp, 
     k_pad = -(-V * cp // 64) * 64
     ft = T.few_channel_tables(t["idx"], t["slots"], n_in, V, cp, k_pad, tile)
     assert ft is not None
+    G = T.FC_GROUP
     spc, nc = 64 // cp, k_pad // 64
     rng = np.random.default_rng(0)
     x = rng.standard_normal((n_in, cp))
@@ -354,28 +357,52 @@ def test_few_channel_tables_rebuild_the_slot_sums(res_in, res_out, k, side, cp, 
     item = ft.item.numpy().view(np.uint32)
     xl = ft.xlist.numpy().view(np.uint16).astype(np.int64)
     xoff = ft.xoff.numpy()
+    comb = ft.comb.numpy().view(np.uint32)
+    coff = ft.comb_off.numpy()
+    split = 0
     for ti in range(ft.lo.shape[0]):
         lo, span = int(ft.lo[ti]), int(ft.span[ti])
-        S = np.zeros((ft.zero_row + 1, cp))
-        S[:span] = x[lo:lo + span]
+        S = x[lo:lo + span]
         for c in range(nc):
             blk = xl[xoff[ti * nc + c]:xoff[ti * nc + c + 1]]
             assert len(blk) <= ft.xmax and len(blk) % 8 == 0
-            got = np.full((tile * spc, cp), np.nan)
+            got = np.zeros((tile * spc, cp))
+            written = np.zeros(tile * spc, bool)
+            P = np.full((ft.pmax, cp), np.nan)
             for w0, w1 in item[ti, c]:
-                cnt, first, dest, off = int(w0 & 0xFFFF), int(w0 >> 16), int(w1 >> 16), int(w1 & 0xFFFF)
-                assert first <= ft.zero_row and (cnt > 0 or first == ft.zero_row)
-                rows = [first] + list(blk[off:off + cnt - 1]) if cnt > 1 else [first]
-                assert off + max(cnt - 1, 0) <= len(blk)
-                assert all(r < span or r == ft.zero_row for r in rows)
-                assert np.isnan(got[dest]).all(), "a (row, slot) is written twice"
-                got[dest] = S[rows].sum(0)
-            assert not np.isnan(got).any(), "a (row, slot) is never written"
+                cnt, part, first = int(w0 & 0xF), int(w0 >> 15) & 1, int(w0 >> 16)
+                dest, off = int(w1 >> 16), int(w1 & 0xFFFF)
+                if cnt == 0:
+                    assert w0 == 0 and w1 == 0
+                    continue
+                assert 1 <= cnt <= G and off + cnt - 1 <= len(blk)
+                rows = [first] + list(blk[off:off + cnt - 1])
+                assert all(0 <= r < span for r in rows)
+                if part:
+                    assert np.isnan(P[dest]).all(), "a partial sum is written twice"
+                    P[dest] = S[rows].sum(0)
+                else:
+                    assert not written[dest], "a (row, slot) is written twice"
+                    written[dest] = True
+                    got[dest] = S[rows].sum(0)
+            for cw in comb[coff[ti * nc + c]:coff[ti * nc + c + 1]]:
+                dest, m, p0 = int(cw & 0xFFF), int(cw >> 12) & 0xFF, int(cw >> 20)
+                assert m >= 2 and not written[dest]
+                assert not np.isnan(P[p0:p0 + m]).any(), "a combined partial is never written"
+                written[dest] = True
+                got[dest] = P[p0:p0 + m].sum(0)
+                split += 1
             got = got.reshape(tile, spc, cp)
             rows = slice(ti * tile, min((ti + 1) * tile, n_out))
-            m = rows.stop - rows.start
-            np.testing.assert_allclose(got[:m], want[rows, c * spc:(c + 1) * spc], rtol=1e-12, atol=1e-12)
-            assert not got[m:].any(), "rows past n_out must be zero"
+            m_rows = rows.stop - rows.start
+            np.testing.assert_allclose(got[:m_rows], want[rows, c * spc:(c + 1) * spc], rtol=1e-12, atol=1e-12)
+            nonempty = (ptr[rows, :] & 0xFFFF)
+            occ = np.zeros((m_rows, nc * spc), bool)
+            occ[:, :V] = nonempty > 0
+            assert (written.reshape(tile, spc)[:m_rows] == occ[:, c * spc:(c + 1) * spc]).all()
+            assert not got[m_rows:].any(), "rows past n_out must be zero"
+    if k == 256:
+        assert split > 0, "the C4 geometry has slots of more than FC_GROUP neighbours"
 
 
 @pytest.mark.parametrize("res_in,res_out,k,side", [(64, 64, 9, None), (64, 32, 49, None), (32, 16, 25, None),
