@@ -188,12 +188,20 @@ __global__ __launch_bounds__(512, 1) void knnconv_fewc_kernel(KnnParams p, FewcT
       *reinterpret_cast<u32x4*>(smem + L.w_off + fc_off(q >> 3, q & 7)) = src[j];
     }
   };
-  // extras of chunk c: uint16 S rows, a block of 8-entry pieces
-  auto load_x = [&](int c, u32x4 (&dst)[XV], int& n16) {
+  // Bounds of chunk c's extras and combine blocks (x = start and 16-byte pieces, y = start and
+  // entries), read a chunk before the blocks themselves so that their loads never wait on them
+  struct Meta { int xb, xn, cb, cn; };
+  auto meta = [&](int c) {
     const int64_t blk = static_cast<int64_t>(t) * NC + c;
-    const int beg = ft.xoff[blk], end = ft.xoff[blk + 1];
-    n16 = (end - beg) >> 3;
-    const u32x4* src = reinterpret_cast<const u32x4*>(ft.xlist + beg);
+    Meta m;
+    m.xb = ft.xoff[blk]; m.xn = (ft.xoff[blk + 1] - m.xb) >> 3;
+    m.cb = ft.comb_off[blk]; m.cn = ft.comb_off[blk + 1] - m.cb;
+    return m;
+  };
+  // extras of a chunk: uint16 S rows, a block of 8-entry pieces
+  auto load_x = [&](const Meta& m, u32x4 (&dst)[XV], int& n16) {
+    n16 = m.xn;
+    const u32x4* src = reinterpret_cast<const u32x4*>(ft.xlist + m.xb);
 #pragma unroll
     for (int j = 0; j < XV; ++j) {
       const int q = j * 512 + tid;
@@ -207,11 +215,8 @@ __global__ __launch_bounds__(512, 1) void knnconv_fewc_kernel(KnnParams p, FewcT
       if (q < n16) *reinterpret_cast<u32x4*>(smem + L.x_off + q * 16) = src[j];
     }
   };
-  // A tile of chunk c into buffer `buf` from this thread's items
   const RowT* S = reinterpret_cast<const RowT*>(smem + L.s_off);
   const uint16_t* X = reinterpret_cast<const uint16_t*>(smem + L.x_off);
-  // Further neighbours in list order (a plain loop: the compiler pipelines its index and row
-  // reads better than a hand-staged prefetch, measured).
   // A-tile address of (row, slot) dest of a chunk in buffer A
   auto a_addr = [&](uint8_t* A, int dest) {
     const int r = dest / SPC, sl = dest - r * SPC;
@@ -219,6 +224,9 @@ __global__ __launch_bounds__(512, 1) void knnconv_fewc_kernel(KnnParams p, FewcT
     return reinterpret_cast<RowT*>(A + fc_off(r, byte >> 4) + (byte & 15));
   };
   float* P = reinterpret_cast<float*>(smem + L.p_off);
+  // A tile of chunk c into buffer `buf` from this thread's items; further neighbours in list
+  // order (a plain loop: the compiler pipelines its index and row reads better than
+  // hand-staged batches of reads, measured)
   auto build = [&](const uint2 (&it)[IT], int buf) {
     uint8_t* A = smem + L.a_off + buf * TM * FC_ROWB;
 #pragma unroll
@@ -264,11 +272,7 @@ __global__ __launch_bounds__(512, 1) void knnconv_fewc_kernel(KnnParams p, FewcT
     }
     *a_addr(A, dest) = R::pack(a);
   };
-  auto load_comb = [&](int c) -> uint32_t {
-    const int64_t blk = static_cast<int64_t>(t) * NC + c;
-    const int beg = ft.comb_off[blk], n = ft.comb_off[blk + 1] - beg;
-    return tid < n ? ft.comb[beg + tid] : 0u;
-  };
+  auto load_comb = [&](const Meta& m) -> uint32_t { return tid < m.cn ? ft.comb[m.cb + tid] : 0u; };
   // zero A buffer `buf` (TM rows of 128 bytes)
   auto clear = [&](int buf) {
     u32x4* A = reinterpret_cast<u32x4*>(smem + L.a_off + buf * TM * FC_ROWB);
@@ -279,18 +283,22 @@ __global__ __launch_bounds__(512, 1) void knnconv_fewc_kernel(KnnParams p, FewcT
   uint2 it_a[IT], it_b[IT];
   u32x4 wreg[WV], xreg[XV];
   int xn = 0;
+  const Meta m0 = meta(0);
+  const Meta m1 = NC > 1 ? meta(1) : m0;
+  const Meta m2 = NC > 2 ? meta(2) : m0;
+  Meta mn = NC > 3 ? meta(3) : m0;          // the next chunk whose blocks are loaded (c + 3)
   load_items(0, it_a);
   if (NC > 1) load_items(1, it_b);
-  uint32_t cw_a = load_comb(0), cw_b = NC > 1 ? load_comb(1) : 0u;
+  uint32_t cw_a = load_comb(m0), cw_b = NC > 1 ? load_comb(m1) : 0u;
   load_w(0, wreg);
-  load_x(0, xreg, xn);
+  load_x(m0, xreg, xn);
   store_w(wreg);
   store_x(xreg, xn);
   clear(0);
   clear(1);
   if (NC > 1) {
     load_w(1, wreg);
-    load_x(1, xreg, xn);
+    load_x(m1, xreg, xn);
   }
   __syncthreads();
   build(it_a, 0);
@@ -302,10 +310,10 @@ __global__ __launch_bounds__(512, 1) void knnconv_fewc_kernel(KnnParams p, FewcT
   __syncthreads();
   combine(cw_a, 0);
   cw_a = cw_b;
-  cw_b = NC > 2 ? load_comb(2) : 0u;
+  cw_b = NC > 2 ? load_comb(m2) : 0u;
   if (NC > 1) {
     store_x(xreg, xn);
-    if (NC > 2) load_x(2, xreg, xn);
+    if (NC > 2) load_x(m2, xreg, xn);
   }
   __syncthreads();
 
@@ -341,15 +349,18 @@ __global__ __launch_bounds__(512, 1) void knnconv_fewc_kernel(KnnParams p, FewcT
     // lists, clear c's buffer for chunk c + 2, stage the next weights and extras
     if (c + 1 < NC) combine(cw_a, (c + 1) & 1);
     if (c + 2 < NC) clear(c & 1);
-    cw_a = cw_b;
-    cw_b = c + 3 < NC ? load_comb(c + 3) : 0u;
+    // everything this window stores was loaded a chunk ago; the next loads are issued after
+    // those uses, so waiting for them never waits for a load issued here
     if (c + 1 < NC) store_w(wreg);
     if (c + 2 < NC) store_x(xreg, xn);
 #pragma unroll
     for (int j = 0; j < IT; ++j) it_a[j] = it_b[j];
+    cw_a = cw_b;
+    cw_b = c + 3 < NC ? load_comb(mn) : 0u;
     if (c + 3 < NC) load_items(c + 3, it_b);
     if (c + 2 < NC) load_w(c + 2, wreg);
-    if (c + 3 < NC) load_x(c + 3, xreg, xn);
+    if (c + 3 < NC) load_x(mn, xreg, xn);
+    if (c + 4 < NC) mn = meta(c + 4);
     __syncthreads();
   }
 
