@@ -333,3 +333,45 @@ def test_deciding_candidates_exact_values():
     mask[0, 10] = False
     need = T._deciding(sq, mask, 2, torch.tensor([0.0]), 2 ** -19, exact_values=True)[0].tolist()
     assert need == [False, True, False, False, False, False, True, True, False, True, False, True, False]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dim,k,offset", [(1, 1, 0.0), (2, 5, 0.0), (3, 16, 1000.0), (2, 64, -300.0)])
+def test_device_euclid_search_edge_cases(dim, k, offset):
+    """One to three dimensions, k = 1 and k = 64, and points far from the origin, where torch's
+    matrix-product cdist cancels (|x|^2 + |y|^2 >> |x - y|^2): the bound on its rounding covers
+    it, and the search still equals the host's bit for bit."""
+    g = torch.Generator().manual_seed(dim * 100 + k)
+    src = torch.rand(64 * k + 37, dim, generator=g) * 3 + offset
+    dst = torch.rand(301, dim, generator=g) * 3 + offset
+    hi, hd = T.knn_euclidean(src, dst, k)
+    gi, gd = T.knn_euclidean_device(src, dst, k, "cuda")
+    assert torch.equal(gi, hi), f"indices differ at {int((gi != hi).sum())} entries"
+    assert torch.equal(gd, hd)
+
+
+@pytest.mark.gpu
+def test_device_slots_degenerate_neighbourhoods():
+    """Neighbourhoods whose points all coincide (radius 0 everywhere: the min-max span is the
+    1e-6 guard, and every step is exact on both sides) or nearly coincide (a 1e-6 jitter, which
+    the normalisation magnifies), and neighbourhoods on one horizontal line: the slots equal
+    the host's."""
+    g = torch.Generator().manual_seed(4)
+    n_src, n_out, k = 200, 40, 9
+    src_c = torch.rand(n_src, 2, generator=g)
+    src_c[:50] = 0.5                                   # a cluster of identical points
+    src_c[150:] = 0.25 + 1e-6 * torch.rand(50, 2, generator=g)   # a nearly coincident cluster
+    src_cart = torch.rand(n_src, 2, generator=g)
+    src_cart[50:100, 1] = 0.25                         # points on a horizontal line
+    idx = torch.stack([torch.randperm(n_src, generator=g)[:k] for _ in range(n_out)], 1)
+    idx[:, :10] = torch.arange(k).unsqueeze(1)         # neighbourhoods inside the cluster
+    idx[:, 10:20] = 50 + torch.arange(k).unsqueeze(1) * 3
+    idx[:, 20:30] = 150 + torch.arange(k).unsqueeze(1) * 5
+    out_c = torch.rand(n_out, 2, generator=g)
+    out_c[:10] = 0.5
+    out_cart = torch.rand(n_out, 2, generator=g)
+    ref, _ = T.reference_grid(k)
+    want = T.local_rf_slots(idx, src_c, src_cart, out_c, out_cart, ref)
+    got, redone = T.local_rf_slots_device(idx, src_c, src_cart, out_c, out_cart, ref, device="cuda")
+    print(f"\n{redone} of {n_out} points recomputed on the host")
+    assert torch.equal(got, want), f"slots differ at {int((got != want).sum())} entries"
