@@ -1,4 +1,8 @@
 // Library-wide C-ABI entry points: version and error reporting.
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "common.h"
 
 namespace fovi {
@@ -18,6 +22,20 @@ void set_error(const char* fmt, ...) {
 }
 
 void clear_error() { g_last_error.clear(); }
+
+hipError_t reserve_dynamic_lds(const void* kernel, size_t bytes) {
+  static std::mutex mu;
+  static std::map<std::pair<const void*, int>, size_t> done;   // (kernel, device) -> bytes reserved
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(mu);
+  size_t& have = done[std::make_pair(kernel, dev)];
+  if (have >= bytes) return hipSuccess;
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+  if (e == hipSuccess) have = bytes;
+  return e;
+}
 
 int check_launch(const char* what) {
   hipError_t e = hipGetLastError();

@@ -19,6 +19,11 @@ void clear_error();
 // Returns 0, or records the HIP error of the last launch and returns 1.
 int check_launch(const char* what);
 
+// hipFuncSetAttribute(MaxDynamicSharedMemorySize) for `kernel` on the current device, called
+// only when `bytes` exceeds what an earlier call reserved (a runtime call per launch costs host
+// time that small layers notice).
+hipError_t reserve_dynamic_lds(const void* kernel, size_t bytes);
+
 // Records (thread-local) the kernel path fovi_knnconv_fwd took; `name` must be
 // a string literal. Read back by fovi_knnconv_last_path().
 void note_path(const char* name);

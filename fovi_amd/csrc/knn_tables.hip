@@ -268,7 +268,7 @@ __global__ __launch_bounds__(KNN_THREADS) void knn_eu_candidates_kernel(KnnEuPar
 
 static int reserve_lds(const void* kernel, size_t lds, const char* what) {
   if (lds > 64 * 1024 &&
-      hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess) {
+      reserve_dynamic_lds(kernel, lds) != hipSuccess) {
     set_error("%s: cannot reserve %zu bytes of LDS", what, lds);
     return 1;
   }

@@ -254,8 +254,7 @@ extern "C" int fovi_knnconv_dw(const fovi_knnconv_dw_args* a, void* stream) {
   const int64_t total = p.S * p.NQ * p.V * p.tiles_o * p.tiles_c;
   const int64_t padded = (total + 7) / 8 * 8;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(&knnconv_dw_kernel),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, DW_LDS) != hipSuccess) {
+  if (reserve_dynamic_lds(reinterpret_cast<const void*>(&knnconv_dw_kernel), DW_LDS) != hipSuccess) {
     set_error("fovi_knnconv_dw: cannot reserve %d bytes of LDS", DW_LDS);
     return 1;
   }

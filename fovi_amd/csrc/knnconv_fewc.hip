@@ -447,7 +447,7 @@ static void launch_fewc_t(const KnnParams& p, const FewcTables& ft, const FewcPl
   const int64_t total = p.B * tiles_per_b;
   const int64_t padded = (total + 7) / 8 * 8;
   auto* k = &knnconv_fewc_kernel<TM, WM, RB, CB, CP, XV>;
-  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize, pl.lds);
+  (void)reserve_dynamic_lds(reinterpret_cast<const void*>(k), pl.lds);
   hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(padded)), dim3(512), pl.lds, s, p, ft, tiles_per_b, total, padded,
                      vec_out);
 }

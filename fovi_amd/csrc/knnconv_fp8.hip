@@ -274,13 +274,11 @@ static void launch_fp8_sv(const KnnParams& p, int out_t, hipStream_t s) {
   const size_t lds = f8_layout(NT, static_cast<int>(p.V), static_cast<int>(p.K), p.zero_row).total;
   dim3 grid(static_cast<unsigned>(padded));
   if (out_t == FOVI_BF16) {
-    hipFuncSetAttribute(reinterpret_cast<const void*>(&knnconv_fp8_kernel<NT, SV, uint16_t>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    (void)reserve_dynamic_lds(reinterpret_cast<const void*>(&knnconv_fp8_kernel<NT, SV, uint16_t>), lds);
     hipLaunchKernelGGL((knnconv_fp8_kernel<NT, SV, uint16_t>), grid, dim3(512), lds, s, p, tiles_per_b, n_tiles_n,
                        total, padded);
   } else {
-    hipFuncSetAttribute(reinterpret_cast<const void*>(&knnconv_fp8_kernel<NT, SV, float>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    (void)reserve_dynamic_lds(reinterpret_cast<const void*>(&knnconv_fp8_kernel<NT, SV, float>), lds);
     hipLaunchKernelGGL((knnconv_fp8_kernel<NT, SV, float>), grid, dim3(512), lds, s, p, tiles_per_b, n_tiles_n,
                        total, padded);
   }

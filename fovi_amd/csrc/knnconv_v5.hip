@@ -483,7 +483,7 @@ static void launch_v5_kernel(const KnnParams& p, hipStream_t s, size_t lds, dim3
                              int64_t n_tiles_n, int64_t total, int64_t padded, int vec_out) {
   const void* fn = F8 ? reinterpret_cast<const void*>(&knnconv_fp8_v5_kernel<SV, OutT, SH>)
                       : reinterpret_cast<const void*>(&knnconv_bf16_v5_kernel<SV, OutT, SH>);
-  (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+  (void)reserve_dynamic_lds(fn, lds);
   if constexpr (F8)
     hipLaunchKernelGGL((knnconv_fp8_v5_kernel<SV, OutT, SH>), grid, dim3(256), lds, s, p, ncb, tiles_per_b, n_tiles_n,
                        total, padded, vec_out);
