@@ -90,7 +90,10 @@ __device__ __forceinline__ int swz32(int r, int q) {
 // Finite inputs are clamped to +-448 first, so out-of-range values saturate;
 // NaN stays NaN.
 __device__ __forceinline__ float sat_e4m3(float f) {
-  return f == f ? __builtin_fminf(__builtin_fmaxf(f, -448.0f), 448.0f) : f;
+  // v_med3_f32 clamps finite values and infinities (it returns a bound for NaN, so NaN is
+  // selected back): three instructions, where fminf(fmaxf()) also canonicalises its input
+  const float c = __builtin_amdgcn_fmed3f(f, -448.0f, 448.0f);
+  return f == f ? c : f;
 }
 template <bool HI>
 __device__ __forceinline__ uint32_t cvt_pk_e4m3(float a, float b, uint32_t old) {

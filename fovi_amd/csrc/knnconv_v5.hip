@@ -106,7 +106,10 @@ template <> struct V5Elem<true> {
     u32x4 out;
 #pragma unroll
     for (int w = 0; w < 4; ++w)
-      out[w] = cvt_pk_e4m3<true>(a[4 * w + 2], a[4 * w + 3], cvt_pk_e4m3<false>(a[4 * w], a[4 * w + 1], 0u));
+      // the low pair's conversion keeps its third operand's high half, which the high pair's
+      // conversion then replaces: any register serves (no zero to materialise)
+      out[w] = cvt_pk_e4m3<true>(a[4 * w + 2], a[4 * w + 3],
+                                 cvt_pk_e4m3<false>(a[4 * w], a[4 * w + 1], __float_as_uint(a[4 * w])));
     return out;
   }
 };
