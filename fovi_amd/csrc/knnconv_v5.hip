@@ -382,6 +382,25 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, af[ks][i]),
                                                                 __builtin_bit_cast(bf16x8, bc[j * 2 + ks]), acc[i][j],
                                                                 0, 0, 0);
+      // Issue order (one wave per SIMD, so the wave's own MFMAs are all that can
+      // cover its LDS and memory latency): each of the first 12 MFMAs followed by
+      // one LDS read (A fragments, the stream's entry and rows, the next sources),
+      // the next 8 each by one weight-fragment load, then the remaining 12. The
+      // scheduler's default (reads bunched next to their first use, the weight
+      // loads in one burst) leaves the matrix pipe idle on every wait: C3 3.66 ->
+      // 3.30 ms with this order (measured against patterns with 8-19 reads first,
+      // the loads first or between the reads, pairs of either: 3.30-3.77 ms).
+#pragma unroll
+      for (int q = 0; q < 12; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // global load
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 12, 0);
     }
 
     unit_rest(sum, ce, pq);
