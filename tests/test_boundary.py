@@ -2,7 +2,8 @@
 Conv2d weight import (reference ``knn.py:649-715``) that DINOv3 uses for pretrained patch
 weights (``dinov3.py:88-91``).
 
-The registry snippet is read from INTEGRATION.md and executed as written, with stand-ins
+The registry snippet is read from the repository's integration guide (the block between its
+registry-snippet markers) and executed as written, with stand-ins
 for the two reference modules it imports (``fovi.arch.knn``: ``KNNBaseLayer``,
 ``KNN_CONV_REGISTRY``, ``get_knn_conv_layer`` as ``knn.py:1007-1030`` defines them;
 ``fovi.arch.knnalexnet``) and coords given as a plain namespace of the reference-written
@@ -26,13 +27,14 @@ from fovi_amd.arch.knn import KNNConvLayer, KNNPoolingLayer
 from fovi_amd.sensing.coords import SamplingCoords
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GUIDE = os.path.join(ROOT, "INTEGRATION.md")
 GOLDEN = np.load(os.path.join(ROOT, "tests", "golden", "tables.npz"))
 
 
 def _registry_snippet():
-    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    text = open(GUIDE).read()
     m = re.search(r"<!-- registry-snippet -->\s*```python\n(.*?)```\s*<!-- /registry-snippet -->", text, re.S)
-    assert m, "INTEGRATION.md lost its registry snippet"
+    assert m, f"{GUIDE} lost its registry snippet"
     return m.group(1)
 
 
@@ -82,7 +84,7 @@ def _run_snippet(monkeypatch, device, tag="c2_l3", c_in=192, c_out=384, k=9):
     coords = _golden_coords(tag)
     env = {"in_channels": c_in, "out_channels": c_out, "k": k, "in_coords": coords, "out_coords": coords,
            "device": device}
-    exec(compile(_registry_snippet(), "INTEGRATION.md", "exec"), env)
+    exec(compile(_registry_snippet(), GUIDE, "exec"), env)
     return env, ref_knn, ref_alex, coords
 
 
