@@ -104,10 +104,27 @@ template <> struct V5Elem<true> {
   }
   static __device__ __forceinline__ u32x4 pack(const Sum& a) {
     u32x4 out;
+    // Without a NaN among the 16 sums the saturation is the v_med3 clamp alone; their sum
+    // is NaN when one is (or when infinities cancel, which takes the exact path too).
+    float t = a[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) t += a[i];
+    if (t == t) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float c0 = __builtin_amdgcn_fmed3f(a[4 * w], -448.0f, 448.0f);
+        const float c1 = __builtin_amdgcn_fmed3f(a[4 * w + 1], -448.0f, 448.0f);
+        const float c2 = __builtin_amdgcn_fmed3f(a[4 * w + 2], -448.0f, 448.0f);
+        const float c3 = __builtin_amdgcn_fmed3f(a[4 * w + 3], -448.0f, 448.0f);
+        // the low pair's conversion keeps its third operand's high half, which the high
+        // pair's conversion then replaces: any register serves (no zero to materialise)
+        const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c0, c1, __float_as_int(c0), false));
+        out[w] = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c2, c3, static_cast<int>(lo), true));
+      }
+      return out;
+    }
 #pragma unroll
     for (int w = 0; w < 4; ++w)
-      // the low pair's conversion keeps its third operand's high half, which the high pair's
-      // conversion then replaces: any register serves (no zero to materialise)
       out[w] = cvt_pk_e4m3<true>(a[4 * w + 2], a[4 * w + 3],
                                  cvt_pk_e4m3<false>(a[4 * w], a[4 * w + 1], __float_as_uint(a[4 * w])));
     return out;

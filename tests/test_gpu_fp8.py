@@ -234,3 +234,33 @@ def test_c5_full_batch_cosines_per_scale():
     print("C5 cosines:", {k: round(v, 6) for k, v in results.items()}, flush=True)
     assert results["amax*32/448"] >= 0.995
     assert results["vs dequantized formula"] >= 0.9995
+
+
+@pytest.mark.gpu
+def test_fp8_fragment_order_kernel_saturation_and_nan():
+    """Collision sums that pass 448 saturate and NaN activations propagate exactly as in the
+    row-packed e4m3 kernel: e4m3 inputs with planted 448s (sums of two or more overflow) and
+    NaN bytes; the plain slot order gives the same bits (NaN at the same outputs)."""
+    layer = _layer(16, 16, 9, 64, 256, True, seed=21)
+    x = torch.randn(2, 64, 256, generator=torch.Generator().manual_seed(22)).bfloat16()
+    xq = layer.quantize_input(x.cuda().transpose(1, 2).contiguous().transpose(1, 2))
+    raw = xq.data.view(torch.uint8)                      # [B, C, N] view of channels-last bytes
+    g = torch.Generator().manual_seed(23)
+    big = torch.randint(0, 256, (40,), generator=g)      # input points given 448 in channel 5
+    raw[0, 5, big.cuda()] = 0x7E
+    raw[1, 9, big.cuda()] = 0xFE                         # -448
+    nanp = torch.randint(0, 256, (3,), generator=g)
+    raw[0, 17, nanp.cuda()] = 0x7F                       # NaN
+    with torch.no_grad():
+        layer.mfma_weights = False
+        y_rows = layer(xq)
+        assert layer.last_weight_layout == "rows"
+        layer.mfma_weights = True
+        layer.set_slot_order(None)
+        y_plain = layer(xq)
+        assert layer.last_weight_layout == "mfma"
+    a, b = y_plain.float().cpu(), y_rows.float().cpu()
+    assert torch.isnan(a).any(), "a NaN activation must reach the output"
+    assert torch.equal(torch.isnan(a), torch.isnan(b))
+    keep = ~torch.isnan(a)
+    assert torch.equal(a[keep], b[keep])
