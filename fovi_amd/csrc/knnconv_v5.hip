@@ -248,6 +248,21 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
     }
   }
   if (tid < 4) *reinterpret_cast<u32x4*>(smem + zr * V5_ROW + tid * 16) = u32x4{0u, 0u, 0u, 0u};
+  __syncthreads();
+  // The A sources become final LDS offsets in 16-byte units (below 160 KB / 16): a
+  // stream-built sum (0xFFFF) is row r of collision tile pos % V5_NB, where pos is
+  // the slot's position in the chunk; other rows keep their offset. The MFMA lanes
+  // then address a fragment with one shift and their part's XOR.
+  {
+    uint16_t* s16 = reinterpret_cast<uint16_t*>(smem + L.src_off);
+    for (int i = tid; i < V * V5_MT; i += 256) {
+      const uint32_t e = s16[i];
+      const int pos = i / V5_MT, r = i % V5_MT;
+      const uint32_t off = e == 0xffffu ? acol + static_cast<uint32_t>(pos % V5_NB) * V5_TILE_BYTES + row_off(r)
+                                        : e << SH;
+      s16[i] = static_cast<uint16_t>(off >> 4);
+    }
+  }
 
   // Collision sums. A unit is (entry, 16-byte part): entry = unit / 4. Its
   // first four neighbours are summed from the entry's words 1-2, neighbours 5
@@ -309,14 +324,10 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // this lane's rows of the A tile and their offsets in a collision tile
-  uint32_t rowm_off[4];
+  // this lane's rows of the A tile
   int rowm[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    rowm[i] = wm * 128 + i * 32 + (lane & 31);
-    rowm_off[i] = acol + row_off(rowm[i]);
-  }
+  for (int i = 0; i < 4; ++i) rowm[i] = wm * 128 + i * 32 + (lane & 31);
   // the two 16-byte parts of a row this lane feeds to the MFMAs: bf16, parts
   // (lane / 32) and 2 + lane / 32 (K halves ks = 0, 1); e4m3, parts
   // 2 (lane / 32) and 2 (lane / 32) + 1 (channels 32 (lane / 32) .. + 32)
@@ -344,12 +355,12 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
   __syncthreads();
 
   int v = 0, cc = 0;
-  uint32_t vb = 0;   // v % V5_NB
   // stream bounds of the current slot, read one iteration ahead
   int need = bpos, lim = 4 * coff[min(V5_NB, V)];
-  for (int it = 0; it < nit; ++it) {
-    u32x4(&bc)[8] = wa;   // this iteration's weight fragments
-    u32x4(&bn)[8] = wb;   // the next iteration's
+  // One iteration: bc holds its weight fragments and ecur its A sources; bn and
+  // enxt receive the next iteration's.
+  auto step = [&](const int it, u32x4 (&bc)[8], u32x4 (&bn)[8], uint32_t (&ecur)[4],
+                  uint32_t (&enxt)[4]) __attribute__((always_inline)) {
     if (bpos < need) {            // slot v incomplete: finish it
       build_range(bpos, need);
       bpos = need;
@@ -362,7 +373,7 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
     u32x4 af[2][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t a = ecur[i] == 0xffffu ? rowm_off[i] + vb * V5_TILE_BYTES : ecur[i] << SH;
+      const uint32_t a = ecur[i] << 4;
       af[0][i] = lds16(smem, a ^ qx0);
       af[1][i] = lds16(smem, a ^ qx1);
     }
@@ -425,11 +436,9 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
     bpos = min(bpos + 256, lim);
     __syncthreads();
     v = vn;
-    vb = vb + 1 == V5_NB ? 0 : vb + 1;
     need = need_n;
     lim = lim_n;
     if (v == 0) {                 // chunk boundary
-      vb = 0;
       ++cc;
       if (more) {                 // every MFMA of the finished chunk is done with S
         store_s();
@@ -441,11 +450,16 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
         __syncthreads();
       }
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ecur[i] = enxt[i];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) wa[k] = wb[k];
+  };
+  // Two iterations per trip with the register sets swapping roles: no copies at
+  // the loop latch, whose moves of the next weight fragments would wait for
+  // their loads (C3 ~1% faster).
+  int it = 0;
+  for (; it + 1 < nit; it += 2) {
+    step(it, wa, wb, ecur, enxt);
+    step(it + 1, wb, wa, enxt, ecur);
   }
+  if (it < nit) step(it, wa, wb, ecur, enxt);
 
   OutT* y = static_cast<OutT*>(p.y) + b * p.ys0;
   float bo[4], sc[4];
