@@ -305,9 +305,11 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
     }
   };
   // units [from, to) of the tile's unit stream (the entry list in slot order,
-  // four 16-byte parts per entry), complete sums; from % 4 == 0
-  auto build_range = [&](int from, int to) {
-    for (int u = from + tid; u < to; u += 256) {
+  // four 16-byte parts per entry), complete sums; from % 4 == 0. A chunk start
+  // deals its units from the last thread down, away from the heavy sums, which
+  // take the first threads.
+  auto build_range = [&](int from, int to, bool from_top = false) {
+    for (int u = from + (from_top ? 255 - tid : tid); u < to; u += 256) {
       const u32x4 ce = cent[u >> 2];
       const uint32_t pq = static_cast<uint32_t>(u & 3) << 4;
       Sum a = unit_sum4(ce, pq);
@@ -348,7 +350,7 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
   // with more than four neighbours finish after the MFMAs.
   int bpos = 4 * coff[1];
   build_heavy();
-  build_range(0, bpos);
+  build_range(0, bpos, true);
   uint32_t ecur[4], enxt[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) ecur[i] = srcs[rowm[i]];
@@ -357,6 +359,18 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
   int v = 0, cc = 0;
   // stream bounds of the current slot, read one iteration ahead
   int need = bpos, lim = 4 * coff[min(V5_NB, V)];
+  // The entry of this thread's next stream unit is read an iteration ahead (the
+  // entry list is static), so the unit's row reads start with the iteration;
+  // read again where the stream position moves otherwise (a catch-up, a chunk
+  // start).
+  const uint32_t pq = static_cast<uint32_t>(tid & 3) << 4;
+  auto read_ce = [&](int at, int bound) {
+    const int u = at + tid;
+    u32x4 e = cent[u < bound ? (u >> 2) : 0];
+    if (u >= bound) e[0] = 0;     // count 0: written to the trash row
+    return e;
+  };
+  u32x4 ce = read_ce(bpos, lim);
   // One iteration: bc holds its weight fragments and ecur its A sources; bn and
   // enxt receive the next iteration's.
   auto step = [&](const int it, u32x4 (&bc)[8], u32x4 (&bn)[8], uint32_t (&ecur)[4],
@@ -365,6 +379,7 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
       build_range(bpos, need);
       bpos = need;
       __syncthreads();
+      ce = read_ce(bpos, lim);
     }
     const bool more = it + 1 < nit;
     const int vn = v + 1 == V ? 0 : v + 1;
@@ -381,10 +396,6 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
 #pragma unroll
     for (int i = 0; i < 4; ++i) enxt[i] = srcs[vn * V5_MT + rowm[i]];
 
-    const int u = bpos + tid;
-    const uint32_t pq = static_cast<uint32_t>(tid & 3) << 4;
-    u32x4 ce = cent[u < lim ? (u >> 2) : 0];
-    if (u >= lim) ce[0] = 0;      // count 0: written to the trash row
     Sum sum = unit_sum4(ce, pq);
 
     if constexpr (F8) {
@@ -434,6 +445,7 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
     unit_rest(sum, ce, pq);
     *reinterpret_cast<u32x4*>(smem + (((ce[0] >> 16) & 0xffu) ? unit_dst(ce, pq) : trash)) = E::pack(sum);
     bpos = min(bpos + 256, lim);
+    ce = read_ce(bpos, lim_n);
     __syncthreads();
     v = vn;
     need = need_n;
@@ -446,7 +458,8 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
         if (cc + 1 < ncc) load_s(cc + 1);
         bpos = 4 * coff[1];
         build_heavy();
-        build_range(0, bpos);
+        build_range(0, bpos, true);
+        ce = read_ce(bpos, lim);
         __syncthreads();
       }
     }
