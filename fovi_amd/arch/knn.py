@@ -257,7 +257,7 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         self._packed = {}
         order = None
         if tiles is not None:
-            order = T.stream_slot_order(T.slot_stream_units(tiles))
+            order = T.stream_slot_order(T.slot_stream_units(tiles), ahead=T.wide_tiles_of(tiles))
         self.set_slot_order(order)
         # tables of the fused few-channel kernel (c_in <= 8): the largest tile whose LDS fits
         self._fc = None
@@ -390,6 +390,7 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         wide = T.wide_tables(tiles, self._k, order) if tiles is not None else None
         self._cent_stride = self._coll_off_stride = self._heavy_stride = self._hlist_stride = 0
         self._wide_units = bool(wide.units) if wide is not None else False
+        self._wide_tiles = wide.tiles if wide is not None else T.WIDE_TILES
         dev = self.weight.device
         for name, field in (("tile_src", "src"), ("tile_cent", "coll"), ("tile_coll_off", "coll_off"),
                             ("tile_heavy", "heavy"), ("tile_hlist", "hlist")):
@@ -432,14 +433,10 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         return packed
 
     def _mfma_lds_bytes(self):
-        """LDS bytes of the fragment-order kernel's tile (its ``v5_layout``): the staged rows plus
-        the zero row and the heavy-sum rows (64 bytes each), 128-byte alignment, three 256 x 32
-        bf16 collision tiles and a trash row, per-(slot, row) sources, per-slot entry offsets,
-        16-byte stream entries, 8-byte heavy entries, the heavy entries' neighbour offsets."""
-        v = self.ref_coords.shape[0]
-        o = ((self._zero_row + 1 + self._heavy_stride) * 64 + 127) & ~127
-        return (o + (3 * 256 + 1) * 32 * 2 + v * 256 * 2 + self._coll_off_stride * 4 + self._cent_stride * 16
-                + self._heavy_stride * 8 + self._hlist_stride * 2)
+        """LDS bytes of the fragment-order kernel's tile (``knn_tables.wide_lds_bytes`` with the
+        layer's collision tiles)."""
+        return T.wide_lds_bytes(self.ref_coords.shape[0], self._zero_row, self._coll_off_stride,
+                                self._cent_stride, self._heavy_stride, self._hlist_stride, self._wide_tiles)
 
     def _mfma_column_use(self):
         """Fraction of the fragment-order kernel's 256-channel output tiles that holds real

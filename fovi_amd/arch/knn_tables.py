@@ -918,9 +918,50 @@ def _row_offset(r):
 STREAM_MAX_COUNT = 6
 # LDS bytes of one collision tile of the wide-layer kernel (256 rows x 64 bytes)
 WIDE_TILE_BYTES = 256 * 64
+# collision tiles of the wide-layer kernel: four when its LDS layout with four fits
+# WIDE_LDS_BYTES, else three (slot position p sums into tile p % tiles)
 WIDE_TILES = 3
+WIDE_TILES_MAX = 4
+WIDE_LDS_BYTES = 160 * 1024
 # staged rows the wide-layer kernel holds (four 16-byte pieces per thread and row, 16 per thread)
 WIDE_MAX_ROWS = 1024
+
+
+def wide_lds_bytes(n_ref, zero_row, coll_off_stride, cent_stride, heavy_stride, hlist_stride, tiles):
+    """LDS bytes of the wide-layer kernel's tile (its ``v5_layout``): the staged rows, the zero
+    row and the heavy-sum rows (64 bytes each), 128-byte alignment, ``tiles`` collision tiles of
+    256 rows and a trash row, per-(slot, row) sources, per-slot entry offsets, 16-byte stream
+    entries, 8-byte heavy entries, the heavy entries' neighbour offsets."""
+    o = ((zero_row + 1 + heavy_stride) * 64 + 127) & ~127
+    return (o + (tiles * 256 + 1) * 64 + n_ref * 256 * 2 + coll_off_stride * 4 + cent_stride * 16
+            + heavy_stride * 8 + hlist_stride * 2)
+
+
+def wide_tile_count(n_ref, zero_row, coll_off_stride, cent_stride, heavy_stride, hlist_stride):
+    """Collision tiles of the wide-layer kernel for these table sizes: ``WIDE_TILES_MAX`` when
+    that layout fits ``WIDE_LDS_BYTES``, else ``WIDE_TILES`` (the kernel applies the same rule)."""
+    big = wide_lds_bytes(n_ref, zero_row, coll_off_stride, cent_stride, heavy_stride, hlist_stride, WIDE_TILES_MAX)
+    return WIDE_TILES_MAX if big <= WIDE_LDS_BYTES else WIDE_TILES
+
+
+def wide_strides(direct):
+    """Table sizes of ``wide_tables`` for ``direct`` (any slot order): ``(coll_off_stride,
+    cent_stride, heavy_stride, hlist_stride)``."""
+    ent = direct[2]
+    n_tiles, n_ref, tile = direct[4].shape
+    e3 = ent.numpy().view(np.uint32).astype(np.int64).reshape(n_tiles, tile, n_ref)
+    cnt = (e3 >> 8) & 0xFF
+    light = (cnt >= 2) & (cnt <= STREAM_MAX_COUNT)
+    heavy = cnt > STREAM_MAX_COUNT
+    stride = max(1, int(light.sum(axis=(1, 2)).max(initial=0)))
+    heavy_stride = max(2, -(-int(heavy.sum(axis=(1, 2)).max(initial=0)) // 2) * 2)
+    hlist_stride = max(8, -(-int(np.where(heavy, cnt, 0).sum(axis=(1, 2)).max(initial=0)) // 8) * 8)
+    return -(-(n_ref + 1) // 4) * 4, stride, heavy_stride, hlist_stride
+
+
+def wide_tiles_of(direct):
+    """Collision tiles the wide-layer kernel uses for ``direct``'s tables."""
+    return wide_tile_count(direct[4].shape[1], direct[6], *wide_strides(direct))
 
 
 class WideTables(NamedTuple):
@@ -933,6 +974,7 @@ class WideTables(NamedTuple):
     hlist: torch.Tensor      # [T, hlist_stride] int16 (uint16 offsets)
     hlist_stride: int
     units: bool              # row offsets in 16-byte units (True) or bytes (False)
+    tiles: int               # collision tiles (slot position p sums into tile p % tiles)
 
 
 def wide_tables(direct, k, order=None):
@@ -954,8 +996,9 @@ def wide_tables(direct, k, order=None):
     * ``coll [T, stride, 4] uint32``: one 16-byte stream entry per (slot,
       collision row with 2 .. ``STREAM_MAX_COUNT`` neighbours), grouped by slot
       position and within a slot by decreasing count. Word 0: bits 0-15 the
-      destination in bytes, relative to the first collision tile (tile ``p % 3``
-      of slot position p, then the row's offset), bits 16-23 the count; words
+      destination in bytes, relative to the first collision tile (tile ``p %
+      tiles`` of slot position p, then the row's offset; ``tiles`` =
+      ``wide_tile_count`` of the table sizes), bits 16-23 the count; words
       1-3: offsets of the staged rows of neighbours 1-6, two per word (low
       half first; the zero row past the count).
     * ``coll_off [T, V + 1 rounded up to 4] int32``: slot position p's entries
@@ -984,8 +1027,8 @@ def wide_tables(direct, k, order=None):
     e3 = e.reshape(n_tiles, tile, n_ref)
     first, cnt, begin = e3 >> 16, (e3 >> 8) & 0xFF, e3 & 0xFF
     heavy_mask = cnt > STREAM_MAX_COUNT                        # [T, tile, V]
-    n_heavy = heavy_mask.sum(axis=(1, 2))
-    heavy_stride = max(2, -(-int(n_heavy.max(initial=0)) // 2) * 2)
+    voff, stride, heavy_stride, hlist_stride = wide_strides(direct)
+    n_tiles_c = wide_tile_count(n_ref, zero_row, voff, stride, heavy_stride, hlist_stride)
     units = zero_row > 1023
     sh = 4 if units else 0                                    # offset = byte offset >> sh
     row_b = 64 >> sh
@@ -997,7 +1040,6 @@ def wide_tables(direct, k, order=None):
 
     # heavy entries: in (slot, row) order of each tile
     heavy_row = np.full((n_tiles, tile, n_ref), -1, np.int64)
-    n_list = np.zeros(n_tiles, np.int64)
     hent = []
     for t in range(n_tiles):
         rr, vv = np.nonzero(heavy_mask[t])
@@ -1005,8 +1047,6 @@ def wide_tables(direct, k, order=None):
         rr, vv = rr[ordv], vv[ordv]
         heavy_row[t, rr, vv] = np.arange(len(rr))
         hent.append((rr, vv))
-        n_list[t] = cnt[t, rr, vv].sum()
-    hlist_stride = max(8, -(-int(n_list.max(initial=0)) // 8) * 8)
     heavy = np.zeros((n_tiles, heavy_stride, 2), np.uint32)
     hlist = np.zeros((n_tiles, hlist_stride), np.uint16)
     for t in range(n_tiles):
@@ -1035,8 +1075,6 @@ def wide_tables(direct, k, order=None):
             rows = rows[cnt[t, rows, v] <= STREAM_MAX_COUNT]
             lists[t][q] = rows
             light_n[t, q] = len(rows)
-    stride = int(max(1, int(light_n.sum(axis=1).max(initial=0))))
-    voff = -(-(n_ref + 1) // 4) * 4
     out = np.zeros((n_tiles, stride, 4), np.uint32)
     coll_off = np.zeros((n_tiles, voff), np.int32)
     for t in range(n_tiles):
@@ -1053,13 +1091,13 @@ def wide_tables(direct, k, order=None):
             r = nb[t, rows, np.minimum(b0 + j, k - 1)]
             nbo.append(np.where(j < c, _row_offset(r) >> sh, zoff))
         n_e = off[-1]
-        dst = (pos % WIDE_TILES) * WIDE_TILE_BYTES + _row_offset(rows)
+        dst = (pos % n_tiles_c) * WIDE_TILE_BYTES + _row_offset(rows)
         out[t, :n_e, 0] = (dst | (c << 16)).astype(np.uint32)
         for w in range(3):
             out[t, :n_e, 1 + w] = (nbo[2 * w] | (nbo[2 * w + 1] << 16)).astype(np.uint32)
     return WideTables(torch.from_numpy(src), torch.from_numpy(out.view(np.int32)), torch.from_numpy(coll_off),
                       stride, torch.from_numpy(heavy.view(np.int32)), heavy_stride,
-                      torch.from_numpy(hlist.view(np.int16)), hlist_stride, units)
+                      torch.from_numpy(hlist.view(np.int16)), hlist_stride, units, n_tiles_c)
 
 
 def slot_stream_units(direct):

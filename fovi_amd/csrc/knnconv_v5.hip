@@ -12,8 +12,8 @@
 //    chunk at a time (S); the next chunk is loaded into registers while the
 //    current one is consumed. MFMA lanes read single-neighbour slots straight
 //    from S (an LDS zero row serves empty slots); slots with 2 to 6
-//    neighbours are summed in fp32 (one RNE rounding) into a ring of three
-//    collision tiles, up to two slots ahead, as a stream over the tile's
+//    neighbours are summed in fp32 (one RNE rounding) into a ring of three or
+//    four collision tiles, up to two or three slots ahead, as a stream over the tile's
 //    collision entries that advances a fixed 256 units per iteration; the few
 //    slots with more neighbours are summed once per chunk into rows of their
 //    own, which the MFMA lanes read like staged rows.
@@ -31,7 +31,10 @@ namespace fovi {
 constexpr int V5_MT = 256;   // output points per tile
 constexpr int V5_NT = 256;   // output channels per tile
 constexpr int V5_ROW = 64;   // bytes of an LDS row: one reduction chunk (32 bf16 or 64 e4m3 channels)
-constexpr int V5_NB = 3;     // collision tiles: slot v uses tile v % 3, so sums run up to two slots ahead
+// Collision tiles: slot position v sums into tile v % nb, so the stream runs up to nb - 1
+// slots ahead of the slot the MFMAs consume; nb = 4 when that layout fits the LDS, else 3
+// (the host tables encode the same rule).
+constexpr int V5_NB_MIN = 3, V5_NB_MAX = 4;
 
 constexpr int V5_STREAM_MAX = 6;   // neighbours of a stream entry; more: a heavy entry
 
@@ -46,12 +49,12 @@ struct V5Layout {
 };
 
 __host__ __device__ inline V5Layout v5_layout(int V, int zero_row, int coff_stride, int cent_stride,
-                                              int heavy_stride, int hlist_stride) {
+                                              int heavy_stride, int hlist_stride, int nb) {
   V5Layout l;
   int o = (zero_row + 1) * V5_ROW;                  // staged rows + zero row
   l.heavy_rows = o; o += heavy_stride * V5_ROW;     // heavy sums, one row per heavy entry
   o = (o + 127) & ~127;
-  l.acol_off = o;   o += (V5_NB * V5_MT + 1) * V5_ROW; // V5_NB collision tiles of 256 rows + a trash row
+  l.acol_off = o;   o += (nb * V5_MT + 1) * V5_ROW; // nb collision tiles of 256 rows + a trash row
   l.src_off = o;    o += V * V5_MT * 2;             // per (slot, row) A source, slot-major
   l.coff_off = o;   o += coff_stride * 4;           // per-slot collision entry offsets
   l.cent_off = o;   o += cent_stride * 16;          // collision entries
@@ -62,6 +65,13 @@ __host__ __device__ inline V5Layout v5_layout(int V, int zero_row, int coff_stri
 }
 
 constexpr uint32_t V5_TILE_BYTES = V5_MT * V5_ROW;   // one collision tile
+
+__host__ __device__ inline int v5_tiles(int V, int zero_row, int coff_stride, int cent_stride, int heavy_stride,
+                                        int hlist_stride) {
+  return v5_layout(V, zero_row, coff_stride, cent_stride, heavy_stride, hlist_stride, V5_NB_MAX).total <= 160 * 1024
+             ? V5_NB_MAX
+             : V5_NB_MIN;
+}
 
 // Byte offset of 16-byte part 0 of 64-byte row r under the swz32 XOR swizzle;
 // part q of the row is at row_off(r) ^ (q << 4).
@@ -147,14 +157,15 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int V = static_cast<int>(p.V);
   const int zr = p.zero_row;
-  const V5Layout L = v5_layout(V, zr, p.coll_off_stride, p.cent_stride, p.heavy_stride, p.hlist_stride);
+  const int nb = v5_tiles(V, zr, p.coll_off_stride, p.cent_stride, p.heavy_stride, p.hlist_stride);
+  const V5Layout L = v5_layout(V, zr, p.coll_off_stride, p.cent_stride, p.heavy_stride, p.hlist_stride, nb);
   const uint16_t* srcs = reinterpret_cast<const uint16_t*>(smem + L.src_off);
   const int32_t* coff = reinterpret_cast<const int32_t*>(smem + L.coff_off);
   const u32x4* cent = reinterpret_cast<const u32x4*>(smem + L.cent_off);
   const uint32_t* heavy = reinterpret_cast<const uint32_t*>(smem + L.heavy_off);
   const uint16_t* hlist = reinterpret_cast<const uint16_t*>(smem + L.hlist_off);
   const uint32_t acol = static_cast<uint32_t>(L.acol_off);
-  const uint32_t trash = acol + V5_NB * V5_TILE_BYTES;
+  const uint32_t trash = acol + nb * V5_TILE_BYTES;
 
   const int64_t tile = xcd_tile(blockIdx.x, padded_tiles);
   if (tile >= total_tiles) return;
@@ -250,7 +261,7 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
   if (tid < 4) *reinterpret_cast<u32x4*>(smem + zr * V5_ROW + tid * 16) = u32x4{0u, 0u, 0u, 0u};
   __syncthreads();
   // The A sources become final LDS offsets in 16-byte units (below 160 KB / 16): a
-  // stream-built sum (0xFFFF) is row r of collision tile pos % V5_NB, where pos is
+  // stream-built sum (0xFFFF) is row r of collision tile pos % nb, where pos is
   // the slot's position in the chunk; other rows keep their offset. The MFMA lanes
   // then address a fragment with one shift and their part's XOR.
   {
@@ -258,7 +269,7 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
     for (int i = tid; i < V * V5_MT; i += 256) {
       const uint32_t e = s16[i];
       const int pos = i / V5_MT, r = i % V5_MT;
-      const uint32_t off = e == 0xffffu ? acol + static_cast<uint32_t>(pos % V5_NB) * V5_TILE_BYTES + row_off(r)
+      const uint32_t off = e == 0xffffu ? acol + static_cast<uint32_t>(pos % nb) * V5_TILE_BYTES + row_off(r)
                                         : e << SH;
       s16[i] = static_cast<uint16_t>(off >> 4);
     }
@@ -348,7 +359,10 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
   // with its slot 0 built; a slot not yet complete when its turn comes is
   // finished first (uniform branch). Masked units write a trash row; entries
   // with more than four neighbours finish after the MFMAs.
-  int bpos = 4 * coff[1];
+  // stream position (units) of the end of slot position i, clamped to the tile's entries so
+  // that inconsistent caller tables cannot run the stream past them
+  auto upos = [&](int i) { return 4 * min(coff[i], p.cent_stride); };
+  int bpos = upos(1);
   build_heavy();
   build_range(0, bpos, true);
   uint32_t ecur[4], enxt[4];
@@ -358,7 +372,7 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
 
   int v = 0, cc = 0;
   // stream bounds of the current slot, read one iteration ahead
-  int need = bpos, lim = 4 * coff[min(V5_NB, V)];
+  int need = bpos, lim = upos(min(nb, V));
   // The entry of this thread's next stream unit is read an iteration ahead (the
   // entry list is static), so the unit's row reads start with the iteration;
   // read again where the stream position moves otherwise (a catch-up, a chunk
@@ -383,7 +397,7 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
     }
     const bool more = it + 1 < nit;
     const int vn = v + 1 == V ? 0 : v + 1;
-    const int need_n = 4 * coff[vn + 1], lim_n = 4 * coff[min(vn + V5_NB, V)];
+    const int need_n = upos(vn + 1), lim_n = upos(min(vn + nb, V));
 
     u32x4 af[2][4];
 #pragma unroll
@@ -456,7 +470,7 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
         store_s();
         __syncthreads();
         if (cc + 1 < ncc) load_s(cc + 1);
-        bpos = 4 * coff[1];
+        bpos = upos(1);
         build_heavy();
         build_range(0, bpos, true);
         ce = read_ce(bpos, lim);
@@ -565,8 +579,10 @@ static void launch_v5_sv(const KnnParams& p, int out_t, hipStream_t s) {
   const int64_t total = p.B * tiles_per_b * n_tiles_n;
   const int64_t padded = (total + 7) / 8 * 8;
   const int ncb = static_cast<int>(n_tiles_n * (V5_NT / 32));
+  const int nb = v5_tiles(static_cast<int>(p.V), p.zero_row, p.coll_off_stride, p.cent_stride, p.heavy_stride,
+                          p.hlist_stride);
   const size_t lds = v5_layout(static_cast<int>(p.V), p.zero_row, p.coll_off_stride, p.cent_stride,
-                               p.heavy_stride, p.hlist_stride).total;
+                               p.heavy_stride, p.hlist_stride, nb).total;
   // 16-byte channels-last bf16 stores: unit channel stride, rows and base 16-byte aligned
   const int vec_out = out_t == FOVI_BF16 && p.ys1 == 1 && p.ys2 % 8 == 0 && p.ys0 % 8 == 0 && p.Cout % 8 == 0 &&
                       reinterpret_cast<uintptr_t>(p.y) % 16 == 0;
@@ -596,7 +612,7 @@ int v5_applies(const KnnParams& p, int f8) {
   if (p.xs1 != 1 || p.xs2 % al != 0 || p.xs0 % al != 0 || reinterpret_cast<uintptr_t>(p.x) % 16 != 0) return 0;
   if (reinterpret_cast<uintptr_t>(p.w) % 16 != 0) return 0;
   return v5_layout(static_cast<int>(p.V), p.zero_row, p.coll_off_stride, p.cent_stride, p.heavy_stride,
-                   p.hlist_stride).total <= 160 * 1024;
+                   p.hlist_stride, V5_NB_MIN).total <= 160 * 1024;
 }
 
 template <bool F8>

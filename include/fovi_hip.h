@@ -179,7 +179,10 @@ typedef struct fovi_knnconv_args {
    *   tile_cent[(t * cent_stride + i) * 4 + 0..3], i in [tile_coll_off[t * coll_off_stride + p],
    *     tile_coll_off[t * coll_off_stride + p + 1]): one 16-byte entry per (position p, row
    *     with 2 to 6 neighbours), decreasing count within a position: word 0 = destination
-   *     ((p % 3) * 16384 + off(row), bytes) | count << 16; words 1-3 = u() of the staged
+   *     ((p % nb) * 16384 + off(row), bytes) | count << 16, nb = 4 collision tiles when the
+   *     kernel's tile layout with four fits 160 KB (64 (zero_row + 1 + heavy_stride) rounded
+   *     up to 128, + (256 nb + 1) 64 + 512 n_ref + 4 coll_off_stride + 16 cent_stride +
+   *     8 heavy_stride + 2 hlist_stride bytes), else 3; words 1-3 = u() of the staged
    *     rows of neighbours 1-6 in list order, two 16-bit halves each (the zero row past the
    *     count);
    *   tile_heavy[(t * heavy_stride + h) * 2 + 0..1]: heavy entry h (more than 6 neighbours):

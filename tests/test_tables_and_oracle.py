@@ -237,6 +237,11 @@ def test_wide_tables_decode_to_the_csr_lists(res_in, res_out, k, permute):
     if wide is None:                      # more rows than the kernel stages
         assert zr > T.WIDE_MAX_ROWS
         return
+    # collision tiles: four exactly when the four-tile layout fits, whatever the slot order
+    sizes = (t["V"], zr, wide.coll_off.shape[1], wide.stride, wide.heavy_stride, wide.hlist_stride)
+    assert T.wide_strides(direct) == sizes[2:]
+    big = T.wide_lds_bytes(*sizes, T.WIDE_TILES_MAX) <= T.WIDE_LDS_BYTES
+    assert wide.tiles == (T.WIDE_TILES_MAX if big else T.WIDE_TILES) == T.wide_tiles_of(direct)
     src, cent, coll_off = wide.src.numpy().astype(np.int64), wide.coll.numpy().view(np.uint32), wide.coll_off.numpy()
     heavy, hlist = wide.heavy.numpy().view(np.uint32), wide.hlist.numpy().view(np.uint16)
     # byte offset -> row: 64-byte rows, swizzle bits only in bits 4-5; the tables hold staged
@@ -262,7 +267,7 @@ def test_wide_tables_decode_to_the_csr_lists(res_in, res_out, k, permute):
                 w0, w1, w2, w3 = (int(x) for x in cent[tt, ei])
                 dst, cnt = w0 & 0xFFFF, (w0 >> 16) & 0xFF
                 assert w0 >> 24 == 0
-                assert dst // T.WIDE_TILE_BYTES == pos % T.WIDE_TILES
+                assert dst // T.WIDE_TILE_BYTES == pos % wide.tiles
                 row = row_of_byte[dst % T.WIDE_TILE_BYTES]
                 n = tt * 256 + row
                 assert 2 <= cnt <= T.STREAM_MAX_COUNT and cnt == (ptr[n, v] & 0xFFFF)
