@@ -354,7 +354,7 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
   __syncthreads();
   // Collision sums run as a stream over the tile's entry list (units in slot
   // order): every iteration takes the next 256 units (one per thread,
-  // straight-line code interleaved with its MFMAs) of slots up to two ahead
+  // straight-line code interleaved with its MFMAs) of slots up to nb - 1 ahead
   // of the one it consumes, so heavy and light slots even out. A chunk starts
   // with its slot 0 built; a slot not yet complete when its turn comes is
   // finished first (uniform branch). Masked units write a trash row; entries
