@@ -64,22 +64,26 @@ __device__ __forceinline__ float pool_result(const PoolAcc& s, int mode) {
 template <typename T> struct Vec16;
 template <> struct Vec16<float> {
   static constexpr int N = 4;
+  static __device__ __forceinline__ void unpack(uint4 a, float (&v)[4]) {
+    v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y);
+    v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
+  }
   static __device__ __forceinline__ void load(const float* p, float (&v)[4]) {
-    const f32x4 a = *reinterpret_cast<const f32x4*>(p);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = a[i];
+    unpack(*reinterpret_cast<const uint4*>(p), v);
   }
 };
 template <> struct Vec16<uint16_t> {
   static constexpr int N = 8;
-  static __device__ __forceinline__ void load(const uint16_t* p, float (&v)[8]) {
-    const uint4 a = *reinterpret_cast<const uint4*>(p);
+  static __device__ __forceinline__ void unpack(uint4 a, float (&v)[8]) {
     const uint32_t w[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       v[2 * i] = __uint_as_float(w[i] << 16);
       v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
     }
+  }
+  static __device__ __forceinline__ void load(const uint16_t* p, float (&v)[8]) {
+    unpack(*reinterpret_cast<const uint4*>(p), v);
   }
 };
 
@@ -157,6 +161,94 @@ __global__ __launch_bounds__(256) void knnpool_rows_kernel(PoolParams p, uint32_
   }
 }
 
+// Channels-last rows, lists of at most POOL_KF neighbours, one reduction mode: the thread
+// reads all its indices, then issues all its row loads (a pad token or a list slot past k
+// reads row 0, discarded), then reduces in list order, branch-free: two memory latencies per
+// thread instead of two per neighbour. The reduction is the one above: a NaN feature adds +0,
+// which leaves a sum that started at +0 unchanged (such a sum is never -0).
+constexpr int POOL_KF = 16;
+
+template <typename InT, typename OutT, int MODE>
+__global__ __launch_bounds__(256) void knnpool_rows_kf_kernel(PoolParams p, uint32_t groups, int vec_out,
+                                                              uint32_t blocks_per_b, int64_t total_blocks,
+                                                              int64_t padded_blocks) {
+  constexpr int NV = Vec16<InT>::N;
+  const int64_t tile = xcd_tile(blockIdx.x, padded_blocks);
+  if (tile >= total_blocks) return;
+  const uint32_t t = static_cast<uint32_t>(tile % blocks_per_b) * 256u + threadIdx.x;
+  if (t >= static_cast<uint32_t>(p.Nout) * groups) return;
+  const uint32_t g = t % groups, n = t / groups;
+  const int64_t b = tile / blocks_per_b;
+  const InT* xb = static_cast<const InT*>(p.x) + b * p.xs0 + g * NV;
+  const int K = static_cast<int>(p.K);
+  const int32_t* nb = p.nbr + static_cast<int64_t>(n) * K;
+  const float* wn = MODE == FOVI_POOL_GAUSSIAN ? p.w + static_cast<int64_t>(n) * K : nullptr;
+  const int32_t nin = static_cast<int32_t>(p.Nin);
+  int32_t idx[POOL_KF];
+  float w[POOL_KF];
+#pragma unroll
+  for (int j = 0; j < POOL_KF; ++j) {
+    idx[j] = j < K ? nb[j] : -1;
+    w[j] = MODE == FOVI_POOL_GAUSSIAN && j < K ? wn[j] : 0.0f;
+  }
+  uint4 raw[POOL_KF];
+#pragma unroll
+  for (int j = 0; j < POOL_KF; ++j) {
+    const bool ok = idx[j] >= 0 && idx[j] < nin;
+    if (j < K) raw[j] = *reinterpret_cast<const uint4*>(xb + static_cast<int64_t>(ok ? idx[j] : 0) * p.xs2);
+  }
+  float a[NV], c[NV];
+#pragma unroll
+  for (int q = 0; q < NV; ++q) {
+    a[q] = MODE == FOVI_POOL_MAX ? -__builtin_inff() : 0.0f;
+    c[q] = 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < POOL_KF; ++j) {
+    if (j < K) {
+      const bool ok = idx[j] >= 0 && idx[j] < nin;
+      float v[NV];
+      Vec16<InT>::unpack(raw[j], v);
+#pragma unroll
+      for (int q = 0; q < NV; ++q) {
+        const bool use = ok && v[q] == v[q];
+        if (MODE == FOVI_POOL_MAX) a[q] = fmaxf(a[q], use ? v[q] : -__builtin_inff());
+        else if (MODE == FOVI_POOL_GAUSSIAN) a[q] += use ? w[j] : 0.0f;
+        else a[q] += use ? v[q] : 0.0f;
+        if (MODE == FOVI_POOL_AVG) c[q] += use ? 1.0f : 0.0f;
+      }
+    }
+  }
+  if (MODE == FOVI_POOL_GAUSSIAN) {
+#pragma unroll
+    for (int j = 0; j < POOL_KF; ++j) {
+      if (j < K) {
+        const bool ok = idx[j] >= 0 && idx[j] < nin;
+        float v[NV];
+        Vec16<InT>::unpack(raw[j], v);
+#pragma unroll
+        for (int q = 0; q < NV; ++q) {
+          const float t = v[q] * (w[j] / (a[q] + 1e-8f));
+          c[q] += ok && v[q] == v[q] ? t : 0.0f;
+        }
+      }
+    }
+  }
+  OutT* yo = static_cast<OutT*>(p.y) + b * p.ys0 + static_cast<int64_t>(n) * p.ys2 + g * NV * p.ys1;
+  float o[NV];
+#pragma unroll
+  for (int q = 0; q < NV; ++q) {
+    PoolAcc s{a[q], c[q]};
+    o[q] = pool_result(s, MODE);
+  }
+  if (vec_out) {
+    Vec16Out<OutT, NV>::store(yo, o);
+  } else {
+#pragma unroll
+    for (int q = 0; q < NV; ++q) Elem<OutT>::store(yo + q * p.ys1, o[q]);
+  }
+}
+
 // any strides: thread = (b, n, c)
 template <typename InT, typename OutT>
 __global__ __launch_bounds__(256) void knnpool_any_kernel(PoolParams p, int64_t total) {
@@ -198,6 +290,19 @@ static void launch_pool(const PoolParams& p, hipStream_t s) {
     // whole channel groups to unit-stride, 16-byte aligned output rows
     const int vec_out = p.ys1 == 1 && (p.ys2 * sizeof(OutT)) % 16 == 0 && (p.ys0 * sizeof(OutT)) % 16 == 0 &&
                         (NV * sizeof(OutT)) % 16 == 0 && reinterpret_cast<uintptr_t>(p.y) % 16 == 0;
+    if (p.K <= POOL_KF) {
+      const auto args = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, p, static_cast<uint32_t>(groups), vec_out,
+                           static_cast<uint32_t>(blocks_per_b), total_blocks, padded);
+      };
+      switch (p.mode) {
+        case FOVI_POOL_MAX: args(knnpool_rows_kf_kernel<InT, OutT, FOVI_POOL_MAX>); break;
+        case FOVI_POOL_AVG: args(knnpool_rows_kf_kernel<InT, OutT, FOVI_POOL_AVG>); break;
+        case FOVI_POOL_SUM: args(knnpool_rows_kf_kernel<InT, OutT, FOVI_POOL_SUM>); break;
+        default: args(knnpool_rows_kf_kernel<InT, OutT, FOVI_POOL_GAUSSIAN>); break;
+      }
+      return;
+    }
     hipLaunchKernelGGL((knnpool_rows_kernel<InT, OutT>), grid, dim3(256), 0, s, p, static_cast<uint32_t>(groups),
                        vec_out, static_cast<uint32_t>(blocks_per_b), total_blocks, padded);
     return;

@@ -104,10 +104,11 @@ def _pool_args(x, nbr_rows, weights, n_out, k, mode, y):
 @pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("channels_last", [True, False])
-def test_knnpool_layer_vs_oracle(mode, dt, channels_last):
+@pytest.mark.parametrize("k", [9, 25])     # channels-last: k <= 16 gathers every row first, k = 25 loops
+def test_knnpool_layer_vs_oracle(mode, dt, channels_last, k):
     ci = SamplingCoords(16, 2.78, 32, style="logpolar")
     co = SamplingCoords(16, 2.78, 16, style="logpolar")
-    layer = KNNPoolingLayer(9, ci, co, mode=mode, device="cuda", gauss_sigma=3.0)
+    layer = KNNPoolingLayer(k, ci, co, mode=mode, device="cuda", gauss_sigma=3.0)
     x = torch.randn(3, 64, 1024, generator=torch.Generator().manual_seed(4)).to(dt)
     x[1, 5, 100:140] = float("nan")                                   # NaN features are skipped
     xd = x.cuda()
