@@ -46,6 +46,23 @@ def test_quantize_matches_torch_cast(dt, layout, headroom):
     assert torch.equal(q.data.cpu().view(torch.uint8), want.view(torch.uint8))
 
 
+def test_quantize_amax_of_a_large_tensor():
+    """A tensor large enough (36M elements) for several trips of the amax kernel's
+    four-pieces-per-trip loop: the scale equals torch's amax * headroom / 448 bit for bit with
+    the largest |x| planted in that loop's range, and a NaN there makes it NaN."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(64, 256, 2200, generator=g).bfloat16()
+    x[31, 100, 1234] = -77.5                          # element 17,680,434: inside the unrolled trips
+    xd = x.cuda()
+    q = quantize_e4m3(xd, 32.0)
+    s = x.float().abs().amax() * 32.0 / 448.0
+    assert q.scale.cpu().view(torch.int32).item() == s.view(torch.int32).item()
+    want = (x[31].float() / s).to(torch.float8_e4m3fn)
+    assert torch.equal(q.data[31].cpu().view(torch.uint8), want.view(torch.uint8))
+    xd[40, 7, 999] = float("nan")
+    assert torch.isnan(quantize_e4m3(xd, 32.0).scale.cpu()).item()
+
+
 def test_quantize_given_scale_saturates_and_zero_tensor():
     x = torch.tensor([[[0.0, 1.0, -1.0, 500.0, -1e4, 0.017]]]).cuda()
     scale = torch.tensor([0.5], device="cuda")
