@@ -196,8 +196,18 @@ __global__ __launch_bounds__(256) void knnconv_dw_reduce_kernel(DwParams p, floa
     const int64_t in_tile = (o % DW_T) * DW_T + c % DW_T;
     const int64_t stride = p.V * p.tiles_o * p.tiles_c * (DW_T * DW_T);   // next (group, chunk)
     const float* src = p.part + (v * p.tiles_o * p.tiles_c + tile) * (DW_T * DW_T) + in_tile;
+    // partials added in (group, chunk) order; four loads in flight per trip
     float sum = 0.0f;
-    for (int64_t sq = 0; sq < p.S * p.NQ; ++sq) sum += src[sq * stride];
+    const int64_t n = p.S * p.NQ;
+    int64_t sq = 0;
+    for (; sq + 4 <= n; sq += 4) {
+      float t[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) t[u] = src[(sq + u) * stride];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) sum += t[u];
+    }
+    for (; sq < n; ++sq) sum += src[sq * stride];
     dw[o * p.C * p.V + c * p.V + v] = sum;
   }
 }
