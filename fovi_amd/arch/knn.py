@@ -204,18 +204,114 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         knn_indices, knn_distances = self._compute_knns(batch_size)
         self._setup(knn_indices, knn_distances, bias)
 
-    def _setup(self, knn_indices, knn_distances, bias, param_device=None):
+    @classmethod
+    def from_tables(cls, in_channels, out_channels, in_coords, out_coords, knn_indices, local_rf=None,
+                    slots=None, device="cuda", arch_flag="", sample_cortex=True, bias=False,
+                    ref_frame_side_length=None, ref_coords=None, ref_grid_size=None, batch_size=None):
+        """A kernel-backed layer on neighbour and ref-slot tables computed elsewhere, such as
+        a reference layer's geodesic ones (``knn.py:59-99``, pygeodesic), which this package
+        does not compute.
+
+        ``knn_indices [k, N_out]``: input indices per output point; entries >= N_in (the pad
+        ring) and < 0 (the -1 padding of a partition, ``knnvit.py:194-198``) carry no input.
+        The slots come as the reference's one-hot ``local_rf [N_out, k, V]`` or as indices
+        ``slots [N_out, k]``. The ref grid is ``ref_coords [V, 2]`` when given, else the one
+        ``compute_reference_coords`` builds from k, ``arch_flag`` and
+        ``ref_frame_side_length``. Parameters are initialised as the constructor does."""
+        _check_coords(in_coords, "in_coords")
+        _check_coords(out_coords, "out_coords")
+        knn_indices = torch.as_tensor(knn_indices).detach().cpu()
+        if knn_indices.dim() != 2 or knn_indices.dtype.is_floating_point or knn_indices.dtype == torch.bool:
+            raise ValueError(f"knn_indices must be an integer [k, N_out] table, got {tuple(knn_indices.shape)} "
+                             f"{knn_indices.dtype}")
+        knn_indices = knn_indices.to(torch.int64)
+        k, n_out = knn_indices.shape
+        if n_out != out_coords.shape[0]:
+            raise ValueError(f"knn_indices has {n_out} columns for {out_coords.shape[0]} output points")
+        n_in = in_coords.shape[0]
+        n_pad = _pad_coords(in_coords).shape[0]
+        if knn_indices.numel() and int(knn_indices.max()) >= n_in + max(n_pad, 1):
+            raise ValueError(f"knn_indices reaches {int(knn_indices.max())}, beyond the {n_in} points and "
+                             f"{n_pad} pad points of in_coords")
+        self = cls.__new__(cls)
+        nn.Module.__init__(self)
+        self.in_channels, self.out_channels = in_channels, out_channels
+        self.in_coords, self.out_coords = in_coords, out_coords
+        self.device, self.arch_flag, self.sample_cortex = device, arch_flag, sample_cortex
+        self.ref_frame_side_length, self.batch_size = ref_frame_side_length, batch_size
+        self.k = torch.tensor(k)
+        self._k = k
+        if ref_coords is not None:
+            ref_coords = torch.as_tensor(ref_coords).detach()
+            if ref_coords.dim() != 2:
+                raise ValueError(f"ref_coords must be [V, 2], got {tuple(ref_coords.shape)}")
+        else:
+            self.compute_reference_coords(arch_flag)
+            ref_coords, ref_grid_size = self.ref_coords, self.ref_grid_size
+        n_ref = ref_coords.shape[0]
+        if (local_rf is None) == (slots is None):
+            raise ValueError("give exactly one of local_rf (one-hot [N_out, k, V]) and slots ([N_out, k])")
+        if local_rf is not None:
+            rf = torch.as_tensor(local_rf).detach().cpu()
+            if tuple(rf.shape) != (n_out, k, n_ref):
+                raise ValueError(f"local_rf must be [N_out, k, V] = {(n_out, k, n_ref)}, got {tuple(rf.shape)}")
+            if not (((rf == 0) | (rf == 1)).all() and (rf.sum(2) == 1).all()):
+                raise ValueError("local_rf must be one-hot over its last axis (one ref slot per neighbour)")
+            slots = rf.argmax(2)
+        slots = torch.as_tensor(slots).detach().cpu().to(torch.int64)
+        if tuple(slots.shape) != (n_out, k):
+            raise ValueError(f"slots must be [N_out, k] = {(n_out, k)}, got {tuple(slots.shape)}")
+        if slots.numel() and (int(slots.min()) < 0 or int(slots.max()) >= n_ref):
+            raise ValueError(f"slots must index the {n_ref} ref points")
+        self._setup(knn_indices, None, bias, param_device="cpu", slots=slots, ref_coords=ref_coords,
+                    ref_grid_size=ref_grid_size)
+        return self
+
+    @classmethod
+    def from_reference(cls, layer, device=None):
+        """The kernel-backed twin of a reference ``KNNConvLayer`` (or patch embedding) ``layer``:
+        its coords objects, neighbour table, one-hot ``local_rf``, ref grid, flags, ``weight``
+        and ``bias`` (copied), and ``transposed`` where it has one (``knnvit.py:17-290``).
+        This is how a layer whose tables this package cannot compute (geodesic neighbourhoods)
+        runs on the kernels; ``device`` defaults to the reference layer's."""
+        dev = getattr(layer, "device", "cuda") if device is None else device
+        new = cls.from_tables(layer.in_channels, layer.out_channels, layer.in_coords, layer.out_coords,
+                              layer.knn_indices, local_rf=layer.local_rf, device=dev,
+                              arch_flag=getattr(layer, "arch_flag", ""),
+                              sample_cortex=getattr(layer, "sample_cortex", True), bias=layer.bias is not None,
+                              ref_frame_side_length=getattr(layer, "ref_frame_side_length", None),
+                              ref_coords=layer.ref_coords, ref_grid_size=getattr(layer, "ref_grid_size", None),
+                              batch_size=getattr(layer, "batch_size", None))
+        if tuple(layer.weight.shape) != tuple(new.weight.shape):
+            raise ValueError(f"reference weight {tuple(layer.weight.shape)} != {tuple(new.weight.shape)}")
+        with torch.no_grad():
+            new.weight.copy_(layer.weight.detach())
+            if new.bias is not None:
+                new.bias.copy_(layer.bias.detach())
+        for attr in ("transposed", "knn_pad_index_token_val", "knn_pad_token_val"):
+            if hasattr(layer, attr):
+                setattr(new, attr, getattr(layer, attr))
+        return new
+
+    def _setup(self, knn_indices, knn_distances, bias, param_device=None, slots=None, ref_coords=None,
+               ref_grid_size=None):
         """Pad tokens, ref grid, parameters (created on ``param_device``, default the layer's
         device, then moved there), ref slots and device tables of a neighbour table
         ``[k, N_out]`` whose entries >= N_in (pad ring) or < 0 (padding of a partition) carry
-        no input (reference ``knn.py:445-471``)."""
+        no input (reference ``knn.py:445-471``). Given ``slots [N_out, k]`` (and the ref grid
+        ``ref_coords [V, 2]`` they index), those are used instead of computed."""
         n_in, device = self.in_coords.shape[0], self.device
         self.knn_indices_pad_mask = (knn_indices >= n_in) | (knn_indices < 0)
         pad_token = knn_indices.clone()
         pad_token[self.knn_indices_pad_mask] = n_in
         self.knn_indices_batch_cache = pad_token
 
-        self.compute_reference_coords(self.arch_flag)
+        if ref_coords is None:
+            self.compute_reference_coords(self.arch_flag)
+        else:
+            self.ref_coords = ref_coords.to(device)
+            self.ref_grid_size = (int(ref_grid_size) if ref_grid_size is not None
+                                  else int(round(ref_coords.shape[0] ** 0.5)))
         n_ref = self.ref_coords.shape[0]
         pdev = device if param_device is None else param_device
         self.weight = nn.Parameter(torch.empty(self.out_channels, self.in_channels * n_ref, device=pdev))
@@ -229,7 +325,7 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
             if self.bias is not None:
                 self.bias.data = self.bias.data.to(device)
 
-        self.slots = self.compute_local_rf_slots(knn_indices)
+        self.slots = self.compute_local_rf_slots(knn_indices) if slots is None else slots
         self.knn_indices = knn_indices.to(device)
         self.knn_distances = None if knn_distances is None else knn_distances.to(device)
         self.knn_indices_pad_token = pad_token.to(device)
@@ -305,13 +401,14 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
             nn.init.zeros_(self.bias)
 
     def compute_reference_coords(self, arch_flag):
-        """Square ref grid of side ``ref_frame_side_length`` or ceil(sqrt(k)) (``knn.py:559-597``)."""
+        """Square ref grid of side ``ref_frame_side_length`` or ceil(sqrt(k)), doubled for a
+        flag containing 'doubleres' (``knn.py:559-597``). Of the flags its docstring names only
+        'doubleres' changes the grid there: 'fovref' and 'circref' give the square grid, here
+        as in the reference."""
         if self.ref_frame_side_length is not None:
             assert not len(arch_flag), "self.ref_frame_side_length is incompatible with use of arch_flag"
             ref, side = T.reference_grid(self._k, side_length=self.ref_frame_side_length)
         else:
-            if "fovref" in arch_flag or "circref" in arch_flag:
-                raise NotImplementedError(f"arch_flag {arch_flag!r}: only square ref grids are built")
             ref, side = T.reference_grid(self._k, doubleres="doubleres" in arch_flag)
         self.ref_grid_size = side
         self.ref_coords = ref.to(self.device, dtype=getattr(self.in_coords, "dtype", torch.float32))

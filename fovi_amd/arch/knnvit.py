@@ -9,8 +9,10 @@ gives every input point to its nearest token centre and pads the groups with
 index -1 to the largest; ``KNNPartitioningPatchEmbedding``
 (``knnvit.py:224-290``) takes k = the most points any centre has nearer than the
 farthest point of its group. Both run the same kernels as any kNN-conv layer
-(pad and -1 entries carry no input) and need Euclidean distances: the
-reference's default ``sample_cortex='geodesic'`` needs pygeodesic and raises.
+(pad and -1 entries carry no input). Their constructors compute Euclidean
+distances; the reference's default ``sample_cortex='geodesic'`` needs pygeodesic
+and raises here. ``from_reference`` (or ``from_tables``) instead runs a layer the
+reference built, geodesic tables included, on the kernels.
 """
 from __future__ import annotations
 
@@ -38,6 +40,9 @@ def _partition(distances, n_in, n_out, allow_empty=False):
 
 
 class KNNPatchEmbedding(KNNConvLayer):
+    # [B, C, N] tokens when set, else [B, N, C] (reference ``knnvit.py:86-95``)
+    transposed = False
+
     def __init__(self, in_channels, embed_dim, in_res, fov, cmf_a, style="isotropic",
                  auto_match_cart_resources=True, in_cart_res=224, cart_patch_size=16, patch_overlap_factor=1,
                  device="cuda", force_patches_less_than_matched=True, new_parameterization=False,

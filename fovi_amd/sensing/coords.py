@@ -31,8 +31,6 @@ so a seeded run builds the reference's sensor.
 """
 from __future__ import annotations
 
-import math
-
 import numpy as np
 import torch
 
@@ -42,6 +40,7 @@ __all__ = [
     "num_sampling_coords",
     "logpolar_ring_radii",
     "xy_to_colrow",
+    "xy_to_rowcol",
     "auto_match_num_coords",
 ]
 
@@ -89,21 +88,15 @@ def isotropic_ring_counts(fov, cmf_a, res):
 
 
 def _ring_points(radii, counts):
-    """fp64 cartesian and polar point sets, ring-major, ``counts[i]`` angles on ring i."""
-    n = int(sum(counts))
-    cart = np.empty((n, 2), dtype=np.float64)
-    polar = np.empty((n, 2), dtype=np.float64)
-    at = 0
-    for r32, cnt in zip(radii.tolist(), counts):
-        # r32 is the exact fp32 radius widened to a Python float (IEEE double)
-        angles = np.linspace(0, 2 * np.pi, cnt, endpoint=False)
-        row = slice(at, at + cnt)
-        cart[row, 0] = [r32 * math.cos(a) for a in angles]
-        cart[row, 1] = [r32 * math.sin(a) for a in angles]
-        polar[row, 0] = r32
-        polar[row, 1] = angles
-        at += cnt
-    return torch.from_numpy(cart), torch.from_numpy(polar)
+    """fp64 cartesian and polar point sets, ring-major, ``counts[i]`` angles on ring i.
+
+    Each point is the exact fp32 radius times torch's fp64 cosine and sine of the numpy
+    angle, the reference's arithmetic (``coords.py:270-278``); libm's ``math.sin`` differs
+    from torch's in the last bit of a few angles, which the fp64 ``cartesian_rowcol`` keeps."""
+    rad = torch.cat([torch.full((cnt,), r32, dtype=torch.float64) for r32, cnt in zip(radii.tolist(), counts)])
+    ang = torch.cat([torch.from_numpy(np.linspace(0, 2 * np.pi, cnt, endpoint=False)) for cnt in counts])
+    cart = torch.stack([rad * torch.cos(ang), rad * torch.sin(ang)], dim=1)
+    return cart, torch.stack([rad, ang], dim=1)
 
 
 def _logpolar_points(fov, cmf_a, res, max_val):
@@ -315,6 +308,13 @@ def xy_to_colrow(xy):
     return torch.stack((xy[:, 0], -xy[:, 1]), dim=1)
 
 
+def xy_to_rowcol(xy):
+    """(x, y) in [-1,1] -> image (row, col) = (-y, x) in [-1,1], the reference's
+    ``xy_to_rowcol(coords, do_norm=False, format='-11')`` (``coords.py:522-548``): no
+    normalisation, the input's dtype and device."""
+    return torch.stack((-xy[:, 1], xy[:, 0]), dim=1)
+
+
 class SamplingCoords:
     """Sensor point set with cartesian, polar and cortical coordinates.
 
@@ -323,7 +323,8 @@ class SamplingCoords:
     [-1,1], ``polar [N,2]`` (radius, angle), ``cortical`` (log-polar: ``[N,2]``
     normalised to [0,1] per column; isotropic: ``[N,3]`` on the cortical manifold;
     uniform: None), ``plotting``, ``cartesian_pad_coords [P,2]`` (the pad ring),
-    ``cortical_pad_coords [P,3]`` (isotropic), ``shape``, ``resolution``, ``style``.
+    ``cortical_pad_coords [P,3]`` (isotropic), ``cartesian_rowcol [N,2]`` (image row, col
+    = (-y, x) before the cast to ``dtype``), ``shape``, ``resolution``, ``style``.
     Points are ring-major: log-polar index ``ring * res + angle``; isotropic rings
     hold ``isotropic_ring_counts`` points each.
     """
@@ -364,6 +365,11 @@ class SamplingCoords:
                 device=device, dtype=dtype)
         else:
             raise ValueError(f"Style {style} not recognized")
+        if res != 1:
+            # image (row, col) of the points before the cast to ``dtype`` (fp64 for the ring
+            # styles, fp32 for 'uniform'), as the reference sets it (``coords.py:41-42``); the
+            # DINOv3 adapter's RoPE reads it (``dinov3.py:97``). A one-point sensor has none.
+            self.cartesian_rowcol = xy_to_rowcol(cart).to(device=device)
         self.cartesian = cart.to(device=device, dtype=dtype)
         self.polar = polar.to(device=device, dtype=dtype)
         self.cortical = None if cortical is None else cortical.to(device=device, dtype=dtype)

@@ -6,6 +6,7 @@ Run only in the build container, where the reference checkout exists:
 
     python tests/golden/make_golden.py               # tables.npz (log-polar layers)
     python tests/golden/make_golden.py --isotropic   # isotropic.npz (isotropic sensor)
+    python tests/golden/make_golden.py --dinov3      # dinov3.npz (the DINOv3 adapter's patch embeddings)
 
 The reference is loaded by file path under a synthetic package name; the two
 modules it imports that are absent here and unused on this path (trimesh in
@@ -194,8 +195,54 @@ def main_isotropic():
     print(f"wrote {ISO_OUT} ({os.path.getsize(ISO_OUT) / 1024:.0f} KiB)")
 
 
+# the DINOv3 adapter's patch embedding as config/fovi-dinov3.yaml and
+# config/pretrained_model/dinov3_lora_layers-1012345.yaml configure it (fovi/arch/dinov3.py:50-91):
+# 64-pixel isotropic sensor, fov 16, cmf_a 2.785765, 8-pixel patches, 16x16 ref grid (the
+# backbone's patch size), ViT-S width 384, bias, transposed tokens. sample_cortex is True
+# (Euclidean cortical distances): the shipped 'geodesic' needs pygeodesic, absent here.
+DINOV3_ARGS = dict(in_channels=3, embed_dim=384, in_res=64, fov=16.0, cmf_a=2.785765, style="isotropic",
+                   auto_match_cart_resources=True, in_cart_res=64, max_coord_val="auto", device="cpu",
+                   arch_flag="", sample_cortex=True, force_patches_less_than_matched=False,
+                   ref_frame_side_length=16, transposed=True, bias=True, cart_patch_size=8)
+DINOV3_OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "dinov3.npz")
+
+
+def main_dinov3():
+    """Writes tests/golden/dinov3.npz: the sensors' ``cartesian_rowcol`` (coords.py:41-42, the
+    RoPE positions of dinov3.py:97, kept in the dtype the reference leaves them in) and the
+    tables of the adapter's patch embeddings in the shipped configuration ('KNN' partitioning
+    patches, knnvit.py:224-290, and the plain partitioning, knnvit.py:102-220)."""
+    coords_mod, knn_mod = load_reference()
+    _load("fovi_ref.arch.vit", os.path.join(REF, "arch", "vit.py"), None)
+    vit_mod = _load("fovi_ref.arch.knnvit", os.path.join(REF, "arch", "knnvit.py"), None)
+    out = {"torch_version": np.array(torch.__version__)}
+    for style, res in (("logpolar", 16), ("isotropic", 16), ("uniform", 8)):
+        c = coords_mod.SamplingCoords(16, 2.78, res, device="cpu", style=style)
+        out[f"rowcol_{style}{res}"] = c.cartesian_rowcol.numpy()
+        print(f"{style} {res}: cartesian_rowcol {tuple(c.cartesian_rowcol.shape)} {c.cartesian_rowcol.dtype}",
+              flush=True)
+    for name, cls in (("dino_kpart", "KNNPartitioningPatchEmbedding"), ("dino_part", "PartitioningPatchEmbedding")):
+        torch.manual_seed(0)
+        layer = getattr(vit_mod, cls)(**DINOV3_ARGS)
+        rf = layer.local_rf.numpy()
+        assert np.all(rf.sum(2) == 1)
+        out[f"{name}__k"] = np.array(int(layer._k))
+        out[f"{name}__idx"] = layer.knn_indices.numpy().astype(np.int16)
+        out[f"{name}__slots"] = rf.argmax(2).astype(np.uint16)
+        out[f"{name}__ref_coords"] = layer.ref_coords.numpy()
+        out[f"{name}__resolutions"] = np.array([layer.in_coords.resolution, layer.out_coords.resolution])
+        out[f"{name}__in_rowcol"] = layer.in_coords.cartesian_rowcol.numpy()
+        out[f"{name}__out_rowcol"] = layer.out_coords.cartesian_rowcol.numpy()
+        print(f"{name}: k={layer._k} n_in={len(layer.in_coords)} n_out={len(layer.out_coords)} "
+              f"V={rf.shape[2]}", flush=True)
+    np.savez_compressed(DINOV3_OUT, **out)
+    print(f"wrote {DINOV3_OUT} ({os.path.getsize(DINOV3_OUT) / 1024:.0f} KiB)")
+
+
 if __name__ == "__main__":
     if "--isotropic" in sys.argv:
         main_isotropic()
+    elif "--dinov3" in sys.argv:
+        main_dinov3()
     else:
         main()

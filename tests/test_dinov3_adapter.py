@@ -1,0 +1,352 @@
+"""The DINOv3 adapter's drop-in (reference ``fovi/arch/dinov3.py:50-97``).
+
+Pins, on the build container's CPU:
+* ``SamplingCoords.cartesian_rowcol`` (``coords.py:41-42``) equals the reference-written
+  vectors bit for bit, dtype included (fp64 for the ring styles, fp32 for 'uniform'); the
+  closed form (row, col) = (-y, x) is checked against the point set's own ``cartesian``,
+  so a swapped axis or a lost sign fails on its own.
+* The adapter's patch embeddings in the shipped configuration (``config/fovi-dinov3.yaml``
+  with ``pretrained_model/dinov3_lora_layers-1012345.yaml``; Euclidean cortical distances,
+  since 'geodesic' needs pygeodesic) build the reference's k, neighbour tables, ref slots,
+  ref grid and token positions (``tests/golden/dinov3.npz``).
+* ``from_reference`` / ``from_tables`` adopt tables computed elsewhere: the golden tables
+  give the same device tables as the constructed layer; malformed tables are refused.
+
+On the GPU, the integration guide's block (between its dinov3-snippet markers) runs as
+written, on a random-initialised ``transformers`` DINOv3 ViT-S/16 backbone (one layer):
+once with Euclidean distances (the drop-in computes the tables) and once with
+``sample_cortex='geodesic'``, where a stand-in of the reference's ``fovi.arch.knnvit``
+builds the layer with graph-geodesic tables (shortest paths over the Delaunay mesh of each
+token's candidate points, with 3-D manifold edge lengths) that the drop-in adopts. Each
+run checks the patch embedding against the oracle on the tables the layer holds (fp32 at
+1e-5, bf16 at 1e-2, and the fp32 weight gradient at 1e-5) and the whole backbone against
+the same backbone on the CPU with the oracle patch embedding (1e-4).
+"""
+import math
+import os
+import re
+import types
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+from scipy.sparse import csr_matrix
+from scipy.sparse.csgraph import dijkstra
+from scipy.spatial import Delaunay
+
+from fovi_amd.arch import knn_tables as T
+from fovi_amd.arch.knn import KNNConvLayer, get_in_out_coords
+from fovi_amd.arch.knnvit import KNNPartitioningPatchEmbedding, PartitioningPatchEmbedding
+from fovi_amd.sensing.coords import SamplingCoords
+from oracle import knnconv_ref
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GUIDE = os.path.join(ROOT, "INTEGRATION.md")
+GOLD = np.load(os.path.join(ROOT, "tests", "golden", "dinov3.npz"))
+
+# the patch embedding as build_fovi_dinov3 configures it (dinov3.py:70-86) under the shipped config
+DINOV3_ARGS = dict(in_channels=3, embed_dim=384, in_res=64, fov=16.0, cmf_a=2.785765, style="isotropic",
+                   auto_match_cart_resources=True, in_cart_res=64, max_coord_val="auto", arch_flag="",
+                   sample_cortex=True, force_patches_less_than_matched=False, ref_frame_side_length=16,
+                   transposed=True, bias=True, cart_patch_size=8)
+GOLD_CLASSES = {"dino_kpart": KNNPartitioningPatchEmbedding, "dino_part": PartitioningPatchEmbedding}
+
+
+def _bits(a):
+    a = np.ascontiguousarray(a.detach().cpu().numpy() if isinstance(a, torch.Tensor) else a)
+    return a.dtype, a.tobytes()
+
+
+# --- cartesian_rowcol (coords.py:41-42) ------------------------------------------------------
+
+@pytest.mark.parametrize("style,res", [("logpolar", 16), ("isotropic", 16), ("uniform", 8)])
+def test_cartesian_rowcol_matches_reference(style, res):
+    c = SamplingCoords(16, 2.78, res, style=style)
+    assert _bits(c.cartesian_rowcol) == _bits(GOLD[f"rowcol_{style}{res}"])
+    # (row, col) = (-y, x) of the same points: the fp32 cartesian is their rounding
+    rc = c.cartesian_rowcol
+    assert torch.equal(rc[:, 1].to(torch.float32), c.cartesian[:, 0])
+    assert torch.equal((-rc[:, 0]).to(torch.float32), c.cartesian[:, 1])
+    # a point right of centre (x > 0, y = 0) sits on the middle row, in the right half
+    j = int(torch.argmax(c.cartesian[:, 0]))
+    assert rc[j, 1] > 0 and abs(float(rc[j, 0])) <= abs(float(c.cartesian[j, 1])) + 1e-7
+
+
+def test_one_point_sensor_has_no_rowcol():
+    # the reference sets cartesian_rowcol only for res > 1 (coords.py:35-42)
+    assert not hasattr(SamplingCoords(16, 2.78, 1, style="isotropic"), "cartesian_rowcol")
+
+
+# --- the adapter's patch embeddings in the shipped configuration -----------------------------
+
+@pytest.mark.parametrize("name", sorted(GOLD_CLASSES))
+def test_dinov3_patch_embedding_matches_reference(name):
+    layer = GOLD_CLASSES[name](device="cpu", **DINOV3_ARGS)
+    assert layer._k == int(GOLD[f"{name}__k"]) and layer.transposed
+    assert [layer.in_coords.resolution, layer.out_coords.resolution] == GOLD[f"{name}__resolutions"].tolist()
+    assert np.array_equal(layer.knn_indices.numpy(), GOLD[f"{name}__idx"].astype(np.int64))
+    assert np.array_equal(layer.slots.numpy(), GOLD[f"{name}__slots"].astype(np.int64))
+    assert _bits(layer.ref_coords) == _bits(GOLD[f"{name}__ref_coords"])
+    assert _bits(layer.in_coords.cartesian_rowcol) == _bits(GOLD[f"{name}__in_rowcol"])
+    assert _bits(layer.out_coords.cartesian_rowcol) == _bits(GOLD[f"{name}__out_rowcol"])
+    assert layer.weight.shape == (384, 3 * 256) and layer.bias.shape == (384,)
+
+
+def _golden_reference_layer(name, layer):
+    """A stand-in of the reference layer: the constructed layer's coords and flags with the
+    reference-written tables (one-hot ``local_rf`` as the reference holds it)."""
+    V = int(GOLD[f"{name}__ref_coords"].shape[0])
+    slots = torch.from_numpy(GOLD[f"{name}__slots"].astype(np.int64))
+    g = torch.Generator().manual_seed(3)
+    return types.SimpleNamespace(
+        in_channels=3, out_channels=384, in_coords=layer.in_coords, out_coords=layer.out_coords,
+        knn_indices=torch.from_numpy(GOLD[f"{name}__idx"].astype(np.int64)),
+        local_rf=nn.functional.one_hot(slots, V).to(torch.float32),
+        ref_coords=torch.from_numpy(GOLD[f"{name}__ref_coords"]), ref_grid_size=torch.tensor(16),
+        weight=torch.randn(384, 3 * V, generator=g), bias=torch.randn(384, generator=g), arch_flag="",
+        sample_cortex="geodesic", ref_frame_side_length=16, transposed=True, device="cpu",
+        knn_pad_index_token_val=-1)
+
+
+@pytest.mark.parametrize("name", sorted(GOLD_CLASSES))
+def test_from_reference_adopts_the_reference_tables(name):
+    cls = GOLD_CLASSES[name]
+    built = cls(device="cpu", **DINOV3_ARGS)
+    ref = _golden_reference_layer(name, built)
+    got = cls.from_reference(ref, device="cpu")
+    assert type(got) is cls and got.transposed and got.sample_cortex == "geodesic"
+    assert got._k == int(GOLD[f"{name}__k"]) and got.ref_grid_size == 16
+    assert torch.equal(got.knn_indices, ref.knn_indices)
+    assert torch.equal(got.slots, ref.local_rf.argmax(2))
+    assert torch.equal(got.weight.detach(), ref.weight) and torch.equal(got.bias.detach(), ref.bias)
+    # the same tables give the same device tables as the constructed layer
+    for buf in ("slot_ptr", "nbr_sorted", "tile_lo", "tile_ent", "tile_nbr", "fc_item", "fc_xlist"):
+        a, b = getattr(got, buf), getattr(built, buf)
+        assert (a is None) == (b is None), buf
+        assert a is None or torch.equal(a, b), buf
+    # -1 (partition padding) stays padding: the lists of the padded columns are shorter
+    if name == "dino_part":
+        assert got.knn_pad_index_token_val == -1 and bool((got.knn_indices < 0).any())
+        assert torch.equal(got.knn_indices_pad_mask, got.knn_indices < 0)
+
+
+def test_from_tables_refuses_malformed_tables():
+    c = SamplingCoords(16, 2.78, 8, style="logpolar")
+    layer = KNNConvLayer(3, 8, 9, c, c, device="cpu")
+    idx, rf = layer.knn_indices, layer.local_rf
+    ok = dict(in_channels=3, out_channels=8, in_coords=c, out_coords=c, device="cpu")
+    two_hot = rf.clone()
+    two_hot[0, 0, (int(rf[0, 0].argmax()) + 1) % 9] = 1
+    bad = [
+        (dict(knn_indices=idx.float(), local_rf=rf), "integer"),
+        (dict(knn_indices=idx[:, :-1], local_rf=rf), "columns"),
+        (dict(knn_indices=idx, local_rf=rf[:, :, :4]), r"\[N_out, k, V\]"),
+        (dict(knn_indices=idx, local_rf=two_hot), "one-hot"),
+        (dict(knn_indices=idx, local_rf=rf, slots=layer.slots), "exactly one"),
+        (dict(knn_indices=idx), "exactly one"),
+        (dict(knn_indices=idx, slots=layer.slots + 9), "index the 9 ref points"),
+        (dict(knn_indices=idx + 1000, slots=layer.slots), "beyond"),
+    ]
+    for extra, msg in bad:
+        with pytest.raises(ValueError, match=msg):
+            KNNConvLayer.from_tables(**ok, **extra)
+    got = KNNConvLayer.from_tables(**ok, knn_indices=idx, slots=layer.slots)
+    assert torch.equal(got.slot_ptr, layer.slot_ptr) and torch.equal(got.ref_coords, layer.ref_coords)
+
+
+@pytest.mark.parametrize("flag", ["fovref", "circref", "circref_fovref"])
+def test_fovref_and_circref_give_the_square_grid(flag):
+    # compute_reference_coords acts only on 'doubleres' (knn.py:578-595)
+    c = SamplingCoords(16, 2.78, 8, style="logpolar")
+    plain = KNNConvLayer(3, 8, 9, c, c, device="cpu")
+    flagged = KNNConvLayer(3, 8, 9, c, c, device="cpu", arch_flag=flag)
+    assert torch.equal(flagged.ref_coords, plain.ref_coords) and flagged.ref_grid_size == 3
+    assert torch.equal(flagged.slots, plain.slots)
+    double = KNNConvLayer(3, 8, 9, c, c, device="cpu", arch_flag=flag + "_doubleres")
+    assert double.ref_grid_size == 6 and double.ref_coords.shape == (36, 2)
+
+
+# --- the integration guide's block ---------------------------------------------------------
+
+def _dinov3_snippet():
+    text = open(GUIDE).read()
+    m = re.search(r"<!-- dinov3-snippet -->\s*```python\n(.*?)```\s*<!-- /dinov3-snippet -->", text, re.S)
+    assert m, f"{GUIDE} lost its dinov3 snippet"
+    return m.group(1)
+
+
+class FoviDinoV3RoPE(nn.Module):
+    """Stand-in of the reference's RoPE over sensor token positions (``knnvit.py:420-465``):
+    angles 2*pi * coords x inv_freq, flattened and tiled, cos and sin in the input's dtype."""
+
+    def __init__(self, base, head_dim, coords, device="cuda"):
+        super().__init__()
+        self.coords = coords
+        inv_freq = 1 / base ** torch.arange(0, 1, 4 / head_dim, dtype=torch.float32, device=device)
+        self.register_buffer("inv_freq", inv_freq, persistent=False)
+
+    def forward(self, pixel_values):
+        angles = 2 * math.pi * self.coords[:, :, None] * self.inv_freq[None, None, :]
+        angles = angles.flatten(1, 2).tile(2)
+        return torch.cos(angles).to(pixel_values.dtype), torch.sin(angles).to(pixel_values.dtype)
+
+
+def _graph_geodesic_knn(in_c, out_c, k, m=4):
+    """k nearest inputs (pad ring included) of each output by shortest paths over the Delaunay
+    mesh of its m*k Euclidean-nearest candidates, edge lengths on the 3-D manifold, from the
+    nearest candidate (the shape of the reference's geodesic search, ``knn.py:59-99``)."""
+    src = torch.cat([in_c.cortical, in_c.cortical_pad_coords]).cpu().double().numpy()
+    cart = torch.cat([in_c.cartesian, in_c.cartesian_pad_coords]).cpu().double().numpy()
+    out = out_c.cortical.cpu().double().numpy()
+    n_cand = min(k * m, in_c.shape[0])
+    idx = np.empty((k, out.shape[0]), dtype=np.int64)
+    for i in range(out.shape[0]):
+        cand = np.argsort(np.linalg.norm(src - out[i], axis=1), kind="stable")[:n_cand]
+        tri = Delaunay(cart[cand])
+        e = np.concatenate([tri.simplices[:, [0, 1]], tri.simplices[:, [1, 2]], tri.simplices[:, [0, 2]]])
+        e = np.unique(np.sort(e, axis=1), axis=0)
+        w = np.linalg.norm(src[cand[e[:, 0]]] - src[cand[e[:, 1]]], axis=1)
+        g = csr_matrix((w, (e[:, 0], e[:, 1])), shape=(n_cand, n_cand))
+        d = dijkstra(g, directed=False, indices=0)
+        idx[:, i] = cand[np.argsort(d, kind="stable")[:k]]
+    return torch.from_numpy(idx)
+
+
+class _GeodesicPatchEmbedding:
+    """Stand-in of the reference's ``KNNPartitioningPatchEmbedding`` under
+    ``sample_cortex='geodesic'``: the reference's coords, graph-geodesic neighbours, ref slots
+    by the reference's recipe (``knn.py:599-647``), seeded parameters."""
+
+    def __init__(self, in_channels, embed_dim, in_res, fov, cmf_a, style, auto_match_cart_resources, in_cart_res,
+                 cart_patch_size, device, force_patches_less_than_matched, transposed, max_coord_val, sample_cortex,
+                 arch_flag, ref_frame_side_length, bias):
+        assert sample_cortex == "geodesic"
+        in_c, out_c, _ = get_in_out_coords(in_res, fov, cmf_a, cart_patch_size, style=style,
+                                           auto_match_cart_resources=auto_match_cart_resources,
+                                           in_cart_res=in_cart_res, device=device,
+                                           force_out_match_less_than=force_patches_less_than_matched,
+                                           max_out_coord_val=max_coord_val)
+        k = int(GOLD["dino_kpart__k"])
+        self.knn_indices = _graph_geodesic_knn(in_c, out_c, k)
+        ref, side = T.reference_grid(k, side_length=ref_frame_side_length)
+        src = torch.cat([in_c.cortical, in_c.cortical_pad_coords]).cpu()
+        src_cart = torch.cat([in_c.cartesian, in_c.cartesian_pad_coords]).cpu()
+        slots = T.local_rf_slots(self.knn_indices, src, src_cart, out_c.cortical.cpu(), out_c.cartesian.cpu(), ref)
+        self.local_rf = nn.functional.one_hot(slots, ref.shape[0]).to(torch.float32)
+        g = torch.Generator().manual_seed(5)
+        self.weight = nn.Parameter(torch.randn(embed_dim, in_channels * ref.shape[0], generator=g) / 40)
+        self.bias = nn.Parameter(torch.randn(embed_dim, generator=g)) if bias else None
+        self.in_channels, self.out_channels, self.in_coords, self.out_coords = in_channels, embed_dim, in_c, out_c
+        self.ref_coords, self.ref_grid_size, self.arch_flag = ref, side, arch_flag
+        self.sample_cortex, self.ref_frame_side_length, self.transposed = sample_cortex, ref_frame_side_length, transposed
+        self.device, self.k, self._k = device, torch.tensor(k), k
+
+
+def _reference_knnvit():
+    mod = types.ModuleType("fovi.arch.knnvit")
+    mod.FoviDinoV3RoPE = FoviDinoV3RoPE
+    mod.KNNPartitioningPatchEmbedding = _GeodesicPatchEmbedding
+    return mod
+
+
+def _config(sample_cortex):
+    ns = types.SimpleNamespace
+    vit = ns(partitioning_patches="KNN", patch_size=8, patch_overlap_factor=None, new_parameterization=None,
+             force_patches_less_than_matched=False)
+    saccades = ns(resize_size=64, fov=16.0, cmf_a=2.785765, mode="isotropic", sample_cortex=sample_cortex)
+    return ns(model=ns(vit=vit), saccades=saccades, pretrained_model=ns(patch_size=16, use_patch_weights=1))
+
+
+def _backbone(device):
+    """DINOv3 ViT-S/16 (hidden 384, 6 heads, 16-pixel patches, 4 register tokens), one
+    layer, random-initialised from a seed: no download."""
+    from transformers import DINOv3ViTConfig, DINOv3ViTModel
+    torch.manual_seed(0)
+    return DINOv3ViTModel(DINOv3ViTConfig(num_hidden_layers=1)).eval().to(device)
+
+
+def _run_snippet(sample_cortex, device):
+    model = _backbone(device)
+    conv = model.embeddings.patch_embeddings
+    conv_w, conv_b = conv.weight.detach().cpu().clone(), conv.bias.detach().cpu().clone()
+    env = {"cfg": _config(sample_cortex), "model": model, "device": device, "ref_knnvit": _reference_knnvit()}
+    exec(compile(_dinov3_snippet(), GUIDE, "exec"), env)
+    return env, conv_w, conv_b
+
+
+@pytest.mark.parametrize("sample_cortex", [True, "geodesic"])
+def test_dinov3_snippet_builds_the_adapter(sample_cortex):
+    env, conv_w, conv_b = _run_snippet(sample_cortex, "cpu")
+    model = env["model"]
+    pe = model.embeddings.patch_embeddings
+    assert type(pe) is KNNPartitioningPatchEmbedding and pe.transposed and pe._k == int(GOLD["dino_kpart__k"])
+    # the backbone's 16x16 Conv2d taps land on the 16x16 ref grid: (row, col) -> (x, y) (knn.py:656)
+    want = conv_w.transpose(-1, -2).flip(-1).reshape(384, -1)
+    assert torch.equal(pe.weight.detach(), want) and torch.equal(pe.bias.detach(), conv_b)
+    rope = model.rope_embeddings
+    assert rope.coords is pe.out_coords.cartesian_rowcol and rope.coords.dtype == torch.float64
+    assert model.total_embed_dim == 384 * pe.out_coords.shape[0]
+    if sample_cortex == "geodesic":
+        euclid = KNNPartitioningPatchEmbedding(device="cpu", **DINOV3_ARGS)
+        assert pe.sample_cortex == "geodesic"
+        assert not torch.equal(pe.knn_indices, euclid.knn_indices)   # the adopted tables are foreign ones
+    else:
+        assert np.array_equal(pe.knn_indices.numpy(), GOLD["dino_kpart__idx"].astype(np.int64))
+
+
+class _OraclePatchEmbedding(nn.Module):
+    """The oracle forward on a layer's tables, as a module the backbone can call."""
+
+    def __init__(self, layer):
+        super().__init__()
+        self.weight = nn.Parameter(layer.weight.detach().cpu().clone())
+        self.bias = nn.Parameter(layer.bias.detach().cpu().clone())
+        self.idx, self.rf, self.n_in = layer.knn_indices.cpu(), layer.local_rf.cpu(), layer.in_coords.shape[0]
+
+    def forward(self, x):
+        return knnconv_ref.knnconv_forward(x, self.idx, self.n_in, self.rf, self.weight, self.bias)
+
+
+def _rel(a, b):
+    return ((a.float().cpu() - b.float()).norm() / b.float().norm()).item()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("sample_cortex", [True, "geodesic"])
+def test_dinov3_snippet_forward_matches_oracle(sample_cortex):
+    dev = torch.device("cuda:0")
+    env, _, _ = _run_snippet(sample_cortex, dev)
+    model = env["model"]
+    pe = model.embeddings.patch_embeddings
+    n_in = pe.in_coords.shape[0]
+    idx, rf = pe.knn_indices.cpu(), pe.local_rf.cpu()
+    w, b = pe.weight.detach().cpu(), pe.bias.detach().cpu()
+    g = torch.Generator().manual_seed(0)
+    x = torch.rand(4, 3, n_in, generator=g)
+    with torch.no_grad():
+        y = pe(x.to(dev))
+        assert y.shape == (4, 384, pe.out_coords.shape[0])
+        assert _rel(y, knnconv_ref.knnconv_forward(x, idx, n_in, rf, w, b)) < 1e-5
+        yb = pe(x.to(dev).bfloat16())
+        ref_b = knnconv_ref.knnconv_forward(x.bfloat16().float(), idx, n_in, rf, w.bfloat16().float(),
+                                            b.bfloat16().float())
+        assert yb.dtype == torch.bfloat16 and _rel(yb, ref_b) < 1e-2
+    # the weight gradient through the adopted or constructed tables (fp32)
+    dy = torch.randn(4, 384, pe.out_coords.shape[0], generator=g)
+    pe.weight.grad = None
+    pe(x.to(dev)).backward(dy.to(dev))
+    wr = w.clone().requires_grad_(True)
+    knnconv_ref.knnconv_forward(x, idx, n_in, rf, wr, b).backward(dy)
+    assert _rel(pe.weight.grad, wr.grad) < 1e-5
+    # the whole backbone against itself on the CPU with the oracle patch embedding
+    with torch.no_grad():
+        out = model(pixel_values=x.to(dev)).last_hidden_state
+        cpu = _backbone("cpu")
+        cpu.embeddings.patch_embeddings = _OraclePatchEmbedding(pe)
+        cpu.rope_embeddings = FoviDinoV3RoPE(model.config.rope_theta, 384 // 6,
+                                             pe.out_coords.cartesian_rowcol.cpu(), device="cpu")
+        want = cpu(pixel_values=x).last_hidden_state
+    assert out.shape == (4, 1 + 4 + pe.out_coords.shape[0], 384)
+    assert _rel(out, want) < 1e-4
+    torch.cuda.synchronize()
