@@ -14,7 +14,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
 
-ABI_VERSION = 29
+ABI_VERSION = 30
 F32, BF16, F8E4M3 = 0, 1, 2
 NEAREST, BILINEAR = 0, 1
 PAD_ZEROS, PAD_BORDER = 0, 1
@@ -30,7 +30,7 @@ EXPORTED = ("fovi_abi_version", "fovi_last_error", "fovi_sampler_fwd", "fovi_knn
             "fovi_quantize_e4m3", "fovi_knnpool_fwd", "fovi_knnconv_slotsum", "fovi_knnconv_bwd_x",
             "fovi_knn_logpolar_candidates", "fovi_knn_select", "fovi_knn_euclid_candidates", "fovi_local_rf_slots", "fovi_knnconv_dw_workspace_bytes",
             "fovi_knnconv_dw", "fovi_knnpool_bwd", "fovi_knnconv_last_path",
-            "fovi_knnconv_fwd_noalloc")
+            "fovi_knnconv_fwd_noalloc", "fovi_knnconv_wide_tiles")
 
 
 class SamplerArgs(C.Structure):
@@ -77,7 +77,7 @@ class KnnConvArgs(C.Structure):
         ("fc_lo", C.c_void_p), ("fc_span", C.c_void_p), ("fc_item", C.c_void_p), ("fc_xlist", C.c_void_p),
         ("fc_xoff", C.c_void_p), ("fc_tile_points", C.c_int32), ("fc_zero_row", C.c_int32),
         ("fc_xmax", C.c_int32), ("wide_units", C.c_int32),
-        ("fc_comb", C.c_void_p), ("fc_comb_off", C.c_void_p), ("fc_pmax", C.c_int32), ("reserved4", C.c_int32),
+        ("fc_comb", C.c_void_p), ("fc_comb_off", C.c_void_p), ("fc_pmax", C.c_int32), ("wide_tiles", C.c_int32),
     ]
 
 
@@ -237,11 +237,24 @@ def load(path: str = LIB_PATH):
     lib.fovi_knnconv_dw.restype = C.c_int
     lib.fovi_knnpool_bwd.argtypes = [C.POINTER(KnnPoolBwdArgs), C.c_void_p]
     lib.fovi_knnpool_bwd.restype = C.c_int
+    lib.fovi_knnconv_wide_tiles.argtypes = [C.c_int64] + [C.c_int32] * 5 + [C.POINTER(C.c_int64)]
+    lib.fovi_knnconv_wide_tiles.restype = C.c_int
     got = lib.fovi_abi_version()
     if got != ABI_VERSION:
         raise RuntimeError(f"{path}: ABI version {got}, expected {ABI_VERSION}")
     _lib = lib
     return lib
+
+
+def knnconv_wide_tiles(n_ref, zero_row, coll_off_stride, cent_stride, heavy_stride, hlist_stride):
+    """(collision tiles, LDS bytes) of the wide-layer kernel's tile layout for tables of these
+    sizes (``fovi_knnconv_wide_tiles``, the kernel's own rule; host only)."""
+    lds = C.c_int64(0)
+    nb = load().fovi_knnconv_wide_tiles(int(n_ref), int(zero_row), int(coll_off_stride), int(cent_stride),
+                                        int(heavy_stride), int(hlist_stride), C.byref(lds))
+    if nb == 0:
+        check(1, "fovi_knnconv_wide_tiles")
+    return nb, lds.value
 
 
 def knnconv_last_path() -> str:

@@ -530,10 +530,10 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         return packed
 
     def _mfma_lds_bytes(self):
-        """LDS bytes of the fragment-order kernel's tile (``knn_tables.wide_lds_bytes`` with the
-        layer's collision tiles)."""
-        return T.wide_lds_bytes(self.ref_coords.shape[0], self._zero_row, self._coll_off_stride,
-                                self._cent_stride, self._heavy_stride, self._hlist_stride, self._wide_tiles)
+        """LDS bytes of the fragment-order kernel's tile for the layer's tables
+        (``knn_tables.wide_layout``)."""
+        return T.wide_layout(self.ref_coords.shape[0], self._zero_row, self._coll_off_stride,
+                             self._cent_stride, self._heavy_stride, self._hlist_stride)[1]
 
     def _mfma_column_use(self):
         """Fraction of the fragment-order kernel's 256-channel output tiles that holds real
@@ -660,6 +660,7 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         a.tile_heavy = self.tile_heavy.data_ptr(); a.tile_hlist = self.tile_hlist.data_ptr()
         a.heavy_stride = self._heavy_stride; a.hlist_stride = self._hlist_stride
         a.wide_units = int(self._wide_units)
+        a.wide_tiles = int(self._wide_tiles)
 
     # -- backward --------------------------------------------------------------
     def _backward(self, x, weight, dy, need_x, need_w):

@@ -31,6 +31,8 @@ from typing import NamedTuple
 import numpy as np
 import torch
 
+from .. import _lib
+
 __all__ = [
     "knn_logpolar",
     "knn_euclidean",
@@ -927,21 +929,18 @@ WIDE_LDS_BYTES = 160 * 1024
 WIDE_MAX_ROWS = 1024
 
 
-def wide_lds_bytes(n_ref, zero_row, coll_off_stride, cent_stride, heavy_stride, hlist_stride, tiles):
-    """LDS bytes of the wide-layer kernel's tile (its ``v5_layout``): the staged rows, the zero
-    row and the heavy-sum rows (64 bytes each), 128-byte alignment, ``tiles`` collision tiles of
-    256 rows and a trash row, per-(slot, row) sources, per-slot entry offsets, 16-byte stream
-    entries, 8-byte heavy entries, the heavy entries' neighbour offsets."""
-    o = ((zero_row + 1 + heavy_stride) * 64 + 127) & ~127
-    return (o + (tiles * 256 + 1) * 64 + n_ref * 256 * 2 + coll_off_stride * 4 + cent_stride * 16
-            + heavy_stride * 8 + hlist_stride * 2)
+def wide_layout(n_ref, zero_row, coll_off_stride, cent_stride, heavy_stride, hlist_stride):
+    """(collision tiles, LDS bytes) of the wide-layer kernel's tile for tables of these sizes:
+    ``WIDE_TILES_MAX`` tiles when that layout fits ``WIDE_LDS_BYTES``, else ``WIDE_TILES``. The
+    rule and the layout are the kernel's own, asked of the library
+    (``fovi_knnconv_wide_tiles``), so the tables and the kernel cannot disagree; the forward
+    refuses tables built for another count."""
+    return _lib.knnconv_wide_tiles(n_ref, zero_row, coll_off_stride, cent_stride, heavy_stride, hlist_stride)
 
 
 def wide_tile_count(n_ref, zero_row, coll_off_stride, cent_stride, heavy_stride, hlist_stride):
-    """Collision tiles of the wide-layer kernel for these table sizes: ``WIDE_TILES_MAX`` when
-    that layout fits ``WIDE_LDS_BYTES``, else ``WIDE_TILES`` (the kernel applies the same rule)."""
-    big = wide_lds_bytes(n_ref, zero_row, coll_off_stride, cent_stride, heavy_stride, hlist_stride, WIDE_TILES_MAX)
-    return WIDE_TILES_MAX if big <= WIDE_LDS_BYTES else WIDE_TILES
+    """Collision tiles of the wide-layer kernel for these table sizes (``wide_layout``)."""
+    return wide_layout(n_ref, zero_row, coll_off_stride, cent_stride, heavy_stride, hlist_stride)[0]
 
 
 def wide_strides(direct):

@@ -1367,6 +1367,12 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
                 f8 ? " and w_scale" : "");
       return 1;
     }
+    const int nb = v5_tiles_of(p);
+    if (a->wide_tiles != nb) {
+      set_error("fovi_knnconv_fwd: the wide-layer tables were built for %d collision tiles; the kernel uses %d "
+                "for their sizes (fovi_knnconv_wide_tiles)", a->wide_tiles, nb);
+      return 1;
+    }
     if ((f8 ? launch_knnconv_fp8_v5(p, a->y_dtype, s) : launch_knnconv_bf16_v5(p, a->y_dtype, s)) != 0) {
       set_error("fovi_knnconv_fwd: tile span too large for the fragment-order kernel");
       return 1;
@@ -1473,31 +1479,42 @@ constexpr int64_t kNoAllocScratchBytes = int64_t(64) << 20;
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
 constexpr int kMaxDevices = 64;
+// Held for a whole call: one call at a time reads and orders the per-device state below.
 static std::mutex g_scratch_mu;
 static void* g_scratch_ptr[kMaxDevices];
+// Recorded on a call's stream after its last use of the scratch; the next call's stream waits
+// for it, so calls on different streams of one GPU take the scratch in host call order.
+static hipEvent_t g_scratch_done[kMaxDevices];
+static bool g_scratch_recorded[kMaxDevices];
 
-// Device address of `scratch` on the current device, looked up once per device (with that
-// device current) and kept.
-static int scratch_address(void** out) {
+// Per-device set-up, once per device with that device current (the caller holds the mutex):
+// the device address of `scratch` and the ordering event. Returns the device index, or -1.
+static int scratch_setup() {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
     set_error("fovi_knnconv_fwd_noalloc: no current device (%s)", hipGetErrorString(e));
-    return 1;
+    return -1;
   }
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
     void* ptr = nullptr;
     e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !ptr) {
       set_error("fovi_knnconv_fwd_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
                 hipGetErrorString(e));
-      return 1;
+      return -1;
     }
+    hipEvent_t ev = nullptr;
+    e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess) {
+      set_error("fovi_knnconv_fwd_noalloc: hipEventCreateWithFlags failed on device %d: %s", dev,
+                hipGetErrorString(e));
+      return -1;
+    }
+    g_scratch_done[dev] = ev;
     g_scratch_ptr[dev] = ptr;
   }
-  *out = g_scratch_ptr[dev];
-  return 0;
+  return dev;
 }
 
 }  // namespace fovi
@@ -1512,11 +1529,7 @@ extern "C" int fovi_knnconv_fwd_noalloc(const fovi_knnconv_args* a, void* stream
     return 1;
   }
   if (!few_channel_rows(a)) return fovi_knnconv_fwd(a, stream);   // a path without scratch
-  if (!a->x || !a->y) { set_error("fovi_knnconv_fwd_noalloc: null pointer argument"); return 1; }
   if (a->batch <= 0 || a->n_out <= 0 || a->k_pad <= 0) { set_error("fovi_knnconv_fwd_noalloc: bad sizes"); return 1; }
-  if (a->y_dtype != FOVI_F32 && a->y_dtype != FOVI_BF16) {
-    set_error("fovi_knnconv_fwd_noalloc: bad y dtype"); return 1;
-  }
   // one image's slot-sum rows must fit the scratch; images are then taken in chunks that fit
   const int64_t per_image = a->n_out * a->k_pad * 2;
   if (a->n_out > kNoAllocScratchBytes || a->k_pad > kNoAllocScratchBytes || per_image > kNoAllocScratchBytes) {
@@ -1525,18 +1538,51 @@ extern "C" int fovi_knnconv_fwd_noalloc(const fovi_knnconv_args* a, void* stream
               (long long)kNoAllocScratchBytes);
     return 1;
   }
-  void* ws = nullptr;
-  if (scratch_address(&ws)) return 1;
+  if (!a->x || !a->y) { set_error("fovi_knnconv_fwd_noalloc: null pointer argument"); return 1; }
+  if (a->y_dtype != FOVI_F32 && a->y_dtype != FOVI_BF16) {
+    set_error("fovi_knnconv_fwd_noalloc: bad y dtype"); return 1;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  const int dev = scratch_setup();
+  if (dev < 0) return 1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // Under stream capture the caller's graph orders the calls; otherwise wait for the previous
+  // call's use of the scratch (a no-op on its own stream) and record this one's.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(s, &cap);
+  if (e != hipSuccess) {
+    set_error("fovi_knnconv_fwd_noalloc: hipStreamIsCapturing failed: %s", hipGetErrorString(e));
+    return 1;
+  }
+  const bool order = cap == hipStreamCaptureStatusNone;
+  if (order && g_scratch_recorded[dev]) {
+    e = hipStreamWaitEvent(s, g_scratch_done[dev], 0);
+    if (e != hipSuccess) {
+      set_error("fovi_knnconv_fwd_noalloc: hipStreamWaitEvent failed: %s", hipGetErrorString(e));
+      return 1;
+    }
+  }
   const int64_t chunk = kNoAllocScratchBytes / per_image;
   const int64_t y_esize = a->y_dtype == FOVI_F32 ? 4 : 2;
   fovi_knnconv_args b = *a;
-  for (int64_t b0 = 0; b0 < a->batch; b0 += chunk) {
+  int rc = 0;
+  for (int64_t b0 = 0; b0 < a->batch && rc == 0; b0 += chunk) {
     b.batch = std::min(chunk, a->batch - b0);
     b.x = static_cast<const char*>(a->x) + b0 * a->x_stride[0] * 2;
     b.y = static_cast<char*>(a->y) + b0 * a->y_stride[0] * y_esize;
-    b.workspace = ws;
+    b.workspace = g_scratch_ptr[dev];
     b.workspace_bytes = kNoAllocScratchBytes;
-    if (fovi_knnconv_fwd(&b, stream) != 0) return 1;
+    rc = fovi_knnconv_fwd(&b, stream);
   }
-  return 0;
+  if (order) {
+    // recorded after whatever was enqueued, also after a failed chunk, so the next call waits for it
+    e = hipEventRecord(g_scratch_done[dev], s);
+    if (e != hipSuccess) {
+      if (rc == 0) set_error("fovi_knnconv_fwd_noalloc: hipEventRecord failed: %s", hipGetErrorString(e));
+      g_scratch_recorded[dev] = false;
+      return 1;
+    }
+    g_scratch_recorded[dev] = true;
+  }
+  return rc;
 }

@@ -124,6 +124,9 @@ int launch_knnconv_fewc(const KnnParams& p, const fovi_knnconv_args* a, int cp, 
 // 1 if the fragment-order kernel takes this call (see knnconv_v5.hip; f8:
 // e4m3 input and weight), 0 if not.
 int v5_applies(const KnnParams& p, int f8);
+// The collision-tile count the fragment-order kernel uses for p's table sizes (4 when that tile
+// layout fits 160 KB of LDS, else 3): the tables must have been built for it.
+int v5_tiles_of(const KnnParams& p);
 int launch_knnconv_bf16_v5(const KnnParams& p, int out_t, hipStream_t s);
 int launch_knnconv_fp8_v5(const KnnParams& p, int out_t, hipStream_t s);
 

@@ -631,6 +631,11 @@ static int launch_v5(const KnnParams& p, int out_t, hipStream_t s) {
   return 0;
 }
 
+int v5_tiles_of(const KnnParams& p) {
+  return v5_tiles(static_cast<int>(p.V), p.zero_row, p.coll_off_stride, p.cent_stride, p.heavy_stride,
+                  p.hlist_stride);
+}
+
 int launch_knnconv_bf16_v5(const KnnParams& p, int out_t, hipStream_t s) { return launch_v5<false>(p, out_t, s); }
 int launch_knnconv_fp8_v5(const KnnParams& p, int out_t, hipStream_t s) { return launch_v5<true>(p, out_t, s); }
 
@@ -663,6 +668,27 @@ __global__ void pack_weight_mfma_kernel(const float* w_ref, int64_t c_out, int64
 }
 
 }  // namespace fovi
+
+extern "C" int fovi_knnconv_wide_tiles(int64_t n_ref, int32_t zero_row, int32_t coll_off_stride,
+                                       int32_t cent_stride, int32_t heavy_stride, int32_t hlist_stride,
+                                       int64_t* lds_bytes) {
+  using namespace fovi;
+  clear_error();
+  // n_ref below 2^16 and sizes up to 2^20 keep the layout's 32-bit byte count below 2^28
+  constexpr int64_t lim = int64_t(1) << 20;
+  if (n_ref < 0 || n_ref >= (int64_t(1) << 16) || zero_row < 0 || zero_row > lim || coll_off_stride < 0 || coll_off_stride > lim ||
+      cent_stride < 0 || cent_stride > lim || heavy_stride < 0 || heavy_stride > lim || hlist_stride < 0 ||
+      hlist_stride > lim) {
+    set_error("fovi_knnconv_wide_tiles: n_ref must lie in [0, 2^16), the other sizes in [0, 2^20]");
+    return 0;
+  }
+  const int V = static_cast<int>(n_ref);
+  const int nb = v5_tiles(V, zero_row, coll_off_stride, cent_stride, heavy_stride, hlist_stride);
+  if (lds_bytes)
+    *lds_bytes = static_cast<int64_t>(
+        v5_layout(V, zero_row, coll_off_stride, cent_stride, heavy_stride, hlist_stride, nb).total);
+  return nb;
+}
 
 extern "C" int64_t fovi_knnconv_weight_mfma_elems(int64_t c_out, int64_t c_in, int64_t n_ref) {
   using namespace fovi;

@@ -170,12 +170,13 @@ struct Taps {
   }
 
   // Channels-last bf16 images (channel stride 1, pixel stride NCH = 3 or 4, image base
-  // 4-byte aligned): the NCH channels of the tap at element offset e with one 8-byte load
-  // of the 4-byte-aligned words at or below it. Those 8 bytes hold the pixel whatever the
-  // alignment (NCH <= 4 - (e & 1)) and stay inside the row unless the pixel is the row's
-  // last and starts at an even element (then NCH = 3 reads two bytes of the next pixel):
-  // there the channels are loaded one by one. One load instead of NCH cuts the distinct
-  // cache lines a wave's gather touches by NCH.
+  // 4-byte aligned, and for NCH = 4 even image and row strides, so every pixel of a 4-channel
+  // image starts at an even element): the NCH channels of the tap at element offset e with
+  // one 8-byte load of the 4-byte-aligned words at or below it. Those 8 bytes hold the pixel
+  // (NCH <= 4 - (e & 1)) and stay inside the row unless the pixel is the row's last and
+  // starts at an even element (then NCH = 3 reads two bytes of the next pixel): there the
+  // channels are loaded one by one. One load instead of NCH cuts the distinct cache lines a
+  // wave's gather touches by NCH.
   template <int NCH>
   __device__ __forceinline__ static void pixel_cl(const uint16_t* s, Off e, Off x, Off W, float (&v)[4]) {
     if (NCH == 4 || (e & 1) || x + 1 < W) {
@@ -381,8 +382,9 @@ static void launch_rings(const SamplerParams& p, uint32_t bpv, uint32_t total, u
   const int vec_out = p.os2 == 1 && p.os1 % VPL == 0 && p.os0 % VPL == 0 &&
                       reinterpret_cast<uintptr_t>(p.out) % 16 == 0;
   if constexpr (std::is_same<InT, uint16_t>::value) {
-    // channels-last bf16 pixels of 3 or 4 channels, 4-byte aligned image starts
-    if (p.is1 == 1 && p.is3 == p.C && (p.C == 3 || p.C == 4) && p.is0 % 2 == 0 &&
+    // channels-last bf16 pixels of 3 or 4 channels, 4-byte aligned image starts; 4-channel
+    // pixels only at even elements (an odd one would need 5 of the 8-byte load's 4 halves)
+    if (p.is1 == 1 && p.is3 == p.C && (p.C == 3 || (p.C == 4 && p.is2 % 2 == 0)) && p.is0 % 2 == 0 &&
         reinterpret_cast<uintptr_t>(p.img) % 4 == 0) {
       if (p.C == 3)
         hipLaunchKernelGGL((sampler_rings_kernel<InT, OutT, MODE, PAD, false, 3, 3>), grid, dim3(256), 0, s, p, bpv,

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 29
+#define FOVI_ABI_VERSION 30
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -234,10 +234,24 @@ typedef struct fovi_knnconv_args {
   const uint32_t* fc_comb;    /* the fused few-channel kernel's combine entries (above) */
   const int32_t* fc_comb_off;
   int32_t fc_pmax;
-  int32_t reserved4;
+  int32_t wide_tiles;         /* (w_layout = FOVI_W_MFMA) the collision-tile count nb the wide-layer
+                                 tables were built for (tile_cent word 0 destinations); must equal
+                                 fovi_knnconv_wide_tiles() of the table sizes, else the call fails */
 } fovi_knnconv_args;
 
 int fovi_knnconv_fwd(const fovi_knnconv_args* args, void* stream);
+
+/*
+ * The wide-layer kernel's LDS layout for tables of these sizes (the fields of
+ * fovi_knnconv_args with the same names): returns the number of collision
+ * tiles nb it uses, 4 when that layout fits 160 KB of LDS, else 3, and writes
+ * the layout's LDS bytes to *lds_bytes when lds_bytes is not NULL (fits when
+ * <= 160 KB). Host only, no device call; returns 0 (with an error message)
+ * unless 0 <= n_ref < 2^16 and the other sizes lie in [0, 2^20]. The tables' builder takes nb from here, so builder and
+ * kernel share one rule. No counterpart in the reference.
+ */
+int fovi_knnconv_wide_tiles(int64_t n_ref, int32_t zero_row, int32_t coll_off_stride, int32_t cent_stride,
+                            int32_t heavy_stride, int32_t hlist_stride, int64_t* lds_bytes);
 
 /*
  * fovi_knnconv_fwd for callers that cannot allocate device memory (code under
@@ -256,9 +270,14 @@ int fovi_knnconv_fwd(const fovi_knnconv_args* args, void* stream);
  *   - workspace must be NULL and workspace_bytes 0;
  *   - one image's slot sums, n_out * k_pad * 2 bytes, must fit the 64 MiB
  *     scratch, or the call fails with an error (no launch);
- *   - every call on a GPU shares that GPU's scratch: calls that overlap on one
- *     GPU (different streams or threads) race. Each chunk's rows are written
- *     in full before they are read, so nothing needs clearing between calls.
+ *   - every call on a GPU shares that GPU's scratch. Calls are ordered in host
+ *     call order: each call's stream waits for a per-device event the previous
+ *     call recorded after its last use of the scratch (created with the
+ *     scratch's address at the first call on a device), and calls from several
+ *     threads take a lock. Calls enqueued under stream capture are not ordered
+ *     this way: the caller's graph must order them, and its replays must not
+ *     overlap other calls on that GPU. Each chunk's rows are written in full
+ *     before they are read, so nothing needs clearing between calls.
  */
 int fovi_knnconv_fwd_noalloc(const fovi_knnconv_args* args, void* stream);
 

@@ -107,3 +107,27 @@ def test_struct_layout_matches_header(py, c, tmp_path):
     assert ctypes.sizeof(py) == size
     for f, off in zip(fields, offs):
         assert getattr(py, f).offset == off, f
+
+
+def test_wide_tile_rule_is_the_header_layout():
+    """fovi_knnconv_wide_tiles (the kernel's rule, which the table builder asks) equals the
+    layout include/fovi_hip.h documents, on both sides of the 160 KB boundary: four collision
+    tiles while the four-tile layout fits, else three, with that layout's bytes."""
+    from fovi_amd.arch import knn_tables as T
+    from tests.test_tables_and_oracle import header_wide_lds_bytes
+    lim = 160 * 1024
+    for n_ref, zero_row, coll_off, heavy, hlist in ((25, 767, 28, 46, 416), (9, 255, 12, 2, 8),
+                                                    (49, 1023, 52, 10, 96), (255, 100, 256, 2, 8)):
+        base = header_wide_lds_bytes(n_ref, zero_row, coll_off, 0, heavy, hlist, 4)
+        edge = (lim - base) // 16                  # the last cent_stride whose four-tile layout fits
+        for cent in sorted({max(0, edge + d) for d in (-300, -2, -1, 0, 1, 2, 300)}):
+            sizes = (n_ref, zero_row, coll_off, cent, heavy, hlist)
+            four = header_wide_lds_bytes(*sizes, 4)
+            nb = 4 if four <= lim else 3
+            assert _lib.knnconv_wide_tiles(*sizes) == (nb, header_wide_lds_bytes(*sizes, nb)), sizes
+            assert T.wide_tile_count(*sizes) == nb
+    lib = _lib.load()
+    assert lib.fovi_knnconv_wide_tiles(25, -1, 28, 10, 2, 8, None) == 0
+    assert b"sizes" in lib.fovi_last_error()
+    assert lib.fovi_knnconv_wide_tiles(1 << 16, 0, 0, 0, 0, 0, None) == 0
+    assert lib.fovi_knnconv_wide_tiles(25, 767, 28, 10, 2, 8, None) in (3, 4)

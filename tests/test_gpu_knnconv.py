@@ -314,6 +314,30 @@ def test_fragment_order_kernel_falls_back_when_tables_exceed_lds():
     assert_close_rel(y.float().cpu(), ref, 1e-2)
 
 
+def test_wide_tables_for_another_tile_count_are_refused():
+    """The wide-layer tables name collision-tile destinations for one tile count; a call that
+    states another count than the kernel's rule for the table sizes is an error, before any
+    launch. C3's tables (four tiles) and C2 layer 2's are both checked; the right count runs."""
+    from fovi_amd import _lib
+    lib = _lib.load()
+    for geom in ((128, 128, 25, 256, 256), (32, 16, 25, 64, 192)):
+        layer = _layer(*geom, seed=16)
+        x = torch.randn(2, geom[3], geom[0] ** 2, generator=torch.Generator().manual_seed(17)).bfloat16()
+        xd = x.cuda().transpose(1, 2).contiguous().transpose(1, 2)
+        a, y, keep = layer.launch_args(xd)
+        assert a.w_layout == _lib.W_MFMA and a.wide_tiles in (3, 4)
+        good = a.wide_tiles
+        a.wide_tiles = 7 - good
+        assert lib.fovi_knnconv_fwd(a, _lib.stream_handle(xd.device)) != 0
+        assert b"collision tiles" in lib.fovi_last_error()
+        a.wide_tiles = good
+        _lib.check(lib.fovi_knnconv_fwd(a, _lib.stream_handle(xd.device)), "fovi_knnconv_fwd")
+        torch.cuda.synchronize()
+        with torch.no_grad():
+            assert torch.equal(y, layer(xd).transpose(1, 2))
+        del keep
+
+
 # Kernel path each benchmark geometry selects (fovi_knnconv_last_path), with the oracle check
 # for the paths no other test reaches on purpose.
 _SELECTION = [

@@ -196,6 +196,28 @@ def test_channels_last_images_equal_channel_planes(mode, pad, channels, width):
     assert torch.equal(got, want)
 
 
+@pytest.mark.parametrize("mode", ["bilinear", "nearest"])
+@pytest.mark.parametrize("channels", [3, 4])
+def test_channels_last_views_with_odd_row_stride(mode, channels):
+    """Channels-last views whose row stride is odd (``as_strided`` over a larger buffer) put
+    the pixels of odd rows at odd elements. Three-channel pixels are read there with the
+    one-load-per-tap path; four-channel ones need even elements, so such a view takes the
+    channel-plane kernel. Either way the samples equal those of a contiguous copy."""
+    g = torch.Generator().manual_seed(13)
+    H, W, B = 90, 101, 2
+    rs = channels * W + 1
+    base = torch.rand(B * H * rs + 8, generator=g).to(torch.bfloat16).cuda()
+    img = base.as_strided((B, channels, H, W), (H * rs, 1, rs, channels))
+    assert img.stride(2) % 2 == 1 and img.stride(0) % 2 == 0
+    fix = torch.tensor([[0.5, 0.5], [0.1, 0.9], [0.8, 0.2], [0.97, 0.97]])
+    sizes = np.array([[H, W]] * 4)
+    vmap = torch.tensor([0, 0, 1, 1])
+    s = GridSampler(16, 2.78, 64, device="cuda", mode=mode, style="logpolar", padding_mode="border")
+    want = s.sample_views(img.contiguous(), fix, sizes, view_image=vmap)
+    got = s.sample_views(img, fix, sizes, view_image=vmap)
+    assert torch.equal(got, want)
+
+
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "tables.npz")
 
 

@@ -223,6 +223,15 @@ def test_direct_tables_lists_and_zero_row(res_in, res_out, k):
             assert np.all(np.diff(c) <= 0)          # decreasing count order
 
 
+def header_wide_lds_bytes(n_ref, zero_row, coll_off_stride, cent_stride, heavy_stride, hlist_stride, tiles):
+    """The wide-layer tile's LDS bytes as include/fovi_hip.h states them (tile_cent): 64 (zero_row
+    + 1 + heavy_stride) rounded up to 128, + (256 nb + 1) 64 + 512 n_ref + 4 coll_off_stride +
+    16 cent_stride + 8 heavy_stride + 2 hlist_stride."""
+    o = ((zero_row + 1 + heavy_stride) * 64 + 127) // 128 * 128
+    return (o + (tiles * 256 + 1) * 64 + 512 * n_ref + 4 * coll_off_stride + 16 * cent_stride
+            + 8 * heavy_stride + 2 * hlist_stride)
+
+
 @pytest.mark.parametrize("res_in,res_out,k,permute", [(32, 32, 25, False), (64, 32, 49, False), (16, 16, 9, False),
                                                       (128, 128, 25, False), (32, 32, 25, True),
                                                       (32, 16, 25, False)])   # C2 layer 2: 1024 staged rows
@@ -240,7 +249,7 @@ def test_wide_tables_decode_to_the_csr_lists(res_in, res_out, k, permute):
     # collision tiles: four exactly when the four-tile layout fits, whatever the slot order
     sizes = (t["V"], zr, wide.coll_off.shape[1], wide.stride, wide.heavy_stride, wide.hlist_stride)
     assert T.wide_strides(direct) == sizes[2:]
-    big = T.wide_lds_bytes(*sizes, T.WIDE_TILES_MAX) <= T.WIDE_LDS_BYTES
+    big = header_wide_lds_bytes(*sizes, T.WIDE_TILES_MAX) <= T.WIDE_LDS_BYTES
     assert wide.tiles == (T.WIDE_TILES_MAX if big else T.WIDE_TILES) == T.wide_tiles_of(direct)
     src, cent, coll_off = wide.src.numpy().astype(np.int64), wide.coll.numpy().view(np.uint32), wide.coll_off.numpy()
     heavy, hlist = wide.heavy.numpy().view(np.uint32), wide.hlist.numpy().view(np.uint16)

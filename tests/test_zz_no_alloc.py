@@ -78,10 +78,11 @@ def test_noalloc_paths_without_scratch_and_workspace_rejected():
 
 def test_noalloc_refuses_slot_sums_beyond_its_scratch():
     """Host-side check, before any HIP call (runs without a GPU): one image's slot sums of
-    n_out x k_pad bf16 above 64 MiB are an error naming the limit."""
+    n_out x k_pad bf16 above 64 MiB are an error naming the limit. Every data pointer is NULL,
+    so were the size check to pass, the null-pointer checks would still refuse the call: no
+    launch can follow, on a GPU host either."""
     lib = _lib.load()
     a = _lib.KnnConvArgs()
-    a.x = 4096; a.y = 4096; a.w = 4096; a.slot_ptr = 4096; a.nbr_sorted = 4096
     a.x_dtype = a.w_dtype = _lib.BF16; a.y_dtype = _lib.BF16; a.w_layout = _lib.W_ROWS
     a.batch, a.c_in, a.n_in, a.c_out = 2, 3, 1024, 64
     a.x_stride[:] = [1024 * 4, 1, 4]
@@ -93,3 +94,43 @@ def test_noalloc_refuses_slot_sums_beyond_its_scratch():
     assert "exceed" in msg and str(SCRATCH) in msg, msg
     a.n_out = SCRATCH // (2 * 1024) + 1                            # just past the limit
     assert lib.fovi_knnconv_fwd_noalloc(a, None) != 0 and "exceed" in lib.fovi_last_error().decode()
+    a.n_out = SCRATCH // (2 * 1024)                                # fits: the NULL pointers are refused
+    assert lib.fovi_knnconv_fwd_noalloc(a, None) != 0 and "null pointer" in lib.fovi_last_error().decode()
+
+
+@pytest.mark.gpu
+def test_noalloc_calls_on_two_streams_take_the_scratch_in_call_order():
+    """Two streams, no synchronisation between the calls: a long call (300 views, three chunks
+    through the scratch) on stream A, then a short one (5 views) on stream B. The second waits
+    for the first's last use of the scratch, so both equal the workspace entry point, and
+    stream B's call completes after stream A's (without the wait the short call, enqueued on
+    an idle stream, would finish first and its slot sums would overwrite A's in flight)."""
+    layer = _layer(128, 16, 256, 3, 384, side=16)
+    layer.few_channel_fused = False
+    g = torch.Generator().manual_seed(4)
+    xs, want = [], []
+    for n_views in (300, 5):
+        x = torch.rand(n_views, 3, 16384, generator=g).bfloat16()
+        _, xv = layer.padded_input(n_views)
+        xv.copy_(x.cuda())
+        xs.append(xv)
+        want.append(_call(layer, xv, "fovi_knnconv_fwd")[0])
+    lib = _lib.load()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    done = [torch.cuda.Event(enable_timing=True) for _ in streams]
+    start = torch.cuda.Event(enable_timing=True)
+    outs, keep = [], []
+    torch.cuda.synchronize()
+    start.record(streams[0])
+    streams[1].wait_event(start)
+    for xv, st, ev in zip(xs, streams, done):
+        with torch.cuda.stream(st):
+            a, y, k = layer.launch_args(xv, workspace=False)
+            _lib.check(lib.fovi_knnconv_fwd_noalloc(a, C.c_void_p(st.cuda_stream)), "fovi_knnconv_fwd_noalloc")
+            ev.record(st)
+        outs.append(y)
+        keep.append(k)
+    torch.cuda.synchronize()
+    for y, w in zip(outs, want):
+        assert torch.equal(y, w)
+    assert start.elapsed_time(done[1]) >= start.elapsed_time(done[0])
