@@ -263,7 +263,7 @@ def _backbone(device):
     layer, random-initialised from a seed: no download."""
     from transformers import DINOv3ViTConfig, DINOv3ViTModel
     torch.manual_seed(0)
-    return DINOv3ViTModel(DINOv3ViTConfig(num_hidden_layers=1)).eval().to(device)
+    return DINOv3ViTModel(DINOv3ViTConfig(num_hidden_layers=1, num_register_tokens=4)).eval().to(device)
 
 
 def _run_snippet(sample_cortex, device):
@@ -347,6 +347,6 @@ def test_dinov3_snippet_forward_matches_oracle(sample_cortex):
         cpu.rope_embeddings = FoviDinoV3RoPE(model.config.rope_theta, 384 // 6,
                                              pe.out_coords.cartesian_rowcol.cpu(), device="cpu")
         want = cpu(pixel_values=x).last_hidden_state
-    assert out.shape == (4, 1 + 4 + pe.out_coords.shape[0], 384)
+    assert out.shape == (4, 1 + model.config.num_register_tokens + pe.out_coords.shape[0], 384)
     assert _rel(out, want) < 1e-4
     torch.cuda.synchronize()
