@@ -205,7 +205,7 @@ def test_channels_last_views_with_odd_row_stride(mode, channels):
     channel-plane kernel. Either way the samples equal those of a contiguous copy."""
     g = torch.Generator().manual_seed(13)
     H, W, B = 90, 101, 2
-    rs = channels * W + 1
+    rs = channels * W + (1 if channels * W % 2 == 0 else 2)    # odd
     base = torch.rand(B * H * rs + 8, generator=g).to(torch.bfloat16).cuda()
     img = base.as_strided((B, channels, H, W), (H * rs, 1, rs, channels))
     assert img.stride(2) % 2 == 1 and img.stride(0) % 2 == 0
