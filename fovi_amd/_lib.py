@@ -14,7 +14,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
 
-ABI_VERSION = 30
+ABI_VERSION = 31
 F32, BF16, F8E4M3 = 0, 1, 2
 NEAREST, BILINEAR = 0, 1
 PAD_ZEROS, PAD_BORDER = 0, 1
@@ -74,9 +74,9 @@ class KnnConvArgs(C.Structure):
         ("coll_off_stride", C.c_int32), ("cent_stride", C.c_int32),
         ("tile_heavy", C.c_void_p), ("tile_hlist", C.c_void_p), ("heavy_stride", C.c_int32),
         ("hlist_stride", C.c_int32),
-        ("fc_lo", C.c_void_p), ("fc_span", C.c_void_p), ("fc_item", C.c_void_p), ("fc_xlist", C.c_void_p),
-        ("fc_xoff", C.c_void_p), ("fc_tile_points", C.c_int32), ("fc_zero_row", C.c_int32),
-        ("fc_xmax", C.c_int32), ("wide_units", C.c_int32),
+        ("fc_lo", C.c_void_p), ("fc_span", C.c_void_p), ("fc_item", C.c_void_p), ("fc_threads", C.c_int32), ("fc_chunk", C.c_int32),
+        ("reserved7", C.c_void_p), ("fc_tile_points", C.c_int32), ("fc_zero_row", C.c_int32),
+        ("fc_pairs", C.c_int32), ("wide_units", C.c_int32),
         ("fc_comb", C.c_void_p), ("fc_comb_off", C.c_void_p), ("fc_pmax", C.c_int32), ("wide_tiles", C.c_int32),
     ]
 

@@ -355,22 +355,8 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         if tiles is not None:
             order = T.stream_slot_order(T.slot_stream_units(tiles), ahead=T.wide_tiles_of(tiles))
         self.set_slot_order(order)
-        # tables of the fused few-channel kernel (c_in <= 8): the largest tile whose LDS fits
-        self._fc = None
-        cp = 4 if self.in_channels <= 4 else (8 if self.in_channels <= 8 else None)
-        fc = None
-        if cp is not None:
-            k_pad = -(-cp * n_ref // _KCHUNK) * _KCHUNK
-            for tile in (256, 128):
-                fc = T.few_channel_tables(knn_indices, slots, n_in, n_ref, cp, k_pad, tile)
-                if fc is not None and T.few_channel_lds_bytes(fc, self.out_channels, cp) <= 160 * 1024:
-                    break
-                fc = None
-        for name, field in (("fc_lo", "lo"), ("fc_span", "span"), ("fc_item", "item"), ("fc_xlist", "xlist"),
-                            ("fc_xoff", "xoff"), ("fc_comb", "comb"), ("fc_comb_off", "comb_off")):
-            self.register_buffer(name, None if fc is None else getattr(fc, field).to(device), persistent=False)
-        if fc is not None:
-            self._fc = (fc.tile, fc.zero_row, fc.xmax, fc.pmax)
+        # tables of the fused few-channel kernel (c_in <= 8): the first geometry whose LDS fits
+        self.set_few_channel_geometry(None, knn_indices, slots, n_in, n_ref, device)
         # few-channel layers: the fused kernel when its tables fit (False: the slot sums through
         # a workspace and a dense GEMM, or the single-pass kernel)
         self.few_channel_fused = True
@@ -393,6 +379,30 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         # 256-channel tiles, tables within LDS): weights in MFMA-fragment order for the
         # 256 x 256-tile kernel (False: the row-packed kernels)
         self.mfma_weights = True
+
+    def set_few_channel_geometry(self, geometries=None, knn_indices=None, slots=None, n_in=None, n_ref=None,
+                                 device=None):
+        """Tables of the fused few-channel kernel (layers with c_in <= 8) for the first of
+        ``geometries`` (``(tile, threads, chunk)`` tuples; default ``knn_tables.FC_GEOMETRIES``)
+        whose tile fits the LDS; none fits: the layer takes the other few-channel paths."""
+        self._fc = None
+        cp = 4 if self.in_channels <= 4 else (8 if self.in_channels <= 8 else None)
+        if knn_indices is None:
+            knn_indices, slots = self.knn_indices.cpu(), self.slots
+            n_in, n_ref, device = self.in_coords.shape[0], self.ref_coords.shape[0], self.weight.device
+        fc = None
+        if cp is not None:
+            k_pad = -(-cp * n_ref // _KCHUNK) * _KCHUNK
+            for tile, threads, chunk in (T.FC_GEOMETRIES if geometries is None else geometries):
+                fc = T.few_channel_tables(knn_indices, slots, n_in, n_ref, cp, k_pad, tile, threads, chunk)
+                if fc is not None and T.few_channel_lds_bytes(fc, self.out_channels, cp) < (1 << 30):
+                    break
+                fc = None
+        for name, field in (("fc_lo", "lo"), ("fc_span", "span"), ("fc_item", "item"), ("fc_comb", "comb"),
+                            ("fc_comb_off", "comb_off")):
+            self.register_buffer(name, None if fc is None else getattr(fc, field).to(device), persistent=False)
+        if fc is not None:
+            self._fc = (fc.tile, fc.zero_row, fc.pmax, fc.pairs, fc.threads, fc.chunk)
 
     # -- setup ---------------------------------------------------------------
     def _init_conv_like(self):
@@ -633,10 +643,9 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         fused = cp is not None and self.few_channel_fused and self._fc is not None
         if fused:
             a.fc_lo = self.fc_lo.data_ptr(); a.fc_span = self.fc_span.data_ptr()
-            a.fc_item = self.fc_item.data_ptr(); a.fc_xlist = self.fc_xlist.data_ptr()
-            a.fc_xoff = self.fc_xoff.data_ptr()
+            a.fc_item = self.fc_item.data_ptr()
             a.fc_comb = self.fc_comb.data_ptr(); a.fc_comb_off = self.fc_comb_off.data_ptr()
-            a.fc_tile_points, a.fc_zero_row, a.fc_xmax, a.fc_pmax = self._fc
+            a.fc_tile_points, a.fc_zero_row, a.fc_pmax, a.fc_pairs, a.fc_threads, a.fc_chunk = self._fc
         ws = None
         if cp is not None and self.two_pass_few_channels and workspace and not fused:
             # slot-sum rows for the two-pass few-channel path (caller-owned scratch)

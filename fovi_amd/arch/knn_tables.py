@@ -733,51 +733,89 @@ def direct_tables(knn_idx, slots, n_in, n_ref, tile=TILE_POINTS):
 class FewChannelTables(NamedTuple):
     lo: torch.Tensor         # [T] int32 first staged input row of tile t
     span: torch.Tensor       # [T] int32 staged rows
-    item: torch.Tensor       # [T, n_chunks, tile * spc, 2] int32 (uint32 words)
-    xlist: torch.Tensor      # [total] int16 (uint16 S rows), per (tile, chunk) blocks of multiples of 8
-    xoff: torch.Tensor       # [T * n_chunks + 1] int32 block starts
-    tile: int
+    item: torch.Tensor       # [T, n_chunks, threads, pairs] int32 (uint32 pair words)
+    pairs: int               # pair words per thread and chunk (FC_PAIR_COUNTS)
+    tile: int                # output points per tile
+    threads: int             # threads of the kernel's workgroup
+    chunk: int               # reduction columns per chunk
     zero_row: int
-    xmax: int
     comb: torch.Tensor       # [total] int32 (uint32 words): per (tile, chunk) combine entries
     comb_off: torch.Tensor   # [T * n_chunks + 1] int32 block starts
     pmax: int                # most partial sums of one chunk
 
 
-FC_CHUNK = 64      # reduction columns per chunk of the fused few-channel kernel
-FC_THREADS = 512   # threads of its workgroup
+# Tile geometries of the fused few-channel kernel, (output points, threads, chunk columns), in
+# the order a layer tries them (fastest first, measured on the C4 patch embedding and C2
+# layer 1: 128 / 512 / 64 0.229 and 0.062 ms, 256 / 512 / 64 -- and 0.073 ms, 64 / 256 / 32,
+# two workgroups per CU, 0.329 and 0.085 ms)
+FC_GEOMETRIES = ((128, 512, 64), (256, 512, 64), (64, 256, 32))
+# Waves along the tile's rows each geometry's kernel is built for, tried in this order (the
+# library's FC_GEOMS); the other waves of the workgroup split the output channels
+FC_WAVE_ROWS = {(64, 256, 32): (1, 2), (128, 512, 64): (2, 4), (256, 512, 64): (2, 4)}
 # Slot sums of few-channel layers run over the neighbour list in groups of this many: each
 # group's fp32 sum in list order from +0, the groups' sums added in order (for up to this many
 # neighbours, the plain list order). The fused kernel sums the groups of one slot on different
 # lanes; the two-pass slot-sum kernel uses the same order.
 FC_GROUP = 8
+# (sum, neighbour) pairs per thread and chunk in the fused kernel's table: the first of these
+# counts whose packing fits the workgroup's threads
+FC_PAIR_COUNTS = (8, 16)
+FC_LAST = 1 << 29      # pair word flag: the last pair of its sum or partial sum
+FC_PARTIAL = 1 << 28   # pair word flag: the run is one group of a long list (an fp32 partial sum)
 
 
-def few_channel_tables(knn_idx, slots, n_in, n_ref, cp, k_pad, tile):
+def _fc_entry(row, slot, cp, chunk):
+    """Index, in units of one slot entry (2 cp bytes), of (row, slot) in the fused kernel's A
+    tile: rows of 2 ``chunk`` bytes whose 16-byte part q sits at part q ^ ((row >> 1) & 7)
+    (128-byte rows) or q ^ g(row), g(r) = (bit1(r) ^ bit3(r)) | bit2(r) << 1 (64-byte rows)."""
+    b = slot * cp * 2
+    if chunk == 64:
+        g = (row >> 1) & 7
+    else:
+        g = (((row >> 1) ^ (row >> 3)) & 1) | ((row >> 1) & 2)
+    off = row * chunk * 2 + (((b >> 4) ^ g) << 4) + (b & 15)
+    return off // (2 * cp)
+
+
+def few_channel_tables(knn_idx, slots, n_in, n_ref, cp, k_pad, tile, threads=512, chunk=64):
     """Tables of the fused few-channel kernel (``knnconv_fewc.hip``; ``fc_*`` in the C-ABI).
 
-    Output points are cut into tiles of ``tile`` (128 or 256) consecutive points; a tile
-    stages input rows ``[lo, lo + span)`` and a zero row ``zero_row`` (the largest span).
-    The reduction runs in chunks of 64 columns, ``64 // cp`` slots each; the kernel clears a
-    chunk's A tile and writes only its non-empty (row, slot) sums. Each is built from items of
-    two uint32 words, ``first << 16 | partial << 15 | count`` and ``dest << 16 | xoff``: the
-    sum in list order of ``count`` (1 .. ``FC_GROUP``) neighbours, the S row of the first and
-    the further ``count - 1`` at ``xoff`` in the chunk's extras block (CSR list order of
-    ``csr_tables``). A slot of at most ``FC_GROUP`` neighbours is one item written to A at
-    ``dest = row * spc + slot``; a longer one is one item per group of ``FC_GROUP`` (partial
-    flag set) writing an fp32 partial sum to ``dest`` in the chunk's partial buffer, and a
-    combine entry ``dest | m << 12 | p0 << 20`` adds its ``m`` partials ``p0 ..`` in order
-    and writes A. Items are sorted by count (largest first) and dealt in a snake over the 512
-    threads (item ``j * 512 + thread``; a wave holds items of similar counts), the rest of the
-    ``tile * spc`` item slots being empty (count 0). Returns ``None`` when a span or an extras
-    block does not fit 16 bits, or a chunk has more items than slots, more than 512 combine
-    entries or more than 4095 partials.
+    Output points are cut into tiles of ``tile`` consecutive points, each run by a workgroup of
+    ``threads`` threads (a geometry of ``FC_GEOMETRIES``); a tile stages input rows ``[lo, lo +
+    span)`` and a zero row ``zero_row`` (the largest span). The reduction runs in chunks of
+    ``chunk`` columns, ``chunk // cp`` slots each; the kernel clears a chunk's A tile and
+    writes only its non-empty (row, slot) sums. They come from (sum, neighbour) pairs,
+    ``pairs`` per thread and chunk: word ``j`` of thread ``th`` in chunk ``c`` of tile ``t`` is
+    ``item[t, c, th, j]`` = the neighbour's S row (bits 0-15; the zero row for an unused pair)
+    | target << 16 | ``FC_PARTIAL`` | ``FC_LAST``. A sum's pairs are consecutive within one
+    thread, in CSR list order (``csr_tables``); the thread adds them in fp32 from +0 and, at the
+    pair flagged ``FC_LAST``, writes the sum rounded to bf16 to A entry ``target``
+    (``_fc_entry``). A slot of more than ``FC_GROUP`` neighbours is one run per group of
+    ``FC_GROUP`` (partial flag set) writing an fp32 partial sum to index ``target`` of the
+    chunk's partial buffer, and a combine entry ``dest | m << 12 | p0 << 20`` (``dest = row *
+    spc + slot``) adds its ``m`` partials ``p0 ..`` in order and writes A. Runs are packed into
+    thread segments in (row, slot) order, a run that does not fit a segment's remaining pairs
+    going to the next, so every thread issues ``pairs`` independent row reads; ``pairs`` is the
+    first of ``FC_PAIR_COUNTS`` for which every chunk fits the threads. The segments are dealt
+    round robin over the workgroup's waves. Returns ``None`` when a span does not fit 16 bits,
+    or a chunk needs more segments than threads, more combine entries than threads or more
+    than 4095 partials.
     """
+    for pairs in FC_PAIR_COUNTS:
+        ft = _few_channel_tables(knn_idx, slots, n_in, n_ref, cp, k_pad, tile, threads, chunk, pairs)
+        if ft != "threads":
+            return ft
+    return None
+
+
+def _few_channel_tables(knn_idx, slots, n_in, n_ref, cp, k_pad, tile, threads, chunk, pairs):
+    """``few_channel_tables`` at ``pairs`` pair words per thread; "threads" when a chunk needs
+    more segments than threads."""
     k, n_out = knn_idx.shape
-    spc = FC_CHUNK // cp
-    n_chunks = k_pad // FC_CHUNK
+    spc = chunk // cp
+    n_chunks = k_pad // chunk
     per_chunk = tile * spc
-    if k_pad % FC_CHUNK or per_chunk % FC_THREADS or n_chunks * spc < n_ref or per_chunk > 4096:
+    if k_pad % chunk or n_chunks * spc < n_ref or per_chunk > 4096:
         return None
     ptr, nbr = csr_tables(knn_idx, slots, n_in, n_ref)
     ptr = ptr.numpy().astype(np.int64)
@@ -804,17 +842,13 @@ def few_channel_tables(knn_idx, slots, n_in, n_ref, cp, k_pad, tile):
     nbr_pad[:n_out] = nbr
     rows_lo = np.repeat(lo, tile)[:, None]
     nbr_rel = np.where(nbr_pad >= 0, nbr_pad - rows_lo, 0)
-    # item slot of each count rank: round j = rank // 512 fills slots j * 512 + thread, odd rounds
-    # backwards (a snake). A wave runs as long as its slowest lane: consecutive ranks share a
-    # wave, and a wave that takes the heaviest items of one round takes light ones in the next
-    rank = np.arange(per_chunk)
-    rnd, pos = rank // FC_THREADS, rank % FC_THREADS
-    slot_of_rank = rnd * FC_THREADS + np.where(rnd % 2 == 0, pos, FC_THREADS - 1 - pos)
-    G = FC_GROUP
-    item = np.zeros((n_tiles, n_chunks, per_chunk, 2), np.int64)
-    blocks, xoff, off = [], [0], 0
+    G, P = FC_GROUP, pairs
+    n_waves = threads // 64
+    item = np.full((n_tiles, n_chunks, threads, P), zero_row, np.int64)
+    seg = np.arange(threads)
+    seg_thread = (seg % n_waves) * 64 + seg // n_waves
     cblocks, coff = [], [0]
-    xmax = pmax = 0
+    pmax = 0
     for t in range(n_tiles):
         rows = slice(t * tile, (t + 1) * tile)
         nrel = nbr_rel[rows]
@@ -822,66 +856,44 @@ def few_channel_tables(knn_idx, slots, n_in, n_ref, cp, k_pad, tile):
             cols = slice(c * spc, (c + 1) * spc)
             cc = cnt[rows, cols].reshape(-1)            # dest = row * spc + slot
             bb = beg[rows, cols].reshape(-1)
-            dests = np.nonzero(cc)[0]
-            # items: (count, first, dest, partial, list start); groups of G for long lists
-            i_cnt, i_first, i_dest, i_part, i_beg = [], [], [], [], []
+            words = np.full((threads, P), zero_row, np.int64)
             comb = []
             n_part = 0
-            for d in dests:
+            th, used = 0, 0
+            for d in np.nonzero(cc)[0]:
                 n, b0 = int(cc[d]), int(bb[d])
-                r = d // spc
+                r, sl = divmod(int(d), spc)
                 if n <= G:
-                    i_cnt.append(n); i_first.append(nrel[r, b0]); i_dest.append(d); i_part.append(0)
-                    i_beg.append((r, b0))
-                    continue
-                m = -(-n // G)
-                if m > 0xFF:
-                    return None
-                comb.append(int(d) | (m << 12) | (n_part << 20))
-                for g in range(m):
-                    gn = min(G, n - g * G)
-                    i_cnt.append(gn); i_first.append(nrel[r, b0 + g * G]); i_dest.append(n_part + g)
-                    i_part.append(1); i_beg.append((r, b0 + g * G))
-                n_part += m
-            n_items = len(i_cnt)
-            if n_items > per_chunk or len(comb) > FC_THREADS or n_part > 0xFFF:
+                    runs = [(b0, n, _fc_entry(r, sl, cp, chunk), 0)]
+                else:
+                    m = -(-n // G)
+                    if m > 0xFF:
+                        return None
+                    comb.append(int(d) | (m << 12) | (n_part << 20))
+                    runs = [(b0 + g * G, min(G, n - g * G), n_part + g, FC_PARTIAL) for g in range(m)]
+                    n_part += m
+                for start, gn, target, part in runs:
+                    if used + gn > P:
+                        th, used = th + 1, 0
+                    if th >= threads:
+                        return "threads"
+                    words[th, used:used + gn] = nrel[r, start:start + gn]
+                    words[th, used + gn - 1] |= (target << 16) | part | FC_LAST
+                    used += gn
+            # thread segments dealt round robin over the waves: segment i to thread
+            # (i % waves) * 64 + i // waves, so every wave builds about the same share
+            item[t, c, seg_thread] = words
+            if len(comb) > threads or n_part > 0xFFF:
                 return None
-            i_cnt = np.asarray(i_cnt, np.int64)
-            order = np.argsort(-i_cnt, kind="stable")
-            extra_n = np.maximum(i_cnt[order] - 1, 0)
-            starts = np.cumsum(extra_n) - extra_n
-            total = int(extra_n.sum())
-            if total > 0xFFFF:
-                return None
-            xl = np.zeros(-(-total // 8) * 8, np.int64)
-            for q, st, ne in zip(order, starts, extra_n):
-                if ne:
-                    r, b0 = i_beg[q]
-                    xl[st:st + ne] = nrel[r, b0 + 1:b0 + 1 + ne]
-            sl = slot_of_rank[:n_items]
-            first = np.asarray(i_first, np.int64)[order]
-            dest = np.asarray(i_dest, np.int64)[order]
-            part = np.asarray(i_part, np.int64)[order]
-            item[t, c, sl, 0] = (first << 16) | (part << 15) | i_cnt[order]
-            item[t, c, sl, 1] = (dest << 16) | starts
-            blocks.append(xl)
-            off += len(xl)
-            xoff.append(off)
-            xmax = max(xmax, len(xl))
             cblocks.append(np.asarray(comb, np.int64))
             coff.append(coff[-1] + len(comb))
             pmax = max(pmax, n_part)
-    xlist = np.concatenate(blocks) if blocks else np.zeros(0, np.int64)
-    if len(xlist) == 0:
-        xlist = np.zeros(8, np.int64)
     comb_all = np.concatenate(cblocks) if cblocks else np.zeros(0, np.int64)
     if len(comb_all) == 0:
         comb_all = np.zeros(1, np.int64)
     return FewChannelTables(
         torch.from_numpy(lo.astype(np.int32)), torch.from_numpy(span.astype(np.int32)),
-        torch.from_numpy(item.astype(np.uint32).view(np.int32)),
-        torch.from_numpy(xlist.astype(np.uint16).view(np.int16)),
-        torch.from_numpy(np.asarray(xoff, np.int32)), tile, zero_row, xmax,
+        torch.from_numpy(item.astype(np.uint32).view(np.int32)), pairs, tile, threads, chunk, zero_row,
         torch.from_numpy(comb_all.astype(np.uint32).view(np.int32)), torch.from_numpy(np.asarray(coff, np.int32)),
         pmax)
 
@@ -889,19 +901,28 @@ def few_channel_tables(knn_idx, slots, n_in, n_ref, cp, k_pad, tile):
 def few_channel_lds_bytes(tables, c_out, cp):
     """LDS bytes the fused few-channel kernel needs for these tables and ``c_out`` (its
     layout: staged rows and the zero row, two A chunks, the weight chunk of ``c_out`` rounded
-    up to 64 columns, the extras block, the partial sums, at least the epilogue's
-    transposition buffers; more
-    than 160 KB when no wave tiling of the kernel covers ``c_out`` at this tile size)."""
+    up to 64 columns, the partial sums, at least the epilogue's transposition buffers), or
+    ``1 << 30`` when no wave tiling of the kernel covers ``c_out`` at this geometry or the
+    layout passes the workgroup's share of the CU's 160 KB (half for 256 threads, whose
+    workgroups run two per CU)."""
     ntp = -(-c_out // 64) * 64
-    # the kernel's wave tilings: 2 x 4 or 4 x 2 waves of rb x cb blocks of 32 x 32, cb <= 4,
-    # rb * cb <= 8; extras blocks of at most 4 pieces of 16 bytes per thread
-    tilings = [(tables.tile // (32 * wm), ntp // (32 * (8 // wm))) for wm in (2, 4)
-               if ntp % (32 * (8 // wm)) == 0]
-    if not any(1 <= cb <= 4 and rb * cb <= 8 for rb, cb in tilings) or tables.xmax > 4 * 512 * 8:
+    nw = tables.threads // 64
+    # the kernel's wave tilings: wm x (nw / wm) waves of rb x cb blocks of 32 x 32, cb <= 4,
+    # rb * cb <= 8, wm among those the geometry is built for
+    fits = []
+    for wm in FC_WAVE_ROWS.get((tables.tile, tables.threads, tables.chunk), ()):
+        if nw % wm or tables.tile % (32 * wm) or ntp % (32 * (nw // wm)):
+            continue
+        rb, cb = tables.tile // (32 * wm), ntp // (32 * (nw // wm))
+        if 1 <= cb <= 4 and rb * cb <= 8:
+            fits.append((rb, cb))
+    if not fits:
         return 1 << 30
+    rb, cb = fits[0]
     s = ((tables.zero_row + 1) * cp * 2 + 15) & ~15
-    body = s + 2 * tables.tile * 128 + ntp * 128 + tables.xmax * 2 + tables.pmax * cp * 4
-    return max(body, tables.tile * ntp * 2)
+    body = s + 2 * tables.tile * tables.chunk * 2 + ntp * tables.chunk * 2 + tables.pmax * cp * 4
+    total = max(body, nw * rb * 32 * cb * 32 * 2)
+    return total if total <= (80 if tables.threads == 256 else 160) * 1024 else 1 << 30
 
 
 def _row_offset(r):

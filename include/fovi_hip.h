@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 30
+#define FOVI_ABI_VERSION 31
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -200,34 +200,38 @@ typedef struct fovi_knnconv_args {
   int32_t hlist_stride;       /* multiple of 8, >= 8 */
   /* Tables of the fused few-channel kernel (the few-channel path: bf16, w_c_slot = 4 or 8 >=
    * c_in, channels-last rows padded to w_c_slot; all NULL to leave it out). Output points are
-   * cut into tiles of fc_tile_points (128 or 256) consecutive points; tile t stages input rows
-   * fc_lo[t] .. fc_lo[t] + fc_span[t] - 1 (S rows 0 .. span - 1) and a zero row fc_zero_row
-   * (>= every span, < 65536). The reduction runs in chunks of 64 columns (64 / w_c_slot slots;
-   * k_pad / 64 chunks, at most 4096 slots). The kernel clears chunk c's A tile and writes its
-   * non-empty (row, slot) sums from items, fc_tile_points * 64 / w_c_slot slots of two words
-   * at fc_item[((t * n_chunks + c) * items + j * 512 + thread) * 2]:
-   *   word 0 = (S row of the first neighbour) << 16 | partial << 15 | count (1 .. 8; 0 = no
-   *            item in this slot);
-   *   word 1 = destination << 16 | offset of the further neighbours (count - 1 S rows, list
-   *            order) in the chunk's extras block;
-   * the destination is row * (64 / w_c_slot) + slot within the chunk (the item's fp32 sum in
-   * list order from +0, rounded once to bf16) or, with the partial bit, an index below
-   * fc_pmax (<= 4095) of the chunk's fp32 partial sums. Combine entries (t, c), fc_comb[
-   * fc_comb_off[t * n_chunks + c] .. fc_comb_off[t * n_chunks + c + 1]) (at most 512), each
-   * destination | m << 12 | p0 << 20, write to A the partials p0 .. p0 + m - 1 added in order
-   * and rounded once. A (row, slot) of up to 8 neighbours is one item; a longer one is one
-   * partial per group of 8 consecutive neighbours and one combine entry. Extras block (t, c)
-   * is fc_xlist[fc_xoff[t * n_chunks + c] .. fc_xoff[t * n_chunks + c + 1]) (uint16, multiples
-   * of 8; fc_xmax = the longest). The slot sums (this grouped order) and the MFMA order equal
-   * the two-pass path's. */
+   * cut into tiles of fc_tile_points consecutive points, each run by a workgroup of fc_threads
+   * threads with chunks of fc_chunk reduction columns: (64, 256, 32), (128, 512, 64) or
+   * (256, 512, 64). Tile t stages input rows fc_lo[t] .. fc_lo[t] + fc_span[t] - 1 (S rows 0 ..
+   * span - 1) and a zero row fc_zero_row (>= every span, < 65536). The reduction runs in
+   * k_pad / fc_chunk chunks of fc_chunk / w_c_slot slots (at most 4096 slots). The kernel
+   * clears chunk c's A tile and writes its non-empty (row, slot) sums from (sum, neighbour)
+   * pairs: thread j of tile t reads the fc_pairs (8 or 16) words
+   * fc_item[((t * n_chunks + c) * fc_threads + j) * fc_pairs ..] (16-byte aligned), each
+   *   S row of the neighbour (bits 0-15; the zero row for an unused word) | target << 16
+   *   (12 bits) | partial << 28 | last << 29.
+   * A run of consecutive words of one thread is one sum: added in fp32 in word (list) order
+   * from +0 and written at the word with the last bit, rounded once to bf16, to A entry
+   * `target` (an index in units of 2 * w_c_slot bytes of the A tile, whose rows of 2 *
+   * fc_chunk bytes hold the chunk's slots in order with 16-byte part q of row r at part
+   * q ^ ((r >> 1) & 7) for 128-byte rows, q ^ g(r) for 64-byte rows, g(r) = (bit1(r) ^
+   * bit3(r)) | bit2(r) << 1), or, with the partial bit, as its fp32 partial sum to index target
+   * (below fc_pmax <= 4095) of the chunk's partial sums. A (row, slot) of up to 8 neighbours is
+   * one run; a longer one is one partial run per group of 8 consecutive neighbours and one
+   * combine entry. Combine entries (t, c), fc_comb[fc_comb_off[t * n_chunks + c] ..
+   * fc_comb_off[t * n_chunks + c + 1]) (at most fc_threads), each destination | m << 12 | p0
+   * << 20 with destination = row * (fc_chunk / w_c_slot) + slot, write to A the partials p0 ..
+   * p0 + m - 1 added in order and rounded once. The slot sums (this grouped order) and the
+   * MFMA order equal the two-pass path's. */
   const int32_t* fc_lo;
   const int32_t* fc_span;
   const uint32_t* fc_item;
-  const uint16_t* fc_xlist;
-  const int32_t* fc_xoff;
+  int32_t fc_threads;         /* threads of the kernel's workgroup the pair table is dealt to: 256 or 512 */
+  int32_t fc_chunk;           /* reduction columns per chunk: 32 or 64 */
+  const void* reserved7;      /* NULL */
   int32_t fc_tile_points;
   int32_t fc_zero_row;
-  int32_t fc_xmax;
+  int32_t fc_pairs;           /* pair words per thread and chunk in fc_item: 8 or 16 */
   int32_t wide_units;         /* 1: the wide-layer tables (tile_src, tile_cent words 1-3, tile_heavy
                                  word 0, tile_hlist) name staged and heavy rows in 16-byte units
                                  (needed past 1023 staged rows); 0: in bytes */

@@ -121,7 +121,7 @@ def test_from_reference_adopts_the_reference_tables(name):
     assert torch.equal(got.slots, ref.local_rf.argmax(2))
     assert torch.equal(got.weight.detach(), ref.weight) and torch.equal(got.bias.detach(), ref.bias)
     # the same tables give the same device tables as the constructed layer
-    for buf in ("slot_ptr", "nbr_sorted", "tile_lo", "tile_ent", "tile_nbr", "fc_item", "fc_xlist"):
+    for buf in ("slot_ptr", "nbr_sorted", "tile_lo", "tile_ent", "tile_nbr", "fc_item", "fc_comb"):
         a, b = getattr(got, buf), getattr(built, buf)
         assert (a is None) == (b is None), buf
         assert a is None or torch.equal(a, b), buf

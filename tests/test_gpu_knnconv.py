@@ -241,13 +241,39 @@ def test_bf16_few_channels_padded_rows(c_in, k, side, c_out):
     assert_close_rel(y_one.float().cpu(), ref, 1e-2)
 
 
-def test_few_channel_fused_c4_patch_embedding_geometry():
+@pytest.mark.parametrize("geom", [(64, 256, 32), (128, 512, 64), (256, 512, 64)])
+def test_few_channel_fused_takes_every_geometry_the_host_accepts(geom):
+    """Whenever the host builds fused tables for a geometry and output width (its mirror of the
+    kernel's wave tilings and LDS layout says they fit), the library launches the fused kernel
+    for them, and its output equals the two-pass path's bit for bit."""
+    from fovi_amd import _lib
+    x = torch.randn(2, 5, 1024, generator=torch.Generator().manual_seed(3)).bfloat16().cuda()
+    accepted = 0
+    for c_out in (32, 64, 96, 128, 160, 200, 256, 320, 384, 512):
+        layer = _layer(32, 16, 9, 5, c_out, None, bias=True, seed=c_out)
+        layer.set_few_channel_geometry([geom])
+        if layer._fc is None:
+            continue
+        accepted += 1
+        with torch.no_grad():
+            y = layer(x)
+            assert _lib.knnconv_last_path() == "bf16 few-channel fused", (geom, c_out)
+            layer.few_channel_fused = False
+            y_two = layer(x)
+        assert torch.equal(y, y_two), (geom, c_out)
+    assert accepted >= 6, accepted
+
+
+@pytest.mark.parametrize("geom", [(64, 256, 32), (128, 512, 64)])
+def test_few_channel_fused_c4_patch_embedding_geometry(geom):
     """C4 patch embedding (16384 -> 256 log-polar points, k = 256, 16 x 16 ref grid, 3 -> 384,
-    bias) at 64 views: the fused kernel (128-point tiles) equals the two-pass path bit for bit,
-    and views 0 and 63 match the oracle."""
+    bias) at 64 views: the fused kernel at each tile geometry (64 points / 256 threads / 32
+    columns, two workgroups per CU; 128 / 512 / 64) equals the two-pass path bit for bit, and
+    views 0 and 63 match the oracle."""
     from fovi_amd import _lib
     layer = _layer(128, 16, 256, 3, 384, 16, bias=True, seed=9)
-    assert layer._fc is not None and layer._fc[0] == 128
+    layer.set_few_channel_geometry([geom])
+    assert layer._fc is not None and (layer._fc[0], layer._fc[4], layer._fc[5]) == geom
     x = torch.rand(64, 3, 16384, generator=torch.Generator().manual_seed(12)).bfloat16()
     _, view = layer.padded_input(64)
     view.copy_(x.cuda())

@@ -336,28 +336,35 @@ def test_stream_slot_order_is_a_permutation_that_lowers_serial_work():
     assert serial(order) < 0.5 * serial(list(range(t["V"])))
 
 
-@pytest.mark.parametrize("res_in,res_out,k,side,cp,tile", [
-    (128, 16, 256, 16, 4, 128),     # C4 patch embedding
-    (64, 32, 49, None, 4, 256),     # C2 layer 1
-    (32, 16, 25, None, 8, 128),     # eight-channel rows
-    (24, 12, 30, None, 4, 128),     # ragged: partial tile, padding slots in the last chunk
+@pytest.mark.parametrize("res_in,res_out,k,side,cp,geom", [
+    (128, 16, 256, 16, 4, (64, 256, 32)),     # C4 patch embedding
+    (128, 16, 256, 16, 4, (128, 512, 64)),
+    (64, 32, 49, None, 4, (256, 512, 64)),    # C2 layer 1
+    (64, 32, 49, None, 4, (64, 256, 32)),
+    (32, 16, 25, None, 8, (128, 512, 64)),    # eight-channel rows
+    (32, 16, 25, None, 8, (64, 256, 32)),
+    (24, 12, 30, None, 4, (128, 512, 64)),    # ragged: partial tile, padding slots in the last chunk
+    (24, 12, 30, None, 4, (64, 256, 32)),
 ])
-def test_few_channel_tables_rebuild_the_slot_sums(res_in, res_out, k, side, cp, tile):
+def test_few_channel_tables_rebuild_the_slot_sums(res_in, res_out, k, side, cp, geom):
     """Emulates the fused few-channel kernel's use of its tables in float64: the A tile starts
-    cleared, every non-empty (row, slot) of a chunk is written exactly once (by an item of at
-    most FC_GROUP neighbours, or by a combine entry adding the partial sums of its groups of
-    FC_GROUP consecutive neighbours in order), every S row read is a staged row, and the
-    rebuilt A chunks equal the slot sums of the CSR lists."""
+    cleared; every thread's FC_PAIRS pair words form runs, each a sum of at most FC_GROUP
+    neighbours written at its last word (to a distinct A entry of the swizzled layout, or as a
+    partial sum that a combine entry adds in order with the other groups of its slot); unused
+    words read the zero row; every S row read is a staged row; every non-empty (row, slot) of a
+    chunk is written exactly once, and the rebuilt A chunks equal the slot sums of the CSR
+    lists."""
     import numpy as np
 
     from fovi_amd.arch import knn_tables as T
     t = layer_tables(res_in, res_out, k, side=side)
     V, n_in, n_out = t["V"], t["n_in"], t["n_out"]
     k_pad = -(-V * cp // 64) * 64
-    ft = T.few_channel_tables(t["idx"], t["slots"], n_in, V, cp, k_pad, tile)
-    assert ft is not None
+    tile, threads, chunk = geom
+    ft = T.few_channel_tables(t["idx"], t["slots"], n_in, V, cp, k_pad, tile, threads, chunk)
+    assert ft is not None and (ft.tile, ft.threads, ft.chunk) == geom
     G = T.FC_GROUP
-    spc, nc = 64 // cp, k_pad // 64
+    spc, nc = chunk // cp, k_pad // chunk
     rng = np.random.default_rng(0)
     x = rng.standard_normal((n_in, cp))
     # reference slot sums [n_out, V, cp] from the CSR lists
@@ -369,36 +376,41 @@ def test_few_channel_tables_rebuild_the_slot_sums(res_in, res_out, k, side, cp, 
             if c:
                 want[n, v] = x[nbr[n, b:b + c]].sum(0)
     item = ft.item.numpy().view(np.uint32)
-    xl = ft.xlist.numpy().view(np.uint16).astype(np.int64)
-    xoff = ft.xoff.numpy()
+    assert item.shape == (ft.lo.shape[0], nc, threads, ft.pairs) and ft.pairs in T.FC_PAIR_COUNTS
+    assert not (item >> 30).any(), "pair words use bits 0-29"
+    # A entries of the swizzled 128-byte rows: one per (row, slot), all distinct
+    entry_dest = {T._fc_entry(r, sl, cp, chunk): r * spc + sl for r in range(tile) for sl in range(spc)}
+    assert len(entry_dest) == tile * spc and max(entry_dest) < tile * chunk * 2 // (2 * cp)
     comb = ft.comb.numpy().view(np.uint32)
     coff = ft.comb_off.numpy()
     split = 0
     for ti in range(ft.lo.shape[0]):
         lo, span = int(ft.lo[ti]), int(ft.span[ti])
-        S = x[lo:lo + span]
+        S = np.concatenate([x[lo:lo + span], np.zeros((1, cp))])[np.r_[0:span, [span] * (ft.zero_row + 1 - span)]]
+        assert ft.zero_row >= span and not S[ft.zero_row].any()
         for c in range(nc):
-            blk = xl[xoff[ti * nc + c]:xoff[ti * nc + c + 1]]
-            assert len(blk) <= ft.xmax and len(blk) % 8 == 0
             got = np.zeros((tile * spc, cp))
             written = np.zeros(tile * spc, bool)
             P = np.full((ft.pmax, cp), np.nan)
-            for w0, w1 in item[ti, c]:
-                cnt, part, first = int(w0 & 0xF), int(w0 >> 15) & 1, int(w0 >> 16)
-                dest, off = int(w1 >> 16), int(w1 & 0xFFFF)
-                if cnt == 0:
-                    assert w0 == 0 and w1 == 0
-                    continue
-                assert 1 <= cnt <= G and off + cnt - 1 <= len(blk)
-                rows = [first] + list(blk[off:off + cnt - 1])
-                assert all(0 <= r < span for r in rows)
-                if part:
-                    assert np.isnan(P[dest]).all(), "a partial sum is written twice"
-                    P[dest] = S[rows].sum(0)
-                else:
-                    assert not written[dest], "a (row, slot) is written twice"
-                    written[dest] = True
-                    got[dest] = S[rows].sum(0)
+            for th in range(threads):
+                run = []
+                for word in item[ti, c, th].tolist():
+                    run.append(word & 0xFFFF)
+                    if not word & T.FC_LAST:
+                        continue
+                    target = (word >> 16) & 0xFFF
+                    assert 1 <= len(run) <= G and all(0 <= r < span for r in run), run
+                    val = S[run].sum(0)
+                    if word & T.FC_PARTIAL:
+                        assert np.isnan(P[target]).all(), "a partial sum is written twice"
+                        P[target] = val
+                    else:
+                        dest = entry_dest[target]
+                        assert not written[dest], "a (row, slot) is written twice"
+                        written[dest] = True
+                        got[dest] = val
+                    run = []
+                assert all(r == ft.zero_row for r in run), "unused pair words read the zero row"
             for cw in comb[coff[ti * nc + c]:coff[ti * nc + c + 1]]:
                 dest, m, p0 = int(cw & 0xFFF), int(cw >> 12) & 0xFF, int(cw >> 20)
                 assert m >= 2 and not written[dest]
