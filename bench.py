@@ -496,22 +496,40 @@ def main():
         line["c3_backward"] = {"workload": "C3 layer backward, bf16: input gradient (kNN-conv forward over the "
                                            "inverse table) and weight gradient (per-slot pair-list MFMA kernel)",
                                "ms": round(bwd["ms"], 4), "TFLOP/s": round(bwd["tflops"], 2)}
+    def traffic_frac(kernel, ms):
+        """HBM bytes per launch from the counter record, over the launch time, as a fraction of peak."""
+        t = measured_traffic(kernel)
+        return None if t is None else round(t / (ms * 1e-3) / (PEAK_HBM_GBS * 1e9), 4)
+
     if c4 is not None:
         line["sampler_c4"] = {
             "workload": "C4 sampler: 128 images 3x512x512 bf16, 4 fixations each (512 views), "
                         "16384 log-polar points, bf16 out",
             "nearest": {"GB/s": round(c4["gbs"], 1), "frac": round(c4["gbs"] / PEAK_HBM_GBS, 4),
+                        "traffic_frac": traffic_frac("sampler_rings_kernel<bf16,nearest>", c4["ms"]),
                         "ms": round(c4["ms"], 4), "images/s": round(c4["images_per_s"], 1)},
             "bilinear": {"GB/s": round(c4b["gbs"], 1), "frac": round(c4b["gbs"] / PEAK_HBM_GBS, 4),
+                         "traffic_frac": traffic_frac("sampler_rings_kernel<bf16,bilinear>", c4b["ms"]),
                          "ms": round(c4b["ms"], 4), "images/s": round(c4b["images_per_s"], 1)},
             "channels_last_images": {
                 "nearest": {"GB/s": round(c4cl["gbs"], 1), "frac": round(c4cl["gbs"] / PEAK_HBM_GBS, 4),
+                            "traffic_frac": traffic_frac("sampler_rings_kernel<bf16,nearest,channels_last>",
+                                                         c4cl["ms"]),
                             "ms": round(c4cl["ms"], 4)},
                 "bilinear": {"GB/s": round(c4bcl["gbs"], 1), "frac": round(c4bcl["gbs"] / PEAK_HBM_GBS, 4),
+                             "traffic_frac": traffic_frac("sampler_rings_kernel<bf16,bilinear,channels_last>",
+                                                          c4bcl["ms"]),
                              "ms": round(c4bcl["ms"], 4)}},
             "roofline": {"bound": "hbm", "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "traffic": {"nearest": measured_traffic("sampler_rings_kernel<bf16,nearest>"),
-                                     "bilinear": measured_traffic("sampler_rings_kernel<bf16,bilinear>")}},
+                                     "bilinear": measured_traffic("sampler_rings_kernel<bf16,bilinear>"),
+                                     "channels_last_nearest":
+                                         measured_traffic("sampler_rings_kernel<bf16,nearest,channels_last>"),
+                                     "channels_last_bilinear":
+                                         measured_traffic("sampler_rings_kernel<bf16,bilinear,channels_last>")},
+                         "note": "frac: algorithmic bytes (distinct in-bounds tap pixels + output) per launch "
+                                 "time; traffic_frac: HBM bytes the counters read per launch (fetch + write) "
+                                 "per launch time, both against 8 TB/s"},
         }
     if pool is not None:
         line["knn_pool"] = {"workload": "kNN max pooling (AlexNet block): 256 images, 64 channels, 1024 -> 256 "
@@ -530,6 +548,7 @@ def main():
                                "images/s": round(c4e["images_per_s"], 1), "ms": round(c4e["ms"], 4),
                                "patch_embed_ms": round(c4e["ms_patch_embed"], 4),
                                "patch_embed_TFLOP/s": round(c4e["patch_embed_tflops"], 1),
+                               "patch_embed_traffic": measured_traffic("knnconv_fewc_kernel<c4>"),
                                "policy_ms": round(c4e["ms_policy"], 4),
                                "policy_note": "MultiRandomSaccadePolicy (near-centre 0.25, eval) forward: host "
                                               "draws + one sampler launch for the 512 views, bf16 out"}

@@ -6,9 +6,9 @@
 // = (slot v, channel c), column v * CP + c, as the row-packed weight
 // (fovi_knnconv_pack_weight with c_slot = CP). A workgroup of NT threads (256
 // or 512: WM x WN waves) owns TM consecutive output points of one image and
-// every output channel (NTP, c_out rounded up to the wave tiling). With 256
-// threads and a tile within 80 KB of LDS two workgroups share a CU, so one's
-// staging, barriers and epilogue run beside the other's MFMAs.
+// every output channel (NTP, c_out rounded up to the wave tiling). The host
+// builds the tables for one geometry (TM, NT, KC) of FC_GEOMS; with 256 threads
+// and a tile within 80 KB of LDS two workgroups share a CU.
 //  * The tile's input rows form one contiguous index range; they are staged
 //    in LDS once (S, CP channels per row, channels >= c_in zeroed), plus a
 //    zero row, with 16-byte loads all in flight at once.
@@ -454,8 +454,6 @@ __global__ __launch_bounds__(NT, 512 / NT) void knnconv_fewc_kernel(KnnParams p,
   }
 }
 
-// The tile geometries a call can take (the host builds its tables for one of them):
-// (output points, threads, chunk columns).
 // Geometries built (tile points, threads, chunk columns) and, as a bit mask, the waves along
 // rows (1, 2, 4) each is instantiated for; the host mirror is knn_tables.FC_WAVE_ROWS.
 struct FewcGeom { int tm, nt, kc, wms; };
