@@ -14,7 +14,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
 
-ABI_VERSION = 31
+ABI_VERSION = 32
 F32, BF16, F8E4M3 = 0, 1, 2
 NEAREST, BILINEAR = 0, 1
 PAD_ZEROS, PAD_BORDER = 0, 1
@@ -78,6 +78,8 @@ class KnnConvArgs(C.Structure):
         ("reserved7", C.c_void_p), ("fc_tile_points", C.c_int32), ("fc_zero_row", C.c_int32),
         ("fc_pairs", C.c_int32), ("wide_units", C.c_int32),
         ("fc_comb", C.c_void_p), ("fc_comb_off", C.c_void_p), ("fc_pmax", C.c_int32), ("wide_tiles", C.c_int32),
+        ("vm_idx", C.c_void_p), ("vm_ev", C.c_void_p), ("vm_off", C.c_void_p), ("vm_j0", C.c_void_p),
+        ("vm_w", C.c_void_p), ("vm_nb", C.c_int32), ("vm_cb", C.c_int32),
     ]
 
 

@@ -360,6 +360,11 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         # few-channel layers: the fused kernel when its tables fit (False: the slot sums through
         # a workspace and a dense GEMM, or the single-pass kernel)
         self.few_channel_fused = True
+        # few-channel layers given view-major input rows (padded_input(..., view_major=True)):
+        # the view-major kernel (False: the two-pass or single-pass paths); its tables are
+        # built on first use
+        self.view_major_kernel = True
+        self._vm = None
         # slot-sum headroom of the fp8 path: the largest neighbour count of a slot
         self._max_slot_count = int((slot_ptr & 0xFFFF).max()) if slot_ptr.numel() else 1
         # quantize every input to e4m3 and run the fp8 kernel
@@ -568,16 +573,56 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
         c = self.in_channels
         return 4 if c <= 4 else (8 if c <= 8 else None)
 
-    def padded_input(self, batch, device=None):
-        """A zeroed channels-last buffer ``[B, N_in, padded_channels]`` (bf16) and its
+    def padded_input(self, batch, device=None, view_major=False):
+        """A zeroed buffer of input rows padded to ``padded_channels`` (bf16) and its
         ``[B, C_in, N_in]`` view: a producer (e.g. the sampler) that writes into the view
-        hands this layer its preferred layout without a copy."""
+        hands this layer its preferred layout without a copy. Point-major ``[B, N_in, cp]``
+        (the fused point-tile kernel), or with ``view_major`` ``[N_in, B, cp]``: the rows of
+        one input point for all images adjacent (the view-major kernel)."""
         cp = self.padded_channels
         if cp is None:
             raise ValueError("padded input rows are for layers with at most 8 input channels")
-        buf = torch.zeros(batch, self.in_coords.shape[0], cp, dtype=torch.bfloat16,
-                          device=device or self.weight.device)
+        dev = device or self.weight.device
+        if view_major:
+            buf = torch.zeros(self.in_coords.shape[0], batch, cp, dtype=torch.bfloat16, device=dev)
+            return buf, buf.permute(1, 2, 0)[:, :self.in_channels]
+        buf = torch.zeros(batch, self.in_coords.shape[0], cp, dtype=torch.bfloat16, device=dev)
         return buf, buf.transpose(1, 2)[:, :self.in_channels]
+
+    @staticmethod
+    def _vm_blocks(c_out):
+        """(32-column blocks per wave, blocks with padding) of the view-major kernel: as few
+        channel groups as blocks of at most 6 allow (each group gathers the inputs again)."""
+        nb = -(-c_out // 32)
+        groups = -(-nb // 6)
+        cb = next(c for c in (1, 2, 3, 4, 6) if c * groups >= nb)
+        return cb, cb * groups
+
+    def _view_major_tables(self, device):
+        """The view-major kernel's round tables (``knn_tables.view_major_tables``), built once."""
+        if self._vm is None or self._vm[0] != device:
+            cp = self.padded_channels
+            k_pad = -(-cp * self.ref_coords.shape[0] // _KCHUNK) * _KCHUNK
+            vt = T.view_major_tables(self.slot_ptr.cpu(), self.nbr_sorted.cpu(), self.in_coords.shape[0],
+                                     self.ref_coords.shape[0], cp, k_pad)
+            self._vm = (device, vt.idx.to(device), vt.ev.to(device), vt.off.to(device), vt.j0.to(device))
+        return self._vm[1:]
+
+    def _packed_weight_vm(self, c_slot):
+        """The view-major kernel's weight fragments (``knn_tables.view_major_weight``), cached
+        per weight version; ``(fragments, blocks, blocks per wave)``."""
+        w = self.weight
+        key = ("vm", c_slot, w._version, w.data_ptr())
+        hit = self._packed.get(("vm", c_slot))
+        if hit is not None and hit[0] == key:
+            return hit[1]
+        cb, nb = self._vm_blocks(self.out_channels)
+        frag = T.view_major_weight(self._packed_weight(torch.bfloat16, c_slot), cb)
+        # skipped reduction steps add nothing only when every weight is finite (0 * inf is NaN)
+        finite = bool(torch.isfinite(w.detach()).all())
+        packed = (frag, nb, cb, finite)
+        self._packed[("vm", c_slot)] = (key, packed)
+        return packed
 
     # -- forward -------------------------------------------------------------
     def _compute_dtype(self, x):
@@ -610,10 +655,13 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
             x = x.to(dt)
         c_slot = self.in_channels
         cp = self.padded_channels if dt == torch.bfloat16 else None
+        view_major = False
         if cp is not None:
             c_slot = cp
-            if not (x.stride(1) == 1 and x.stride(2) == cp and x.stride(0) % cp == 0
-                    and x.data_ptr() % (2 * cp) == 0):
+            view_major = (x.stride(1) == 1 and x.stride(0) == cp and x.stride(2) % cp == 0
+                          and x.stride(2) >= cp and x.data_ptr() % (2 * cp) == 0)
+            if not view_major and not (x.stride(1) == 1 and x.stride(2) == cp and x.stride(0) % cp == 0
+                                       and x.data_ptr() % (2 * cp) == 0):
                 buf, view = self.padded_input(x.shape[0], x.device)
                 view.copy_(x)
                 x = view
@@ -640,14 +688,22 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
             raise ValueError(f"activation must be None or 'relu', got {activation!r}")
         a.activation = _lib.ACT_RELU if activation == "relu" else _lib.ACT_NONE
         a.w_c_slot = c_slot
-        fused = cp is not None and self.few_channel_fused and self._fc is not None
+        vm = None
+        if view_major and self.view_major_kernel:
+            frag, nb, cb, finite = self._packed_weight_vm(c_slot)
+            if finite:
+                vm = (self._view_major_tables(x.device), frag, nb, cb)
+        if vm is not None:
+            (a.vm_idx, a.vm_ev, a.vm_off, a.vm_j0), a.vm_w = [t.data_ptr() for t in vm[0]], vm[1].data_ptr()
+            a.vm_nb, a.vm_cb = vm[2], vm[3]
+        fused = cp is not None and self.few_channel_fused and self._fc is not None and not view_major
         if fused:
             a.fc_lo = self.fc_lo.data_ptr(); a.fc_span = self.fc_span.data_ptr()
             a.fc_item = self.fc_item.data_ptr()
             a.fc_comb = self.fc_comb.data_ptr(); a.fc_comb_off = self.fc_comb_off.data_ptr()
             a.fc_tile_points, a.fc_zero_row, a.fc_pmax, a.fc_pairs, a.fc_threads, a.fc_chunk = self._fc
         ws = None
-        if cp is not None and self.two_pass_few_channels and workspace and not fused:
+        if cp is not None and self.two_pass_few_channels and workspace and not fused and vm is None:
             # slot-sum rows for the two-pass few-channel path (caller-owned scratch)
             ws = torch.empty(bsz * n_out * w.shape[1], dtype=torch.bfloat16, device=x.device)
             a.workspace = ws.data_ptr(); a.workspace_bytes = ws.numel() * 2
@@ -659,7 +715,7 @@ class KNNConvLayer(nn.Module, KNNBaseLayer):
             a.zero_row = self._zero_row
         if mfma:
             self._set_wide_tables(a)
-        return a, y, (x, w, bias, ws)
+        return a, y, (x, w, bias, ws, vm)
 
     def _set_wide_tables(self, a):
         """The fragment-order kernel's tables, into the ``fovi_knnconv_args`` ``a``."""

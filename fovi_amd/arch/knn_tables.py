@@ -925,6 +925,109 @@ def few_channel_lds_bytes(tables, c_out, cp):
     return total if total <= (80 if tables.threads == 256 else 160) * 1024 else 1 << 30
 
 
+# The view-major few-channel kernel (input rows of one point for every image adjacent in memory,
+# [N_in, B, CP]): an MFMA block's 32 rows are 32 images of one output point, so a reduction step
+# of 16 columns (16 / CP slots) that is empty for the point is skipped for all of them, and each
+# lane gathers its image's rows with one load per neighbour.
+VM_CHUNK = 8           # rounds per event / index load of the kernel
+VM_G, VM_P, VM_S = 1, 2, 4   # event flags: close a group of FC_GROUP; end of phase A; end of the step
+VM_J_NONE = 0x1FFF     # no next step
+
+
+class ViewMajorTables(NamedTuple):
+    idx: torch.Tensor    # int32 [2 * rounds]: per point, half 0's input row per round, then half 1's
+    ev: torch.Tensor     # int16 [rounds]: per round, flags | next active step << 3 (at a step's end)
+    off: torch.Tensor    # int32 [n_out + 1]: first round of each point (multiples of VM_CHUNK)
+    j0: torch.Tensor     # int32 [n_out]: each point's first active step (-1: none)
+    pad: int             # the input row a padding round names (n_in: past the rows, read as zeros)
+    steps: int           # active steps over all points
+
+
+def view_major_tables(slot_ptr, nbr_sorted, n_in, n_ref, cp, k_pad):
+    """Tables of the view-major few-channel kernel from the CSR lists (``csr_tables``).
+
+    Reduction step j covers columns 16 j .. 16 j + 15, i.e. slots ``16 / cp * j ..``; lane half h
+    of an MFMA block holds columns 8 h .. 8 h + 7 of it: for cp = 4 slots 4j + 2h (phase A) and
+    4j + 2h + 1 (phase B), for cp = 8 slot 2j + h (one phase). A point's steps with no neighbour
+    in any of their slots are left out. For each active step and phase the kernel runs
+    max(count of half 0's slot, count of half 1's slot) rounds; in round q each half adds
+    neighbour q of its slot's list (CSR order) or, past its count, a padding row (+0). The
+    sums are the two-pass path's (``slotsum_kernel``): groups of FC_GROUP neighbours summed in
+    fp32 from +0 in list order, the groups' sums added in order (VM_G closes a group),
+    one rounding to bf16 at the phase's end (VM_P: phase A's sum; VM_S: the step's last sum,
+    then its MFMAs; a step whose phase B is empty ends on phase A's last round with both
+    flags). The S event also names the next active step, whose weight fragments the kernel
+    loads then. Each point's rounds are padded to a multiple of VM_CHUNK."""
+    if cp not in (4, 8) or k_pad % 16:
+        raise ValueError(f"view-major tables need cp in (4, 8) and k_pad % 16 == 0, got {cp}, {k_pad}")
+    ptr = slot_ptr.numpy().astype(np.int64)
+    nbr = nbr_sorted.numpy().astype(np.int64)
+    n_out = ptr.shape[0]
+    ks, spk = k_pad // 16, 16 // cp
+    if ks >= VM_J_NONE:
+        raise ValueError(f"k_pad={k_pad} has more reduction steps than the event word holds")
+    cnt = np.zeros((n_out, ks * spk), np.int64)
+    beg = np.zeros((n_out, ks * spk), np.int64)
+    cnt[:, :n_ref] = ptr & 0xFFFF
+    beg[:, :n_ref] = ptr >> 16
+    phases = ((0, 2), (1, 3)) if cp == 4 else ((0, 1),)
+    pad = int(n_in)
+    idx_parts, ev_parts, off, j0 = [], [], [0], []
+    n_steps = 0
+    for t in range(n_out):
+        c_t, b_t = cnt[t].reshape(ks, spk), beg[t].reshape(ks, spk)
+        active = np.nonzero(c_t.sum(1))[0]
+        rows = ([], [])
+        evs = []
+        ends = []
+        for j in active:
+            for pi, qs in enumerate(phases):
+                m = [int(c_t[j, q]) for q in qs]
+                r = max(m)
+                if r == 0:
+                    continue
+                for hh in range(2):
+                    b = int(b_t[j, qs[hh]])
+                    rows[hh].extend(nbr[t, b:b + m[hh]].tolist())
+                    rows[hh].extend([pad] * (r - m[hh]))
+                e = [0] * r
+                for q in range(FC_GROUP - 1, r - 1, FC_GROUP):
+                    e[q] |= VM_G
+                if cp == 4 and pi == 0:
+                    e[-1] |= VM_P
+                evs.extend(e)
+            evs[-1] |= VM_S
+            ends.append(len(evs) - 1)
+        for i, er in enumerate(ends):
+            evs[er] |= (int(active[i + 1]) if i + 1 < len(active) else VM_J_NONE) << 3
+        n_r = -(-len(evs) // VM_CHUNK) * VM_CHUNK
+        fill = n_r - len(evs)
+        idx_parts.append(np.asarray(rows[0] + [pad] * fill + rows[1] + [pad] * fill, np.int64))
+        ev_parts.append(np.asarray(evs + [0] * fill, np.int64))
+        off.append(off[-1] + n_r)
+        j0.append(int(active[0]) if len(active) else -1)
+        n_steps += len(active)
+    idx = np.concatenate(idx_parts) if idx_parts else np.zeros(0, np.int64)
+    ev = np.concatenate(ev_parts) if ev_parts else np.zeros(0, np.int64)
+    return ViewMajorTables(torch.from_numpy(idx.astype(np.int32)),
+                           torch.from_numpy(ev.astype(np.uint16).view(np.int16)),
+                           torch.from_numpy(np.asarray(off, np.int32)), torch.from_numpy(np.asarray(j0, np.int32)),
+                           pad, n_steps)
+
+
+def view_major_weight(w_rows, cb):
+    """The view-major kernel's weight: fragments ``[k_pad / 16, n_blocks, 64, 8]`` of the
+    row-packed weight ``w_rows`` [c_out, k_pad] (bf16), 32-column blocks padded with zero
+    columns to a multiple of ``cb`` blocks: lane l of fragment (j, b) holds columns
+    16 j + 8 (l / 32) .. + 7 of row 32 b + l % 32, the MFMA B operand of step j and block b."""
+    c_out, k_pad = w_rows.shape
+    nb = -(-c_out // 32)
+    nb = -(-nb // cb) * cb
+    wp = torch.zeros(nb * 32, k_pad, dtype=w_rows.dtype, device=w_rows.device)
+    wp[:c_out] = w_rows
+    return wp.view(nb, 32, k_pad // 16, 2, 8).permute(2, 0, 3, 1, 4).contiguous().view(k_pad // 16, nb, 64, 8)
+
+
 def _row_offset(r):
     """Byte offset in the kernel's LDS of 16-byte part 0 of staged row ``r``: rows are 64
     bytes, and part q of row r sits at ``(64 r + 16 g(r)) ^ 16 q`` with

@@ -15,7 +15,8 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libfovi_hip.so")
 SOURCES = ["abi.hip", "sampler.hip", "knnconv.hip", "knnconv_v5.hip", "knnconv_fp8.hip", "quantize.hip",
-           "knnpool.hip", "knnconv_bwd.hip", "knn_tables.hip", "knnconv_dw.hip", "knnconv_fewc.hip"]
+           "knnpool.hip", "knnconv_bwd.hip", "knn_tables.hip", "knnconv_dw.hip", "knnconv_fewc.hip",
+           "knnconv_fewc_vm.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

@@ -1295,12 +1295,14 @@ extern "C" int fovi_knnconv_pack_weight(const float* w_ref, int64_t c_out, int64
 namespace fovi {
 
 // The few-channel bf16 path: a weight packed with w_c_slot = 4 or 8 >= c_in channels per slot and
-// channels-last input rows padded to w_c_slot channels.
+// input rows padded to w_c_slot channels: point-major (rows of one image adjacent, x_stride[2] ==
+// w_c_slot) or view-major (rows of one point for all images adjacent, x_stride[0] == w_c_slot).
 static bool few_channel_rows(const fovi_knnconv_args* a) {
   const int64_t cp = a->w_c_slot;
   return a->x_dtype == FOVI_BF16 && a->w_dtype == FOVI_BF16 && a->w_layout == FOVI_W_ROWS &&
-         (cp == 4 || cp == 8) && cp >= a->c_in && a->x_stride[1] == 1 && a->x_stride[2] == cp &&
-         a->x_stride[0] % cp == 0 && reinterpret_cast<uintptr_t>(a->x) % (2 * cp) == 0;
+         (cp == 4 || cp == 8) && cp >= a->c_in && a->x_stride[1] == 1 && a->x_stride[0] % cp == 0 &&
+         a->x_stride[2] % cp == 0 && (a->x_stride[2] == cp || a->x_stride[0] == cp) &&
+         reinterpret_cast<uintptr_t>(a->x) % (2 * cp) == 0;
 }
 
 }  // namespace fovi
@@ -1403,6 +1405,10 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
     // packed weight with padded slots: only the few-channel kernels read it
     const int cp = p.w_c_slot;
     if (few_channel_rows(a)) {
+      if (launch_knnconv_fewc_vm(p, a, cp, s)) {
+        note_path("bf16 few-channel view-major");
+        return check_launch("fovi_knnconv_fwd(bf16 few-channel view-major)");
+      }
       if (launch_knnconv_fewc(p, a, cp, s)) {
         note_path("bf16 few-channel fused");
         return check_launch("fovi_knnconv_fwd(bf16 few-channel fused)");
@@ -1420,7 +1426,7 @@ extern "C" int fovi_knnconv_fwd(const fovi_knnconv_args* a, void* stream) {
       note_path("bf16 few-channel");
       return check_launch("fovi_knnconv_fwd(bf16 small-c)");
     }
-    set_error("fovi_knnconv_fwd: w_c_slot=%d needs channels-last input rows padded to it", cp);
+    set_error("fovi_knnconv_fwd: w_c_slot=%d needs input rows padded to it (point- or view-major)", cp);
     return 1;
   }
   if (p.w_c_slot != p.C) {

@@ -538,7 +538,8 @@ static int launch_fewc_cp(const KnnParams& p, const FewcTables& ft, const FewcPl
 
 // 1 if launched, 0 if the fused kernel does not take this call (caller falls back).
 int launch_knnconv_fewc(const KnnParams& p, const fovi_knnconv_args* a, int cp, hipStream_t s) {
-  if (!a->fc_lo || !a->fc_span || !a->fc_item || !a->fc_comb || !a->fc_comb_off || a->y_dtype != FOVI_BF16)
+  if (!a->fc_lo || !a->fc_span || !a->fc_item || !a->fc_comb || !a->fc_comb_off || a->y_dtype != FOVI_BF16 ||
+      p.xs2 != cp)   // a tile stages a contiguous range of one image's rows
     return 0;
   const int kc = a->fc_chunk;
   if (a->fc_zero_row <= 0 || a->fc_zero_row > 0xffff || a->fc_pmax < 0 || a->fc_pmax > 0xfff ||

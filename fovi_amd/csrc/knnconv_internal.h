@@ -121,6 +121,8 @@ int launch_knnconv_fp8(const KnnParams& p, int out_t, hipStream_t s);
 // The fused few-channel kernel (knnconv_fewc.hip): 1 if it took the call, 0 if its tables are
 // absent or the tiling does not fit (the caller falls back).
 int launch_knnconv_fewc(const KnnParams& p, const fovi_knnconv_args* a, int cp, hipStream_t s);
+// 1 if launched, 0 if the view-major few-channel kernel does not take this call.
+int launch_knnconv_fewc_vm(const KnnParams& p, const fovi_knnconv_args* a, int cp, hipStream_t s);
 // 1 if the fragment-order kernel takes this call (see knnconv_v5.hip; f8:
 // e4m3 input and weight), 0 if not.
 int v5_applies(const KnnParams& p, int f8);

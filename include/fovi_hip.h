@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 31
+#define FOVI_ABI_VERSION 32
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -241,6 +241,32 @@ typedef struct fovi_knnconv_args {
   int32_t wide_tiles;         /* (w_layout = FOVI_W_MFMA) the collision-tile count nb the wide-layer
                                  tables were built for (tile_cent word 0 destinations); must equal
                                  fovi_knnconv_wide_tiles() of the table sizes, else the call fails */
+  /*
+   * The view-major few-channel kernel (optional; NULL vm_idx: not used). It takes bf16 input
+   * whose rows of one point for all images are adjacent, x_stride = (w_c_slot, 1, row stride
+   * s, a multiple of w_c_slot): element (b, c, n) at x[n * s + b * w_c_slot + c], channels
+   * >= c_in zero or ignored by zero weight columns, (n_in + 1) * s * 2 < 2^31, bf16 output.
+   * Reduction step j is columns 16 j .. 16 j + 15 of the row-packed weight. Per output point
+   * p, rounds vm_off[p] .. vm_off[p + 1] - 1 (R of them, a multiple of 8): half h of the MFMA
+   * lanes (h = 0: columns 8 h .. 8 h + 7 of a step) adds, in round q, input row
+   * vm_idx[2 * vm_off[p] + h * R + q] (rows >= n_in read as zeros) to a group sum, and the
+   * round's event vm_ev[vm_off[p] + q] (bit 0: add the group sum to the slot sum; bit 1: end
+   * of the step's first slot, w_c_slot = 4; bit 2: end of the step; bits 3-15 at a step's
+   * end: the point's next active step, 0x1FFF none) closes sums as knn_tables.view_major_tables
+   * describes; vm_j0[p] is the point's first active step (-1: none). vm_w holds the weight
+   * in fragment order: 16 bytes per lane at ((j * vm_nb + b) * 64 + lane) * 16, lane l
+   * holding columns 16 j + 8 (l / 32) .. + 7 of output channel 32 b + l % 32 (zero past c_out);
+   * vm_nb >= c_out / 32 blocks, a multiple of vm_cb (1, 2, 3, 4 or 6 blocks per wave).
+   * Sums, rounding and MFMA order are the two-pass path's: outputs equal it bit for bit for
+   * finite weights. Tables and weight 16-byte aligned.
+   */
+  const uint32_t* vm_idx;
+  const uint16_t* vm_ev;
+  const int32_t* vm_off;
+  const int32_t* vm_j0;
+  const void* vm_w;
+  int32_t vm_nb;
+  int32_t vm_cb;
 } fovi_knnconv_args;
 
 int fovi_knnconv_fwd(const fovi_knnconv_args* args, void* stream);
@@ -288,7 +314,7 @@ int fovi_knnconv_fwd_noalloc(const fovi_knnconv_args* args, void* stream);
 /*
  * The kernel path the last successful fovi_knnconv_fwd call on this thread
  * took ("" before any, or after a failed call): "f32", "bf16 v5", "fp8 v5",
- * "fp8 rows", "bf16 v4", "bf16 v2", "bf16 few-channel fused", "bf16 few-channel",
+ * "fp8 rows", "bf16 v4", "bf16 v2", "bf16 few-channel view-major", "bf16 few-channel fused", "bf16 few-channel",
  * "bf16 few-channel two-pass", "bf16 generic (rows)" or "bf16 generic". Diagnostics only (no
  * counterpart in the reference, whose forward is a fixed op sequence,
  * fovi/arch/knn.py:538-557); tests use it to check which kernel a layer

@@ -264,6 +264,61 @@ def test_few_channel_fused_takes_every_geometry_the_host_accepts(geom):
     assert accepted >= 6, accepted
 
 
+@pytest.mark.parametrize("res_in,res_out,k,side,c_in,c_out,bsz,act", [
+    (128, 16, 256, 16, 3, 384, 64, None),     # C4 patch embedding
+    (128, 16, 256, 16, 3, 384, 300, None),    # a partial block of 128 images
+    (64, 32, 49, None, 3, 64, 256, "relu"),   # C2 layer 1
+    (32, 16, 25, None, 5, 96, 40, None),      # eight-channel rows, three 32-channel blocks
+    (24, 12, 30, None, 4, 200, 33, "relu"),   # ragged: padding slots, 200 = 7 blocks (+1 zero block)
+])
+def test_view_major_kernel_equals_the_two_pass_path(res_in, res_out, k, side, c_in, c_out, bsz, act):
+    """Few-channel input written view-major (padded_input(..., view_major=True): the rows of
+    one point for all images adjacent) takes the view-major kernel; its output equals the
+    two-pass path on the same input and the point-major fused kernel on the same values bit for
+    bit (same grouped slot sums, same MFMA order; skipped steps add +0), and two images match
+    the oracle."""
+    from fovi_amd import _lib
+    layer = _layer(res_in, res_out, k, c_in, c_out, side, bias=True, seed=13)
+    n_in = layer.in_coords.shape[0]
+    x = torch.randn(bsz, c_in, n_in, generator=torch.Generator().manual_seed(14)).bfloat16()
+    buf, view = layer.padded_input(bsz, view_major=True)
+    assert buf.shape == (n_in, bsz, layer.padded_channels) and view.stride(0) == layer.padded_channels
+    buf[..., c_in:] = torch.nan          # padding channels must not leak into the result
+    view.copy_(x.cuda())
+    with torch.no_grad():
+        y = layer(view) if act is None else layer._launch(view, act)
+        assert _lib.knnconv_last_path() == "bf16 few-channel view-major"
+        layer.view_major_kernel = False
+        y_two = layer(view) if act is None else layer._launch(view, act)
+        assert _lib.knnconv_last_path() == "bf16 few-channel two-pass"
+        _, pm = layer.padded_input(bsz)
+        pm.copy_(x.cuda())
+        y_pm = layer(pm) if act is None else layer._launch(pm, act)
+        assert _lib.knnconv_last_path() == "bf16 few-channel fused"
+    assert torch.equal(y, y_two), "view-major and two-pass paths differ"
+    assert torch.equal(y, y_pm), "view-major and point-major kernels differ"
+    w = layer.weight.detach().cpu().bfloat16().float()
+    for b in (0, bsz - 1):
+        ref = _oracle(layer, x[b:b + 1], w)
+        if act == "relu":
+            ref = torch.relu(ref)
+        assert_close_rel(y[b:b + 1].float().cpu(), ref, 1e-2, f"image {b}")
+
+
+def test_view_major_kernel_is_not_used_with_non_finite_weights():
+    """A skipped reduction step adds nothing only for finite weights (0 x inf is NaN): with an
+    infinite weight the layer takes the two-pass path, which multiplies every column."""
+    from fovi_amd import _lib
+    layer = _layer(64, 32, 49, 3, 64, None, bias=False, seed=15)
+    with torch.no_grad():
+        layer.weight[0, 5] = float("inf")
+    _, view = layer.padded_input(4, view_major=True)
+    view.copy_(torch.rand(4, 3, layer.in_coords.shape[0]).bfloat16().cuda())
+    with torch.no_grad():
+        layer(view)
+    assert _lib.knnconv_last_path() == "bf16 few-channel two-pass"
+
+
 @pytest.mark.parametrize("geom", [(64, 256, 32), (128, 512, 64)])
 def test_few_channel_fused_c4_patch_embedding_geometry(geom):
     """C4 patch embedding (16384 -> 256 log-polar points, k = 256, 16 x 16 ref grid, 3 -> 384,

@@ -431,6 +431,103 @@ def test_few_channel_tables_rebuild_the_slot_sums(res_in, res_out, k, side, cp, 
         assert split > 0, "the C4 geometry has slots of more than FC_GROUP neighbours"
 
 
+def _grouped_slot_sum(rows, group):
+    """fp32 slot sum of bf16-valued rows in the two-pass path's order: groups of ``group``
+    summed from +0 in list order, the groups' sums added in order from +0."""
+    total = np.zeros(rows.shape[1:], np.float32)
+    for g0 in range(0, rows.shape[0], group):
+        part = np.zeros(rows.shape[1:], np.float32)
+        for r in rows[g0:g0 + group]:
+            part = (part + r).astype(np.float32)
+        total = (total + part).astype(np.float32)
+    return total
+
+
+@pytest.mark.parametrize("res_in,res_out,k,side,cp", [
+    (128, 16, 256, 16, 4),     # C4 patch embedding: foveal slots of up to 121 neighbours
+    (64, 32, 49, None, 4),     # C2 layer 1
+    (32, 16, 25, None, 8),     # eight-channel rows: one phase per step
+    (24, 12, 30, None, 4),     # ragged: padding slots in the last step
+])
+def test_view_major_tables_rebuild_the_slot_sums(res_in, res_out, k, side, cp):
+    """Emulates the view-major kernel's rounds in fp32 for 32 images at once: per point, each
+    lane half adds its round's input row (a padding row: zeros) to a group sum; the events close
+    groups, end phase A (its sum rounded to bf16 into A dwords 0-1) and end steps (the last sum
+    into the rest, then the step's columns are emitted) and name the next active step. The A
+    rows rebuilt this way equal the grouped fp32 slot sums of the CSR lists rounded to bf16 bit
+    for bit, skipped steps are exactly those with no neighbour, and every round's input row is
+    a real row or the padding row."""
+    import torch
+    from fovi_amd.arch import knn_tables as T
+    t = layer_tables(res_in, res_out, k, side=side)
+    V, n_in, n_out = t["V"], t["n_in"], t["n_out"]
+    k_pad = -(-V * cp // 64) * 64
+    ks, spk = k_pad // 16, 16 // cp
+    vt = T.view_major_tables(t["ptr"], t["nbr"], n_in, V, cp, k_pad)
+    idx = vt.idx.numpy().astype(np.int64)
+    ev = vt.ev.numpy().view(np.uint16).astype(np.int64)
+    off, j0 = vt.off.numpy(), vt.j0.numpy()
+    assert vt.pad == n_in and (np.diff(off) % T.VM_CHUNK == 0).all() and len(idx) == 2 * off[-1]
+    rng = np.random.default_rng(1)
+    B = 32
+    x = torch.from_numpy(rng.standard_normal((n_in, B, cp)).astype(np.float32)).bfloat16().float().numpy()
+    xpad = np.concatenate([x, np.zeros((1, B, cp), np.float32)])
+    bf = lambda a: torch.from_numpy(np.ascontiguousarray(a)).bfloat16().float().numpy()
+    ptr, nbr = t["ptr"].numpy(), t["nbr"].numpy()
+    n_active = 0
+    for p in range(n_out):
+        # the grouped slot sums of the CSR lists, [k_pad / cp slots, B, cp], rounded to bf16
+        want = np.zeros((ks * spk, B, cp), np.float32)
+        for v in range(V):
+            b, c = ptr[p, v] >> 16, ptr[p, v] & 0xFFFF
+            if c:
+                want[v] = bf(_grouped_slot_sum(x[nbr[p, b:b + c]], T.FC_GROUP))
+        active = [j for j in range(ks) if (ptr[p, j * spk:(j + 1) * spk] & 0xFFFF).sum() > 0
+                  and j * spk < V]
+        assert j0[p] == (active[0] if active else -1)
+        n_active += len(active)
+        got = np.zeros_like(want)
+        R = off[p + 1] - off[p]
+        rows = [idx[2 * off[p] + h * R: 2 * off[p] + (h + 1) * R] for h in range(2)]
+        assert all(((r >= 0) & (r <= n_in)).all() for r in rows)
+        part = np.zeros((2, B, cp), np.float32)
+        acc = np.zeros((2, B, cp), np.float32)
+        a = np.zeros((2, 2, B, cp), np.float32)        # [half, dword pair (phase), image, channel]
+        steps = iter(active)
+        j_cur = next(steps, None)
+        for q in range(R):
+            e = int(ev[off[p] + q])
+            if j_cur is None:
+                assert e == 0 and rows[0][q] == n_in and rows[1][q] == n_in, "tail rounds are padding"
+                continue
+            for h in range(2):
+                part[h] = (part[h] + xpad[rows[h][q]]).astype(np.float32)
+            if e & 7:
+                acc = (acc + part).astype(np.float32)
+                part[:] = 0
+                if e & (T.VM_P | T.VM_S):
+                    ph = 0 if (cp == 8 or e & T.VM_P) else 1
+                    a[:, ph] = bf(acc)
+                    acc[:] = 0
+                if e & T.VM_S:
+                    assert j_cur is not None, "a step end past the point's active steps"
+                    for h in range(2):
+                        if cp == 4:
+                            got[4 * j_cur + 2 * h] = a[h, 0]
+                            got[4 * j_cur + 2 * h + 1] = a[h, 1]
+                        else:
+                            got[2 * j_cur + h] = a[h, 0]
+                    a[:] = 0
+                    j_next = next(steps, None)
+                    assert (e >> 3) == (T.VM_J_NONE if j_next is None else j_next)
+                    j_cur = j_next
+        assert j_cur is None, "every active step ends"
+        np.testing.assert_array_equal(got, want)
+    assert n_active == vt.steps
+    if k == 256:
+        assert (np.diff(off) > 0).all() and vt.steps < n_out * ks
+
+
 @pytest.mark.parametrize("res_in,res_out,k,side", [(64, 64, 9, None), (64, 32, 49, None), (32, 16, 25, None),
                                                     (128, 16, 256, 16), (24, 12, 30, None)])
 def test_local_rf_slots_of_a_subset_equal_the_full_computation(res_in, res_out, k, side):
