@@ -363,6 +363,84 @@ __global__ __launch_bounds__(256) void sampler_rings_kernel(SamplerParams p, uin
     if (c < C) Elem<OutT>::store(out + o + c * static_cast<int32_t>(p.os1), st[c][tid]);
 }
 
+// View-major output (bf16 rows of 4 elements holding C <= 4 channels, the rows of one point for
+// all views adjacent: element (v, c, n) at n * os2 + v * 4 + c), the input layout of the
+// view-major few-channel kNN-conv kernel. A block samples the blocked path's 256 points (8
+// rings x 32 angles) for VM_VIEWS consecutive views, one view at a time with the blocked path's
+// tap code (same values bit for bit), staging each sample's channels in LDS; it then writes
+// each point's views as one run of VM_VIEWS rows (128 bytes), one row per lane: 4 lines per
+// store instruction, where one view per block would write 64 lines of 8 bytes. Only the C
+// channels of a row are written.
+constexpr int VM_VIEWS = 16;
+constexpr int VM_RS = 34;                      // LDS entries per ring of a view (32 + 2: banks)
+constexpr int VM_VS = 8 * VM_RS + 2;           // LDS entries per view
+
+template <typename InT, int MODE, int PAD, bool PAIRS, int NC, int CL = 0>
+__global__ __launch_bounds__(256) void sampler_rings_vm_kernel(SamplerParams p, uint32_t blocks_per_view,
+                                                               uint32_t n_views, uint32_t total_blocks,
+                                                               uint32_t padded_blocks) {
+  typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+  __shared__ u32x2v st[VM_VIEWS * VM_VS];
+  const uint32_t per = padded_blocks >> 3;
+  const uint32_t lb = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  if (lb >= total_blocks) return;
+  const uint32_t vg = lb / blocks_per_view;
+  const uint32_t b = lb - vg * blocks_per_view;
+  const uint32_t ring_len = static_cast<uint32_t>(p.ring_len);
+  const uint32_t segs = ring_len >> 5;
+  const uint32_t band = b / segs;
+  const uint32_t ring0 = band * 8, ang0 = (b - band * segs) * 32;
+  const int tid = threadIdx.x;
+  const uint32_t r_in = (tid & 63) >> 3, a_in = (tid >> 6) * 8 + (tid & 7);
+  const uint32_t pt = (ring0 + r_in) * ring_len + ang0 + a_in;
+  const int C = NC > 0 ? NC : static_cast<int>(p.C);
+  for (int vi = 0; vi < VM_VIEWS; ++vi) {
+    const uint32_t v = vg * VM_VIEWS + vi;
+    float val[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (v < n_views) {
+      const int64_t img = p.view_image ? static_cast<int64_t>(p.view_image[v]) : static_cast<int64_t>(v);
+      const Taps<InT, MODE, PAD, PAIRS, int32_t> t(p, v, pt);
+      if (img >= 0 && img < p.n_img) {
+        const InT* src = static_cast<const InT*>(p.img) + img * p.is0;
+        if constexpr (CL > 0) {
+          t.template values_cl<CL>(src, static_cast<int32_t>(p.W), val);
+        } else {
+          const int32_t is1 = static_cast<int32_t>(p.is1);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) val[c] = c < C ? t.value(src + c * is1) : 0.0f;
+        }
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (c >= C) val[c] = 0.0f;
+    st[vi * VM_VS + r_in * VM_RS + a_in] =
+        u32x2v{static_cast<uint32_t>(f32_to_bf16_bits(val[0])) | (static_cast<uint32_t>(f32_to_bf16_bits(val[1])) << 16),
+               static_cast<uint32_t>(f32_to_bf16_bits(val[2])) | (static_cast<uint32_t>(f32_to_bf16_bits(val[3])) << 16)};
+  }
+  __syncthreads();
+  uint16_t* out = static_cast<uint16_t*>(p.out);
+#pragma unroll
+  for (int k = 0; k < VM_VIEWS; ++k) {
+    const int q = k * 256 + tid;
+    const int ln = q >> 4, vi = q & (VM_VIEWS - 1);     // point of the block, view of the group
+    const uint32_t v = vg * VM_VIEWS + vi;
+    if (v < n_views) {
+      const uint32_t point = (ring0 + (ln >> 5)) * ring_len + ang0 + (ln & 31);
+      uint16_t* o = out + static_cast<int64_t>(point) * p.os2 + static_cast<int64_t>(v) * 4;
+      const u32x2v w = st[vi * VM_VS + (ln >> 5) * VM_RS + (ln & 31)];
+      // exactly channels 0 .. C - 1 of the row (a fourth element outside the view is not written)
+      if (C == 4) {
+        *reinterpret_cast<u32x2v*>(o) = w;
+      } else {
+        if (C >= 2) *reinterpret_cast<uint32_t*>(o) = w[0];
+        else o[0] = static_cast<uint16_t>(w[0]);
+        if (C == 3) o[2] = static_cast<uint16_t>(w[1]);
+      }
+    }
+  }
+}
+
 // Whether the blocked path applies (see sampler_rings_kernel).
 static bool rings_path(const SamplerParams& p, int64_t n_views) {
   if (!(p.ring_len > 0 && p.ring_len % 32 == 0 && p.N % (8 * p.ring_len) == 0 && p.C <= 4)) return false;
@@ -374,8 +452,44 @@ static bool rings_path(const SamplerParams& p, int64_t n_views) {
   return img_ext < lim && out_ext < lim && (p.N / 256) * n_views + 8 < lim;
 }
 
+// View-major bf16 output rows of 4 channels (see sampler_rings_vm_kernel): os0 == 4, os1 == 1,
+// 8-byte aligned rows.
+static bool vm_out(const SamplerParams& p, bool bf16_out) {
+  return bf16_out && p.os0 == 4 && p.os1 == 1 && p.os2 % 4 == 0 && p.os2 >= 4 &&
+         reinterpret_cast<uintptr_t>(p.out) % 8 == 0;
+}
+
+template <typename InT, int MODE, int PAD, bool PAIRS>
+static void launch_rings_vm(const SamplerParams& p, uint32_t bpv, int64_t n_views, hipStream_t s) {
+  const uint32_t groups = static_cast<uint32_t>((n_views + VM_VIEWS - 1) / VM_VIEWS);
+  const uint32_t total = bpv * groups, padded = (total + 7) / 8 * 8;
+  const uint32_t nv = static_cast<uint32_t>(n_views);
+  if constexpr (std::is_same<InT, uint16_t>::value) {
+    if (p.is1 == 1 && p.is3 == p.C && (p.C == 3 || (p.C == 4 && p.is2 % 2 == 0)) && p.is0 % 2 == 0 &&
+        reinterpret_cast<uintptr_t>(p.img) % 4 == 0) {
+      if (p.C == 3)
+        hipLaunchKernelGGL((sampler_rings_vm_kernel<InT, MODE, PAD, false, 3, 3>), dim3(padded), dim3(256), 0, s,
+                           p, bpv, nv, total, padded);
+      else
+        hipLaunchKernelGGL((sampler_rings_vm_kernel<InT, MODE, PAD, false, 4, 4>), dim3(padded), dim3(256), 0, s,
+                           p, bpv, nv, total, padded);
+      return;
+    }
+  }
+  if (p.C == 3)
+    hipLaunchKernelGGL((sampler_rings_vm_kernel<InT, MODE, PAD, PAIRS, 3>), dim3(padded), dim3(256), 0, s, p, bpv,
+                       nv, total, padded);
+  else
+    hipLaunchKernelGGL((sampler_rings_vm_kernel<InT, MODE, PAD, PAIRS, 0>), dim3(padded), dim3(256), 0, s, p, bpv,
+                       nv, total, padded);
+}
+
 template <typename InT, typename OutT, int MODE, int PAD, bool PAIRS>
 static void launch_rings(const SamplerParams& p, uint32_t bpv, uint32_t total, uint32_t padded, hipStream_t s) {
+  if (vm_out(p, std::is_same<OutT, uint16_t>::value)) {
+    launch_rings_vm<InT, MODE, PAD, PAIRS>(p, bpv, total / bpv, s);
+    return;
+  }
   dim3 grid(padded);
   // unit-stride channel planes with 16-byte aligned plane and view starts: whole 16-byte runs
   constexpr int64_t VPL = 16 / sizeof(OutT);

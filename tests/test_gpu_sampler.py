@@ -218,6 +218,32 @@ def test_channels_last_views_with_odd_row_stride(mode, channels):
     assert torch.equal(got, want)
 
 
+@pytest.mark.parametrize("mode", ["bilinear", "nearest"])
+@pytest.mark.parametrize("channels,layout,n_views", [(3, "planes", 37), (3, "channels_last", 40),
+                                                     (4, "channels_last", 16), (1, "planes", 20),
+                                                     (2, "planes", 19)])
+def test_view_major_output_equals_the_view_planes(mode, channels, layout, n_views):
+    """Output into a view-major buffer [N, V, 4] (the rows of one point for all views
+    adjacent, as the view-major kNN-conv kernel reads them; a sampler block writes 16 views of
+    a point as one run) holds the samples of the ordinary [V, C, N] output bit for bit, for
+    partial groups of 16 views, and leaves the row elements past the channels untouched."""
+    g = torch.Generator().manual_seed(16)
+    n_img = (n_views + 3) // 4
+    img = torch.rand(n_img, channels, 120, 131, generator=g).to(torch.bfloat16).cuda()
+    if layout == "channels_last":
+        img = img.contiguous(memory_format=torch.channels_last)
+    fix = 0.2 + 0.6 * torch.rand(n_views, 2, generator=g)
+    sizes = np.array([[120, 131]] * n_views)
+    vmap = torch.arange(n_views) // 4
+    s = GridSampler(16, 2.78, 64, device="cuda", mode=mode, style="logpolar", padding_mode="zeros")
+    want = s.sample_views(img, fix, sizes, view_image=vmap, out_dtype=torch.bfloat16)
+    buf = torch.full((64 * 64, n_views, 4), 7.0, dtype=torch.bfloat16, device="cuda")
+    view = buf.permute(1, 2, 0)[:, :channels]
+    s.sample_views(img, fix, sizes, view_image=vmap, out=view)
+    assert torch.equal(view, want)
+    assert (buf[..., channels:] == 7.0).all(), "elements past the channels were written"
+
+
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "tables.npz")
 
 
