@@ -263,8 +263,9 @@ def bench_c2(steps, warmup, dev):
     log(f"[c2] model built in {time.time() - t0:.1f}s")
     imgs = [cpu_rand((B, 3, S, S), i, dev=dev) for i in range(2)]
     views = sampler.prepare_views(torch.full((B, 2), 0.5), np.array([[S, S]] * B), B, dev)
-    # the sampler writes channels-last rows padded to 4 channels: the layout the first layer reads
-    _, feats = net.layers[0].conv.padded_input(B)
+    # the sampler writes the first layer's input rows padded to 4 channels, view-major (the rows
+    # of one sensor point for all images adjacent): the layout its view-major kernel reads
+    _, feats = net.layers[0].conv.padded_input(B, view_major=True)
     state = {"i": 0}
 
     def step():
@@ -304,13 +305,21 @@ def bench_c4_frontend(steps, warmup, dev):
     fix = 0.25 + 0.5 * torch.rand(B * Fx, 2, generator=gf)
     views = sampler.prepare_views(fix, np.array([[S, S]] * (B * Fx)), B, dev,
                                   view_image=torch.arange(B).repeat_interleave(Fx))
-    _, feats = pe.padded_input(B * Fx)
+    # the sampler writes the patch embedding's input view-major (the layout of its view-major
+    # kernel); the point-major layout ([views, points, 4], the point-tile kernel) is timed too
+    _, feats = pe.padded_input(B * Fx, view_major=True)
+    _, feats_pm = pe.padded_input(B * Fx)
     state = {"i": 0}
 
     def step():
         sampler.sample_views(imgs[state["i"] & 1], out=feats, views=views)
         state["i"] += 1
         return pe(feats)
+
+    def step_pm():
+        sampler.sample_views(imgs[state["i"] & 1], out=feats_pm, views=views)
+        state["i"] += 1
+        return pe(feats_pm)
 
     # the drop-in policy path: near-centre fixations drawn on the host (numpy, the reference's
     # draw order), all B x F views sampled in one launch
@@ -329,12 +338,16 @@ def bench_c4_frontend(steps, warmup, dev):
     with torch.no_grad():
         ms = time_steps(step, steps, warmup)
         ms_pe = time_steps(lambda: pe(feats), steps, warmup)
+        ms_pm = time_steps(step_pm, steps, warmup)
+        ms_pe_pm = time_steps(lambda: pe(feats_pm), steps, warmup)
         ms_pol = time_steps(policy_step, steps, warmup)
     flops = 2.0 * B * Fx * 256 * 384 * 3 * 256
     log(f"[c4] {ms:.3f} ms/step  {B / (ms * 1e-3):.0f} images/s  (patch embed alone {ms_pe:.3f} ms = "
-        f"{flops / (ms_pe * 1e-3) / 1e12:.1f} TFLOP/s; policy draws + fused views {ms_pol:.3f} ms)")
+        f"{flops / (ms_pe * 1e-3) / 1e12:.1f} TFLOP/s; point-major input {ms_pm:.3f} ms, patch embed "
+        f"{ms_pe_pm:.3f} ms; policy draws + fused views {ms_pol:.3f} ms)")
     return dict(ms=ms, images_per_s=B / (ms * 1e-3), ms_patch_embed=ms_pe,
-                patch_embed_tflops=flops / (ms_pe * 1e-3) / 1e12, ms_policy=ms_pol)
+                patch_embed_tflops=flops / (ms_pe * 1e-3) / 1e12, ms_policy=ms_pol,
+                ms_point_major=ms_pm, ms_patch_embed_point_major=ms_pe_pm)
 
 
 def copy_probe(dev, mib=256, reps=3):
@@ -544,11 +557,14 @@ def main():
                               "GFLOP/batch": round(c2["gflop"], 2), "TFLOP/s": round(c2["tflops"], 1)}
     if c4e is not None:
         line["c4_frontend"] = {"workload": "C4: 128 images 3x512x512 bf16 x 4 fixations -> nearest sampler "
-                                           "(16384 pts) -> kNN patch embed 3->384, k=256, 256 tokens",
+                                           "(16384 pts) -> kNN patch embed 3->384, k=256, 256 tokens; "
+                                           "sampler output view-major, the patch embedding's view-major kernel",
                                "images/s": round(c4e["images_per_s"], 1), "ms": round(c4e["ms"], 4),
                                "patch_embed_ms": round(c4e["ms_patch_embed"], 4),
                                "patch_embed_TFLOP/s": round(c4e["patch_embed_tflops"], 1),
-                               "patch_embed_traffic": measured_traffic("knnconv_fewc_kernel<c4>"),
+                               "point_major_ms": round(c4e["ms_point_major"], 4),
+                               "point_major_patch_embed_ms": round(c4e["ms_patch_embed_point_major"], 4),
+                               "patch_embed_traffic": measured_traffic("knnconv_fewc_vm_kernel<c4>"),
                                "policy_ms": round(c4e["ms_policy"], 4),
                                "policy_note": "MultiRandomSaccadePolicy (near-centre 0.25, eval) forward: host "
                                               "draws + one sampler launch for the 512 views, bf16 out"}

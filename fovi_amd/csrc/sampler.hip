@@ -366,16 +366,17 @@ __global__ __launch_bounds__(256) void sampler_rings_kernel(SamplerParams p, uin
 // View-major output (bf16 rows of 4 elements holding C <= 4 channels, the rows of one point for
 // all views adjacent: element (v, c, n) at n * os2 + v * 4 + c), the input layout of the
 // view-major few-channel kNN-conv kernel. A block samples the blocked path's 256 points (8
-// rings x 32 angles) for VM_VIEWS consecutive views, one view at a time with the blocked path's
-// tap code (same values bit for bit), staging each sample's channels in LDS; it then writes
-// each point's views as one run of VM_VIEWS rows (128 bytes), one row per lane: 4 lines per
-// store instruction, where one view per block would write 64 lines of 8 bytes. Only the C
-// channels of a row are written.
-constexpr int VM_VIEWS = 16;
+// rings x 32 angles) for VM_VIEWS consecutive views with the blocked path's tap code (same
+// values bit for bit), one view after another, staging each sample's channels in LDS; it then
+// writes each point's views as one run of VM_VIEWS rows, one row per lane. Only the C channels
+// of a row are written. More views per block write longer runs but leave fewer blocks: 16
+// views when that still gives 2048 blocks, else 4 (C4 nearest, 512 views of 16384 points:
+// 16 views 82 us, 8 92, 4 99, 2 115; C2 bilinear, 256 views of 4096 points: 4 views 27 us,
+// 8 29, 16 41).
 constexpr int VM_RS = 34;                      // LDS entries per ring of a view (32 + 2: banks)
 constexpr int VM_VS = 8 * VM_RS + 2;           // LDS entries per view
 
-template <typename InT, int MODE, int PAD, bool PAIRS, int NC, int CL = 0>
+template <typename InT, int MODE, int PAD, bool PAIRS, int NC, int CL = 0, int VM_VIEWS = 16>
 __global__ __launch_bounds__(256) void sampler_rings_vm_kernel(SamplerParams p, uint32_t blocks_per_view,
                                                                uint32_t n_views, uint32_t total_blocks,
                                                                uint32_t padded_blocks) {
@@ -394,6 +395,8 @@ __global__ __launch_bounds__(256) void sampler_rings_vm_kernel(SamplerParams p, 
   const uint32_t r_in = (tid & 63) >> 3, a_in = (tid >> 6) * 8 + (tid & 7);
   const uint32_t pt = (ring0 + r_in) * ring_len + ang0 + a_in;
   const int C = NC > 0 ? NC : static_cast<int>(p.C);
+  // the views' gathers in flight together
+#pragma unroll
   for (int vi = 0; vi < VM_VIEWS; ++vi) {
     const uint32_t v = vg * VM_VIEWS + vi;
     float val[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -423,7 +426,7 @@ __global__ __launch_bounds__(256) void sampler_rings_vm_kernel(SamplerParams p, 
 #pragma unroll
   for (int k = 0; k < VM_VIEWS; ++k) {
     const int q = k * 256 + tid;
-    const int ln = q >> 4, vi = q & (VM_VIEWS - 1);     // point of the block, view of the group
+    const int ln = q / VM_VIEWS, vi = q % VM_VIEWS;      // point of the block, view of the group
     const uint32_t v = vg * VM_VIEWS + vi;
     if (v < n_views) {
       const uint32_t point = (ring0 + (ln >> 5)) * ring_len + ang0 + (ln & 31);
@@ -459,29 +462,37 @@ static bool vm_out(const SamplerParams& p, bool bf16_out) {
          reinterpret_cast<uintptr_t>(p.out) % 8 == 0;
 }
 
-template <typename InT, int MODE, int PAD, bool PAIRS>
-static void launch_rings_vm(const SamplerParams& p, uint32_t bpv, int64_t n_views, hipStream_t s) {
-  const uint32_t groups = static_cast<uint32_t>((n_views + VM_VIEWS - 1) / VM_VIEWS);
+template <typename InT, int MODE, int PAD, bool PAIRS, int VMV>
+static void launch_rings_vm_v(const SamplerParams& p, uint32_t bpv, int64_t n_views, hipStream_t s) {
+  const uint32_t groups = static_cast<uint32_t>((n_views + VMV - 1) / VMV);
   const uint32_t total = bpv * groups, padded = (total + 7) / 8 * 8;
   const uint32_t nv = static_cast<uint32_t>(n_views);
   if constexpr (std::is_same<InT, uint16_t>::value) {
     if (p.is1 == 1 && p.is3 == p.C && (p.C == 3 || (p.C == 4 && p.is2 % 2 == 0)) && p.is0 % 2 == 0 &&
         reinterpret_cast<uintptr_t>(p.img) % 4 == 0) {
       if (p.C == 3)
-        hipLaunchKernelGGL((sampler_rings_vm_kernel<InT, MODE, PAD, false, 3, 3>), dim3(padded), dim3(256), 0, s,
-                           p, bpv, nv, total, padded);
+        hipLaunchKernelGGL((sampler_rings_vm_kernel<InT, MODE, PAD, false, 3, 3, VMV>), dim3(padded), dim3(256), 0,
+                           s, p, bpv, nv, total, padded);
       else
-        hipLaunchKernelGGL((sampler_rings_vm_kernel<InT, MODE, PAD, false, 4, 4>), dim3(padded), dim3(256), 0, s,
-                           p, bpv, nv, total, padded);
+        hipLaunchKernelGGL((sampler_rings_vm_kernel<InT, MODE, PAD, false, 4, 4, VMV>), dim3(padded), dim3(256), 0,
+                           s, p, bpv, nv, total, padded);
       return;
     }
   }
   if (p.C == 3)
-    hipLaunchKernelGGL((sampler_rings_vm_kernel<InT, MODE, PAD, PAIRS, 3>), dim3(padded), dim3(256), 0, s, p, bpv,
-                       nv, total, padded);
+    hipLaunchKernelGGL((sampler_rings_vm_kernel<InT, MODE, PAD, PAIRS, 3, 0, VMV>), dim3(padded), dim3(256), 0, s, p,
+                       bpv, nv, total, padded);
   else
-    hipLaunchKernelGGL((sampler_rings_vm_kernel<InT, MODE, PAD, PAIRS, 0>), dim3(padded), dim3(256), 0, s, p, bpv,
-                       nv, total, padded);
+    hipLaunchKernelGGL((sampler_rings_vm_kernel<InT, MODE, PAD, PAIRS, 0, 0, VMV>), dim3(padded), dim3(256), 0, s, p,
+                       bpv, nv, total, padded);
+}
+
+template <typename InT, int MODE, int PAD, bool PAIRS>
+static void launch_rings_vm(const SamplerParams& p, uint32_t bpv, int64_t n_views, hipStream_t s) {
+  if (static_cast<int64_t>(bpv) * ((n_views + 15) / 16) >= 2048)
+    launch_rings_vm_v<InT, MODE, PAD, PAIRS, 16>(p, bpv, n_views, s);
+  else
+    launch_rings_vm_v<InT, MODE, PAD, PAIRS, 4>(p, bpv, n_views, s);
 }
 
 template <typename InT, typename OutT, int MODE, int PAD, bool PAIRS>

@@ -219,14 +219,16 @@ def test_channels_last_views_with_odd_row_stride(mode, channels):
 
 
 @pytest.mark.parametrize("mode", ["bilinear", "nearest"])
-@pytest.mark.parametrize("channels,layout,n_views", [(3, "planes", 37), (3, "channels_last", 40),
-                                                     (4, "channels_last", 16), (1, "planes", 20),
-                                                     (2, "planes", 19)])
-def test_view_major_output_equals_the_view_planes(mode, channels, layout, n_views):
+@pytest.mark.parametrize("channels,layout,n_views,res", [(3, "planes", 37, 64), (3, "channels_last", 40, 64),
+                                                         (4, "channels_last", 16, 64), (1, "planes", 20, 64),
+                                                         (2, "planes", 19, 64), (3, "planes", 517, 128),
+                                                         (3, "channels_last", 512, 128)])
+def test_view_major_output_equals_the_view_planes(mode, channels, layout, n_views, res):
     """Output into a view-major buffer [N, V, 4] (the rows of one point for all views
-    adjacent, as the view-major kNN-conv kernel reads them; a sampler block writes 16 views of
-    a point as one run) holds the samples of the ordinary [V, C, N] output bit for bit, for
-    partial groups of 16 views, and leaves the row elements past the channels untouched."""
+    adjacent, as the view-major kNN-conv kernel reads them; a sampler block writes 4 or 16
+    views of a point as one run, 16 at the C4 size) holds the samples of the ordinary
+    [V, C, N] output bit for bit, for partial groups of views, and leaves the row elements past
+    the channels untouched."""
     g = torch.Generator().manual_seed(16)
     n_img = (n_views + 3) // 4
     img = torch.rand(n_img, channels, 120, 131, generator=g).to(torch.bfloat16).cuda()
@@ -235,9 +237,9 @@ def test_view_major_output_equals_the_view_planes(mode, channels, layout, n_view
     fix = 0.2 + 0.6 * torch.rand(n_views, 2, generator=g)
     sizes = np.array([[120, 131]] * n_views)
     vmap = torch.arange(n_views) // 4
-    s = GridSampler(16, 2.78, 64, device="cuda", mode=mode, style="logpolar", padding_mode="zeros")
+    s = GridSampler(16, 2.78, res, device="cuda", mode=mode, style="logpolar", padding_mode="zeros")
     want = s.sample_views(img, fix, sizes, view_image=vmap, out_dtype=torch.bfloat16)
-    buf = torch.full((64 * 64, n_views, 4), 7.0, dtype=torch.bfloat16, device="cuda")
+    buf = torch.full((res * res, n_views, 4), 7.0, dtype=torch.bfloat16, device="cuda")
     view = buf.permute(1, 2, 0)[:, :channels]
     s.sample_views(img, fix, sizes, view_image=vmap, out=view)
     assert torch.equal(view, want)
