@@ -370,9 +370,10 @@ __global__ __launch_bounds__(256) void sampler_rings_kernel(SamplerParams p, uin
 // values bit for bit), one view after another, staging each sample's channels in LDS; it then
 // writes each point's views as one run of VM_VIEWS rows, one row per lane. Only the C channels
 // of a row are written. More views per block write longer runs but leave fewer blocks: 16
-// views when that still gives 2048 blocks, else 4 (C4 nearest, 512 views of 16384 points:
-// 16 views 82 us, 8 92, 4 99, 2 115; C2 bilinear, 256 views of 4096 points: 4 views 27 us,
-// 8 29, 16 41).
+// views when that still gives 2048 blocks, else 4 (C4 nearest, 512 views of 16384 points,
+// images alternating between two sets: 16 views 123 us, 8 128, 4 141; warm images 82, 92,
+// 99; C2 bilinear, 256 views of 4096 points: 4 views 30 us, 8 32; warm 16 views 41). Unrolling
+// the view loop changes nothing measurable.
 constexpr int VM_RS = 34;                      // LDS entries per ring of a view (32 + 2: banks)
 constexpr int VM_VS = 8 * VM_RS + 2;           // LDS entries per view
 
@@ -395,8 +396,6 @@ __global__ __launch_bounds__(256) void sampler_rings_vm_kernel(SamplerParams p, 
   const uint32_t r_in = (tid & 63) >> 3, a_in = (tid >> 6) * 8 + (tid & 7);
   const uint32_t pt = (ring0 + r_in) * ring_len + ang0 + a_in;
   const int C = NC > 0 ? NC : static_cast<int>(p.C);
-  // the views' gathers in flight together
-#pragma unroll
   for (int vi = 0; vi < VM_VIEWS; ++vi) {
     const uint32_t v = vg * VM_VIEWS + vi;
     float val[4] = {0.0f, 0.0f, 0.0f, 0.0f};
