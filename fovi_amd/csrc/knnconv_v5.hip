@@ -286,6 +286,12 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
     E::acc(a, lds16(smem, ((ce[2] >> 16) << SH) ^ pq));
     return a;
   };
+  auto unit_sum2 = [&](const u32x4 ce, uint32_t pq) {
+    Sum a = {};
+    E::acc(a, lds16(smem, ((ce[1] & 0xffffu) << SH) ^ pq));
+    E::acc(a, lds16(smem, ((ce[1] >> 16) << SH) ^ pq));
+    return a;
+  };
   auto unit_rest = [&](Sum& a, const u32x4 ce, uint32_t pq) {
     if (((ce[0] >> 16) & 0xffu) > 4) {
       E::acc(a, lds16(smem, ((ce[3] & 0xffffu) << SH) ^ pq));
@@ -361,7 +367,25 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
   // with more than four neighbours finish after the MFMAs.
   // stream position (units) of the end of slot position i, clamped to the tile's entries so
   // that inconsistent caller tables cannot run the stream past them
-  auto upos = [&](int i) { return 4 * min(coff[i], p.cent_stride); };
+  // e4m3: the slot bounds live in two VGPRs, 16 bits each (lane l of c_lo: coff[2l] and
+  // coff[2l + 1]; c_hi: the next 128), read with v_readlane at a uniform index, so the bounds
+  // cost no LDS read and wait inside the MFMA block (C5 -2%; bf16 gains nothing from it). The
+  // bounds fit 16 bits: 16-byte entries within 160 KB of LDS number fewer than 2^14.
+  uint32_t c_lo = 0u, c_hi = 0u;
+  if constexpr (F8) {
+    auto ent = [&](int i) { return i <= V ? static_cast<uint32_t>(min(coff[i], p.cent_stride)) : 0u; };
+    c_lo = ent(2 * lane) | (ent(2 * lane + 1) << 16);
+    c_hi = ent(128 + 2 * lane) | (ent(129 + 2 * lane) << 16);
+  }
+  auto upos = [&](int i) {
+    if constexpr (F8) {
+      const uint32_t lo = __builtin_amdgcn_readlane(c_lo, (i >> 1) & 63);
+      const uint32_t hi = __builtin_amdgcn_readlane(c_hi, (i >> 1) & 63);
+      return static_cast<int>(4u * (((i < 128 ? lo : hi) >> ((i & 1) * 16)) & 0xffffu));
+    } else {
+      return 4 * min(coff[i], p.cent_stride);
+    }
+  };
   int bpos = upos(1);
   build_heavy();
   build_range(0, bpos, true);
@@ -410,7 +434,14 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
 #pragma unroll
     for (int i = 0; i < 4; ++i) enxt[i] = srcs[vn * V5_MT + rowm[i]];
 
-    Sum sum = unit_sum4(ce, pq);
+    // e4m3: rows 1-2 of the unit are summed in the MFMA block, rows 3-4 after it only when a
+    // unit of this wave has more than two (a uniform branch; C5 -3%: 58% of the C5 waves'
+    // units have two rows at most). The sum of e4m3 values is exact in fp32, and the skipped
+    // zero rows would add +0 to a sum that is never -0: the same bits either way. bf16: the
+    // exposed adds of the other waves cost more than the skipped ones save (C3 +2%).
+    const bool wave_full = !F8 || __builtin_amdgcn_ballot_w64(((ce[0] >> 16) & 0xffu) > 2u) != 0;
+    Sum sum;
+    if constexpr (F8) sum = unit_sum2(ce, pq); else sum = unit_sum4(ce, pq);
 
     if constexpr (F8) {
       // one 32x32x64 e4m3 MFMA per block (unit scales); lane operands: 32
@@ -456,7 +487,15 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
       __builtin_amdgcn_sched_group_barrier(0x008, 12, 0);
     }
 
-    unit_rest(sum, ce, pq);
+    if constexpr (F8) {
+      if (wave_full) {
+        E::acc(sum, lds16(smem, ((ce[2] & 0xffffu) << SH) ^ pq));
+        E::acc(sum, lds16(smem, ((ce[2] >> 16) << SH) ^ pq));
+        unit_rest(sum, ce, pq);
+      }
+    } else {
+      unit_rest(sum, ce, pq);
+    }
     *reinterpret_cast<u32x4*>(smem + (((ce[0] >> 16) & 0xffu) ? unit_dst(ce, pq) : trash)) = E::pack(sum);
     bpos = min(bpos + 256, lim);
     ce = read_ce(bpos, lim_n);
