@@ -14,7 +14,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfovi_hip.so")
 
-ABI_VERSION = 32
+ABI_VERSION = 33
 F32, BF16, F8E4M3 = 0, 1, 2
 NEAREST, BILINEAR = 0, 1
 PAD_ZEROS, PAD_BORDER = 0, 1

@@ -931,7 +931,9 @@ def few_channel_lds_bytes(tables, c_out, cp):
 # lane gathers its image's rows with one load per neighbour.
 VM_CHUNK = 8           # rounds per event / index load of the kernel
 VM_G, VM_P, VM_S = 1, 2, 4   # event flags: close a group of FC_GROUP; end of phase A; end of the step
-VM_J_NONE = 0x1FFF     # no next step
+VM_X, VM_Q = 8, 16     # step pairings (cp = 4): exchange slots 1 and 2 between the halves; half 1 phases swapped
+VM_JSHIFT = 5          # the next step's index sits in bits 5-15 of a step's last event
+VM_J_NONE = 0x7FF      # no next step
 
 
 class ViewMajorTables(NamedTuple):
@@ -947,17 +949,24 @@ def view_major_tables(slot_ptr, nbr_sorted, n_in, n_ref, cp, k_pad):
     """Tables of the view-major few-channel kernel from the CSR lists (``csr_tables``).
 
     Reduction step j covers columns 16 j .. 16 j + 15, i.e. slots ``16 / cp * j ..``; lane half h
-    of an MFMA block holds columns 8 h .. 8 h + 7 of it: for cp = 4 slots 4j + 2h (phase A) and
-    4j + 2h + 1 (phase B), for cp = 8 slot 2j + h (one phase). A point's steps with no neighbour
-    in any of their slots are left out. For each active step and phase the kernel runs
-    max(count of half 0's slot, count of half 1's slot) rounds; in round q each half adds
-    neighbour q of its slot's list (CSR order) or, past its count, a padding row (+0). The
-    sums are the two-pass path's (``slotsum_kernel``): groups of FC_GROUP neighbours summed in
-    fp32 from +0 in list order, the groups' sums added in order (VM_G closes a group),
-    one rounding to bf16 at the phase's end (VM_P: phase A's sum; VM_S: the step's last sum,
-    then its MFMAs; a step whose phase B is empty ends on phase A's last round with both
-    flags). The S event also names the next active step, whose weight fragments the kernel
-    loads then. Each point's rounds are padded to a multiple of VM_CHUNK."""
+    of an MFMA block holds columns 8 h .. 8 h + 7 of it when the step's MFMAs run: for cp = 4
+    slots 4j + 2h and 4j + 2h + 1, for cp = 8 slot 2j + h (one phase). A point's steps with no
+    neighbour in any of their slots are left out. For cp = 4 a step's four slots s0..s3 are
+    summed in two phases, each pairing a slot of half 0 with one of half 1; per point and step
+    the pairing with the fewest rounds is taken (ties: the first):
+      (s0|s2, s1|s3): the halves sum their own slots;
+      (s0|s3, s1|s2), VM_Q: half 1 puts phase A's sum in its second slot, phase B's in its first;
+      (s0|s1, s2|s3), VM_X: after the step's last sum half 0's second slot (s2) and half 1's
+        first (s1) change halves (v_permlane32_swap).
+    For each active step and phase the kernel runs max(count of half 0's slot, count of half 1's
+    slot) rounds; in round q each half adds neighbour q of its slot's list (CSR order) or, past
+    its count, a padding row (+0). The sums are the two-pass path's (``slotsum_kernel``): groups
+    of FC_GROUP neighbours summed in fp32 from +0 in list order, the groups' sums added in order
+    (VM_G closes a group), one rounding to bf16 at the phase's end (VM_P: phase A's sum; VM_S:
+    the step's last sum, then its MFMAs; a step whose phase B is empty ends on phase A's last
+    round with both flags); VM_Q and VM_X ride on those events. The S event also names the next
+    active step (bits VM_JSHIFT..15), whose weight fragments the kernel loads then. Each
+    point's rounds are padded to a multiple of VM_CHUNK."""
     if cp not in (4, 8) or k_pad % 16:
         raise ValueError(f"view-major tables need cp in (4, 8) and k_pad % 16 == 0, got {cp}, {k_pad}")
     ptr = slot_ptr.numpy().astype(np.int64)
@@ -970,7 +979,9 @@ def view_major_tables(slot_ptr, nbr_sorted, n_in, n_ref, cp, k_pad):
     beg = np.zeros((n_out, ks * spk), np.int64)
     cnt[:, :n_ref] = ptr & 0xFFFF
     beg[:, :n_ref] = ptr >> 16
-    phases = ((0, 2), (1, 3)) if cp == 4 else ((0, 1),)
+    # (phases, flags) per pairing: phase = (slot of half 0, slot of half 1)
+    pairings = ((((0, 2), (1, 3)), 0), (((0, 3), (1, 2)), VM_Q), (((0, 1), (2, 3)), VM_X)) if cp == 4 \
+        else ((((0, 1),), 0),)
     pad = int(n_in)
     idx_parts, ev_parts, off, j0 = [], [], [0], []
     n_steps = 0
@@ -981,6 +992,8 @@ def view_major_tables(slot_ptr, nbr_sorted, n_in, n_ref, cp, k_pad):
         evs = []
         ends = []
         for j in active:
+            cost = [sum(max(int(c_t[j, a]), int(c_t[j, b])) for a, b in ph) for ph, _ in pairings]
+            phases, flag = pairings[int(np.argmin(cost))]
             for pi, qs in enumerate(phases):
                 m = [int(c_t[j, q]) for q in qs]
                 r = max(m)
@@ -994,12 +1007,12 @@ def view_major_tables(slot_ptr, nbr_sorted, n_in, n_ref, cp, k_pad):
                 for q in range(FC_GROUP - 1, r - 1, FC_GROUP):
                     e[q] |= VM_G
                 if cp == 4 and pi == 0:
-                    e[-1] |= VM_P
+                    e[-1] |= VM_P | flag
                 evs.extend(e)
-            evs[-1] |= VM_S
+            evs[-1] |= VM_S | flag
             ends.append(len(evs) - 1)
         for i, er in enumerate(ends):
-            evs[er] |= (int(active[i + 1]) if i + 1 < len(active) else VM_J_NONE) << 3
+            evs[er] |= (int(active[i + 1]) if i + 1 < len(active) else VM_J_NONE) << VM_JSHIFT
         n_r = -(-len(evs) // VM_CHUNK) * VM_CHUNK
         fill = n_r - len(evs)
         idx_parts.append(np.asarray(rows[0] + [pad] * fill + rows[1] + [pad] * fill, np.int64))

@@ -18,7 +18,12 @@
 //    round (uniform, read with scalar loads) close a group of FC_GROUP (added to the slot
 //    sum), end phase A (the slot sum rounded once to bf16 into A operand dwords 0-1) or end the
 //    step (the last sum into the remaining dwords, then CB MFMAs 32x32x16 in ascending column
-//    order, and the next active step's weight fragments are loaded). The slot sums are the
+//    order, and the next active step's weight fragments are loaded). With four-channel rows a
+//    step's two phases pair a slot of each half; the table picks per point and step the
+//    pairing with the fewest rounds (C4 patch embedding: 201 -> 168 rounds per point), and
+//    the step's events say where the sums go: VM_Q, half 1 writes phase A's sum into its
+//    second slot; VM_X, half 0's second slot and half 1's first change halves at the step's
+//    end (v_permlane32_swap), so the MFMA operands are those of the natural pairing. The slot sums are the
 //    two-pass path's (slotsum_kernel) bit for bit; a skipped step's columns are zero in its A
 //    rows, whose products add +0 to an accumulator that is never -0, so the outputs equal the
 //    dense GEMM's for finite weights.
@@ -33,7 +38,8 @@ namespace fovi {
 
 namespace {
 
-constexpr uint32_t VM_G = 1u, VM_P = 2u, VM_S = 4u, VM_J_NONE = 0x1FFFu;
+constexpr uint32_t VM_G = 1u, VM_P = 2u, VM_S = 4u, VM_X = 8u, VM_Q = 16u;
+constexpr uint32_t VM_JSHIFT = 5u, VM_J_NONE = 0x7FFu;
 constexpr int VM_WAVES = 4;                  // waves (groups of 32 images) per workgroup
 constexpr int VM_IMAGES = VM_WAVES * 32;
 
@@ -91,6 +97,7 @@ __global__ __launch_bounds__(VM_WAVES * 64, 2) void knnconv_fewc_vm_kernel(KnnPa
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = lane >> 5;
+  const bool h1 = h != 0;
   const int64_t v0 = vb * VM_IMAGES + wave * 32;     // the wave's first image
   if (v0 >= p.B) return;                            // no barrier follows: whole waves may leave
   const uint32_t row_bytes = static_cast<uint32_t>(p.xs2) * 2u;
@@ -139,11 +146,12 @@ __global__ __launch_bounds__(VM_WAVES * 64, 2) void knnconv_fewc_vm_kernel(KnnPa
       for (int c = 0; c < CP; ++c) { sum[c] += part[c]; part[c] = 0.0f; }
       if (e & (VM_P | VM_S)) {
         if constexpr (CP == 4) {
-          // phase A's slot into dwords 0-1, phase B's into 2-3 (selects: no indexed registers)
+          // phase A's slot into dwords 0-1, phase B's into 2-3; in half 1 the other way round
+          // under VM_Q (selects: no indexed registers)
           const uint32_t lo = cvt_pk_bf16(sum[0], sum[1]) & cm[0], hi = cvt_pk_bf16(sum[2], sum[3]) & cm[1];
-          const bool pa = (e & VM_P) != 0;
-          a0 = pa ? lo : a0; a1 = pa ? hi : a1;
-          a2 = pa ? a2 : lo; a3 = pa ? a3 : hi;
+          const bool first = ((e & VM_P) != 0) != (h1 && (e & VM_Q) != 0);
+          a0 = first ? lo : a0; a1 = first ? hi : a1;
+          a2 = first ? a2 : lo; a3 = first ? a3 : hi;
         } else {
           a0 = cvt_pk_bf16(sum[0], sum[1]) & cm[0]; a1 = cvt_pk_bf16(sum[2], sum[3]) & cm[1];
           a2 = cvt_pk_bf16(sum[4], sum[5]) & cm[2]; a3 = cvt_pk_bf16(sum[6], sum[7]) & cm[3];
@@ -152,12 +160,19 @@ __global__ __launch_bounds__(VM_WAVES * 64, 2) void knnconv_fewc_vm_kernel(KnnPa
         for (int c = 0; c < CP; ++c) sum[c] = 0.0f;
       }
       if (e & VM_S) {
+        if constexpr (CP == 4) {
+          if (e & VM_X) {   // half 0's second slot and half 1's first change halves
+            const auto s0 = __builtin_amdgcn_permlane32_swap(a0, a2, false, false);
+            const auto s1 = __builtin_amdgcn_permlane32_swap(a1, a3, false, false);
+            a0 = s0[0]; a2 = s0[1]; a1 = s1[0]; a3 = s1[1];
+          }
+        }
         const bf16x8 a = __builtin_bit_cast(bf16x8, u32x4{a0, a1, a2, a3});
 #pragma unroll
         for (int b = 0; b < CB; ++b)
           acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, __builtin_bit_cast(bf16x8, wf[b]), acc[b], 0, 0, 0);
         a0 = a1 = a2 = a3 = 0u;
-        const uint32_t jn = e >> 3;
+        const uint32_t jn = e >> VM_JSHIFT;
         if (jn != VM_J_NONE) load_w(static_cast<int>(jn));
       }
     }

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FOVI_ABI_VERSION 32
+#define FOVI_ABI_VERSION 33
 
 enum fovi_dtype { FOVI_F32 = 0, FOVI_BF16 = 1, FOVI_F8E4M3 = 2 };
 enum fovi_interp { FOVI_NEAREST = 0, FOVI_BILINEAR = 1 };
@@ -251,9 +251,11 @@ typedef struct fovi_knnconv_args {
    * lanes (h = 0: columns 8 h .. 8 h + 7 of a step) adds, in round q, input row
    * vm_idx[2 * vm_off[p] + h * R + q] (rows >= n_in read as zeros) to a group sum, and the
    * round's event vm_ev[vm_off[p] + q] (bit 0: add the group sum to the slot sum; bit 1: end
-   * of the step's first slot, w_c_slot = 4; bit 2: end of the step; bits 3-15 at a step's
-   * end: the point's next active step, 0x1FFF none) closes sums as knn_tables.view_major_tables
-   * describes; vm_j0[p] is the point's first active step (-1: none). vm_w holds the weight
+   * of the step's first phase, w_c_slot = 4; bit 2: end of the step; bit 3 (at a step's end):
+   * half 0's second slot and half 1's first change halves; bit 4 (at phase ends): half 1 holds
+   * its slots in the other order; bits 5-15 at a step's end: the point's next active step,
+   * 0x7FF none) closes sums as knn_tables.view_major_tables describes; vm_j0[p] is the
+   * point's first active step (-1: none). vm_w holds the weight
    * in fragment order: 16 bytes per lane at ((j * vm_nb + b) * 64 + lane) * 16, lane l
    * holding columns 16 j + 8 (l / 32) .. + 7 of output channel 32 b + l % 32 (zero past c_out);
    * vm_nb >= c_out / 32 blocks, a multiple of vm_cb (1, 2, 3, 4 or 6 blocks per wave).

@@ -452,8 +452,9 @@ def _grouped_slot_sum(rows, group):
 def test_view_major_tables_rebuild_the_slot_sums(res_in, res_out, k, side, cp):
     """Emulates the view-major kernel's rounds in fp32 for 32 images at once: per point, each
     lane half adds its round's input row (a padding row: zeros) to a group sum; the events close
-    groups, end phase A (its sum rounded to bf16 into A dwords 0-1) and end steps (the last sum
-    into the rest, then the step's columns are emitted) and name the next active step. The A
+    groups, end phase A (its sum rounded to bf16 into A dwords 0-1, half 1 into 2-3 under
+    VM_Q) and end steps (the last sum into the rest, half 0's second and half 1's first slot
+    exchanged under VM_X, then the step's columns are emitted) and name the next active step. The A
     rows rebuilt this way equal the grouped fp32 slot sums of the CSR lists rounded to bf16 bit
     for bit, skipped steps are exactly those with no neighbour, and every round's input row is
     a real row or the padding row."""
@@ -474,7 +475,7 @@ def test_view_major_tables_rebuild_the_slot_sums(res_in, res_out, k, side, cp):
     xpad = np.concatenate([x, np.zeros((1, B, cp), np.float32)])
     bf = lambda a: torch.from_numpy(np.ascontiguousarray(a)).bfloat16().float().numpy()
     ptr, nbr = t["ptr"].numpy(), t["nbr"].numpy()
-    n_active = 0
+    n_active = n_x = n_q = 0
     for p in range(n_out):
         # the grouped slot sums of the CSR lists, [k_pad / cp slots, B, cp], rounded to bf16
         want = np.zeros((ks * spk, B, cp), np.float32)
@@ -506,11 +507,16 @@ def test_view_major_tables_rebuild_the_slot_sums(res_in, res_out, k, side, cp):
                 acc = (acc + part).astype(np.float32)
                 part[:] = 0
                 if e & (T.VM_P | T.VM_S):
-                    ph = 0 if (cp == 8 or e & T.VM_P) else 1
-                    a[:, ph] = bf(acc)
+                    for h in range(2):
+                        first = cp == 8 or (bool(e & T.VM_P) != (h == 1 and bool(e & T.VM_Q)))
+                        a[h, 0 if first else 1] = bf(acc[h])
                     acc[:] = 0
                 if e & T.VM_S:
                     assert j_cur is not None, "a step end past the point's active steps"
+                    if e & T.VM_X:       # half 0's second slot and half 1's first change halves
+                        a[0, 1], a[1, 0] = a[1, 0].copy(), a[0, 1].copy()
+                        n_x += 1
+                    n_q += bool(e & T.VM_Q)
                     for h in range(2):
                         if cp == 4:
                             got[4 * j_cur + 2 * h] = a[h, 0]
@@ -519,11 +525,13 @@ def test_view_major_tables_rebuild_the_slot_sums(res_in, res_out, k, side, cp):
                             got[2 * j_cur + h] = a[h, 0]
                     a[:] = 0
                     j_next = next(steps, None)
-                    assert (e >> 3) == (T.VM_J_NONE if j_next is None else j_next)
+                    assert (e >> T.VM_JSHIFT) == (T.VM_J_NONE if j_next is None else j_next)
                     j_cur = j_next
         assert j_cur is None, "every active step ends"
         np.testing.assert_array_equal(got, want)
     assert n_active == vt.steps
+    if cp == 4:                  # both other pairings occur
+        assert n_x > 0 and n_q > 0, (n_x, n_q)
     if k == 256:
         assert (np.diff(off) > 0).all() and vt.steps < n_out * ks
 
