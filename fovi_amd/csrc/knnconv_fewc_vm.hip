@@ -60,9 +60,11 @@ template <> struct VmRow<4> {
   static __device__ __forceinline__ T load(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
   }
+  template <int NCH>
   static __device__ __forceinline__ void acc(float* a, T v) {
     a[0] += __uint_as_float(v[0] << 16); a[1] += __uint_as_float(v[0] & 0xffff0000u);
-    a[2] += __uint_as_float(v[1] << 16); a[3] += __uint_as_float(v[1] & 0xffff0000u);
+    a[2] += __uint_as_float(v[1] << 16);
+    if constexpr (NCH == 4) a[3] += __uint_as_float(v[1] & 0xffff0000u);
   }
 };
 template <> struct VmRow<8> {
@@ -70,6 +72,7 @@ template <> struct VmRow<8> {
   static __device__ __forceinline__ T load(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
   }
+  template <int NCH>
   static __device__ __forceinline__ void acc(float* a, T v) {
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -79,7 +82,9 @@ template <> struct VmRow<8> {
   }
 };
 
-template <int CP, int CB>
+// NCH: channels summed per row; CP (channels >= c_in cleared by masks in the packed sums) or 3
+// (c_in = 3 of CP = 4: the fourth channel is neither summed nor packed, its bf16 is +0)
+template <int CP, int CB, int NCH>
 __global__ __launch_bounds__(VM_WAVES * 64, 2) void knnconv_fewc_vm_kernel(KnnParams p, VmTables t, int n_cg,
                                                                           int64_t total, int64_t padded,
                                                                           int vec_out) {
@@ -130,6 +135,7 @@ __global__ __launch_bounds__(VM_WAVES * 64, 2) void knnconv_fewc_vm_kernel(KnnPa
   float part[CP], sum[CP];
 #pragma unroll
   for (int c = 0; c < CP; ++c) { part[c] = 0.0f; sum[c] = 0.0f; }
+  constexpr bool MASK = NCH == CP;
   // channels >= c_in of the padded rows are cleared in the packed sums (whatever they hold:
   // the sums are per channel, so a NaN there stays in its own column)
   uint32_t cm[CP / 2];
@@ -140,24 +146,30 @@ __global__ __launch_bounds__(VM_WAVES * 64, 2) void knnconv_fewc_vm_kernel(KnnPa
 
   // one round: add this lane's row to the group sum, then the round's events (uniform)
   auto round = [&](const RowT& x, uint32_t e) {
-    R::acc(part, x);
+    R::template acc<NCH>(part, x);
     if (e & 7u) {
-#pragma unroll
-      for (int c = 0; c < CP; ++c) { sum[c] += part[c]; part[c] = 0.0f; }
       if (e & (VM_P | VM_S)) {
+        // the slot sum: the groups' sums added in order (a branch on whether the phase has
+        // more than one group, to use a lone group's sum as it is, cost C4 5%)
+        float v[CP];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) { v[c] = sum[c] + part[c]; sum[c] = 0.0f; part[c] = 0.0f; }
         if constexpr (CP == 4) {
           // phase A's slot into dwords 0-1, phase B's into 2-3; in half 1 the other way round
           // under VM_Q (selects: no indexed registers)
-          const uint32_t lo = cvt_pk_bf16(sum[0], sum[1]) & cm[0], hi = cvt_pk_bf16(sum[2], sum[3]) & cm[1];
+          uint32_t lo = cvt_pk_bf16(v[0], v[1]), hi = cvt_pk_bf16(v[2], NCH == 4 ? v[3] : 0.0f);
+          if constexpr (MASK) { lo &= cm[0]; hi &= cm[1]; }
           const bool first = ((e & VM_P) != 0) != (h1 && (e & VM_Q) != 0);
           a0 = first ? lo : a0; a1 = first ? hi : a1;
           a2 = first ? a2 : lo; a3 = first ? a3 : hi;
         } else {
-          a0 = cvt_pk_bf16(sum[0], sum[1]) & cm[0]; a1 = cvt_pk_bf16(sum[2], sum[3]) & cm[1];
-          a2 = cvt_pk_bf16(sum[4], sum[5]) & cm[2]; a3 = cvt_pk_bf16(sum[6], sum[7]) & cm[3];
+          a0 = cvt_pk_bf16(v[0], v[1]) & cm[0]; a1 = cvt_pk_bf16(v[2], v[3]) & cm[1];
+          a2 = cvt_pk_bf16(v[4], v[5]) & cm[2]; a3 = cvt_pk_bf16(v[6], v[7]) & cm[3];
         }
+      } else {
+        // a group of FC_GROUP closes inside the phase
 #pragma unroll
-        for (int c = 0; c < CP; ++c) sum[c] = 0.0f;
+        for (int c = 0; c < NCH; ++c) { sum[c] += part[c]; part[c] = 0.0f; }
       }
       if (e & VM_S) {
         if constexpr (CP == 4) {
@@ -255,26 +267,26 @@ __global__ __launch_bounds__(VM_WAVES * 64, 2) void knnconv_fewc_vm_kernel(KnnPa
   }
 }
 
-template <int CP, int CB>
+template <int CP, int CB, int NCH>
 int launch_vm(const KnnParams& p, const VmTables& t, int n_cg, int vec_out, hipStream_t s) {
   const int64_t n_vb = (p.B + VM_IMAGES - 1) / VM_IMAGES;
   const int64_t total = n_vb * p.Nout * n_cg;
   const int64_t padded = (total + 7) / 8 * 8;
   if (padded > 0x7fffffff) return 0;
   const size_t lds = static_cast<size_t>(VM_WAVES) * 32 * (CB * 32 + 8) * 2;
-  hipLaunchKernelGGL((knnconv_fewc_vm_kernel<CP, CB>), dim3(static_cast<unsigned>(padded)), dim3(VM_WAVES * 64),
+  hipLaunchKernelGGL((knnconv_fewc_vm_kernel<CP, CB, NCH>), dim3(static_cast<unsigned>(padded)), dim3(VM_WAVES * 64),
                      lds, s, p, t, n_cg, total, padded, vec_out);
   return 1;
 }
 
-template <int CP>
+template <int CP, int NCH>
 int launch_vm_cb(const KnnParams& p, const VmTables& t, int cb, int n_cg, int vec_out, hipStream_t s) {
   switch (cb) {
-    case 1: return launch_vm<CP, 1>(p, t, n_cg, vec_out, s);
-    case 2: return launch_vm<CP, 2>(p, t, n_cg, vec_out, s);
-    case 3: return launch_vm<CP, 3>(p, t, n_cg, vec_out, s);
-    case 4: return launch_vm<CP, 4>(p, t, n_cg, vec_out, s);
-    case 6: return launch_vm<CP, 6>(p, t, n_cg, vec_out, s);
+    case 1: return launch_vm<CP, 1, NCH>(p, t, n_cg, vec_out, s);
+    case 2: return launch_vm<CP, 2, NCH>(p, t, n_cg, vec_out, s);
+    case 3: return launch_vm<CP, 3, NCH>(p, t, n_cg, vec_out, s);
+    case 4: return launch_vm<CP, 4, NCH>(p, t, n_cg, vec_out, s);
+    case 6: return launch_vm<CP, 6, NCH>(p, t, n_cg, vec_out, s);
   }
   return 0;
 }
@@ -304,7 +316,8 @@ int launch_knnconv_fewc_vm(const KnnParams& p, const fovi_knnconv_args* a, int c
   const int n_cg = a->vm_nb / cb;
   const int vec_out = p.ys1 == 1 && p.ys2 % 8 == 0 && p.ys0 % 8 == 0 && p.Cout % 8 == 0 &&
                       reinterpret_cast<uintptr_t>(p.y) % 16 == 0;
-  return cp == 4 ? launch_vm_cb<4>(p, t, cb, n_cg, vec_out, s) : launch_vm_cb<8>(p, t, cb, n_cg, vec_out, s);
+  if (cp == 8) return launch_vm_cb<8, 8>(p, t, cb, n_cg, vec_out, s);
+  return p.C == 3 ? launch_vm_cb<4, 3>(p, t, cb, n_cg, vec_out, s) : launch_vm_cb<4, 4>(p, t, cb, n_cg, vec_out, s);
 }
 
 }  // namespace fovi

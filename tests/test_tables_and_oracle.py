@@ -504,13 +504,15 @@ def test_view_major_tables_rebuild_the_slot_sums(res_in, res_out, k, side, cp):
             for h in range(2):
                 part[h] = (part[h] + xpad[rows[h][q]]).astype(np.float32)
             if e & 7:
-                acc = (acc + part).astype(np.float32)
-                part[:] = 0
                 if e & (T.VM_P | T.VM_S):
+                    val = (acc + part).astype(np.float32)
                     for h in range(2):
                         first = cp == 8 or (bool(e & T.VM_P) != (h == 1 and bool(e & T.VM_Q)))
-                        a[h, 0 if first else 1] = bf(acc[h])
+                        a[h, 0 if first else 1] = bf(val[h])
                     acc[:] = 0
+                else:
+                    acc = (acc + part).astype(np.float32)
+                part[:] = 0
                 if e & T.VM_S:
                     assert j_cur is not None, "a step end past the point's active steps"
                     if e & T.VM_X:       # half 0's second slot and half 1's first change halves
