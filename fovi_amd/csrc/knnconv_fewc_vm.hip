@@ -184,8 +184,10 @@ __global__ __launch_bounds__(VM_WAVES * 64, 2) void knnconv_fewc_vm_kernel(KnnPa
         for (int b = 0; b < CB; ++b)
           acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, __builtin_bit_cast(bf16x8, wf[b]), acc[b], 0, 0, 0);
         a0 = a1 = a2 = a3 = 0u;
+        // unconditional (the last step loads step 0's fragments again): a branch here cost
+        // C4 4%
         const uint32_t jn = e >> VM_JSHIFT;
-        if (jn != VM_J_NONE) load_w(static_cast<int>(jn));
+        load_w(jn != VM_J_NONE ? static_cast<int>(jn) : 0);
       }
     }
   };
@@ -202,9 +204,14 @@ __global__ __launch_bounds__(VM_WAVES * 64, 2) void knnconv_fewc_vm_kernel(KnnPa
 #pragma unroll
     for (int u = 0; u < 4; ++u) x[4 + u] = R::load(rs, __umul24(in1[u], row_bytes) + img_off);
   };
-  // chunk c: its rows are in cur; the next chunk's rows are issued into nxt first
-  auto chunk = [&](int c, RowT (&cur)[8], RowT (&nxt)[8]) __attribute__((always_inline)) {
-    if (c + 1 < nch) {
+  // chunk c: its rows are in cur; the next chunk's rows are issued into nxt first,
+  // unconditionally where the caller knows they exist (then the compiler counts the loads in
+  // flight exactly at every wait; loads in a branch make it wait for all of them)
+  auto chunk = [&](int c, RowT (&cur)[8], RowT (&nxt)[8], bool inside) __attribute__((always_inline)) {
+    if (inside) {
+      issue_rows(nxt);
+      load_idx(c + 2);
+    } else if (c + 1 < nch) {
       issue_rows(nxt);
       if (c + 2 < nch) load_idx(c + 2);
     }
@@ -219,9 +226,16 @@ __global__ __launch_bounds__(VM_WAVES * 64, 2) void knnconv_fewc_vm_kernel(KnnPa
     issue_rows(xa);
     if (nch > 1) load_idx(1);
   }
-  for (int c = 0; c < nch; c += 2) {
-    chunk(c, xa, xb);
-    if (c + 1 < nch) chunk(c + 1, xb, xa);
+  // chunk pairs whose prefetches stay inside the point's rounds, then the last ones (C4 -5%;
+  // prefetching past the rounds everywhere, with out-of-range rows, cost C2 layer 1 4%)
+  int c = 0;
+  for (; c + 3 < nch; c += 2) {
+    chunk(c, xa, xb, true);
+    chunk(c + 1, xb, xa, true);
+  }
+  for (; c < nch; c += 2) {
+    chunk(c, xa, xb, false);
+    if (c + 1 < nch) chunk(c + 1, xb, xa, false);
   }
 
   // Epilogue: y = acc + bias (ReLU optional), channels-last rows of images v0 .. v0 + 31
