@@ -435,10 +435,11 @@ __device__ __forceinline__ void v5_body(const KnnParams& p, int ncb, int64_t til
     for (int i = 0; i < 4; ++i) enxt[i] = srcs[vn * V5_MT + rowm[i]];
 
     // e4m3: rows 1-2 of the unit are summed in the MFMA block, rows 3-4 after it only when a
-    // unit of this wave has more than two (a uniform branch; C5 -3%: 58% of the C5 waves'
-    // units have two rows at most). The sum of e4m3 values is exact in fp32, and the skipped
-    // zero rows would add +0 to a sum that is never -0: the same bits either way. bf16: the
-    // exposed adds of the other waves cost more than the skipped ones save (C3 +2%).
+    // unit of this wave has more than two (a uniform branch; C5 -3%: in 58% of the C5 stream's
+    // 16-entry windows no entry has more than two rows). Rows are still added in list order,
+    // and the skipped ones are the zero row, whose +0 leaves a sum that is never -0 unchanged:
+    // the same bits either way. bf16: the adds this exposes after the MFMA block in the other
+    // waves cost more than the skipped ones save (C3 +2%).
     const bool wave_full = !F8 || __builtin_amdgcn_ballot_w64(((ce[0] >> 16) & 0xffu) > 2u) != 0;
     Sum sum;
     if constexpr (F8) sum = unit_sum2(ce, pq); else sum = unit_sum4(ce, pq);
