@@ -270,6 +270,8 @@ def test_few_channel_fused_takes_every_geometry_the_host_accepts(geom):
     (64, 32, 49, None, 3, 64, 256, "relu"),   # C2 layer 1
     (32, 16, 25, None, 5, 96, 40, None),      # eight-channel rows, three 32-channel blocks
     (24, 12, 30, None, 4, 200, 33, "relu"),   # ragged: padding slots, 200 = 7 blocks (+1 zero block)
+    (32, 16, 25, None, 2, 64, 40, None),      # two channels of four-channel rows (masked sums)
+    (32, 16, 25, None, 1, 32, 17, "relu"),    # one channel
 ])
 def test_view_major_kernel_equals_the_two_pass_path(res_in, res_out, k, side, c_in, c_out, bsz, act):
     """Few-channel input written view-major (padded_input(..., view_major=True): the rows of
