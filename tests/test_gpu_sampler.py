@@ -222,11 +222,13 @@ def test_channels_last_views_with_odd_row_stride(mode, channels):
 @pytest.mark.parametrize("channels,layout,n_views,res", [(3, "planes", 37, 64), (3, "channels_last", 40, 64),
                                                          (4, "channels_last", 16, 64), (1, "planes", 20, 64),
                                                          (2, "planes", 19, 64), (3, "planes", 517, 128),
-                                                         (3, "channels_last", 512, 128)])
+                                                         (3, "channels_last", 512, 128), (1, "planes", 512, 128),
+                                                         (2, "planes", 520, 128), (4, "planes", 512, 128)])
 def test_view_major_output_equals_the_view_planes(mode, channels, layout, n_views, res):
     """Output into a view-major buffer [N, V, 4] (the rows of one point for all views
     adjacent, as the view-major kNN-conv kernel reads them; a sampler block writes 4 or 16
-    views of a point as one run, 16 at the C4 size) holds the samples of the ordinary
+    views of a point as one run, 16 at the C4 size, where nearest sampling from channel planes
+    takes eight views at a time, 1 to 4 channels) holds the samples of the ordinary
     [V, C, N] output bit for bit, for partial groups of views, and leaves the row elements past
     the channels untouched."""
     g = torch.Generator().manual_seed(16)
