@@ -272,6 +272,7 @@ def test_few_channel_fused_takes_every_geometry_the_host_accepts(geom):
     (24, 12, 30, None, 4, 200, 33, "relu"),   # ragged: padding slots, 200 = 7 blocks (+1 zero block)
     (32, 16, 25, None, 2, 64, 40, None),      # two channels of four-channel rows (masked sums)
     (32, 16, 25, None, 1, 32, 17, "relu"),    # one channel
+    (48, 12, 64, 8, 3, 96, 20, None),         # 8 x 8 ref grid: collisions on every point
 ])
 def test_view_major_kernel_equals_the_two_pass_path(res_in, res_out, k, side, c_in, c_out, bsz, act):
     """Few-channel input written view-major (padded_input(..., view_major=True): the rows of

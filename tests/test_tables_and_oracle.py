@@ -448,6 +448,8 @@ def _grouped_slot_sum(rows, group):
     (64, 32, 49, None, 4),     # C2 layer 1
     (32, 16, 25, None, 8),     # eight-channel rows: one phase per step
     (24, 12, 30, None, 4),     # ragged: padding slots in the last step
+    (48, 12, 64, 8, 4),        # 8 x 8 ref grid, collisions on every point
+    (40, 20, 49, None, 8),     # eight-channel rows, 49 slots
 ])
 def test_view_major_tables_rebuild_the_slot_sums(res_in, res_out, k, side, cp):
     """Emulates the view-major kernel's rounds in fp32 for 32 images at once: per point, each
